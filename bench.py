@@ -1,0 +1,212 @@
+"""Decode LI+TopK+Fetch throughput on one MI355X (BASELINE config 2 by default).
+
+One step = one decode round of the hot path over one batch of synthetic input that
+is already resident in HBM: lightning-indexer scoring of every context token of the
+64 requests, TopK-2048 per request, and the Fetch gather of the 2048 selected
+656-byte KV rows per request into a contiguous [64, 2048, 656] buffer.
+
+Prints one JSON line (rank 0): queries/s, per-kernel HIP-event timings, the roofline
+of the dominant kernel against MI355X's 8 TB/s HBM peak, and the CPU baseline (the
+oracle timed on a bounded sample of the same workload on this host).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+TOPK = 2048
+
+
+def parse():
+    p = argparse.ArgumentParser(description=__doc__)
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--config", default="c2", choices=["c1", "c2"])
+    p.add_argument("--seed", type=int, default=2026)
+    p.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU-baseline sample")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--copy-calibration", action="store_true",
+                   help="also run a plain 1 GiB device copy (for rocprof FETCH/WRITE_SIZE scaling)")
+    return p.parse_args()
+
+
+def algorithmic_bytes(wl, heads, has_qscale):
+    """Per-kernel algorithmic HBM bytes of one step (score materialisation excluded)."""
+    ctx = wl.ctx.astype(np.int64)
+    rows = len(ctx) * wl.rows_per_request
+    elem = 1 if wl.query.element_size() == 1 else 2
+    key_bytes = 128 * elem + (4 if wl.key_scale is not None else 0)
+    score = int((ctx * key_bytes).sum() + (4 * ((ctx + 127) // 128)).sum())
+    score += rows * (heads * 128 * elem + heads * wl.weights.element_size() + (heads * 4 if has_qscale else 0))
+    row_bytes = int(wl.kv_cache.shape[2])
+    live = np.minimum(ctx, TOPK).repeat(wl.rows_per_request)
+    topk = rows * TOPK * 4
+    gather = int(live.sum()) * row_bytes * 2
+    return {"indexer": score, "topk": topk, "fetch": gather}
+
+
+def cpu_baseline(torch, wl, rot, budget_s):
+    """The oracle (oracle/indexer.py) on the first rows of the same workload until the
+    time budget is spent: LI keys, TopK-2048, Fetch gather, per query row."""
+    from oracle import indexer as ref
+
+    try:
+        from threadpoolctl import threadpool_info
+
+        blas_threads = max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
+    except Exception:  # noqa: BLE001 - informational only
+        blas_threads = 1
+    q = ref.fp8_e4m3_decode(wl.query.view(torch.uint8).cpu().numpy()) if wl.query.element_size() == 1 \
+        else wl.query.float().cpu().numpy()
+    w = wl.weights.float().cpu().numpy()
+    table = wl.block_table.cpu().numpy()
+    ks_all = None if wl.key_scale is None else wl.key_scale.cpu().numpy()
+    kv = wl.kv_cache.cpu().numpy()
+    keys_dev = wl.keys
+    done, elapsed = 0, 0.0
+    for r in range(rot.rows):
+        b = r // wl.rows_per_request
+        v = int(wl.ctx[b])
+        pages = table[b, :(v + 127) // 128]
+        kraw = keys_dev[torch.from_numpy(pages.astype(np.int64)).to(keys_dev.device)]
+        kvals = ref.fp8_e4m3_decode(kraw.view(torch.uint8).cpu().numpy()) if kraw.element_size() == 1 \
+            else kraw.float().cpu().numpy()
+        kvals = kvals.reshape(-1, 128)[:v]
+        ks = None if ks_all is None else ks_all[pages].reshape(-1)[:v]
+        t0 = time.perf_counter()
+        keys = ref.li_keys(q[r], kvals, w[r], None, ks)
+        sel = ref.topk_reference(keys, v)
+        ref.fetch_gather(kv, table[b:b + 1], sel[None, :])
+        elapsed += time.perf_counter() - t0
+        done += 1
+        if elapsed >= budget_s:
+            break
+    return {"value": round(done / elapsed, 3), "unit": "queries/s", "cores": int(blas_threads),
+            "kind": "port",
+            "sample": f"{done} of {rot.rows} query rows of the same workload (numpy oracle: float64 dot "
+                      f"products on {blas_threads} BLAS threads, single-threaded head reduction, TopK, gather); "
+                      f"{elapsed:.1f} s; host has {os.cpu_count()} logical CPUs"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU only (the path shards by request with no "
+              "exchange; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    import kvip_amd
+    from kvip_amd import synthetic
+
+    device = "cuda:0"
+    torch.cuda.set_device(0)
+    wl = synthetic.config_workload(torch, args.config, device, seed=args.seed)
+    rot, upd, fwd = synthetic.bind(torch, kvip_amd, wl)
+    heads = int(wl.query.shape[1])
+    per_kernel_bytes = algorithmic_bytes(wl, heads, wl.query_scale is not None)
+    step_bytes = sum(per_kernel_bytes.values())
+
+    for _ in range(args.warmup):
+        fwd()
+    torch.cuda.synchronize()
+    if int(rot.status.item()) != 0:
+        raise RuntimeError(f"device status {int(rot.status.item())} after warm-up")
+
+    stream = torch.cuda.current_stream()
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s in range(args.steps):
+        e = ev[s]
+        e[0].record(stream)
+        fwd.score()
+        e[1].record(stream)
+        fwd.select()
+        e[2].record(stream)
+        fwd.fetch()
+        e[3].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    times = {name: float(np.mean([ev[s][i].elapsed_time(ev[s][i + 1]) for s in range(args.steps)]))
+             for i, name in enumerate(["indexer", "topk", "fetch"])}
+    event_span_ms = ev[0][0].elapsed_time(ev[-1][3])
+    ms_per_step = wall * 1e3 / args.steps
+
+    # Whole round as one hipGraph replay (informational).
+    graph_ms = None
+    try:
+        side = torch.cuda.Stream()
+        side.wait_stream(stream)
+        with torch.cuda.stream(side):
+            fwd()
+        stream.wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            fwd()
+        for _ in range(5):
+            graph.replay()
+        torch.cuda.synchronize()
+        g0 = time.perf_counter()
+        for _ in range(args.steps):
+            graph.replay()
+        torch.cuda.synchronize()
+        graph_ms = (time.perf_counter() - g0) * 1e3 / args.steps
+    except Exception as exc:  # noqa: BLE001 - informational only
+        graph_ms = f"capture failed: {exc}"
+
+    if args.copy_calibration:
+        src = torch.empty(1 << 30, dtype=torch.uint8, device=device)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+
+    rows = rot.rows
+    dominant = max(times, key=times.get)
+    achieved = per_kernel_bytes[dominant] / (times[dominant] * 1e-3) / 1e9
+    result = {
+        "metric": "decode queries/sec LI+TopK+Fetch, B=64 ctx 32k; achieved HBM GB/s vs peak",
+        "value": round(rows * args.steps / wall, 1),
+        "unit": "queries/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8" if wl.query.element_size() == 1 else "bf16",
+        "data": "synthetic (seeded N(0,1) fp8 Q/K, U(0.5,2) key scales, random KV bytes)",
+        "config": {"workload": f"{args.config}: decode LI+TopK-2048+Fetch, batch {wl.batch}, "
+                               f"ctx U[{int(wl.ctx.min())},{int(wl.ctx.max())}] (mean {wl.ctx.mean():.0f}), "
+                               f"{heads} heads x 128, KV rows {int(wl.kv_cache.shape[2])} B",
+                   "batch": wl.batch, "context_tokens": int(wl.ctx.sum()), "seed": args.seed},
+        "hbm_gbs_step": round(step_bytes / (ms_per_step * 1e-3) / 1e9, 1),
+        "step_bytes": step_bytes,
+        "kernels": {k: {"ms": round(v, 5), "bytes": per_kernel_bytes[k],
+                        "gbs": round(per_kernel_bytes[k] / (v * 1e-3) / 1e9, 1)} for k, v in times.items()},
+        "event_span_ms_per_step": round(event_span_ms / args.steps, 4),
+        "graph_ms_per_step": graph_ms if not isinstance(graph_ms, float) else round(graph_ms, 4),
+        "roofline": {"kernel": dominant, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(torch, wl, rot, args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,143 @@
+/*
+ * kvip_hip.h - C ABI of the MI355X (gfx950) lightning-indexer-with-fetch library
+ * (libkvip_hip.so).
+ *
+ * Plain pointers, sizes and a hipStream_t passed as void*. Every entry point only
+ * enqueues work on the given stream: no allocation, no host synchronisation, no
+ * device-to-host read, so each one can be captured into a hipGraph. Device-side
+ * problems (out-of-range block ids or tokens, inconsistent histograms) are reported
+ * by OR-ing KVIP_STATUS_* bits into an optional device status word; host-side
+ * argument errors return KVIP_ERR_INVALID before anything is launched.
+ *
+ * Reference interfaces replaced (paths relative to the KVIP reference tree):
+ *   kvip_hip_lifetch_forward  <- kvip_lifetch_streaming_forward
+ *                                (csrc/operators/lightning_indexer_with_fetch/include/api.h:7,
+ *                                 op_host/launch.cpp:76-83)
+ *   kvip_hip_indexer_decode   <- v9_li / QuantLightningIndexerKernel scoring
+ *                                (op_host/launch.cpp:16; op_kernel/indexer.cpp:23-86;
+ *                                 op_kernel/indexer/indexer_score.h:384-426)
+ *   kvip_hip_topk             <- LITopk<uint16_t> inside QLIVector::ProcessTopK
+ *                                (op_kernel/indexer/indexer_vector.h:799-973; topk.h:122-197)
+ *   kvip_hip_fetch_gather     <- kvaf_device::KvafBatchGetDevice as called by FetchQueryGroup
+ *                                (op_kernel/streaming.cpp:365-500, :445;
+ *                                 patches/kvaf-ubmem-device-get.patch:41-90)
+ */
+#ifndef KVIP_HIP_H
+#define KVIP_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KVIP_HIP_ABI_VERSION 1u
+
+#define KVIP_TOPK 2048
+#define KVIP_BLOCK_TOKENS 128
+#define KVIP_INDEX_DIM 128
+#define KVIP_KV_ROW_BYTES 656
+
+/* Return codes: 0 on success, KVIP_ERR_INVALID when the arguments are rejected
+ * (nothing launched), otherwise the hipError_t reported by the launch. Same
+ * convention as the reference's kvip_lifetch_streaming_forward (launch.cpp:76-83). */
+#define KVIP_OK 0u
+#define KVIP_ERR_INVALID 100000u
+
+/* Element types. */
+#define KVIP_DTYPE_FP8_E4M3 0
+#define KVIP_DTYPE_BF16 1
+#define KVIP_DTYPE_FP32 2
+
+/* Device status bits, OR-ed into *status when status is not NULL. */
+#define KVIP_STATUS_BAD_BLOCK 1u     /* a block-table entry outside [0, num_blocks) */
+#define KVIP_STATUS_HISTOGRAM 2u     /* TopK histogram inconsistent with the row length */
+#define KVIP_STATUS_BAD_TOKEN 4u     /* a TopK token id outside the block table */
+
+/* Lightning-indexer scoring over a paged index-K cache.
+ *
+ * For query row r of request b = r / rows_per_request and token t < valid(r):
+ *   w'_h      = float(weights[r,h]) * query_scale[r,h]
+ *   qk_h      = sum_d q[r,h,d] * k[t,d]                (fp32 accumulation)
+ *   score     = key_scale[t] * sum_h max(qk_h, 0) * w'_h
+ *   key[r,t]  = sortable(bf16_round_half_away(score))
+ * valid(r) = min(seq_lens[b], query_ends[r]) (query_ends NULL: seq_lens[b]).
+ * The kernel also adds the 256-bin histogram of key>>8 over t < valid(r) into
+ * histogram[r, :]; that buffer must be zero before the first launch and is
+ * re-zeroed by kvip_hip_topk when it consumes it. */
+typedef struct KvipIndexerArgs {
+    const void* query;           /* [rows, heads, 128], fp8 e4m3 or bf16 (qk_dtype) */
+    const void* weights;         /* [rows, heads], fp32 or bf16 (weight_dtype) */
+    const float* query_scale;    /* [rows, heads], or NULL for 1.0 */
+    const void* keys;            /* index-K row t of block k: keys + k*key_block_stride + (t%128)*128*elem */
+    const float* key_scale;      /* per-token scale key_scale[k*scale_block_stride + t%128], or NULL for 1.0 */
+    const int32_t* block_table;  /* [batch, max_blocks] block ids */
+    const int32_t* seq_lens;     /* [batch] context tokens per request */
+    const int32_t* query_ends;   /* [rows] per-row visible bound (<= 0: padding row), or NULL */
+    uint16_t* score_keys;        /* [rows, key_stride] sortable bf16 keys */
+    uint32_t* histogram;         /* [rows, 256] high-byte counts */
+    uint32_t* status;            /* device status word, or NULL */
+    int64_t key_block_stride;    /* bytes between index-K blocks (multiple of 16) */
+    int64_t scale_block_stride;  /* floats between key-scale blocks */
+    int32_t batch;               /* requests */
+    int32_t rows_per_request;    /* 1, 2 or 4 query rows per request (decode + MTP) */
+    int32_t heads;               /* 32 or 64 index heads */
+    int32_t max_blocks;          /* block_table row length */
+    int32_t num_blocks;          /* valid block ids are [0, num_blocks) */
+    int32_t key_stride;          /* score_keys row stride: multiple of 8, >= max_blocks*128 */
+    int32_t qk_dtype;            /* KVIP_DTYPE_FP8_E4M3 or KVIP_DTYPE_BF16 */
+    int32_t weight_dtype;        /* KVIP_DTYPE_FP32 or KVIP_DTYPE_BF16 */
+} KvipIndexerArgs;
+
+/* Exact TopK-2048 of sortable uint16 keys per query row.
+ * valid < 2048: out = [0, 1, ..., valid-1, -1, ...].
+ * valid >= 2048: the 2048 tokens that come first in the order (key desc, index asc),
+ * written as the tokens with key > kth in ascending index order followed by the
+ * tokens with key == kth in ascending index order. */
+typedef struct KvipTopkArgs {
+    const uint16_t* score_keys;  /* [rows, key_stride] */
+    uint32_t* histogram;         /* [rows, 256] from kvip_hip_indexer_decode (re-zeroed here), or NULL */
+    const int32_t* seq_lens;     /* [batch] */
+    const int32_t* query_ends;   /* [rows] or NULL */
+    int32_t* topk;               /* [rows, 2048] token ids, -1 = empty */
+    uint32_t* status;            /* device status word, or NULL */
+    int32_t batch;
+    int32_t rows_per_request;
+    int32_t key_stride;          /* multiple of 8 */
+} KvipTopkArgs;
+
+/* Gather of the selected KV rows from a paged KV cache into a contiguous buffer:
+ *   output[r, i, :] = kv row topk[r, i] of request r / rows_per_request, or zeros for -1. */
+typedef struct KvipFetchArgs {
+    const int32_t* topk;         /* [rows, 2048] */
+    const uint8_t* kv_cache;     /* KV row t of block k: kv_cache + k*kv_block_stride + (t%128)*row_stride */
+    const int32_t* block_table;  /* [batch, max_blocks] */
+    uint8_t* output;             /* [rows, 2048, row_bytes] */
+    uint32_t* status;            /* device status word, or NULL */
+    int64_t kv_block_stride;     /* bytes, multiple of 16 */
+    int32_t row_stride;          /* bytes between rows of one block, multiple of 16 */
+    int32_t row_bytes;           /* bytes per KV row, multiple of 16 (656 for MLA latent rows) */
+    int32_t batch;
+    int32_t rows_per_request;
+    int32_t max_blocks;
+    int32_t num_blocks;
+} KvipFetchArgs;
+
+/* One decode round: scoring -> TopK-2048 -> Fetch gather, stream-ordered. */
+typedef struct KvipLIFetchArgs {
+    KvipIndexerArgs indexer;
+    KvipTopkArgs topk;
+    KvipFetchArgs fetch;
+} KvipLIFetchArgs;
+
+uint32_t kvip_hip_abi_version(void);
+uint32_t kvip_hip_indexer_decode(const KvipIndexerArgs* args, void* stream);
+uint32_t kvip_hip_topk(const KvipTopkArgs* args, void* stream);
+uint32_t kvip_hip_fetch_gather(const KvipFetchArgs* args, void* stream);
+uint32_t kvip_hip_lifetch_forward(const KvipLIFetchArgs* args, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KVIP_HIP_H */

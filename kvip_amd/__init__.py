@@ -1,0 +1,30 @@
+"""MI355X-native lightning-indexer-with-fetch (KVIP's LIFetch path) on gfx950.
+
+Public names are resolved lazily, as in the reference package
+(python/kvip/__init__.py:18-43). Every compute call goes through libkvip_hip.so;
+there is no CPU fallback.
+"""
+from importlib import import_module
+
+__all__ = [
+    "LIFetch",
+    "LIFetchBinding",
+    "ContiguousFetch",
+    "build_libraries",
+    "load_library",
+]
+
+_EXPORTS = {
+    "LIFetch": ("operators.lifetch.forward", "LIFetchForward"),
+    "LIFetchBinding": ("operators.lifetch.binding", "LIFetchBinding"),
+    "ContiguousFetch": ("operators.lifetch.binding", "ContiguousFetch"),
+    "build_libraries": ("runtime.build", "build_libraries"),
+    "load_library": ("runtime.abi", "load_library"),
+}
+
+
+def __getattr__(name):
+    if name not in _EXPORTS:
+        raise AttributeError(name)
+    module, symbol = _EXPORTS[name]
+    return getattr(import_module(f"{__name__}.{module}"), symbol)

@@ -1,0 +1,93 @@
+// Device helpers shared by the gfx950 kernels of libkvip_hip.so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "kvip_hip.h"
+
+#define KVIP_DEVICE __device__ __forceinline__
+
+namespace kvip {
+
+constexpr int kTopK = KVIP_TOPK;
+constexpr int kBlockTokens = KVIP_BLOCK_TOKENS;
+constexpr int kIndexDim = KVIP_INDEX_DIM;
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+
+KVIP_DEVICE int lane_id() { return __lane_id(); }
+
+// fp32 -> bf16 bits, rounding half away from zero on the magnitude (the Ascend
+// CAST_ROUND mode the reference scores use: tests/operators/lifetch/support/
+// workloads.py:233-235, op_kernel/indexer/indexer_score.h:105-140).
+KVIP_DEVICE uint32_t bf16_bits_half_away(float x) {
+    return (__float_as_uint(x) + 0x8000u) >> 16;
+}
+
+// bf16 bits -> order-preserving uint16 key (op_kernel/indexer/score_common.h:66-97):
+// the canonical NaN 0x7FC0 becomes 0xFFFF first; negative values are inverted,
+// non-negative values get the sign bit flipped.
+KVIP_DEVICE uint32_t sortable_key(uint32_t bits) {
+    bits = (bits == 0x7FC0u) ? 0xFFFFu : bits;
+    return (bits & 0x8000u) ? (~bits & 0xFFFFu) : (bits ^ 0x8000u);
+}
+
+KVIP_DEVICE float bf16_to_float(uint16_t bits) { return __uint_as_float(static_cast<uint32_t>(bits) << 16); }
+
+KVIP_DEVICE void report(uint32_t* status, uint32_t bits) {
+    if (status != nullptr && bits != 0) atomicOr(status, bits);
+}
+
+// Histogram add where the 64 lanes of a wave often share a bin: one LDS atomic per
+// distinct bin present in the wave. Must be called by the whole wave.
+KVIP_DEVICE void wave_hist_add(uint32_t* hist, uint32_t bin, bool live) {
+    unsigned long long pending = __ballot(live);
+    while (pending) {
+        const int leader = __ffsll(pending) - 1;
+        const uint32_t lead_bin = __shfl(bin, leader);
+        const bool same = live && bin == lead_bin;
+        const unsigned long long group = __ballot(same);
+        if (lane_id() == leader) atomicAdd(&hist[lead_bin], static_cast<uint32_t>(__popcll(group)));
+        live = live && !same;
+        pending &= ~group;
+    }
+}
+
+KVIP_DEVICE uint32_t wave_inclusive_scan(uint32_t v) {
+    const int lane = lane_id();
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const uint32_t t = __shfl_up(v, d);
+        if (lane >= d) v += t;
+    }
+    return v;
+}
+
+// Exclusive prefix sum over the whole workgroup (blockDim.x a multiple of 64, at most
+// 1024). `wave_sums` is __shared__ scratch of blockDim.x/64 words. Returns the
+// exclusive prefix of this thread and writes the workgroup total into *total.
+// Contains two __syncthreads and must be reached by every thread.
+KVIP_DEVICE uint32_t block_exclusive_scan(uint32_t v, uint32_t* wave_sums, uint32_t* total) {
+    const int lane = lane_id();
+    const int wave = threadIdx.x >> 6;
+    const int waves = blockDim.x >> 6;
+    const uint32_t incl = wave_inclusive_scan(v);
+    __syncthreads();  // previous users of wave_sums are done
+    if (lane == 63) wave_sums[wave] = incl;
+    __syncthreads();
+    uint32_t before = 0, all = 0;
+    for (int w = 0; w < waves; ++w) {
+        const uint32_t s = wave_sums[w];
+        before += (w < wave) ? s : 0u;
+        all += s;
+    }
+    *total = all;
+    return before + incl - v;
+}
+
+}  // namespace kvip

@@ -1,0 +1,188 @@
+// Exact TopK-2048 over sortable uint16 score keys, one 1024-thread workgroup per
+// query row, as a two-level radix select:
+//   1. high-byte histogram (taken from the scoring kernel, or built here) -> the bin
+//      that holds the 2048th largest key;
+//   2. low-byte histogram of the keys in that bin -> the kth key K and the number of
+//      keys strictly above it (n_gt);
+//   3. one ordered emission pass: keys > K in ascending token order, then the first
+//      2048 - n_gt keys == K in ascending token order.
+// The selected set equals the first 2048 entries of the order (key desc, token asc),
+// which is what the reference's trunked GT-then-EQ select with prior-winner-first
+// merging produces (op_kernel/indexer/topk.h:155-187, topk_common.h:1000-1067,
+// :1094-1122). Row bounds follow QLIVector::ProcessTopK
+// (op_kernel/indexer/indexer_vector.h:849-873, :943-957): valid <= 0 -> all -1,
+// valid < 2048 -> [0..valid-1, -1...].
+#include "kvip_device.h"
+
+namespace kvip {
+namespace {
+
+constexpr int kTopkThreads = 1024;
+constexpr int kKeysPerThread = 8;
+constexpr int kTileKeys = kTopkThreads * kKeysPerThread;
+
+struct Keys8 {
+    uint32_t k[kKeysPerThread];
+    int count;  // keys of this thread below `valid`
+};
+
+KVIP_DEVICE Keys8 load_keys(const uint16_t* keys, int idx0, int valid) {
+    Keys8 r;
+    if (idx0 + kKeysPerThread <= valid) {
+        const v4i v = *reinterpret_cast<const v4i*>(keys + idx0);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            r.k[2 * j] = static_cast<uint32_t>(v[j]) & 0xFFFFu;
+            r.k[2 * j + 1] = static_cast<uint32_t>(v[j]) >> 16;
+        }
+        r.count = kKeysPerThread;
+    } else {
+        r.count = max(0, min(kKeysPerThread, valid - idx0));
+#pragma unroll
+        for (int j = 0; j < kKeysPerThread; ++j) r.k[j] = j < r.count ? keys[idx0 + j] : 0u;
+    }
+    return r;
+}
+
+// Finds the bin holding the target-th largest element of a 256-bin histogram
+// (bin 255 = largest keys). Writes {bin, count strictly above the bin} to sel[0..1]
+// (sel[0] stays -1 when the histogram holds fewer than `target` elements).
+KVIP_DEVICE void select_bin(const uint32_t* hist, uint32_t target, int* sel, uint32_t* wave_sums) {
+    const int tid = threadIdx.x;
+    const uint32_t c = tid < 256 ? hist[255 - tid] : 0u;
+    uint32_t total;
+    const uint32_t excl = block_exclusive_scan(c, wave_sums, &total);
+    if (tid < 256 && c != 0u && excl < target && excl + c >= target) {
+        sel[0] = 255 - tid;
+        sel[1] = static_cast<int>(excl);
+    }
+    __syncthreads();
+}
+
+__global__ __launch_bounds__(kTopkThreads) void topk_kernel(const KvipTopkArgs p) {
+    __shared__ uint32_t s_hist[256];
+    __shared__ uint32_t s_wave[kTopkThreads / 64];
+    __shared__ int s_sel[4];
+
+    const int tid = threadIdx.x;
+    const int row = blockIdx.x;
+    const int b = row / p.rows_per_request;
+    int valid = max(p.seq_lens[b], 0);
+    if (p.query_ends != nullptr) valid = min(valid, p.query_ends[row]);
+    valid = min(max(valid, 0), p.key_stride);
+    int32_t* out = p.topk + static_cast<size_t>(row) * kTopK;
+    const uint16_t* keys = p.score_keys + static_cast<size_t>(row) * p.key_stride;
+    uint32_t* ghist = p.histogram != nullptr ? p.histogram + static_cast<size_t>(row) * 256 : nullptr;
+
+    if (valid < kTopK) {
+        for (int i = tid; i < kTopK; i += kTopkThreads) out[i] = i < valid ? i : -1;
+        if (ghist != nullptr && tid < 256) ghist[tid] = 0u;
+        return;
+    }
+
+    // Level 1: high byte.
+    if (tid < 256) s_hist[tid] = ghist != nullptr ? ghist[tid] : 0u;
+    if (tid == 0) {
+        s_sel[0] = -1;
+        s_sel[2] = -1;
+    }
+    __syncthreads();
+    if (ghist != nullptr) {
+        if (tid < 256) ghist[tid] = 0u;  // ready for the next scoring launch
+    } else {
+        for (int base = tid * kKeysPerThread; base < valid; base += kTileKeys) {
+            const Keys8 r = load_keys(keys, base, valid);
+#pragma unroll
+            for (int j = 0; j < kKeysPerThread; ++j) {
+                wave_hist_add(s_hist, r.k[j] >> 8, j < r.count);
+            }
+        }
+    }
+    __syncthreads();
+    select_bin(s_hist, kTopK, s_sel, s_wave);
+    const int hb = s_sel[0];
+    const uint32_t gt_hi = static_cast<uint32_t>(s_sel[1]);
+    if (hb < 0) {
+        for (int i = tid; i < kTopK; i += kTopkThreads) out[i] = -1;
+        if (tid == 0) report(p.status, KVIP_STATUS_HISTOGRAM);
+        return;
+    }
+
+    // Level 2: low byte among keys whose high byte is hb.
+    if (tid < 256) s_hist[tid] = 0u;
+    __syncthreads();
+    for (int base = tid * kKeysPerThread; base < valid; base += kTileKeys) {
+        const Keys8 r = load_keys(keys, base, valid);
+#pragma unroll
+        for (int j = 0; j < kKeysPerThread; ++j) {
+            if (j < r.count && static_cast<int>(r.k[j] >> 8) == hb) atomicAdd(&s_hist[r.k[j] & 0xFFu], 1u);
+        }
+    }
+    __syncthreads();
+    select_bin(s_hist, kTopK - gt_hi, s_sel + 2, s_wave);
+    if (s_sel[2] < 0) {
+        for (int i = tid; i < kTopK; i += kTopkThreads) out[i] = -1;
+        if (tid == 0) report(p.status, KVIP_STATUS_HISTOGRAM);
+        return;
+    }
+    const uint32_t kth = (static_cast<uint32_t>(hb) << 8) | static_cast<uint32_t>(s_sel[2]);
+    const uint32_t n_gt = gt_hi + static_cast<uint32_t>(s_sel[3]);
+    const uint32_t need = kTopK - n_gt;
+
+    // Level 3: ordered emission. gt_base/eq_base are identical in every thread.
+    uint32_t gt_base = 0, eq_base = 0;
+    for (int tile = 0; tile < valid; tile += kTileKeys) {
+        const int idx0 = tile + tid * kKeysPerThread;
+        const Keys8 r = load_keys(keys, idx0, valid);
+        uint32_t ngt = 0, neq = 0;
+#pragma unroll
+        for (int j = 0; j < kKeysPerThread; ++j) {
+            const bool in = j < r.count;
+            ngt += (in && r.k[j] > kth) ? 1u : 0u;
+            neq += (in && r.k[j] == kth) ? 1u : 0u;
+        }
+        uint32_t total;
+        const uint32_t excl = block_exclusive_scan((ngt << 16) | neq, s_wave, &total);
+        uint32_t pg = gt_base + (excl >> 16);
+        uint32_t pe = eq_base + (excl & 0xFFFFu);
+#pragma unroll
+        for (int j = 0; j < kKeysPerThread; ++j) {
+            if (j < r.count) {
+                if (r.k[j] > kth) {
+                    out[pg++] = idx0 + j;
+                } else if (r.k[j] == kth) {
+                    if (pe < need) out[n_gt + pe] = idx0 + j;
+                    ++pe;
+                }
+            }
+        }
+        gt_base += total >> 16;
+        eq_base += total & 0xFFFFu;
+        if (gt_base >= n_gt && eq_base >= need) break;  // uniform
+    }
+}
+
+}  // namespace
+
+uint32_t validate_topk(const KvipTopkArgs* a) {
+    if (a == nullptr) return KVIP_ERR_INVALID;
+    const bool ok = a->score_keys != nullptr && a->seq_lens != nullptr && a->topk != nullptr &&
+                    (a->rows_per_request == 1 || a->rows_per_request == 2 || a->rows_per_request == 4) &&
+                    a->batch >= 1 && static_cast<int64_t>(a->batch) * a->rows_per_request <= (1 << 24) &&
+                    a->key_stride >= 8 && a->key_stride % 8 == 0 && a->key_stride <= (1 << 24) &&
+                    (reinterpret_cast<uintptr_t>(a->score_keys) & 15u) == 0;
+    return ok ? KVIP_OK : KVIP_ERR_INVALID;
+}
+
+hipError_t launch_topk(const KvipTopkArgs& a, hipStream_t stream) {
+    hipLaunchKernelGGL(topk_kernel, dim3(a.batch * a.rows_per_request), dim3(kTopkThreads), 0, stream, a);
+    return hipGetLastError();
+}
+
+}  // namespace kvip
+
+extern "C" uint32_t kvip_hip_topk(const KvipTopkArgs* args, void* stream) {
+    const uint32_t rc = kvip::validate_topk(args);
+    if (rc != KVIP_OK) return rc;
+    return static_cast<uint32_t>(kvip::launch_topk(*args, static_cast<hipStream_t>(stream)));
+}

@@ -1,0 +1,51 @@
+"""`kvip_amd.LIFetch(rotating, update)`: the graph-capturable decode round.
+
+Keeps the reference's call shape (python/kvip/operators/lifetch/forward.py:7-17,
+streaming.py:115-131): construction validates and packs every device address once;
+``forward()`` takes no arguments, enqueues the round on the current stream through
+one C call and returns None. It never allocates, synchronises or reads back, so it
+can be captured into a hipGraph; argument problems raise ValueError at construction,
+a failed launch raises RuntimeError.
+"""
+from __future__ import annotations
+
+import ctypes
+
+from kvip_amd.runtime import abi
+from kvip_amd.operators.lifetch.binding import ContiguousFetch, LIFetchBinding
+
+
+class LIFetchForward:
+    def __init__(self, rotating, update):
+        if not isinstance(rotating, LIFetchBinding):
+            raise ValueError("LIFetch rotating must be a kvip_amd LIFetchBinding")
+        if not isinstance(update, ContiguousFetch):
+            raise ValueError("LIFetch update must be a kvip_amd ContiguousFetch")
+        if update.rotating is not rotating:
+            raise ValueError("Fetch destination was built for another LIFetch binding")
+        if rotating.device != update.device:
+            raise ValueError("Fetch and Index update must use the same device")
+        self.rotating, self.update, self.torch = rotating, update, rotating.torch
+        self.library = abi.load_library()
+        self.args = abi.LIFetchArgs(rotating.indexer_args(), rotating.topk_args(), update.fetch_args())
+        self._args_ref = ctypes.byref(self.args)
+        # Stage-wise argument blocks for score()/select()/fetch().
+        self._indexer = ctypes.byref(self.args.indexer)
+        self._topk = ctypes.byref(self.args.topk)
+        self._fetch = ctypes.byref(self.args.fetch)
+
+    def _stream(self):
+        return abi.stream_handle(self.torch, self.rotating.device)
+
+    def __call__(self):
+        abi.check(self.library.kvip_hip_lifetch_forward(self._args_ref, self._stream()), "LIFetch forward")
+
+    # Individual stages (same kernels as the fused forward).
+    def score(self):
+        abi.check(self.library.kvip_hip_indexer_decode(self._indexer, self._stream()), "LI scoring")
+
+    def select(self):
+        abi.check(self.library.kvip_hip_topk(self._topk, self._stream()), "TopK")
+
+    def fetch(self):
+        abi.check(self.library.kvip_hip_fetch_gather(self._fetch, self._stream()), "Fetch gather")

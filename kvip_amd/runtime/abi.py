@@ -1,0 +1,115 @@
+"""ctypes view of include/kvip_hip.h and the loader of libkvip_hip.so.
+
+The library is the only compute path: there is no CPU or PyTorch fallback. Loading
+fails loudly when the in-tree library is missing or was built for another ABI.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+LIBRARY = Path(__file__).resolve().parents[1] / "_lib" / "libkvip_hip.so"
+ABI_VERSION = 1
+
+KVIP_OK = 0
+KVIP_ERR_INVALID = 100000
+
+DTYPE_FP8_E4M3 = 0
+DTYPE_BF16 = 1
+DTYPE_FP32 = 2
+
+STATUS_BAD_BLOCK = 1
+STATUS_HISTOGRAM = 2
+STATUS_BAD_TOKEN = 4
+
+_p = ctypes.c_void_p
+_i32 = ctypes.c_int32
+_i64 = ctypes.c_int64
+
+
+class IndexerArgs(ctypes.Structure):
+    _fields_ = [
+        ("query", _p), ("weights", _p), ("query_scale", _p), ("keys", _p), ("key_scale", _p),
+        ("block_table", _p), ("seq_lens", _p), ("query_ends", _p), ("score_keys", _p),
+        ("histogram", _p), ("status", _p),
+        ("key_block_stride", _i64), ("scale_block_stride", _i64),
+        ("batch", _i32), ("rows_per_request", _i32), ("heads", _i32), ("max_blocks", _i32),
+        ("num_blocks", _i32), ("key_stride", _i32), ("qk_dtype", _i32), ("weight_dtype", _i32),
+    ]
+
+
+class TopkArgs(ctypes.Structure):
+    _fields_ = [
+        ("score_keys", _p), ("histogram", _p), ("seq_lens", _p), ("query_ends", _p), ("topk", _p),
+        ("status", _p),
+        ("batch", _i32), ("rows_per_request", _i32), ("key_stride", _i32),
+    ]
+
+
+class FetchArgs(ctypes.Structure):
+    _fields_ = [
+        ("topk", _p), ("kv_cache", _p), ("block_table", _p), ("output", _p), ("status", _p),
+        ("kv_block_stride", _i64),
+        ("row_stride", _i32), ("row_bytes", _i32), ("batch", _i32), ("rows_per_request", _i32),
+        ("max_blocks", _i32), ("num_blocks", _i32),
+    ]
+
+
+class LIFetchArgs(ctypes.Structure):
+    _fields_ = [("indexer", IndexerArgs), ("topk", TopkArgs), ("fetch", FetchArgs)]
+
+
+# name -> (argtypes, restype); must list every function declared in include/kvip_hip.h.
+PROTOTYPES = {
+    "kvip_hip_abi_version": ([], ctypes.c_uint32),
+    "kvip_hip_indexer_decode": ([ctypes.POINTER(IndexerArgs), _p], ctypes.c_uint32),
+    "kvip_hip_topk": ([ctypes.POINTER(TopkArgs), _p], ctypes.c_uint32),
+    "kvip_hip_fetch_gather": ([ctypes.POINTER(FetchArgs), _p], ctypes.c_uint32),
+    "kvip_hip_lifetch_forward": ([ctypes.POINTER(LIFetchArgs), _p], ctypes.c_uint32),
+}
+
+_LIB = None
+
+
+def load_library(path: Path | None = None):
+    """Load libkvip_hip.so once and bind the prototypes. Raises RuntimeError if the
+    library is missing or its ABI version differs."""
+    global _LIB
+    if _LIB is not None and path is None:
+        return _LIB
+    path = Path(path) if path is not None else LIBRARY
+    # torch ships its own libamdhip64 (same soname): load it first so that the library
+    # binds to the one HIP runtime that owns torch's streams and allocations.
+    import torch  # noqa: F401
+
+    if not path.exists():
+        raise RuntimeError(
+            f"{path} is not built: run `python -c 'import __graft_entry__ as g; g.build()'` "
+            "(kvip_amd has no CPU fallback)"
+        )
+    lib = ctypes.CDLL(str(path))
+    for name, (argtypes, restype) in PROTOTYPES.items():
+        fn = getattr(lib, name)
+        fn.argtypes, fn.restype = argtypes, restype
+    version = lib.kvip_hip_abi_version()
+    if version != ABI_VERSION:
+        raise RuntimeError(f"libkvip_hip.so ABI {version} != expected {ABI_VERSION}; rebuild")
+    if path == LIBRARY:
+        _LIB = lib
+    return lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc == KVIP_ERR_INVALID:
+        raise ValueError(f"{what}: arguments rejected by libkvip_hip")
+    if rc != KVIP_OK:
+        raise RuntimeError(f"{what}: HIP launch failed with hipError {rc}")
+
+
+def ptr(tensor) -> int:
+    """Device address of a tensor, or 0 for None."""
+    return 0 if tensor is None else int(tensor.data_ptr())
+
+
+def stream_handle(torch, device) -> int:
+    return int(torch.cuda.current_stream(device).cuda_stream)

@@ -1,0 +1,95 @@
+"""C ABI: the library loads on the CPU, exports every declared symbol, the ctypes
+structs match the C layout, and invalid arguments are rejected before any launch."""
+import ctypes
+import re
+import subprocess
+import textwrap
+
+import pytest
+
+from kvip_amd.runtime import abi
+from tests.conftest import ROOT
+
+HEADER = ROOT / "include" / "kvip_hip.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*uint32_t\s+(kvip_hip_\w+)\s*\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = abi.load_library()
+    names = declared_functions()
+    assert names, "no entry points parsed from the header"
+    for name in names:
+        assert hasattr(lib, name), name
+        assert name in abi.PROTOTYPES, f"{name} has no ctypes prototype"
+    assert set(abi.PROTOTYPES) == set(names)
+    assert lib.kvip_hip_abi_version() == abi.ABI_VERSION
+
+
+STRUCTS = {
+    "KvipIndexerArgs": abi.IndexerArgs,
+    "KvipTopkArgs": abi.TopkArgs,
+    "KvipFetchArgs": abi.FetchArgs,
+    "KvipLIFetchArgs": abi.LIFetchArgs,
+}
+
+
+def test_ctypes_layout_matches_c(tmp_path):
+    lines = []
+    for cname, cls in STRUCTS.items():
+        lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
+        for field, _ in cls._fields_:
+            lines.append(f'printf("{cname} {field} %zu\\n", offsetof({cname}, {field}));')
+    src = tmp_path / "layout.c"
+    src.write_text(textwrap.dedent(
+        '#include <stddef.h>\n#include <stdio.h>\n#include "kvip_hip.h"\nint main(void){\n'
+        + "\n".join(lines) + "\nreturn 0;}\n"))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", f"-I{ROOT / 'include'}", str(src), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split("\n")
+    c_layout = {(a, b): int(c) for a, b, c in (line.split() for line in out if line)}
+    for cname, cls in STRUCTS.items():
+        assert c_layout[(cname, "size")] == ctypes.sizeof(cls), cname
+        for field, _ in cls._fields_:
+            assert c_layout[(cname, field)] == getattr(cls, field).offset, (cname, field)
+
+
+def test_invalid_arguments_rejected_before_launch():
+    lib = abi.load_library()
+    assert lib.kvip_hip_indexer_decode(None, None) == abi.KVIP_ERR_INVALID
+    assert lib.kvip_hip_topk(None, None) == abi.KVIP_ERR_INVALID
+    assert lib.kvip_hip_fetch_gather(None, None) == abi.KVIP_ERR_INVALID
+    assert lib.kvip_hip_lifetch_forward(None, None) == abi.KVIP_ERR_INVALID
+    # Well-formed pointers but an unsupported head count / unaligned key stride.
+    args = abi.IndexerArgs(query=16, weights=16, keys=16, block_table=16, seq_lens=16, score_keys=16,
+                           histogram=16, key_block_stride=16384, batch=1, rows_per_request=1, heads=48,
+                           max_blocks=1, num_blocks=1, key_stride=128, qk_dtype=abi.DTYPE_FP8_E4M3,
+                           weight_dtype=abi.DTYPE_FP32)
+    assert lib.kvip_hip_indexer_decode(ctypes.byref(args), None) == abi.KVIP_ERR_INVALID
+    args.heads = 64
+    args.key_stride = 100
+    assert lib.kvip_hip_indexer_decode(ctypes.byref(args), None) == abi.KVIP_ERR_INVALID
+    topk = abi.TopkArgs(score_keys=16, seq_lens=16, topk=16, batch=1, rows_per_request=3, key_stride=128)
+    assert lib.kvip_hip_topk(ctypes.byref(topk), None) == abi.KVIP_ERR_INVALID
+    fetch = abi.FetchArgs(topk=16, kv_cache=16, block_table=16, output=16, kv_block_stride=128 * 656,
+                          row_stride=656, row_bytes=650, batch=1, rows_per_request=1, max_blocks=1, num_blocks=1)
+    assert lib.kvip_hip_fetch_gather(ctypes.byref(fetch), None) == abi.KVIP_ERR_INVALID
+
+
+def test_binding_validation_cpu():
+    torch = pytest.importorskip("torch")
+    from kvip_amd.operators.lifetch.binding import LIFetchBinding
+
+    with pytest.raises(ValueError):
+        LIFetchBinding(torch, batch=0, max_context=4096, device="cpu")
+    with pytest.raises(ValueError):
+        LIFetchBinding(torch, batch=1, max_context=4096, device="cpu", heads=16)
+    rot = LIFetchBinding(torch, batch=2, max_context=1000, device="cpu")
+    assert rot.max_blocks == 8 and rot.key_stride == 1024
+    with pytest.raises(ValueError):
+        rot.bind_index_cache(torch.zeros((4, 128, 128), dtype=torch.bfloat16))
+    with pytest.raises(ValueError):
+        rot.indexer_args()

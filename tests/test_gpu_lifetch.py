@@ -1,0 +1,210 @@
+"""GPU parity of the decode LIFetch path (scoring -> TopK-2048 -> Fetch gather) against
+the CPU oracle, through the C ABI of libkvip_hip.so.
+
+Bars (written in each test): scores within 3e-2 relative for fp8 and 1e-2 for bf16
+(with an absolute floor of the same fraction of the row's largest |score|, for
+scores that cancel to near zero); TopK bit-exact, order included, when fed the
+oracle's keys; gather byte-exact."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import kvip_amd
+from kvip_amd import synthetic
+from kvip_amd.runtime import abi
+from oracle import indexer as ref
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*args):
+    print(*args, flush=True)
+
+
+def host_values(torch, t):
+    if t is None:
+        return None
+    if t.dtype == torch.float8_e4m3fn:
+        return ref.fp8_e4m3_decode(t.view(torch.uint8).cpu().numpy())
+    return t.float().cpu().numpy()
+
+
+def oracle_keys(torch, wl, rot):
+    return ref.decode_keys_paged(
+        host_values(torch, wl.query), host_values(torch, wl.weights), host_values(torch, wl.query_scale),
+        host_values(torch, wl.keys), host_values(torch, wl.key_scale), wl.block_table.cpu().numpy(), wl.ctx,
+        rows_per_request=wl.rows_per_request,
+        query_ends=None if rot.query_ends is None else rot.query_ends.cpu().numpy(), key_stride=rot.key_stride)
+
+
+def gpu_keys(rot):
+    return rot.score_keys.cpu().numpy().view(np.uint16)
+
+
+def assert_scores_close(got_keys, want_keys, valid, rtol):
+    for r, v in enumerate(valid):
+        if v == 0:
+            continue
+        g = ref.score_values(got_keys[r, :v]).astype(np.float64)
+        w = ref.score_values(want_keys[r, :v]).astype(np.float64)
+        floor = rtol * np.abs(w).max()
+        bad = np.abs(g - w) > rtol * np.abs(w) + floor
+        assert not bad.any(), f"row {r}: {bad.sum()} scores outside rtol {rtol}"
+    same = np.mean([np.mean(got_keys[r, :v] == want_keys[r, :v]) for r, v in enumerate(valid) if v])
+    say(f"  identical keys: {same:.5f}")
+    assert same > 0.99
+
+
+CASES = [
+    # name, qk, heads, weight dtype, key scale, query scale, ctx
+    ("fp8_h64_fp32w", "fp8", 64, "f32", True, True, [1, 100, 2047, 2048, 5000, 9000]),
+    ("fp8_h32_bf16w", "fp8", 32, "bf16", True, False, [4096, 3000, 129]),
+    ("bf16_h64_c1", "bf16", 64, "f32", False, False, [4096, 4096, 4096, 4096]),
+]
+
+
+@pytest.mark.parametrize("name,qk,heads,wdt,kscale,qscale,ctx", CASES, ids=[c[0] for c in CASES])
+def test_indexer_scores_match_oracle(torch_gpu, name, qk, heads, wdt, kscale, qscale, ctx):
+    torch = torch_gpu
+    say(f"case {name}")
+    wl = synthetic.decode_workload(torch, batch=len(ctx), ctx=ctx, device="cuda", heads=heads, qk=qk,
+                                   weight_dtype=torch.float32 if wdt == "f32" else torch.bfloat16,
+                                   key_scale=kscale, query_scale=qscale, seed=11)
+    rot, upd, fwd = synthetic.bind(torch, kvip_amd, wl)
+    fwd.score()
+    torch.cuda.synchronize()
+    want, valid = oracle_keys(torch, wl, rot)
+    assert_scores_close(gpu_keys(rot), want, valid, 3e-2 if qk == "fp8" else 1e-2)
+    assert int(rot.status.item()) == 0
+    # Histogram of high bytes over the valid prefix equals the keys' own histogram.
+    hist = rot.histogram.cpu().numpy()
+    for r, v in enumerate(valid):
+        assert np.array_equal(hist[r], np.bincount(gpu_keys(rot)[r, :v] >> 8, minlength=256)), r
+
+
+def run_topk(torch, rot, use_histogram):
+    lib = abi.load_library()
+    args = rot.topk_args(use_histogram)
+    rc = lib.kvip_hip_topk(ctypes.byref(args), abi.stream_handle(torch, rot.device))
+    abi.check(rc, "topk")
+    torch.cuda.synchronize()
+    return rot.topk.cpu().numpy()
+
+
+def keys_case(kind, n, rng):
+    if kind == "random":
+        return ref.sortable_key(ref.bf16_round_half_away(rng.standard_normal(n).astype(np.float32) * 8))
+    if kind == "few_levels":
+        return (0x8000 + rng.integers(0, 5, n)).astype(np.uint16)
+    if kind == "all_equal":
+        return np.full(n, 0xC200, np.uint16)
+    if kind == "one_bin":
+        return (0xC200 + rng.integers(0, 256, n)).astype(np.uint16)
+    raise ValueError(kind)
+
+
+@pytest.mark.parametrize("kind,ctx", [
+    ("random", [32768, 20000, 2048, 2047, 0, 8193]),
+    ("few_levels", [16384, 30000]),
+    ("all_equal", [4096, 2048]),
+    ("one_bin", [131072]),
+])
+def test_topk_bit_exact_on_oracle_keys(torch_gpu, kind, ctx):
+    torch = torch_gpu
+    say(f"case topk {kind} {ctx}")
+    rng = np.random.default_rng(len(ctx) * 7 + ctx[0])
+    rot = kvip_amd.LIFetchBinding(torch, batch=len(ctx), max_context=max(max(ctx), 1), device="cuda")
+    keys = np.zeros((len(ctx), rot.key_stride), np.uint16)
+    for r, v in enumerate(ctx):
+        keys[r, :v] = keys_case(kind, v, rng)
+    rot.score_keys.copy_(torch.from_numpy(keys.view(np.int16)))
+    rot.seq_lens.copy_(torch.tensor(ctx, dtype=torch.int32))
+    got = run_topk(torch, rot, use_histogram=False)
+    for r, v in enumerate(ctx):
+        want = ref.topk_reference(keys[r], v)
+        assert np.array_equal(got[r], want), f"row {r} valid {v}"
+    assert int(rot.status.item()) == 0
+
+
+def test_topk_from_scoring_histogram_equals_standalone(torch_gpu):
+    torch = torch_gpu
+    wl = synthetic.decode_workload(torch, batch=5, ctx=[9000, 2048, 100, 17000, 4097], device="cuda", seed=3)
+    rot, upd, fwd = synthetic.bind(torch, kvip_amd, wl)
+    fwd.score()
+    fwd.select()
+    torch.cuda.synchronize()
+    fused = rot.topk.cpu().numpy().copy()
+    assert not rot.histogram.cpu().numpy().any(), "TopK must re-zero the histogram"
+    alone = run_topk(torch, rot, use_histogram=False)
+    assert np.array_equal(fused, alone)
+    keys = gpu_keys(rot)
+    for r, v in enumerate(wl.ctx):
+        assert np.array_equal(fused[r], ref.topk_reference(keys[r], v))
+
+
+def test_fetch_gather_byte_exact(torch_gpu):
+    torch = torch_gpu
+    wl = synthetic.decode_workload(torch, batch=4, ctx=[3000, 1000, 6000, 2048], device="cuda", seed=5)
+    rot, upd, fwd = synthetic.bind(torch, kvip_amd, wl)
+    fwd()
+    torch.cuda.synchronize()
+    topk = rot.topk.cpu().numpy()
+    want = ref.fetch_gather(wl.kv_cache.cpu().numpy(), wl.block_table.cpu().numpy(), topk)
+    assert np.array_equal(upd.output.cpu().numpy(), want)
+    assert (topk[1, 1000:] == -1).all() and not upd.output[1, 1000:].any()
+    assert int(rot.status.item()) == 0
+
+
+def test_forward_end_to_end_against_oracle_scores(torch_gpu):
+    torch = torch_gpu
+    wl = synthetic.decode_workload(torch, batch=8, ctx_low=8192, ctx_high=20000, device="cuda", seed=2026)
+    rot, upd, fwd = synthetic.bind(torch, kvip_amd, wl)
+    fwd()
+    torch.cuda.synchronize()
+    want, valid = oracle_keys(torch, wl, rot)
+    topk = rot.topk.cpu().numpy()
+    for r, v in enumerate(valid):
+        assert ref.validate_topk_band(topk[r], ref.score_values(want[r, :v])), r
+        # Bit-exact against the oracle's TopK of the GPU's own keys.
+        assert np.array_equal(topk[r], ref.topk_reference(gpu_keys(rot)[r], v))
+    out = upd.output.cpu().numpy()
+    assert np.array_equal(out, ref.fetch_gather(wl.kv_cache.cpu().numpy(), wl.block_table.cpu().numpy(), topk))
+
+
+def test_graph_replay_matches_eager(torch_gpu):
+    torch = torch_gpu
+    wl = synthetic.decode_workload(torch, batch=6, ctx_low=3000, ctx_high=12000, device="cuda", seed=9)
+    rot, upd, fwd = synthetic.bind(torch, kvip_amd, wl)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        fwd()  # warm-up on the capture stream
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        fwd()
+    gen = torch.Generator(device="cuda")
+    for step in range(3):
+        gen.manual_seed(100 + step)
+        new_q = synthetic.saturating_fp8(torch, torch.randn(rot.query.shape, generator=gen, device="cuda"))
+        rot.query.copy_(new_q)
+        graph.replay()
+        torch.cuda.synchronize()
+        g_topk, g_out = rot.topk.clone(), upd.output.clone()
+        rot.topk.fill_(-7)
+        fwd()
+        torch.cuda.synchronize()
+        assert torch.equal(g_topk, rot.topk), step
+        assert torch.equal(g_out, upd.output), step
+
+
+def test_bad_block_id_is_reported_not_faulted(torch_gpu):
+    torch = torch_gpu
+    wl = synthetic.decode_workload(torch, batch=2, ctx=[4096, 4096], device="cuda", seed=1)
+    rot, upd, fwd = synthetic.bind(torch, kvip_amd, wl)
+    rot.block_table[1, 3] = rot.num_blocks + 5  # out of range: kernels skip the access
+    fwd()
+    torch.cuda.synchronize()
+    assert int(rot.status.item()) & abi.STATUS_BAD_BLOCK

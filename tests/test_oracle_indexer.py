@@ -1,0 +1,177 @@
+"""Pins of the CPU oracle (oracle/indexer.py) against the reference's known answers,
+closed forms and brute force, so that the oracle itself can be trusted as the
+checker of the HIP kernels. Paths in comments are relative to the KVIP reference."""
+import numpy as np
+import pytest
+
+from oracle import indexer as ref
+
+
+# ---------------------------------------------------------------- element decoding
+def test_fp8_decode_matches_torch_on_all_codes():
+    torch = pytest.importorskip("torch")
+    codes = np.arange(256, dtype=np.uint8)
+    ours = ref.fp8_e4m3_decode(codes)
+    theirs = torch.from_numpy(codes).view(torch.float8_e4m3fn).float().numpy()
+    assert np.array_equal(np.isnan(ours), np.isnan(theirs))
+    ok = ~np.isnan(ours)
+    assert np.array_equal(ours[ok], theirs[ok])
+    # A few hand values: 0x38 = 1.0, 0x40 = 2.0, 0x44 = 3.0 (workloads.py:207 key codes).
+    assert list(ref.fp8_e4m3_decode(np.array([0x38, 0x40, 0x44, 0xB8, 0x01], np.uint8))) == \
+        [1.0, 2.0, 3.0, -1.0, 2.0 ** -9]
+
+
+def test_bf16_round_half_away_known_answers_and_torch_on_non_ties():
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal(200000).astype(np.float32) * np.float32(1e3) ** rng.uniform(-3, 3, 200000).astype(np.float32)
+    bits = x.view(np.uint32)
+    non_tie = (bits & 0xFFFF) != 0x8000
+    rne = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    ours = ref.bf16_round_half_away(x)
+    assert np.array_equal(ours[non_tie], rne[non_tie])
+    # Exact ties move away from zero (CAST_ROUND), unlike round-to-nearest-even.
+    ties = np.array([0x3F808000, 0xBF808000, 0x3F818000, 0x40008000], np.uint32).view(np.float32)
+    assert list(ref.bf16_round_half_away(ties)) == [0x3F81, 0xBF81, 0x3F82, 0x4001]
+
+
+def test_sortable_key_known_answers():
+    # support/correctness.py:198-202: key 0x8000 is +0 and 0xC200 is bf16 +32.
+    assert ref.sortable_key(ref.bf16_round_half_away(np.float32([0.0, 32.0]))).tolist() == [0x8000, 0xC200]
+    assert ref.sortable_key(np.array([0x8000, 0x7FC0, 0xFF80, 0x7F80], np.uint16)).tolist() == \
+        [0x7FFF, 0x0000, 0x007F, 0xFF80]
+    assert ref.score_values(np.array([0xC200, 0x8000], np.uint16)).tolist() == [32.0, 0.0]
+
+
+def test_sortable_key_orders_every_bf16_value():
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    values = ref.bf16_decode(bits)
+    finite = ~np.isnan(values)
+    keys = ref.sortable_key(bits[finite]).astype(np.int64)
+    v = values[finite].astype(np.float64)
+    order = np.argsort(keys)
+    assert np.all(np.diff(v[order]) >= 0)  # key order is value order (-0 just below +0)
+    assert len(np.unique(keys)) == len(keys)
+    assert np.array_equal(ref.score_values(ref.sortable_key(bits[finite])).view(np.uint32) >> 16, bits[finite])
+
+
+# ---------------------------------------------------------------- LI score
+def exact_binary_fixture(tokens, queries, seed):
+    """The construction of workloads.py:196-283 (own code): index-K values in {0,1,2,3}
+    (fp8 codes 0, 0x38, 0x40, 0x44), one-hot 1.0 queries per head at column
+    (h + 16 q) % 128, exact-binary query scales {0.5,1,2} and weights {1,2,0.5}, key
+    scales U(0.25, 2). Every partial sum is exact, so the expected key is fixed by the
+    float32 formula of the fixture whatever the accumulation order."""
+    rng = np.random.default_rng(seed)
+    values = rng.integers(0, 4, (tokens, 128), dtype=np.uint8)
+    key_codes = np.array([0, 0x38, 0x40, 0x44], np.uint8)[values]
+    head = np.arange(64)[None, :]
+    qi = np.arange(queries)[:, None]
+    qscale = np.array([0.5, 1.0, 2.0], np.float32)[(head + qi) % 3]
+    weights = np.array([1.0, 2.0, 0.5], np.float32)[(head * 2 + qi) % 3]
+    scale = rng.uniform(0.25, 2, tokens).astype(np.float32)
+    query_codes = np.zeros((queries, 64, 128), np.uint8)
+    expected = []
+    for q in range(queries):
+        cols = (np.arange(64) + q * 16) % 128
+        query_codes[q, np.arange(64), cols] = 0x38
+        score = (values[:, cols].astype(np.float32) * (weights[q] * qscale[q])).sum(-1) * scale
+        expected.append(((score.view(np.uint32) + 0x8000) >> 16).astype(np.uint16))
+    return query_codes, key_codes, weights, qscale, scale, np.stack(expected)
+
+
+@pytest.mark.parametrize("seed", [73121, 7])
+def test_li_score_exact_binary_fixture(seed):
+    q, k, w, qs, ks, expected_bf16 = exact_binary_fixture(1024, 4, seed)
+    kf = ref.fp8_e4m3_decode(k)
+    for r in range(4):
+        keys = ref.li_keys(ref.fp8_e4m3_decode(q[r]), kf, w[r], qs[r], ks)
+        assert np.array_equal(keys, ref.sortable_key(expected_bf16[r]))
+
+
+def test_li_score_relu_and_signed_weights_closed_form():
+    # Head h sees dot = d_h; negative dots are dropped by ReLU, weights may be negative.
+    heads = 64
+    q = np.zeros((heads, 128), np.float32)
+    q[np.arange(heads), np.arange(heads)] = 1.0
+    k = np.zeros((3, 128), np.float32)
+    k[0, :heads] = np.where(np.arange(heads) % 2, 3.0, -2.0)       # odd heads +3, even heads -2
+    k[1, :heads] = -1.0                                             # all negative -> score +0
+    k[2, 5] = 4.0                                                   # only head 5
+    w = np.where(np.arange(heads) % 4 == 1, -0.5, 0.25).astype(np.float32)
+    s = ref.li_scores(q, k, w, None, np.float32([1.0, 1.0, 2.0]))
+    odd = np.arange(1, heads, 2)
+    assert s[0] == np.float32(3.0 * w[odd].sum())
+    assert s[1] == 0.0 and not np.signbit(s[1])
+    assert s[2] == np.float32(4.0 * w[5] * 2.0)
+
+
+# ---------------------------------------------------------------- TopK
+def test_topk_edge_rules():
+    keys = np.arange(5000, dtype=np.uint16)
+    assert (ref.topk_reference(keys, 0) == -1).all()
+    assert (ref.topk_reference(keys, -3) == -1).all()
+    out = ref.topk_reference(keys, 100)
+    assert out[:100].tolist() == list(range(100)) and (out[100:] == -1).all()
+    # valid == 2048 goes through the select (GT-then-EQ order), not the identity path.
+    rev = np.arange(2048, 0, -1).astype(np.uint16)
+    rev[10] = rev[11]
+    out = ref.topk_reference(rev, 2048)
+    assert sorted(out.tolist()) == list(range(2048))
+
+
+def test_topk_gt_then_eq_order_known_answer():
+    keys = np.array([5, 9, 7, 9, 7, 7, 1, 9, 7], np.uint16)
+    # top 5: 9,9,9 (GT 7) at 1,3,7 then the first two 7s at 2,4.
+    assert ref.topk_reference(keys, len(keys), topk=5).tolist() == [1, 3, 7, 2, 4]
+
+
+@pytest.mark.parametrize("valid,levels,trunk", [
+    (20000, 65536, ref.TRUNK_SINGLE_ROW), (20000, 40, ref.TRUNK_SINGLE_ROW), (40000, 3, ref.TRUNK_Q4),
+    (9000, 7, None), (131072, 300, ref.TRUNK_SINGLE_ROW)])
+def test_topk_set_matches_closed_form_any_trunk(valid, levels, trunk):
+    rng = np.random.default_rng(valid + levels)
+    keys = (0x8000 + rng.integers(0, levels, valid)).astype(np.uint16)
+    got = ref.topk_reference(keys, valid, trunk=trunk)
+    want = ref.topk_set_rule(keys, valid)
+    assert len(np.unique(got)) == 2048
+    assert np.array_equal(np.sort(got), np.sort(want))
+
+
+def test_topk_brute_force_tiny():
+    rng = np.random.default_rng(3)
+    for _ in range(200):
+        n = int(rng.integers(5, 40))
+        k = int(rng.integers(1, n + 1))
+        keys = rng.integers(0, 4, n).astype(np.uint16)
+        got = ref.topk_reference(keys, n, topk=k)
+        # brute force: every pair in the chosen set beats every pair outside it.
+        chosen = set(got.tolist())
+        assert len(chosen) == k
+        for a in chosen:
+            for b in set(range(n)) - chosen:
+                assert (keys[a], -a) > (keys[b], -b)
+
+
+def test_validate_topk_band():
+    rng = np.random.default_rng(1)
+    scores = rng.standard_normal(10000).astype(np.float32)
+    keys = ref.sortable_key(ref.bf16_round_half_away(scores))
+    sel = ref.topk_reference(keys, 10000)
+    assert ref.validate_topk_band(sel, ref.score_values(keys))
+    bad = sel.copy()
+    bad[0] = int(np.argmin(scores))
+    assert not ref.validate_topk_band(bad, ref.score_values(keys))
+
+
+# ---------------------------------------------------------------- Fetch
+def test_fetch_gather_known_answer():
+    kv = np.stack([ref.identity_rows(np.arange(128) + 1000 * blk, 32) for blk in range(3)])
+    table = np.array([[2, 0], [1, 2]], np.int32)
+    topk = np.array([[0, 130, -1], [127, 5, 128]])
+    out = ref.fetch_gather(kv, table, topk)
+    assert np.array_equal(out[0, 0], kv[2, 0]) and np.array_equal(out[0, 1], kv[0, 2])
+    assert not out[0, 2].any()
+    assert np.array_equal(out[1, 0], kv[1, 127]) and np.array_equal(out[1, 2], kv[2, 0])
+    rows = ref.identity_rows(np.arange(4096))
+    assert len({r.tobytes() for r in rows}) == 4096
