@@ -131,6 +131,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const KvipTopkArgs p
 
     // Level 3: ordered emission. gt_base/eq_base are identical in every thread.
     uint32_t gt_base = 0, eq_base = 0;
+    uint32_t err = 0;
     for (int tile = 0; tile < valid; tile += kTileKeys) {
         const int idx0 = tile + tid * kKeysPerThread;
         const Keys8 r = load_keys(keys, idx0, valid);
@@ -149,7 +150,11 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const KvipTopkArgs p
         for (int j = 0; j < kKeysPerThread; ++j) {
             if (j < r.count) {
                 if (r.k[j] > kth) {
-                    out[pg++] = idx0 + j;
+                    // pg < n_gt whenever the histogram matches the keys; the guard keeps a
+                    // stale histogram from writing past the row.
+                    if (pg < n_gt) out[pg] = idx0 + j;
+                    else err = KVIP_STATUS_HISTOGRAM;
+                    ++pg;
                 } else if (r.k[j] == kth) {
                     if (pe < need) out[n_gt + pe] = idx0 + j;
                     ++pe;
@@ -160,6 +165,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const KvipTopkArgs p
         eq_base += total & 0xFFFFu;
         if (gt_base >= n_gt && eq_base >= need) break;  // uniform
     }
+    report(p.status, err);
 }
 
 }  // namespace
