@@ -15,45 +15,73 @@ namespace kvip {
 namespace {
 
 constexpr int kGatherThreads = 256;
-constexpr int kPiecesPerThread = 4;
+constexpr int kRowsPerWave = 32;
+constexpr int kRowsPerBlock = kRowsPerWave * (kGatherThreads / 64);
 
+// One wave moves 32 consecutive selected rows: lanes 0..31 translate the token ids to
+// source rows (token id -> block table -> byte offset), then all 64 lanes copy the
+// 32*PIECES 16-byte pieces (21 loads in flight per lane for 656-byte rows). Because the
+// destination rows are consecutive, the wave's
+// output is one contiguous range written with fully coalesced 16-byte stores.
 template <int PIECES>
-__global__ __launch_bounds__(kGatherThreads) void fetch_gather_kernel(const KvipFetchArgs p, uint64_t total) {
+__global__ __launch_bounds__(kGatherThreads) void fetch_gather_kernel(const KvipFetchArgs p, uint32_t selections) {
     const int pieces = PIECES > 0 ? PIECES : p.row_bytes / 16;
-    const uint64_t base = static_cast<uint64_t>(blockIdx.x) * (kGatherThreads * kPiecesPerThread) + threadIdx.x;
+    const int lane = threadIdx.x & 63;
+    const uint32_t sel0 = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6) * kRowsPerWave;
+    if (sel0 >= selections) return;
     const int capacity = p.max_blocks * kBlockTokens;
     uint32_t err = 0;
-    v4i val[kPiecesPerThread];
-    uint64_t dst[kPiecesPerThread];
-#pragma unroll
-    for (int u = 0; u < kPiecesPerThread; ++u) {
-        const uint64_t c = base + static_cast<uint64_t>(u) * kGatherThreads;
-        val[u] = v4i{0, 0, 0, 0};
-        dst[u] = ~0ull;
-        if (c >= total) continue;
-        const uint32_t sel = static_cast<uint32_t>(c / static_cast<uint32_t>(pieces));
-        const uint32_t piece = static_cast<uint32_t>(c - static_cast<uint64_t>(sel) * pieces);
-        const int row = static_cast<int>(sel / kTopK);
-        const int b = row / p.rows_per_request;
+
+    // Source byte offset of row (sel0 + lane), or -1 for an empty / invalid entry.
+    int64_t src = -1;
+    if (lane < kRowsPerWave && sel0 + lane < selections) {
+        const uint32_t sel = sel0 + lane;
         const int t = p.topk[sel];
-        dst[u] = static_cast<uint64_t>(sel) * p.row_bytes + piece * 16u;
-        if (t < 0) continue;
+        const int b = static_cast<int>(sel / kTopK) / p.rows_per_request;
         if (t >= capacity) {
             err |= KVIP_STATUS_BAD_TOKEN;
-            continue;
+        } else if (t >= 0) {
+            const int blk = p.block_table[static_cast<size_t>(b) * p.max_blocks + (t >> 7)];
+            if (static_cast<unsigned>(blk) < static_cast<unsigned>(p.num_blocks)) {
+                src = static_cast<int64_t>(blk) * p.kv_block_stride + static_cast<int64_t>(t & 127) * p.row_stride;
+            } else {
+                err |= KVIP_STATUS_BAD_BLOCK;
+            }
         }
-        const int blk = p.block_table[static_cast<size_t>(b) * p.max_blocks + (t >> 7)];
-        if (static_cast<unsigned>(blk) >= static_cast<unsigned>(p.num_blocks)) {
-            err |= KVIP_STATUS_BAD_BLOCK;
-            continue;
-        }
-        const uint8_t* src = p.kv_cache + static_cast<size_t>(blk) * p.kv_block_stride +
-                             static_cast<size_t>(t & 127) * p.row_stride + piece * 16u;
-        val[u] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(src));
     }
+    const int rows = min(kRowsPerWave, static_cast<int>(selections - sel0));
+    const int total = rows * pieces;
+    uint8_t* dst = p.output + static_cast<size_t>(sel0) * p.row_bytes;
+    constexpr int kMaxIters = PIECES > 0 ? (kRowsPerWave * PIECES + 63) / 64 : 1;
+    if constexpr (PIECES > 0) {
+        v4i val[kMaxIters];
 #pragma unroll
-    for (int u = 0; u < kPiecesPerThread; ++u) {
-        if (dst[u] != ~0ull) *reinterpret_cast<v4i*>(p.output + dst[u]) = val[u];
+        for (int it = 0; it < kMaxIters; ++it) {
+            const int idx = it * 64 + lane;
+            const int r = idx / PIECES;
+            const int piece = idx - r * PIECES;
+            const int64_t base = __shfl(src, min(r, kRowsPerWave - 1));
+            val[it] = v4i{0, 0, 0, 0};
+            if (idx < total && base >= 0) {
+                val[it] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(p.kv_cache + base + piece * 16));
+            }
+        }
+#pragma unroll
+        for (int it = 0; it < kMaxIters; ++it) {
+            const int idx = it * 64 + lane;
+            if (idx < total) *reinterpret_cast<v4i*>(dst + static_cast<size_t>(idx) * 16) = val[it];
+        }
+    } else {
+        const int iters = (kRowsPerWave * pieces + 63) / 64;  // uniform: every lane joins each shuffle
+        for (int it = 0; it < iters; ++it) {
+            const int idx = it * 64 + lane;
+            const int r = idx / pieces;
+            const int piece = idx - r * pieces;
+            const int64_t base = __shfl(src, min(r, kRowsPerWave - 1));
+            v4i v = v4i{0, 0, 0, 0};
+            if (idx < total && base >= 0) v = *reinterpret_cast<const v4i*>(p.kv_cache + base + piece * 16);
+            if (idx < total) *reinterpret_cast<v4i*>(dst + static_cast<size_t>(idx) * 16) = v;
+        }
     }
     report(p.status, err);
 }
@@ -77,13 +105,13 @@ uint32_t validate_fetch(const KvipFetchArgs* a) {
 }
 
 hipError_t launch_fetch(const KvipFetchArgs& a, hipStream_t stream) {
-    const uint64_t total = static_cast<uint64_t>(a.batch) * a.rows_per_request * kTopK * (a.row_bytes / 16);
-    const uint64_t per_block = kGatherThreads * kPiecesPerThread;
-    const dim3 grid(static_cast<unsigned>((total + per_block - 1) / per_block));
+    const uint32_t selections = static_cast<uint32_t>(a.batch) * a.rows_per_request * kTopK;
+    const dim3 grid((selections + kRowsPerBlock - 1) / kRowsPerBlock);
     if (a.row_bytes == KVIP_KV_ROW_BYTES) {
-        hipLaunchKernelGGL(fetch_gather_kernel<KVIP_KV_ROW_BYTES / 16>, grid, dim3(kGatherThreads), 0, stream, a, total);
+        hipLaunchKernelGGL(fetch_gather_kernel<KVIP_KV_ROW_BYTES / 16>, grid, dim3(kGatherThreads), 0, stream, a,
+                           selections);
     } else {
-        hipLaunchKernelGGL(fetch_gather_kernel<0>, grid, dim3(kGatherThreads), 0, stream, a, total);
+        hipLaunchKernelGGL(fetch_gather_kernel<0>, grid, dim3(kGatherThreads), 0, stream, a, selections);
     }
     return hipGetLastError();
 }

@@ -9,11 +9,15 @@
 // (row, token) leave the kernel, plus a 256-bin histogram of the key's high byte
 // that lets TopK skip one pass over the keys.
 //
-// Work split: one workgroup = 4 waves = one 1024-token chunk of one request; each
-// wave streams 8 tiles of 32 tokens, prefetching tile i+1 while tile i is in the
-// MFMA. Lane (n = lane%32, g = lane/32) loads 64*elem contiguous bytes of token n's
-// index-K row at byte offset 64*elem*g, and the Q fragments are loaded with the same
-// lane->byte assignment, so the contraction pairs identical dims in both operands.
+// Work split: one workgroup = 4 waves = one 512-token chunk of one request; each
+// wave streams 4 tiles of 32 tokens (4 KiB of fp8 index-K) through a three-deep
+// register pipeline. Tile loads are fully coalesced (lane L reads the L-th 16 bytes
+// of each KiB) and are transposed into MFMA B fragments through a swizzled per-wave
+// LDS tile; lane (n = lane%32, g = lane/32) then holds 64*elem contiguous bytes of
+// token n's row at byte offset 64*elem*g, and the Q fragments (A operand) use the
+// same lane->byte assignment, so the contraction pairs identical dims in both
+// operands. Keys are staged in LDS and written once per chunk, so the tile loop's
+// only vector-memory operations are its loads (exact vmcnt waits).
 //
 // Reference: QLIMatmul::ComputeMm1 (op_kernel/indexer/indexer_cube.h:161-322),
 // MulWeightAndReduceSum bf16-weight variant (indexer_score.h:384-426, loop :60-103,
@@ -26,8 +30,8 @@ namespace {
 constexpr int kLiWaves = 4;
 constexpr int kLiThreads = kLiWaves * 64;
 constexpr int kTileTokens = 32;
-constexpr int kTilesPerWave = 8;
-constexpr int kChunkTokens = kLiWaves * kTilesPerWave * kTileTokens;  // 1024
+constexpr int kTilesPerWave = 4;
+constexpr int kChunkTokens = kLiWaves * kTilesPerWave * kTileTokens;  // 512
 
 // ELEM = bytes per Q/K element (1: fp8 e4m3, 2: bf16). Each lane holds NV = 4*ELEM
 // 16-byte vectors of one Q or K row.
@@ -60,6 +64,12 @@ struct Mma<2> {
     }
 };
 
+// LDS piece swizzle of a staged K row (8 or 16 pieces of 16 bytes per row).
+template <int ELEM>
+KVIP_DEVICE int swizzle(int row) {
+    return ELEM == 1 ? ((row >> 1) & 7) : (row & 15);
+}
+
 template <int ELEM, int HEADS, int RPR, bool W_BF16>
 __global__ __launch_bounds__(kLiThreads) void indexer_decode_kernel(const KvipIndexerArgs p) {
     constexpr int MT = HEADS / 32;
@@ -67,6 +77,8 @@ __global__ __launch_bounds__(kLiThreads) void indexer_decode_kernel(const KvipIn
     constexpr int ROW_BYTES = kIndexDim * ELEM;
     __shared__ __align__(16) float s_w[RPR * HEADS];
     __shared__ uint32_t s_hist[RPR * 256];
+    __shared__ __align__(16) uint16_t s_keys[RPR * kChunkTokens];
+    __shared__ __align__(16) uint8_t s_tile[kLiWaves * kTileTokens * ROW_BYTES];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -123,34 +135,60 @@ __global__ __launch_bounds__(kLiThreads) void indexer_decode_kernel(const KvipIn
     const int32_t* table = p.block_table + static_cast<size_t>(b) * p.max_blocks;
     uint32_t err = 0;
 
-    auto load_tile = [&](int t0, v4i (&kb)[NV], float& ks) {
-        const int blk = table[t0 >> 7];
-        const int slot = (t0 & 127) + n;
-        if (static_cast<unsigned>(blk) >= static_cast<unsigned>(p.num_blocks)) {
+    // The wave's 256 tokens span two pages; their block ids are read once (scalar). Tiles
+    // past the row end reload the wave's last live tile so that every load in the
+    // pipeline is unconditional (exact vmcnt waits); their results are discarded.
+    constexpr int kWavePages = kTilesPerWave * kTileTokens / kBlockTokens;
+    constexpr int kTilesPerPage = kBlockTokens / kTileTokens;
+    const int wave_t0 = chunk0 + __builtin_amdgcn_readfirstlane(wave) * (kTilesPerWave * kTileTokens);
+    const int ntiles = min(max((vmax - wave_t0 + kTileTokens - 1) / kTileTokens, 0), kTilesPerWave);
+    int page[kWavePages];
+    float page_ok[kWavePages];
 #pragma unroll
-            for (int v = 0; v < NV; ++v) kb[v] = v4i{0, 0, 0, 0};
-            ks = 0.0f;
-            err |= KVIP_STATUS_BAD_BLOCK;
-            return;
-        }
-        const v4i* src = reinterpret_cast<const v4i*>(kbase + static_cast<size_t>(blk) * p.key_block_stride +
-                                                      slot * ROW_BYTES + g * (ROW_BYTES / 2));
+    for (int j = 0; j < kWavePages; ++j) {
+        const int jj = min(j, max(ntiles - 1, 0) / kTilesPerPage);
+        const int id = table[min((wave_t0 >> 7) + jj, p.max_blocks - 1)];
+        const bool ok = static_cast<unsigned>(id) < static_cast<unsigned>(p.num_blocks);
+        if (!ok && j * kTilesPerPage < ntiles) err |= KVIP_STATUS_BAD_BLOCK;
+        page[j] = ok ? id : 0;
+        page_ok[j] = ok ? 1.0f : 0.0f;
+    }
+
+    // Tile loads are fully coalesced: lane L reads 16-byte piece L of each 1 KiB of the
+    // tile. They are transposed into MFMA fragments through the wave's own LDS tile.
+    auto issue = [&](int i, v4i (&kb)[NV], float& ks) {
+        const int ii = min(i, max(ntiles - 1, 0));
+        const int pg = page[(ii * kTileTokens) / kBlockTokens];
+        const int first = (ii * kTileTokens) & 127;
+        const v4i* src = reinterpret_cast<const v4i*>(kbase + static_cast<size_t>(pg) * p.key_block_stride +
+                                                      first * ROW_BYTES);
 #pragma unroll
-        for (int v = 0; v < NV; ++v) kb[v] = __builtin_nontemporal_load(src + v);
-        ks = p.key_scale != nullptr ? p.key_scale[static_cast<size_t>(blk) * p.scale_block_stride + slot] : 1.0f;
+        for (int v = 0; v < NV; ++v) kb[v] = src[v * 64 + lane];
+        ks = p.key_scale != nullptr ? p.key_scale[static_cast<size_t>(pg) * p.scale_block_stride + first + n] : 1.0f;
+        ks *= page_ok[(ii * kTileTokens) / kBlockTokens];  // a bad block id scores 0
     };
 
-    const int wave_t0 = chunk0 + wave * (kTilesPerWave * kTileTokens);
-    const int ntiles = min(max((vmax - wave_t0 + kTileTokens - 1) / kTileTokens, 0), kTilesPerWave);
-
-    v4i kb[NV];
-    v4i kn[NV];
-    float ks = 0.0f, ksn = 0.0f;
-    if (ntiles > 0) load_tile(wave_t0, kb, ks);
-    for (int i = 0; i < ntiles; ++i) {
-        const int t0 = wave_t0 + i * kTileTokens;
-        if (i + 1 < ntiles) load_tile(t0 + kTileTokens, kn, ksn);
-        const int tok = t0 + n;
+    // Keys of the chunk are staged in LDS and written out once, so the tile loop's only
+    // vector-memory operations are its loads.
+    auto compute = [&](int i, const v4i (&staged)[NV], float ks) {
+        const int local = wave * (kTilesPerWave * kTileTokens) + i * kTileTokens + n;
+        const int tok = chunk0 + local;
+        // Row r's 16-byte piece j lives at r*ROW_BYTES + (j ^ swz(r))*16 in the wave's LDS
+        // tile: the 16 lanes of each ds_*_b128 pass then touch 16 distinct bank groups.
+        uint8_t* tile = s_tile + wave * (kTileTokens * ROW_BYTES);
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+            const int d = v * 1024 + lane * 16;
+            const int r = d / ROW_BYTES;
+            const int j = (d % ROW_BYTES) / 16;
+            *reinterpret_cast<v4i*>(tile + r * ROW_BYTES + ((j ^ swizzle<ELEM>(r)) * 16)) = staged[v];
+        }
+        v4i kb[NV];
+#pragma unroll
+        for (int u = 0; u < NV; ++u) {
+            const int j = g * NV + u;
+            kb[u] = *reinterpret_cast<const v4i*>(tile + n * ROW_BYTES + ((j ^ swizzle<ELEM>(n)) * 16));
+        }
 #pragma unroll
         for (int q = 0; q < RPR; ++q) {
             v16f acc[MT];
@@ -167,21 +205,50 @@ __global__ __launch_bounds__(kLiThreads) void indexer_decode_kernel(const KvipIn
                 for (int r4 = 0; r4 < 4; ++r4) {
                     const v4f w = *reinterpret_cast<const v4f*>(&s_w[q * HEADS + mt * 32 + r4 * 8 + g * 4]);
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) part = fmaf(fmaxf(acc[mt][r4 * 4 + j], 0.0f), w[j], part);
+                    for (int j = 0; j < 4; ++j) {
+                        // ReLU as an integer max: every negative float (sign bit set) maps to
+                        // +0, one instruction without NaN canonicalisation.
+                        const float relu = __int_as_float(max(__float_as_int(acc[mt][r4 * 4 + j]), 0));
+                        part = fmaf(relu, w[j], part);
+                    }
                 }
             }
             part += __shfl_xor(part, 32);
             const float score = part * ks;
             const uint32_t key = sortable_key(bf16_bits_half_away(score));
-            const bool live = (g == 0) && tok < valid[q];
-            if (live) p.score_keys[static_cast<size_t>(b * RPR + q) * p.key_stride + tok] = static_cast<uint16_t>(key);
-            wave_hist_add(s_hist + q * 256, key >> 8, live);
+            if (g == 0) {
+                s_keys[q * kChunkTokens + local] = static_cast<uint16_t>(key);
+                if (tok < valid[q]) atomicAdd(&s_hist[q * 256 + (key >> 8)], 1u);
+            }
         }
+    };
+
+    // Three-deep register pipeline over the wave's tiles, fully unrolled so that the
+    // buffers rotate by name (no register copies).
+    v4i buf[3][NV];
+    float ksb[3];
+    issue(0, buf[0], ksb[0]);
+    issue(1, buf[1], ksb[1]);
 #pragma unroll
-        for (int v = 0; v < NV; ++v) kb[v] = kn[v];
-        ks = ksn;
+    for (int i = 0; i < kTilesPerWave; ++i) {
+        if (i + 2 < kTilesPerWave) issue(i + 2, buf[(i + 2) % 3], ksb[(i + 2) % 3]);
+        if (i < ntiles) compute(i, buf[i % 3], ksb[i % 3]);
     }
     __syncthreads();
+
+    // Write the chunk's keys (8 bytes per thread per store) and histogram.
+#pragma unroll
+    for (int q = 0; q < RPR; ++q) {
+        const int live = min(valid[q] - chunk0, kChunkTokens);
+        uint16_t* dst = p.score_keys + static_cast<size_t>(b * RPR + q) * p.key_stride + chunk0;
+        for (int t = tid * 4; t < live; t += kLiThreads * 4) {
+            if (t + 4 <= live) {
+                *reinterpret_cast<uint2*>(dst + t) = *reinterpret_cast<const uint2*>(&s_keys[q * kChunkTokens + t]);
+            } else {
+                for (int u = t; u < live; ++u) dst[u] = s_keys[q * kChunkTokens + u];
+            }
+        }
+    }
     for (int i = tid; i < RPR * 256; i += kLiThreads) {
         const uint32_t c = s_hist[i];
         if (c != 0u) atomicAdd(&p.histogram[static_cast<size_t>(b) * RPR * 256 + i], c);

@@ -168,6 +168,131 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const KvipTopkArgs p
     report(p.status, err);
 }
 
+
+// Register-resident variant for rows of at most 1024*KPT keys (KPT <= 64): thread t holds keys
+// [t*KPT, (t+1)*KPT) (packed two per register), loaded in one batch, so the whole
+// select costs one round of key loads, two LDS histograms and one workgroup scan.
+template <int KPT>
+__global__ __launch_bounds__(kTopkThreads) void topk_regs_kernel(const KvipTopkArgs p) {
+    constexpr int W = KPT / 2;  // packed registers per thread
+    __shared__ uint32_t s_hist[256];
+    __shared__ uint32_t s_wave[kTopkThreads / 64];
+    __shared__ int s_sel[4];
+
+    const int tid = threadIdx.x;
+    const int row = blockIdx.x;
+    const int b = row / p.rows_per_request;
+    int valid = max(p.seq_lens[b], 0);
+    if (p.query_ends != nullptr) valid = min(valid, p.query_ends[row]);
+    valid = min(max(valid, 0), min(p.key_stride, kTopkThreads * KPT));
+    int32_t* out = p.topk + static_cast<size_t>(row) * kTopK;
+    const uint16_t* keys = p.score_keys + static_cast<size_t>(row) * p.key_stride;
+    uint32_t* ghist = p.histogram != nullptr ? p.histogram + static_cast<size_t>(row) * 256 : nullptr;
+
+    if (valid < kTopK) {
+        for (int i = tid; i < kTopK; i += kTopkThreads) out[i] = i < valid ? i : -1;
+        if (ghist != nullptr && tid < 256) ghist[tid] = 0u;
+        return;
+    }
+
+    // Keys of this thread; positions >= valid read as 0 and are masked by `count`.
+    const int first = tid * KPT;
+    const int count = max(0, min(KPT, valid - first));
+    uint32_t kk[W];
+    if (count == KPT) {
+#pragma unroll
+        for (int v = 0; v < W / 4; ++v) {
+            const v4i x = *reinterpret_cast<const v4i*>(keys + first + v * 8);
+            kk[4 * v] = x[0];
+            kk[4 * v + 1] = x[1];
+            kk[4 * v + 2] = x[2];
+            kk[4 * v + 3] = x[3];
+        }
+    } else {
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+            const uint32_t lo = 2 * w < count ? keys[first + 2 * w] : 0u;
+            const uint32_t hi = 2 * w + 1 < count ? keys[first + 2 * w + 1] : 0u;
+            kk[w] = lo | (hi << 16);
+        }
+    }
+    auto key_at = [&](int j) -> uint32_t { return (j & 1) ? (kk[j >> 1] >> 16) : (kk[j >> 1] & 0xFFFFu); };
+
+    // Level 1: high byte.
+    if (tid < 256) s_hist[tid] = ghist != nullptr ? ghist[tid] : 0u;
+    if (tid == 0) {
+        s_sel[0] = -1;
+        s_sel[2] = -1;
+    }
+    __syncthreads();
+    if (ghist != nullptr) {
+        if (tid < 256) ghist[tid] = 0u;  // ready for the next scoring launch
+    } else {
+#pragma unroll
+        for (int j = 0; j < KPT; ++j) wave_hist_add(s_hist, key_at(j) >> 8, j < count);
+    }
+    __syncthreads();
+    select_bin(s_hist, kTopK, s_sel, s_wave);
+    const int hb = s_sel[0];
+    const uint32_t gt_hi = static_cast<uint32_t>(s_sel[1]);
+    if (hb < 0) {
+        for (int i = tid; i < kTopK; i += kTopkThreads) out[i] = -1;
+        if (tid == 0) report(p.status, KVIP_STATUS_HISTOGRAM);
+        return;
+    }
+
+    // Level 2: low byte among keys whose high byte is hb.
+    if (tid < 256) s_hist[tid] = 0u;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+        const uint32_t k = key_at(j);
+        if (j < count && static_cast<int>(k >> 8) == hb) atomicAdd(&s_hist[k & 0xFFu], 1u);
+    }
+    __syncthreads();
+    select_bin(s_hist, kTopK - gt_hi, s_sel + 2, s_wave);
+    if (s_sel[2] < 0) {
+        for (int i = tid; i < kTopK; i += kTopkThreads) out[i] = -1;
+        if (tid == 0) report(p.status, KVIP_STATUS_HISTOGRAM);
+        return;
+    }
+    const uint32_t kth = (static_cast<uint32_t>(hb) << 8) | static_cast<uint32_t>(s_sel[2]);
+    const uint32_t n_gt = gt_hi + static_cast<uint32_t>(s_sel[3]);
+    const uint32_t need = kTopK - n_gt;
+
+    // Level 3: one scan of (gt, eq) counts packed as gt << 20 | eq (gt < 2048, eq < 2^20).
+    uint32_t ngt = 0, neq = 0;
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+        const uint32_t k = key_at(j);
+        const bool in = j < count;
+        ngt += (in && k > kth) ? 1u : 0u;
+        neq += (in && k == kth) ? 1u : 0u;
+    }
+    uint32_t total;
+    const uint32_t excl = block_exclusive_scan((ngt << 20) | neq, s_wave, &total);
+    uint32_t pg = excl >> 20;
+    uint32_t pe = excl & 0xFFFFFu;
+    uint32_t err = 0;
+    if (ngt != 0u || (neq != 0u && pe < need)) {
+#pragma unroll
+        for (int j = 0; j < KPT; ++j) {
+            const uint32_t k = key_at(j);
+            if (j < count) {
+                if (k > kth) {
+                    if (pg < n_gt) out[pg] = first + j;
+                    else err = KVIP_STATUS_HISTOGRAM;
+                    ++pg;
+                } else if (k == kth) {
+                    if (pe < need) out[n_gt + pe] = first + j;
+                    ++pe;
+                }
+            }
+        }
+    }
+    report(p.status, err);
+}
+
 }  // namespace
 
 uint32_t validate_topk(const KvipTopkArgs* a) {
@@ -181,7 +306,20 @@ uint32_t validate_topk(const KvipTopkArgs* a) {
 }
 
 hipError_t launch_topk(const KvipTopkArgs& a, hipStream_t stream) {
-    hipLaunchKernelGGL(topk_kernel, dim3(a.batch * a.rows_per_request), dim3(kTopkThreads), 0, stream, a);
+    const dim3 grid(a.batch * a.rows_per_request);
+    const dim3 block(kTopkThreads);
+    // Rows that fit 1024*KPT keys use the register-resident select.
+    if (a.key_stride <= kTopkThreads * 8) {
+        hipLaunchKernelGGL(topk_regs_kernel<8>, grid, block, 0, stream, a);
+    } else if (a.key_stride <= kTopkThreads * 16) {
+        hipLaunchKernelGGL(topk_regs_kernel<16>, grid, block, 0, stream, a);
+    } else if (a.key_stride <= kTopkThreads * 32) {
+        hipLaunchKernelGGL(topk_regs_kernel<32>, grid, block, 0, stream, a);
+    } else if (a.key_stride <= kTopkThreads * 64) {
+        hipLaunchKernelGGL(topk_regs_kernel<64>, grid, block, 0, stream, a);
+    } else {
+        hipLaunchKernelGGL(topk_kernel, grid, block, 0, stream, a);
+    }
     return hipGetLastError();
 }
 

@@ -31,6 +31,9 @@ HIPCC_FLAGS = [
     "-shared",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-command-line-argument",
+    # MFMA accumulators in VGPRs (gfx950 has a unified register file): the epilogue then
+    # reads them without v_accvgpr_read moves.
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
 ]
 
 
