@@ -26,21 +26,17 @@ struct Keys8 {
     int count;  // keys of this thread below `valid`
 };
 
-KVIP_DEVICE Keys8 load_keys(const uint16_t* keys, int idx0, int valid) {
+// Keys [idx0, idx0+8) of a row with `stride` keys; positions >= valid are masked by
+// `count`. The 16-byte load is unconditional with its start clamped into the row.
+KVIP_DEVICE Keys8 load_keys(const uint16_t* keys, int idx0, int valid, int stride) {
     Keys8 r;
-    if (idx0 + kKeysPerThread <= valid) {
-        const v4i v = *reinterpret_cast<const v4i*>(keys + idx0);
+    const v4i v = *reinterpret_cast<const v4i*>(keys + min(idx0, stride - kKeysPerThread));
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            r.k[2 * j] = static_cast<uint32_t>(v[j]) & 0xFFFFu;
-            r.k[2 * j + 1] = static_cast<uint32_t>(v[j]) >> 16;
-        }
-        r.count = kKeysPerThread;
-    } else {
-        r.count = max(0, min(kKeysPerThread, valid - idx0));
-#pragma unroll
-        for (int j = 0; j < kKeysPerThread; ++j) r.k[j] = j < r.count ? keys[idx0 + j] : 0u;
+    for (int j = 0; j < 4; ++j) {
+        r.k[2 * j] = static_cast<uint32_t>(v[j]) & 0xFFFFu;
+        r.k[2 * j + 1] = static_cast<uint32_t>(v[j]) >> 16;
     }
+    r.count = max(0, min(kKeysPerThread, valid - idx0));
     return r;
 }
 
@@ -91,7 +87,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const KvipTopkArgs p
         if (tid < 256) ghist[tid] = 0u;  // ready for the next scoring launch
     } else {
         for (int base = tid * kKeysPerThread; base < valid; base += kTileKeys) {
-            const Keys8 r = load_keys(keys, base, valid);
+            const Keys8 r = load_keys(keys, base, valid, p.key_stride);
 #pragma unroll
             for (int j = 0; j < kKeysPerThread; ++j) {
                 wave_hist_add(s_hist, r.k[j] >> 8, j < r.count);
@@ -112,7 +108,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const KvipTopkArgs p
     if (tid < 256) s_hist[tid] = 0u;
     __syncthreads();
     for (int base = tid * kKeysPerThread; base < valid; base += kTileKeys) {
-        const Keys8 r = load_keys(keys, base, valid);
+        const Keys8 r = load_keys(keys, base, valid, p.key_stride);
 #pragma unroll
         for (int j = 0; j < kKeysPerThread; ++j) {
             if (j < r.count && static_cast<int>(r.k[j] >> 8) == hb) atomicAdd(&s_hist[r.k[j] & 0xFFu], 1u);
@@ -134,7 +130,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const KvipTopkArgs p
     uint32_t err = 0;
     for (int tile = 0; tile < valid; tile += kTileKeys) {
         const int idx0 = tile + tid * kKeysPerThread;
-        const Keys8 r = load_keys(keys, idx0, valid);
+        const Keys8 r = load_keys(keys, idx0, valid, p.key_stride);
         uint32_t ngt = 0, neq = 0;
 #pragma unroll
         for (int j = 0; j < kKeysPerThread; ++j) {
@@ -178,6 +174,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_regs_kernel(const KvipTopkA
     __shared__ uint32_t s_hist[256];
     __shared__ uint32_t s_wave[kTopkThreads / 64];
     __shared__ int s_sel[4];
+    __shared__ __align__(16) int32_t s_out[kTopK];
 
     const int tid = threadIdx.x;
     const int row = blockIdx.x;
@@ -198,23 +195,17 @@ __global__ __launch_bounds__(kTopkThreads) void topk_regs_kernel(const KvipTopkA
     // Keys of this thread; positions >= valid read as 0 and are masked by `count`.
     const int first = tid * KPT;
     const int count = max(0, min(KPT, valid - first));
+    // Every vector load is unconditional: its start is clamped into the row (the row
+    // stride is a multiple of 8 keys), and keys past `valid` are masked by `count`.
     uint32_t kk[W];
-    if (count == KPT) {
 #pragma unroll
-        for (int v = 0; v < W / 4; ++v) {
-            const v4i x = *reinterpret_cast<const v4i*>(keys + first + v * 8);
-            kk[4 * v] = x[0];
-            kk[4 * v + 1] = x[1];
-            kk[4 * v + 2] = x[2];
-            kk[4 * v + 3] = x[3];
-        }
-    } else {
-#pragma unroll
-        for (int w = 0; w < W; ++w) {
-            const uint32_t lo = 2 * w < count ? keys[first + 2 * w] : 0u;
-            const uint32_t hi = 2 * w + 1 < count ? keys[first + 2 * w + 1] : 0u;
-            kk[w] = lo | (hi << 16);
-        }
+    for (int v = 0; v < W / 4; ++v) {
+        const int at = min(first + v * 8, p.key_stride - 8);
+        const v4i x = *reinterpret_cast<const v4i*>(keys + at);
+        kk[4 * v] = x[0];
+        kk[4 * v + 1] = x[1];
+        kk[4 * v + 2] = x[2];
+        kk[4 * v + 3] = x[3];
     }
     auto key_at = [&](int j) -> uint32_t { return (j & 1) ? (kk[j >> 1] >> 16) : (kk[j >> 1] & 0xFFFFu); };
 
@@ -274,22 +265,28 @@ __global__ __launch_bounds__(kTopkThreads) void topk_regs_kernel(const KvipTopkA
     uint32_t pg = excl >> 20;
     uint32_t pe = excl & 0xFFFFFu;
     uint32_t err = 0;
+    // The row is assembled in LDS and written with one coalesced 8-byte store per thread.
+    reinterpret_cast<int2*>(s_out)[tid] = int2{-1, -1};
+    __syncthreads();
     if (ngt != 0u || (neq != 0u && pe < need)) {
 #pragma unroll
         for (int j = 0; j < KPT; ++j) {
             const uint32_t k = key_at(j);
             if (j < count) {
                 if (k > kth) {
-                    if (pg < n_gt) out[pg] = first + j;
+                    if (pg < n_gt) s_out[pg] = first + j;
                     else err = KVIP_STATUS_HISTOGRAM;
                     ++pg;
                 } else if (k == kth) {
-                    if (pe < need) out[n_gt + pe] = first + j;
+                    if (pe < need) s_out[n_gt + pe] = first + j;
                     ++pe;
                 }
             }
         }
     }
+    __syncthreads();
+    static_assert(kTopK == 2 * kTopkThreads, "one int2 per thread");
+    reinterpret_cast<int2*>(out)[tid] = reinterpret_cast<const int2*>(s_out)[tid];
     report(p.status, err);
 }
 
