@@ -56,6 +56,21 @@ def algorithmic_bytes(wl, heads, has_qscale):
     return {"indexer": score, "topk": topk, "fetch": gather}
 
 
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
+    summary, when it was taken on the current library sources; otherwise None."""
+    from kvip_amd.runtime.build import source_digest
+
+    path = ROOT / "profiles" / "decode_c2_traffic.json"
+    try:
+        data = json.loads(path.read_text())
+    except (OSError, ValueError):
+        return None
+    if data.get("source_digest") != source_digest():
+        return None
+    return data.get("traffic_bytes", {}).get(kernel)
+
+
 def cpu_baseline(torch, wl, rot, budget_s):
     """The oracle (oracle/indexer.py) on the first rows of the same workload until the
     time budget is spent: LI keys, TopK-2048, Fetch gather, per query row."""
@@ -217,7 +232,8 @@ def main():
         "kernels": {k: {"ms": round(v, 5), "bytes": int(mean_bytes[k]),
                         "gbs": round(mean_bytes[k] / (v * 1e-3) / 1e9, 1)} for k, v in times.items()},
         "roofline": {"kernel": dominant, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic(dominant) if args.config == "c2" else None},
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(torch, wl, rot, args.cpu_seconds)
