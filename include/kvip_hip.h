@@ -21,6 +21,11 @@
  *   kvip_hip_fetch_gather     <- kvaf_device::KvafBatchGetDevice as called by FetchQueryGroup
  *                                (op_kernel/streaming.cpp:365-500, :445;
  *                                 patches/kvaf-ubmem-device-get.patch:41-90)
+ *   kvip_hip_update_abc       <- kvip.update_abc (python/kvip/cache/abc.py:5-33; the NPU launch
+ *                                of cache/_abc_kernel.py:9-34)
+ *   kvip_hip_lru_reset/extend/commit
+ *                             <- SlotLRU.resize / SlotLRU.commit (python/kvip/cache/lru.py:33-118)
+ *                                and their numba kernels (cache/_lru_kernel.py:33-199)
  */
 #ifndef KVIP_HIP_H
 #define KVIP_HIP_H
@@ -130,11 +135,49 @@ typedef struct KvipLIFetchArgs {
     KvipFetchArgs fetch;
 } KvipLIFetchArgs;
 
+/* ABC ring maps: token_to_slot / slot_to_token are int32 [layers, pool, tokens];
+ * descriptors int32 [groups, rows, 4] of (layer, owner, begin, end); the first `requests`
+ * rows of every group are applied in group-major order. Descriptors naming an out-of-range
+ * layer/owner/token are skipped and reported with KVIP_STATUS_BAD_TOKEN. */
+typedef struct KvipAbcArgs {
+    int32_t* token_to_slot;
+    int32_t* slot_to_token;
+    const int32_t* descriptors;
+    uint32_t* status;            /* device status word, or NULL */
+    int32_t groups;
+    int32_t rows;                /* descriptors.shape[1] */
+    int32_t requests;            /* rows applied per group, <= rows */
+    int32_t layers;
+    int32_t pool;
+    int32_t t2s_tokens;          /* token_to_slot.shape[2] */
+    int32_t s2t_tokens;          /* slot_to_token.shape[2], >= history + tail */
+    int32_t history;
+    int32_t tail;
+} KvipAbcArgs;
+
+/* Slot LRU of one request/layer chain on the device. order[i] is the slot at LRU position
+ * i (0 = least recently used) for i < active; slots [2048] = the min(2048, active) oldest
+ * slots (-1 padded); bitmap [bitmap_words] = their membership bits; scratch [capacity] is
+ * work memory. capacity <= 133632 slots. */
+typedef struct KvipLruArgs {
+    int32_t* order;
+    int32_t* scratch;
+    int32_t* slots;
+    int32_t* bitmap;
+    int32_t capacity;
+    int32_t bitmap_words;
+} KvipLruArgs;
+
 uint32_t kvip_hip_abi_version(void);
 uint32_t kvip_hip_indexer_decode(const KvipIndexerArgs* args, void* stream);
 uint32_t kvip_hip_topk(const KvipTopkArgs* args, void* stream);
 uint32_t kvip_hip_fetch_gather(const KvipFetchArgs* args, void* stream);
 uint32_t kvip_hip_lifetch_forward(const KvipLIFetchArgs* args, void* stream);
+uint32_t kvip_hip_update_abc(const KvipAbcArgs* args, void* stream);
+uint32_t kvip_hip_lru_reset(const KvipLruArgs* args, int32_t committed, void* stream);
+uint32_t kvip_hip_lru_extend(const KvipLruArgs* args, int32_t active, int32_t committed, void* stream);
+uint32_t kvip_hip_lru_commit(const KvipLruArgs* args, const int32_t* destinations, int32_t count, int32_t active,
+                             void* stream);
 
 #ifdef __cplusplus
 }

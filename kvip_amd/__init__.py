@@ -10,6 +10,8 @@ __all__ = [
     "LIFetch",
     "LIFetchBinding",
     "ContiguousFetch",
+    "SlotLRU",
+    "update_abc",
     "build_libraries",
     "load_library",
 ]
@@ -18,6 +20,8 @@ _EXPORTS = {
     "LIFetch": ("operators.lifetch.forward", "LIFetchForward"),
     "LIFetchBinding": ("operators.lifetch.binding", "LIFetchBinding"),
     "ContiguousFetch": ("operators.lifetch.binding", "ContiguousFetch"),
+    "SlotLRU": ("cache.lru", "SlotLRU"),
+    "update_abc": ("cache.abc", "update_abc"),
     "build_libraries": ("runtime.build", "build_libraries"),
     "load_library": ("runtime.abi", "load_library"),
 }

@@ -1,0 +1,201 @@
+// Cache-state operators on gfx950: ABC ring maps and the resident-slot LRU.
+//
+// update_abc (reference: python/kvip/cache/abc.py:5-33, CPU golden :23-33). For every
+// descriptor (layer, owner, begin, end) in group-major order, token_to_slot[layer, owner,
+// t] = history + t % tail for t in [begin, end), and the ring slot_to_token[layer, owner,
+// history : history+tail] is reset to -1 and refilled with the range's tokens, a later
+// token overwriting an earlier one on the same ring slot. One workgroup per descriptor:
+// the token_to_slot values depend only on t, so descriptors that overlap write identical
+// values; the ring of a (layer, owner) is written only by the last descriptor naming it,
+// with the closed form "largest t in [begin, end) with t % tail == s" per ring slot s.
+//
+// Slot LRU (reference: python/kvip/cache/lru.py:14-118, _lru_kernel.py:33-199). The
+// doubly linked list of the reference is held as its order array: order[i] is the slot at
+// LRU position i (0 = oldest). commit moves the unique committed slots (< active) to the
+// end in ascending slot-id order: a stable partition of the order, done by one workgroup
+// with LDS membership bits and block scans. The victims are order[0 .. min(2048, active)),
+// with their bitmap.
+#include "kvip_device.h"
+
+namespace kvip {
+namespace {
+
+constexpr int kAbcThreads = 256;
+constexpr int kLruThreads = 1024;
+constexpr int kLruMaxSlots = (1 << 17) + 20 * 128;   // resident capacity bound (reference MAX_CACHE_TOKENS)
+constexpr int kLruBitmapWords = (kLruMaxSlots + 31) / 32;
+
+__global__ __launch_bounds__(kAbcThreads) void update_abc_kernel(const KvipAbcArgs p) {
+    const int r = blockIdx.x;  // row within the group, < requests
+    const int grp = blockIdx.y;
+    const int32_t* d = p.descriptors + (static_cast<size_t>(grp) * p.rows + r) * 4;
+    const int layer = d[0], owner = d[1], begin = d[2], end = d[3];
+    auto in_range = [&](int l, int o) {
+        return l >= 0 && l < p.layers && o >= 0 && o < p.pool;
+    };
+    const bool ok = in_range(layer, owner) && begin >= 0 && (end <= begin || end <= p.t2s_tokens);
+    if (!ok) {
+        if (threadIdx.x == 0) report(p.status, KVIP_STATUS_BAD_TOKEN);
+        return;
+    }
+    const size_t base = (static_cast<size_t>(layer) * p.pool + owner);
+    int32_t* t2s = p.token_to_slot + base * p.t2s_tokens;
+    for (int t = begin + static_cast<int>(threadIdx.x); t < end; t += kAbcThreads) t2s[t] = p.history + t % p.tail;
+
+    // Is a later (group-major) descriptor naming the same (layer, owner)? Then its ring wins.
+    const int total = p.groups * p.requests;
+    const int self = grp * p.requests + r;
+    int later = 0;
+    for (int k = self + 1 + static_cast<int>(threadIdx.x); k < total; k += kAbcThreads) {
+        const int32_t* e = p.descriptors + (static_cast<size_t>(k / p.requests) * p.rows + k % p.requests) * 4;
+        const bool valid = in_range(e[0], e[1]) && e[2] >= 0 && (e[3] <= e[2] || e[3] <= p.t2s_tokens);
+        later |= (valid && e[0] == layer && e[1] == owner) ? 1 : 0;
+    }
+    if (__syncthreads_or(later)) return;
+
+    int32_t* ring = p.slot_to_token + base * p.s2t_tokens + p.history;
+    for (int s = threadIdx.x; s < p.tail; s += kAbcThreads) {
+        int token = -1;
+        if (end > begin) {
+            const int hi = end - 1;
+            const int back = ((hi - s) % p.tail + p.tail) % p.tail;
+            const int t = hi - back;  // largest t <= hi with t % tail == s
+            token = t >= begin ? t : -1;
+        }
+        ring[s] = token;
+    }
+}
+
+// order[0, committed) = 0, 1, ..., committed-1 (a cold LRU in ascending slot order) and
+// the victim list/bitmap of it.
+__global__ __launch_bounds__(kLruThreads) void lru_reset_kernel(const KvipLruArgs p, int committed) {
+    for (int i = blockIdx.x * kLruThreads + threadIdx.x; i < p.capacity; i += gridDim.x * kLruThreads) {
+        p.order[i] = i < committed ? i : -1;
+    }
+}
+
+// Appends slots [first, committed) at the end of the order (growth keeps LRU order).
+__global__ __launch_bounds__(kLruThreads) void lru_extend_kernel(const KvipLruArgs p, int first, int committed) {
+    for (int i = first + blockIdx.x * kLruThreads + threadIdx.x; i < committed; i += gridDim.x * kLruThreads) {
+        p.order[i] = i;
+    }
+}
+
+// One workgroup: stable partition of order[0, active) into (not committed, committed in
+// ascending slot order) through `scratch`, then the victims of the new order.
+__global__ __launch_bounds__(kLruThreads) void lru_commit_kernel(const KvipLruArgs p, const int32_t* dest, int count,
+                                                                 int active, int commit) {
+    __shared__ uint32_t s_member[kLruBitmapWords];
+    __shared__ uint32_t s_wave[kLruThreads / 64];
+    const int tid = threadIdx.x;
+    const int words = (active + 31) / 32;
+    for (int i = tid; i < words; i += kLruThreads) s_member[i] = 0u;
+    __syncthreads();
+    if (commit) {
+        for (int i = tid; i < count; i += kLruThreads) {
+            const int s = dest[i];
+            if (s >= 0 && s < active) atomicOr(&s_member[s >> 5], 1u << (s & 31));
+        }
+    }
+    __syncthreads();
+
+    // Kept slots, in order, then committed slots in ascending id order.
+    uint32_t kept_base = 0;
+    for (int tile = 0; tile < active; tile += kLruThreads * 8) {
+        int v[8];
+        uint32_t keep = 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int i = tile + tid * 8 + j;
+            v[j] = i < active ? p.order[i] : -1;
+            const bool k = v[j] >= 0 && !((s_member[v[j] >> 5] >> (v[j] & 31)) & 1u);
+            keep |= (k ? 1u : 0u) << j;
+        }
+        uint32_t tile_total;
+        uint32_t pos = kept_base + block_exclusive_scan(__popc(keep), s_wave, &tile_total);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            if ((keep >> j) & 1u) p.scratch[pos++] = v[j];
+        }
+        kept_base += tile_total;
+    }
+    uint32_t moved_base = kept_base;
+    for (int w0 = 0; w0 < words; w0 += kLruThreads) {
+        const int w = w0 + tid;
+        const uint32_t bits = w < words ? s_member[w] : 0u;
+        uint32_t tile_total;
+        uint32_t pos = moved_base + block_exclusive_scan(__popc(bits), s_wave, &tile_total);
+        uint32_t rest = bits;
+        while (rest) {
+            const int b = __ffs(rest) - 1;
+            p.scratch[pos++] = w * 32 + b;
+            rest &= rest - 1;
+        }
+        moved_base += tile_total;
+    }
+    __syncthreads();  // scratch complete (workgroup fence + barrier)
+    for (int i = tid; i < active; i += kLruThreads) p.order[i] = p.scratch[i];
+
+    // Victims: the oldest min(2048, active) slots and their bitmap.
+    const int victims = min(kTopK, active);
+    for (int i = tid; i < kTopK; i += kLruThreads) p.slots[i] = i < victims ? p.scratch[i] : -1;
+    __syncthreads();
+    for (int i = tid; i < p.bitmap_words; i += kLruThreads) s_member[i] = 0u;
+    __syncthreads();
+    for (int i = tid; i < victims; i += kLruThreads) {
+        const int s = p.scratch[i];
+        atomicOr(&s_member[s >> 5], 1u << (s & 31));
+    }
+    __syncthreads();
+    for (int i = tid; i < p.bitmap_words; i += kLruThreads) p.bitmap[i] = static_cast<int32_t>(s_member[i]);
+}
+
+}  // namespace
+}  // namespace kvip
+
+extern "C" uint32_t kvip_hip_update_abc(const KvipAbcArgs* a, void* stream) {
+    if (a == nullptr || a->token_to_slot == nullptr || a->slot_to_token == nullptr || a->descriptors == nullptr ||
+        a->groups < 0 || a->requests < 0 || a->rows < a->requests || a->layers < 1 || a->pool < 1 ||
+        a->t2s_tokens < 1 || a->tail < 1 || a->history < 0 ||
+        static_cast<int64_t>(a->history) + a->tail > a->s2t_tokens || a->groups > 65535) {
+        return KVIP_ERR_INVALID;
+    }
+    if (a->groups == 0 || a->requests == 0) return KVIP_OK;
+    hipLaunchKernelGGL(kvip::update_abc_kernel, dim3(a->requests, a->groups), dim3(kvip::kAbcThreads), 0,
+                       static_cast<hipStream_t>(stream), *a);
+    return static_cast<uint32_t>(hipGetLastError());
+}
+
+static bool lru_ok(const KvipLruArgs* a) {
+    return a != nullptr && a->order != nullptr && a->scratch != nullptr && a->slots != nullptr &&
+           a->bitmap != nullptr && a->capacity >= 1 && a->capacity <= kvip::kLruMaxSlots &&
+           a->bitmap_words >= (a->capacity + 31) / 32 && a->bitmap_words <= kvip::kLruBitmapWords;
+}
+
+extern "C" uint32_t kvip_hip_lru_reset(const KvipLruArgs* a, int32_t committed, void* stream) {
+    if (!lru_ok(a) || committed < 0 || committed > a->capacity) return KVIP_ERR_INVALID;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    const int grid = (a->capacity + kvip::kLruThreads - 1) / kvip::kLruThreads;
+    hipLaunchKernelGGL(kvip::lru_reset_kernel, dim3(grid), dim3(kvip::kLruThreads), 0, s, *a, committed);
+    hipLaunchKernelGGL(kvip::lru_commit_kernel, dim3(1), dim3(kvip::kLruThreads), 0, s, *a, nullptr, 0, committed, 0);
+    return static_cast<uint32_t>(hipGetLastError());
+}
+
+extern "C" uint32_t kvip_hip_lru_extend(const KvipLruArgs* a, int32_t active, int32_t committed, void* stream) {
+    if (!lru_ok(a) || active < 0 || committed < active || committed > a->capacity) return KVIP_ERR_INVALID;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    const int grid = max(1, (committed - active + kvip::kLruThreads - 1) / kvip::kLruThreads);
+    hipLaunchKernelGGL(kvip::lru_extend_kernel, dim3(grid), dim3(kvip::kLruThreads), 0, s, *a, active, committed);
+    hipLaunchKernelGGL(kvip::lru_commit_kernel, dim3(1), dim3(kvip::kLruThreads), 0, s, *a, nullptr, 0, committed, 0);
+    return static_cast<uint32_t>(hipGetLastError());
+}
+
+extern "C" uint32_t kvip_hip_lru_commit(const KvipLruArgs* a, const int32_t* destinations, int32_t count,
+                                        int32_t active, void* stream) {
+    if (!lru_ok(a) || count < 0 || (count > 0 && destinations == nullptr) || active < 0 || active > a->capacity) {
+        return KVIP_ERR_INVALID;
+    }
+    hipLaunchKernelGGL(kvip::lru_commit_kernel, dim3(1), dim3(kvip::kLruThreads), 0, static_cast<hipStream_t>(stream),
+                       *a, destinations, count, active, 1);
+    return static_cast<uint32_t>(hipGetLastError());
+}

@@ -51,7 +51,7 @@ class LIFetchBinding:
         weight_dtype = torch.float32 if weight_dtype is None else weight_dtype
         if weight_dtype not in (torch.float32, torch.bfloat16):
             raise ValueError("LIFetch weights must be float32 or bfloat16")
-        self.torch, self.device = torch, torch.device(device)
+        self.torch, self.device = torch, abi.device_of(torch, device)
         self.batch, self.heads, self.rows_per_request = batch, heads, rows_per_request
         self.rows = batch * rows_per_request
         self.max_blocks = (max_context + BLOCK_TOKENS - 1) // BLOCK_TOKENS

@@ -59,6 +59,21 @@ class LIFetchArgs(ctypes.Structure):
     _fields_ = [("indexer", IndexerArgs), ("topk", TopkArgs), ("fetch", FetchArgs)]
 
 
+class AbcArgs(ctypes.Structure):
+    _fields_ = [
+        ("token_to_slot", _p), ("slot_to_token", _p), ("descriptors", _p), ("status", _p),
+        ("groups", _i32), ("rows", _i32), ("requests", _i32), ("layers", _i32), ("pool", _i32),
+        ("t2s_tokens", _i32), ("s2t_tokens", _i32), ("history", _i32), ("tail", _i32),
+    ]
+
+
+class LruArgs(ctypes.Structure):
+    _fields_ = [
+        ("order", _p), ("scratch", _p), ("slots", _p), ("bitmap", _p),
+        ("capacity", _i32), ("bitmap_words", _i32),
+    ]
+
+
 # name -> (argtypes, restype); must list every function declared in include/kvip_hip.h.
 PROTOTYPES = {
     "kvip_hip_abi_version": ([], ctypes.c_uint32),
@@ -66,6 +81,10 @@ PROTOTYPES = {
     "kvip_hip_topk": ([ctypes.POINTER(TopkArgs), _p], ctypes.c_uint32),
     "kvip_hip_fetch_gather": ([ctypes.POINTER(FetchArgs), _p], ctypes.c_uint32),
     "kvip_hip_lifetch_forward": ([ctypes.POINTER(LIFetchArgs), _p], ctypes.c_uint32),
+    "kvip_hip_update_abc": ([ctypes.POINTER(AbcArgs), _p], ctypes.c_uint32),
+    "kvip_hip_lru_reset": ([ctypes.POINTER(LruArgs), _i32, _p], ctypes.c_uint32),
+    "kvip_hip_lru_extend": ([ctypes.POINTER(LruArgs), _i32, _i32, _p], ctypes.c_uint32),
+    "kvip_hip_lru_commit": ([ctypes.POINTER(LruArgs), _p, _i32, _i32, _p], ctypes.c_uint32),
 }
 
 _LIB = None
@@ -109,6 +128,14 @@ def check(rc: int, what: str) -> None:
 def ptr(tensor) -> int:
     """Device address of a tensor, or 0 for None."""
     return 0 if tensor is None else int(tensor.data_ptr())
+
+
+def device_of(torch, device):
+    """torch.device with an explicit index ("cuda" -> "cuda:<current>")."""
+    device = torch.device(device)
+    if device.type == "cuda" and device.index is None:
+        device = torch.device("cuda", torch.cuda.current_device())
+    return device
 
 
 def stream_handle(torch, device) -> int:

@@ -34,6 +34,8 @@ STRUCTS = {
     "KvipTopkArgs": abi.TopkArgs,
     "KvipFetchArgs": abi.FetchArgs,
     "KvipLIFetchArgs": abi.LIFetchArgs,
+    "KvipAbcArgs": abi.AbcArgs,
+    "KvipLruArgs": abi.LruArgs,
 }
 
 

@@ -1,0 +1,113 @@
+"""GPU parity of the cache operators (update_abc, SlotLRU) against oracle/cache.py,
+bit-exact, through the C ABI."""
+import numpy as np
+import pytest
+
+import kvip_amd
+from kvip_amd.runtime import abi
+from oracle import cache as ref
+
+pytestmark = pytest.mark.gpu
+
+
+def run_abc(torch, t2s, s2t, desc, requests, history, tail):
+    dt2s, ds2t = torch.from_numpy(t2s).cuda(), torch.from_numpy(s2t).cuda()
+    status = torch.zeros(1, dtype=torch.int32, device="cuda")
+    kvip_amd.update_abc(dt2s, ds2t, torch.from_numpy(desc).cuda(), requests, history, tail, status=status)
+    torch.cuda.synchronize()
+    ref.update_abc(t2s, s2t, desc, requests, history, tail)
+    return dt2s.cpu().numpy(), ds2t.cpu().numpy(), int(status.item())
+
+
+def test_update_abc_known_answer_and_shifted_rings(torch_gpu):
+    torch = torch_gpu
+    t2s = np.full((2, 3, 2048), -1, np.int32)
+    s2t = t2s.copy()
+    g2, g3, st = run_abc(torch, t2s, s2t, np.array([[[1, 2, 383, 390]]], np.int32), 1, 1024, 384)
+    assert np.array_equal(g2, t2s) and np.array_equal(g3, s2t) and st == 0
+    desc = np.array([[[2, 4, 350, 734], [2, 1, 768, 768]], [[0, 3, 383, 390], [0, 2, 128, 140]]], np.int32)
+    t2s = np.full((3, 5, 2048), 99, np.int32)
+    s2t = t2s.copy()
+    dt2s, ds2t = torch.from_numpy(t2s).cuda(), torch.from_numpy(s2t).cuda()
+    for shift in (0, 128):
+        desc[:, :, 2:] += shift
+        kvip_amd.update_abc(dt2s, ds2t, torch.from_numpy(desc).cuda(), 2, 1024, 384)
+        ref.update_abc(t2s, s2t, desc, 2, 1024, 384)
+        torch.cuda.synchronize()
+        assert np.array_equal(dt2s.cpu().numpy(), t2s) and np.array_equal(ds2t.cpu().numpy(), s2t), shift
+
+
+def test_update_abc_random_duplicates_long_and_empty_ranges(torch_gpu):
+    torch = torch_gpu
+    rng = np.random.default_rng(12)
+    for trial in range(4):
+        layers, pool, tokens, history, tail = 3, 4, 3000, 2000, 384
+        groups, rows = int(rng.integers(1, 5)), int(rng.integers(1, 7))
+        desc = np.zeros((groups, rows, 4), np.int32)
+        desc[..., 0] = rng.integers(0, layers, (groups, rows))
+        desc[..., 1] = rng.integers(0, 2, (groups, rows))  # few owners -> duplicate targets
+        begin = rng.integers(0, 2500, (groups, rows))
+        length = rng.choice([0, 5, 383, 384, 385, 1000], (groups, rows))
+        desc[..., 2] = begin
+        desc[..., 3] = np.minimum(begin + length, tokens)
+        t2s = rng.integers(-3, 5000, (layers, pool, tokens)).astype(np.int32)
+        s2t = rng.integers(-3, 5000, (layers, pool, tokens)).astype(np.int32)
+        requests = int(rng.integers(1, rows + 1))
+        g2, g3, st = run_abc(torch, t2s, s2t, desc, requests, history, tail)
+        assert np.array_equal(g2, t2s), trial
+        assert np.array_equal(g3, s2t), trial
+        assert st == 0
+
+
+def test_update_abc_rejects_and_reports(torch_gpu):
+    torch = torch_gpu
+    t2s = torch.zeros((1, 2, 512), dtype=torch.int32, device="cuda")
+    s2t = torch.zeros((1, 2, 512), dtype=torch.int32, device="cuda")
+    with pytest.raises(ValueError):
+        kvip_amd.update_abc(t2s.cpu(), s2t.cpu(), torch.zeros((1, 1, 4), dtype=torch.int32), 1, 100, 50)
+    with pytest.raises(ValueError):
+        kvip_amd.update_abc(t2s, s2t, torch.zeros((1, 1, 4), dtype=torch.int32, device="cuda"), 1, 500, 50)
+    status = torch.zeros(1, dtype=torch.int32, device="cuda")
+    bad = torch.tensor([[[0, 7, 0, 10]]], dtype=torch.int32, device="cuda")  # owner out of range
+    kvip_amd.update_abc(t2s, s2t, bad, 1, 100, 50, status=status)
+    torch.cuda.synchronize()
+    assert int(status.item()) & abi.STATUS_BAD_TOKEN
+    assert not t2s.any() and not s2t.any()
+
+
+def check_lru(torch, gpu, cpu):
+    assert gpu.active == cpu.active
+    assert gpu.slots.cpu().numpy()[0].tolist() == cpu.slots.tolist()
+    words = cpu.bitmap.shape[0]
+    assert np.array_equal(gpu.bitmap.cpu().numpy()[0][:words].view(np.uint32), cpu.bitmap)
+    assert gpu.order[: gpu.active].cpu().numpy().tolist() == cpu.order()
+
+
+def test_slot_lru_matches_oracle(torch_gpu):
+    torch = torch_gpu
+    rng = np.random.default_rng(9)
+    gpu, cpu = kvip_amd.SlotLRU("cuda"), ref.SlotLRU()
+    gpu.resize(16384, 16384)
+    cpu.resize(16384, 16384)
+    check_lru(torch, gpu, cpu)
+    first = gpu.slots.clone()
+    for step in range(40):
+        if step in (10, 25):
+            committed = int(rng.integers(1, 16384))
+            gpu.resize(16384, committed)
+            cpu.resize(16384, committed)
+        elif step == 30:
+            gpu.resize(40000, 30000)
+            cpu.resize(40000, 30000)
+        else:
+            dest = rng.integers(-3, cpu.active + 20, int(rng.integers(0, 9000))).astype(np.int32)
+            gpu.commit(torch.from_numpy(dest).cuda())
+            cpu.commit(dest)
+        torch.cuda.synchronize()
+        check_lru(torch, gpu, cpu)
+    assert not torch.equal(first, gpu.slots)
+    gpu.resize(40000, 100)
+    cpu.resize(40000, 100)
+    torch.cuda.synchronize()
+    check_lru(torch, gpu, cpu)
+    assert (gpu.slots[0, 100:] == -1).all()
