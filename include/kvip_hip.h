@@ -26,6 +26,12 @@
  *   kvip_hip_lru_reset/extend/commit
  *                             <- SlotLRU.resize / SlotLRU.commit (python/kvip/cache/lru.py:33-118)
  *                                and their numba kernels (cache/_lru_kernel.py:33-199)
+ *   kvip_hip_lidu             <- kvip.lidu = lidu_fused_batch_get_prepare_mtp_out
+ *                                (python/kvip/operators/lidu.py:4-8; torch_extension/csrc/
+ *                                 lidu_fused_batch_get_prepare_mtp_ops.cpp:195-270, schema :386-399;
+ *                                 op_kernel/a5_lidu_fused_batch_get_prepare_mtp.cpp)
+ *   kvip_hip_lidu_workspace_bytes
+ *                             <- the op's workspace sizing (op_host/a5_lidu_fused_batch_get_prepare_mtp.cpp:101, :282-288)
  */
 #ifndef KVIP_HIP_H
 #define KVIP_HIP_H
@@ -168,6 +174,64 @@ typedef struct KvipLruArgs {
     int32_t bitmap_words;
 } KvipLruArgs;
 
+/* LIDU limits (a5_lidu_fused_batch_get_prepare_mtp.cpp:36-57). */
+#define KVIP_LIDU_MAX_QUERIES 4
+#define KVIP_LIDU_MISS_CAPACITY (KVIP_TOPK * KVIP_LIDU_MAX_QUERIES)
+#define KVIP_LIDU_MAX_SOURCE_TOKENS ((1 << 20) + 20 * 128)
+#define KVIP_LIDU_MAX_CACHE_TOKENS ((1 << 17) + 20 * 128)
+#define KVIP_LIDU_BITMAP_WORDS 4176 /* miss_slot_bitmap words per request */
+
+/* LIDU transaction over a batch of requests, each with 1-4 packed query rows. Tensors are
+ * int32 and contiguous, named and shaped as in the reference out-variant op. Per request:
+ * the TopK tokens of each query row are classified (hit = token_to_slot maps it to a slot
+ * below the resident budget whose miss_slot_bitmap bit is clear), each row of
+ * destination_slots becomes [miss prefix, hit slots], the request's distinct misses get
+ * miss_slots[0..2047] and then slots scanned from eviction_cursors[pool] over the slots
+ * neither in the bitmap nor hit, victims are cleared, maps installed, the miss prefixes
+ * refilled with the new slots, and the compact descriptors (indices, offsets,
+ * output_indices) written at the request's prefix of miss_counts. A rejected batch
+ * (query layout, aliased pool rows) gives -1 rows and miss_counts -1; a rejected request
+ * gives -1 rows and miss_counts[b] = -1 and leaves the maps untouched.
+ * profile_enabled[0] is read on the device: 2 = graph-dummy mode (membership ignored,
+ * out-of-range tokens read as token 0), 1 = write wall-clock stamps (100 MHz ticks) into
+ * profiling[b][0][0..8] at the phase boundaries when profiling is not NULL.
+ * The workspace holds kvip_hip_lidu_workspace_bytes(batch) bytes (no initialisation
+ * needed); calls that share a workspace must be stream-ordered. */
+typedef struct KvipLiduArgs {
+    const int32_t* topk;                      /* [packed_queries, 2048] (8-byte aligned) */
+    const int32_t* actual_seq_lengths_query;  /* [batch] cumulative query ends */
+    const int32_t* req_pool_entries;          /* [batch] pool row of each request */
+    int32_t* token_to_slot;                   /* [pool_size, source_capacity] */
+    int32_t* slot_to_token;                   /* [pool_size, resident_capacity] */
+    int32_t* eviction_cursors;                /* [pool_size] */
+    const int32_t* cache_tokens;              /* [batch] resident budget */
+    const int32_t* candidate_lens;            /* [batch] */
+    const int32_t* miss_slots;                /* [batch, 2048] */
+    const int32_t* miss_slot_bitmap;          /* [batch, 4176] */
+    const int32_t* resident_block_table;      /* [batch, resident_blocks] */
+    const int32_t* logical_seq_lengths;       /* [batch] */
+    const int32_t* profile_enabled;           /* [1] */
+    int32_t* destination_slots;               /* [packed_queries, 2048] (16-byte aligned) */
+    int32_t* miss_counts;                     /* [batch + 1], last = total */
+    int32_t* indices;                         /* [batch * 8192] */
+    int32_t* offsets;                         /* [batch * 8192] */
+    int32_t* output_indices;                  /* [batch * 8192] */
+    int32_t* resident_seq_lengths;            /* [batch] */
+    int64_t* profiling;                       /* [batch, 8, 32], or NULL */
+    void* workspace;                          /* 16-byte aligned */
+    int64_t workspace_bytes;
+    int32_t batch;
+    int32_t packed_queries;
+    int32_t pool_size;
+    int32_t source_capacity;
+    int32_t resident_capacity;
+    int32_t resident_blocks;
+    int32_t layer_id;
+    int32_t num_layers;
+    int32_t max_num_reqs;
+    int32_t qcap;
+} KvipLiduArgs;
+
 uint32_t kvip_hip_abi_version(void);
 uint32_t kvip_hip_indexer_decode(const KvipIndexerArgs* args, void* stream);
 uint32_t kvip_hip_topk(const KvipTopkArgs* args, void* stream);
@@ -178,6 +242,8 @@ uint32_t kvip_hip_lru_reset(const KvipLruArgs* args, int32_t committed, void* st
 uint32_t kvip_hip_lru_extend(const KvipLruArgs* args, int32_t active, int32_t committed, void* stream);
 uint32_t kvip_hip_lru_commit(const KvipLruArgs* args, const int32_t* destinations, int32_t count, int32_t active,
                              void* stream);
+uint64_t kvip_hip_lidu_workspace_bytes(int32_t batch);
+uint32_t kvip_hip_lidu(const KvipLiduArgs* args, void* stream);
 
 #ifdef __cplusplus
 }

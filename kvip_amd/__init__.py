@@ -12,6 +12,8 @@ __all__ = [
     "ContiguousFetch",
     "SlotLRU",
     "update_abc",
+    "lidu",
+    "lidu_prepare",
     "build_libraries",
     "load_library",
 ]
@@ -22,6 +24,8 @@ _EXPORTS = {
     "ContiguousFetch": ("operators.lifetch.binding", "ContiguousFetch"),
     "SlotLRU": ("cache.lru", "SlotLRU"),
     "update_abc": ("cache.abc", "update_abc"),
+    "lidu": ("operators.lidu", "lidu"),
+    "lidu_prepare": ("operators.lidu", "lidu_prepare"),
     "build_libraries": ("runtime.build", "build_libraries"),
     "load_library": ("runtime.abi", "load_library"),
 }

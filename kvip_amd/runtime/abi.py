@@ -74,6 +74,20 @@ class LruArgs(ctypes.Structure):
     ]
 
 
+class LiduArgs(ctypes.Structure):
+    _fields_ = [
+        ("topk", _p), ("actual_seq_lengths_query", _p), ("req_pool_entries", _p), ("token_to_slot", _p),
+        ("slot_to_token", _p), ("eviction_cursors", _p), ("cache_tokens", _p), ("candidate_lens", _p),
+        ("miss_slots", _p), ("miss_slot_bitmap", _p), ("resident_block_table", _p), ("logical_seq_lengths", _p),
+        ("profile_enabled", _p), ("destination_slots", _p), ("miss_counts", _p), ("indices", _p),
+        ("offsets", _p), ("output_indices", _p), ("resident_seq_lengths", _p), ("profiling", _p),
+        ("workspace", _p), ("workspace_bytes", _i64),
+        ("batch", _i32), ("packed_queries", _i32), ("pool_size", _i32), ("source_capacity", _i32),
+        ("resident_capacity", _i32), ("resident_blocks", _i32), ("layer_id", _i32), ("num_layers", _i32),
+        ("max_num_reqs", _i32), ("qcap", _i32),
+    ]
+
+
 # name -> (argtypes, restype); must list every function declared in include/kvip_hip.h.
 PROTOTYPES = {
     "kvip_hip_abi_version": ([], ctypes.c_uint32),
@@ -85,6 +99,8 @@ PROTOTYPES = {
     "kvip_hip_lru_reset": ([ctypes.POINTER(LruArgs), _i32, _p], ctypes.c_uint32),
     "kvip_hip_lru_extend": ([ctypes.POINTER(LruArgs), _i32, _i32, _p], ctypes.c_uint32),
     "kvip_hip_lru_commit": ([ctypes.POINTER(LruArgs), _p, _i32, _i32, _p], ctypes.c_uint32),
+    "kvip_hip_lidu_workspace_bytes": ([_i32], ctypes.c_uint64),
+    "kvip_hip_lidu": ([ctypes.POINTER(LiduArgs), _p], ctypes.c_uint32),
 }
 
 _LIB = None

@@ -15,7 +15,7 @@ HEADER = ROOT / "include" / "kvip_hip.h"
 
 def declared_functions():
     text = HEADER.read_text()
-    return sorted(set(re.findall(r"^\s*uint32_t\s+(kvip_hip_\w+)\s*\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*uint(?:32|64)_t\s+(kvip_hip_\w+)\s*\(", text, re.M)))
 
 
 def test_library_exports_every_declared_symbol():
@@ -36,6 +36,7 @@ STRUCTS = {
     "KvipLIFetchArgs": abi.LIFetchArgs,
     "KvipAbcArgs": abi.AbcArgs,
     "KvipLruArgs": abi.LruArgs,
+    "KvipLiduArgs": abi.LiduArgs,
 }
 
 
@@ -79,6 +80,25 @@ def test_invalid_arguments_rejected_before_launch():
     fetch = abi.FetchArgs(topk=16, kv_cache=16, block_table=16, output=16, kv_block_stride=128 * 656,
                           row_stride=656, row_bytes=650, batch=1, rows_per_request=1, max_blocks=1, num_blocks=1)
     assert lib.kvip_hip_fetch_gather(ctypes.byref(fetch), None) == abi.KVIP_ERR_INVALID
+
+
+def test_lidu_arguments_rejected_before_launch():
+    lib = abi.load_library()
+    assert lib.kvip_hip_lidu(None, None) == abi.KVIP_ERR_INVALID
+    assert lib.kvip_hip_lidu_workspace_bytes(0) == 0
+    need = lib.kvip_hip_lidu_workspace_bytes(2)
+    assert need >= 2 * (3 * 8192 + 16) * 4
+    names = [f for f, _ in abi.LiduArgs._fields_ if f not in ("profiling", "workspace_bytes")][:20]
+    good = dict({n: 256 for n in names}, workspace_bytes=need, batch=2, packed_queries=8, pool_size=2,
+                source_capacity=4096, resident_capacity=4096, resident_blocks=32, layer_id=0, num_layers=1,
+                max_num_reqs=2, qcap=32)
+    bad_cases = [dict(batch=0), dict(packed_queries=9), dict(packed_queries=1), dict(resident_capacity=2047),
+                 dict(source_capacity=(1 << 20) + 20 * 128 + 1), dict(layer_id=1), dict(max_num_reqs=1),
+                 dict(workspace_bytes=need - 1), dict(topk=260), dict(destination_slots=264),
+                 dict(qcap=1 << 30, num_layers=1, max_num_reqs=4), dict(topk=0)]
+    for case in bad_cases:
+        args = abi.LiduArgs(**dict(good, **case))
+        assert lib.kvip_hip_lidu(ctypes.byref(args), None) == abi.KVIP_ERR_INVALID, case
 
 
 def test_binding_validation_cpu():
