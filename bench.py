@@ -6,8 +6,9 @@ is already resident in HBM: lightning-indexer scoring of every context token of 
 656-byte KV rows per request into a contiguous [64, 2048, 656] buffer.
 
 Prints one JSON line (rank 0): queries/s, per-kernel HIP-event timings, the roofline
-of the dominant kernel against MI355X's 8 TB/s HBM peak, and the CPU baseline (the
-oracle timed on a bounded sample of the same workload on this host).
+of the dominant kernel against MI355X's 8 TB/s HBM peak, the CPU baseline (the
+oracle timed on a bounded sample of the same workload on this host) and, under
+"lidu", the device time of one kvip.lidu resolver call at the config-4 shape.
 """
 from __future__ import annotations
 
@@ -36,6 +37,7 @@ def parse():
     p.add_argument("--seed", type=int, default=2026)
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU-baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-lidu", action="store_true", help="skip the kvip.lidu timing leg")
     p.add_argument("--copy-calibration", action="store_true",
                    help="also run a plain 1 GiB device copy (for rocprof FETCH/WRITE_SIZE scaling)")
     return p.parse_args()
@@ -113,6 +115,49 @@ def cpu_baseline(torch, wl, rot, budget_s):
             "sample": f"{done} query rows (cycling over the {rot.rows} rows) of the same workload (numpy oracle: float64 dot "
                       f"products on {blas_threads} BLAS threads, single-threaded head reduction, TopK, gather); "
                       f"{elapsed:.1f} s; host has {os.cpu_count()} logical CPUs"}
+
+
+def lidu_leg(torch, kvip_amd, device, seed, iters=50):
+    """Device time of one kvip.lidu call at the BASELINE config-4 shape (16 MTP requests x
+    4 query rows, resident budget 16384 of a 131072-token history, ~80 % hits). Each call
+    must start from the same maps, so two graphs are replayed back to back `iters` times:
+    one restores the maps, the other restores them and runs lidu; the difference of the
+    two is lidu's time with host launch latency hidden behind the queued replays."""
+    from kvip_amd import synthetic
+
+    dev, outs, args = synthetic.lidu_workload(torch, device, seed=seed)
+    names = ("token_to_slot_pool", "slot_to_token_pool", "eviction_cursors")
+    saved = {k: dev[k].clone() for k in names}
+
+    def restore():
+        for k in names:
+            dev[k].copy_(saved[k])
+
+    kvip_amd.lidu(*args)  # allocates the per-batch workspace before capture
+    torch.cuda.synchronize()
+    graphs = []
+    for body in (restore, lambda: (restore(), kvip_amd.lidu(*args))):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            body()
+        graphs.append(g)
+    times = []
+    for g in graphs:
+        for _ in range(3):
+            g.replay()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(iters):
+            g.replay()
+        end.record()
+        end.synchronize()
+        times.append(start.elapsed_time(end) * 1e3 / iters)
+    counts = outs["miss_counts"].cpu().numpy()
+    if (counts[:-1] < 0).any():
+        raise RuntimeError(f"lidu rejected a request: {counts.tolist()}")
+    return {"workload": "c4 shape: 16 requests x 4 MTP rows, budget 16384, history 131072, ~80% hits",
+            "us_per_call": round(times[1] - times[0], 2), "restore_us": round(times[0], 2),
+            "unique_misses_per_request": round(float(counts[:-1].mean()), 1), "calls": iters}
 
 
 def main():
@@ -235,6 +280,8 @@ def main():
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(dominant) if args.config == "c2" else None},
     }
+    if not args.no_lidu:
+        result["lidu"] = lidu_leg(torch, kvip_amd, device, args.seed)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(torch, wl, rot, args.cpu_seconds)
     print(json.dumps(result), flush=True)

@@ -124,3 +124,72 @@ def bind(torch, kvip, wl, *, query_ends=None):
     rot.bind_index_cache(wl.keys, wl.key_scale)
     upd = kvip.ContiguousFetch(torch, rot, wl.kv_cache)
     return rot, upd, kvip.LIFetch(rot, upd)
+
+
+def _bitmap_words(torch, slots, words):
+    """int32 [words] membership bitmap of distinct slot ids (device tensor)."""
+    acc = torch.zeros(words, dtype=torch.int64, device=slots.device)
+    acc.index_add_(0, (slots >> 5).long(), (1 << (slots & 31).long()))
+    return ((acc + (1 << 31)) % (1 << 32) - (1 << 31)).to(torch.int32)
+
+
+def lidu_workload(torch, device, *, seed=2026, batch=16, queries=4, budget=16384, cand=131072, hit=0.8,
+                  query_overlap=0.9, num_layers=61, layer_id=7):
+    """Inputs of one kvip.lidu call in the reference argument order (BASELINE config 4
+    shape: `batch` MTP requests of `queries` rows, resident budget `budget` of a
+    `cand`-token history). Every request owns a pool row holding a random resident set
+    of `budget` history tokens; each TopK row takes `hit` of its tokens from the resident
+    set, consecutive query rows of a request share `query_overlap` of their tokens, and
+    the victims are 2048 random resident slots. Returns (inputs, outputs, call args)."""
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    pool = batch + 1  # + the reserved graph-padding entry
+    t2s = torch.full((pool, cand), -1, dtype=torch.int32)
+    s2t = torch.full((pool, budget), -1, dtype=torch.int32)
+    miss_slots = torch.empty((batch, 2048), dtype=torch.int32)
+    topk = torch.empty((batch * queries, 1, 2048), dtype=torch.int32)
+    n_hit = int(2048 * hit)
+    for b in range(batch):
+        resident = torch.randperm(cand, generator=g)[:budget]
+        slots = torch.randperm(budget, generator=g)
+        t2s[b, resident] = slots.int()
+        s2t[b, slots] = resident.int()
+        miss_slots[b] = torch.randperm(budget, generator=g)[:2048].int()
+        cold = torch.ones(cand, dtype=torch.bool)
+        cold[resident] = False
+        cold = cold.nonzero().view(-1)
+        hits = resident[torch.randperm(budget, generator=g)[:n_hit]]
+        misses = cold[torch.randperm(len(cold), generator=g)[:2048 - n_hit]]
+        row = torch.cat((hits, misses))
+        for q in range(queries):
+            if q:
+                keep = int(2048 * query_overlap)
+                fresh_h = resident[torch.randperm(budget, generator=g)[:2048]]
+                fresh_h = fresh_h[~torch.isin(fresh_h, row)][:int((2048 - keep) * hit)]
+                fresh_m = cold[torch.randperm(len(cold), generator=g)[:4096]]
+                fresh_m = fresh_m[~torch.isin(fresh_m, row)][:2048 - keep - len(fresh_h)]
+                row = torch.cat((row[torch.randperm(2048, generator=g)[:keep]], fresh_h, fresh_m))
+            topk[b * queries + q, 0] = row[torch.randperm(2048, generator=g)].int()
+    blocks = torch.randperm(1 << 20, generator=g)[:batch * (budget // 128)].int().view(batch, -1)
+    dev = dict(
+        topk=topk, actual_seq_lengths_query=torch.arange(1, batch + 1, dtype=torch.int32) * queries,
+        req_pool_entries=torch.arange(batch, dtype=torch.int32), token_to_slot_pool=t2s, slot_to_token_pool=s2t,
+        eviction_cursors=torch.zeros(pool, dtype=torch.int32), cache_tokens=torch.full((batch,), budget, dtype=torch.int32),
+        candidate_lens=torch.full((batch,), cand, dtype=torch.int32), miss_slots=miss_slots,
+        resident_block_table=blocks, logical_seq_lengths=torch.full((batch,), cand + 1, dtype=torch.int32),
+        profile_enabled=torch.zeros(1, dtype=torch.int32),
+    )
+    dev = {k: v.to(device) for k, v in dev.items()}
+    dev["miss_slot_bitmap"] = torch.stack([_bitmap_words(torch, dev["miss_slots"][b], 4176) for b in range(batch)])
+    cap = batch * 8192
+    outs = dict(destination_slots=torch.empty_like(dev["topk"]),
+                miss_counts=torch.empty(batch + 1, dtype=torch.int32, device=device),
+                indices=torch.empty(cap, dtype=torch.int32, device=device),
+                offsets=torch.empty(cap, dtype=torch.int32, device=device),
+                output_indices=torch.empty(cap, dtype=torch.int32, device=device),
+                resident_seq_lengths=torch.empty(batch, dtype=torch.int32, device=device),
+                profiling=torch.zeros((batch, 8, 32), dtype=torch.int64, device=device))
+    order = ("topk", "actual_seq_lengths_query", "req_pool_entries", "token_to_slot_pool", "slot_to_token_pool",
+             "eviction_cursors", "cache_tokens", "candidate_lens", "miss_slots", "miss_slot_bitmap",
+             "resident_block_table", "logical_seq_lengths", "profile_enabled")
+    args = [dev[k] for k in order] + list(outs.values()) + [layer_id, num_layers, pool, (cand + 127) // 128]
+    return dev, outs, args
