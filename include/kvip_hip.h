@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define KVIP_HIP_ABI_VERSION 1u
+#define KVIP_HIP_ABI_VERSION 2u
 
 #define KVIP_TOPK 2048
 #define KVIP_BLOCK_TOKENS 128
@@ -105,9 +105,13 @@ typedef struct KvipIndexerArgs {
  * valid >= 2048: the 2048 tokens that come first in the order (key desc, index asc),
  * written as the tokens with key > kth in ascending index order followed by the
  * tokens with key == kth in ascending index order. */
+#define KVIP_TOPK_SEGMENT_KEYS 4096
+#define KVIP_TOPK_SEGMENT_WORDS 260
 typedef struct KvipTopkArgs {
     const uint16_t* score_keys;  /* [rows, key_stride] */
     uint32_t* histogram;         /* [rows, 256] from kvip_hip_indexer_decode (re-zeroed here), or NULL */
+    uint32_t* segments;          /* with a histogram: work memory of rows * ceil(key_stride / 4096) * 260
+                                    words for the multi-workgroup select; NULL: one workgroup per row */
     const int32_t* seq_lens;     /* [batch] */
     const int32_t* query_ends;   /* [rows] or NULL */
     int32_t* topk;               /* [rows, 2048] token ids, -1 = empty */

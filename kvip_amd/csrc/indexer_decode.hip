@@ -59,29 +59,28 @@ __device__ float kUnitScale[kBlockTokens] = {
 template <int ELEM>
 struct Mma;
 
+// step(s) adds the s-th K slice of the 128-dim contraction; MT head tiles interleave
+// their slices (tile 0 slice 0, tile 1 slice 0, tile 0 slice 1, ...) so consecutive
+// MFMAs are independent.
 template <>
 struct Mma<1> {
     static constexpr int NV = 4;
-    KVIP_DEVICE static void run(const v4i (&a)[NV], const v4i (&b)[NV], v16f& acc) {
-#pragma unroll
-        for (int s = 0; s < 2; ++s) {
-            const v8i av = __builtin_shufflevector(a[2 * s], a[2 * s + 1], 0, 1, 2, 3, 4, 5, 6, 7);
-            const v8i bv = __builtin_shufflevector(b[2 * s], b[2 * s + 1], 0, 1, 2, 3, 4, 5, 6, 7);
-            // Format 0 = fp8 e4m3 for both operands; E8M0 scale 127 = 2^0.
-            acc = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av, bv, acc, 0, 0, 0, 127, 0, 127);
-        }
+    static constexpr int STEPS = 2;
+    KVIP_DEVICE static void step(int s, const v4i (&a)[NV], const v4i (&b)[NV], v16f& acc) {
+        const v8i av = __builtin_shufflevector(a[2 * s], a[2 * s + 1], 0, 1, 2, 3, 4, 5, 6, 7);
+        const v8i bv = __builtin_shufflevector(b[2 * s], b[2 * s + 1], 0, 1, 2, 3, 4, 5, 6, 7);
+        // Format 0 = fp8 e4m3 for both operands; E8M0 scale 127 = 2^0.
+        acc = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av, bv, acc, 0, 0, 0, 127, 0, 127);
     }
 };
 
 template <>
 struct Mma<2> {
     static constexpr int NV = 8;
-    KVIP_DEVICE static void run(const v4i (&a)[NV], const v4i (&b)[NV], v16f& acc) {
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, a[s]),
-                                                          __builtin_bit_cast(v8bf, b[s]), acc, 0, 0, 0);
-        }
+    static constexpr int STEPS = 8;
+    KVIP_DEVICE static void step(int s, const v4i (&a)[NV], const v4i (&b)[NV], v16f& acc) {
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, a[s]), __builtin_bit_cast(v8bf, b[s]),
+                                                      acc, 0, 0, 0);
     }
 };
 
@@ -146,7 +145,11 @@ struct Tile {
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
             acc[mt] = v16f{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-            Mma<ELEM>::run(qa[mt], kb, acc[mt]);
+        }
+#pragma unroll
+        for (int s = 0; s < Mma<ELEM>::STEPS; ++s) {
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) Mma<ELEM>::step(s, qa[mt], kb, acc[mt]);
         }
         // acc[mt][r] holds head mt*32 + 8*(r/4) + 4*g + r%4 for token n. Four independent
         // FMA chains (one per r%4) keep the reduction off the critical path.

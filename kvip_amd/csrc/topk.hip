@@ -290,6 +290,179 @@ __global__ __launch_bounds__(kTopkThreads) void topk_regs_kernel(const KvipTopkA
     report(p.status, err);
 }
 
+// Split select for rows scored by kvip_hip_indexer_decode (the high-byte histogram is
+// given): the row is cut into 4096-key segments, one 256-thread workgroup each, in two
+// launches, so a batch of long rows spreads over many CUs instead of one workgroup per
+// row.
+//   topk_segment_kernel: every segment workgroup derives the high-byte bin hb from the
+//     row histogram and writes its own low-byte histogram of the keys in hb and its count
+//     of keys above hb.
+//   topk_emit_kernel: every segment workgroup sums those records into the row's kth key
+//     and its own segment prefix (keys > kth and keys == kth in earlier segments), then
+//     emits its segment's selected tokens at their final positions.
+// Record of segment s of a row: words [0, 256) low-byte histogram, [256] keys above hb;
+// segment 0 also holds [257] hb (-1: inconsistent histogram) and [258] keys above hb in
+// the row.
+constexpr int kSplitThreads = 256;
+constexpr int kSplitKeys = KVIP_TOPK_SEGMENT_KEYS / kSplitThreads;  // 16 per thread
+constexpr int kSegWords = KVIP_TOPK_SEGMENT_WORDS;
+
+KVIP_DEVICE int row_valid(const KvipTopkArgs& p, int row) {
+    int valid = max(p.seq_lens[row / p.rows_per_request], 0);
+    if (p.query_ends != nullptr) valid = min(valid, p.query_ends[row]);
+    return min(max(valid, 0), p.key_stride);
+}
+
+KVIP_DEVICE void load_segment(const uint16_t* keys, int first, int stride, uint32_t* kk) {
+#pragma unroll
+    for (int v = 0; v < kSplitKeys / 8; ++v) {
+        const v4i x = *reinterpret_cast<const v4i*>(keys + min(first + v * 8, stride - 8));
+        kk[4 * v] = x[0];
+        kk[4 * v + 1] = x[1];
+        kk[4 * v + 2] = x[2];
+        kk[4 * v + 3] = x[3];
+    }
+}
+
+__global__ __launch_bounds__(kSplitThreads) void topk_segment_kernel(const KvipTopkArgs p) {
+    __shared__ uint32_t s_hist[256];
+    __shared__ uint32_t s_wave[kSplitThreads / 64];
+    __shared__ int s_sel[2];
+    const int tid = threadIdx.x;
+    const int seg = blockIdx.x;
+    const int row = blockIdx.y;
+    const int valid = row_valid(p, row);
+    const int nseg = (valid + KVIP_TOPK_SEGMENT_KEYS - 1) / KVIP_TOPK_SEGMENT_KEYS;
+    if (valid < kTopK || seg >= nseg) return;
+    int32_t* out = p.topk + static_cast<size_t>(row) * kTopK;
+    uint32_t* rec = p.segments + (static_cast<size_t>(row) * gridDim.x + seg) * kSegWords;
+    // The segment's keys are requested first so that their latency overlaps the bin select.
+    const int first = seg * KVIP_TOPK_SEGMENT_KEYS + tid * kSplitKeys;
+    const int count = max(0, min(kSplitKeys, valid - first));
+    uint32_t kk[kSplitKeys / 2];
+    load_segment(p.score_keys + static_cast<size_t>(row) * p.key_stride, first, p.key_stride, kk);
+    // Positions a stale histogram would leave unwritten read -1.
+    for (int i = seg * kTopK / nseg + tid; i < (seg + 1) * kTopK / nseg; i += kSplitThreads) out[i] = -1;
+
+    s_hist[tid] = p.histogram[static_cast<size_t>(row) * 256 + tid];
+    if (tid == 0) s_sel[0] = -1;
+    __syncthreads();
+    select_bin(s_hist, kTopK, s_sel, s_wave);
+    const int hb = s_sel[0];
+    if (hb < 0) {
+        if (seg == 0 && tid == 0) rec[257] = 0xFFFFFFFFu;
+        return;
+    }
+    s_hist[tid] = 0u;
+    __syncthreads();
+    uint32_t above = 0;
+#pragma unroll
+    for (int j = 0; j < kSplitKeys; ++j) {
+        const uint32_t k = (j & 1) ? (kk[j >> 1] >> 16) : (kk[j >> 1] & 0xFFFFu);
+        const int high = static_cast<int>(k >> 8);
+        if (j < count) {
+            above += high > hb ? 1u : 0u;
+            if (high == hb) atomicAdd(&s_hist[k & 0xFFu], 1u);
+        }
+    }
+    uint32_t total;
+    block_exclusive_scan(above, s_wave, &total);  // its barriers also complete the histogram
+    rec[tid] = s_hist[tid];
+    if (tid == 0) {
+        rec[256] = total;
+        if (seg == 0) {
+            rec[257] = static_cast<uint32_t>(hb);
+            rec[258] = static_cast<uint32_t>(s_sel[1]);
+        }
+    }
+}
+
+__global__ __launch_bounds__(kSplitThreads) void topk_emit_kernel(const KvipTopkArgs p) {
+    __shared__ uint32_t s_hist[256];
+    __shared__ uint32_t s_wave[kSplitThreads / 64];
+    __shared__ int s_sel[2];
+    __shared__ uint32_t s_eq_before;
+    const int tid = threadIdx.x;
+    const int seg = blockIdx.x;
+    const int row = blockIdx.y;
+    const int valid = row_valid(p, row);
+    int32_t* out = p.topk + static_cast<size_t>(row) * kTopK;
+    if (seg == 0) p.histogram[static_cast<size_t>(row) * 256 + tid] = 0u;  // ready for the next scoring launch
+    if (valid < kTopK) {
+        if (seg == 0) {
+            for (int i = tid; i < kTopK; i += kSplitThreads) out[i] = i < valid ? i : -1;
+        }
+        return;
+    }
+    const int nseg = (valid + KVIP_TOPK_SEGMENT_KEYS - 1) / KVIP_TOPK_SEGMENT_KEYS;
+    if (seg >= nseg) return;
+    const int first = seg * KVIP_TOPK_SEGMENT_KEYS + tid * kSplitKeys;
+    const int count = max(0, min(kSplitKeys, valid - first));
+    uint32_t kk[kSplitKeys / 2];
+    load_segment(p.score_keys + static_cast<size_t>(row) * p.key_stride, first, p.key_stride, kk);
+    const uint32_t* recs = p.segments + static_cast<size_t>(row) * gridDim.x * kSegWords;
+    const int hb = static_cast<int>(recs[257]);
+    if (hb < 0) {
+        if (seg == 0 && tid == 0) report(p.status, KVIP_STATUS_HISTOGRAM);
+        return;
+    }
+    const uint32_t gt_hi = recs[258];
+    // Row histogram of the low byte within hb, and this segment's share of earlier counts.
+    uint32_t all = 0, before = 0;
+    for (int s = 0; s < nseg; ++s) {
+        const uint32_t c = recs[s * kSegWords + tid];
+        all += c;
+        before += s < seg ? c : 0u;
+    }
+    uint32_t above_before = 0;
+    for (int s = tid; s < seg; s += kSplitThreads) above_before += recs[s * kSegWords + 256];
+    s_hist[tid] = all;
+    if (tid == 0) s_sel[0] = -1;
+    __syncthreads();
+    select_bin(s_hist, kTopK - gt_hi, s_sel, s_wave);
+    const int lo = s_sel[0];
+    if (lo < 0) {
+        if (seg == 0 && tid == 0) report(p.status, KVIP_STATUS_HISTOGRAM);
+        return;
+    }
+    const uint32_t kth = (static_cast<uint32_t>(hb) << 8) | static_cast<uint32_t>(lo);
+    const uint32_t n_gt = gt_hi + static_cast<uint32_t>(s_sel[1]);
+    const uint32_t need = kTopK - n_gt;
+    if (tid == lo) s_eq_before = before;
+    uint32_t gt_before;
+    block_exclusive_scan(above_before + (tid > lo ? before : 0u), s_wave, &gt_before);
+    const uint32_t eq_before = s_eq_before;
+    uint32_t ngt = 0, neq = 0;
+#pragma unroll
+    for (int j = 0; j < kSplitKeys; ++j) {
+        const uint32_t k = (j & 1) ? (kk[j >> 1] >> 16) : (kk[j >> 1] & 0xFFFFu);
+        ngt += (j < count && k > kth) ? 1u : 0u;
+        neq += (j < count && k == kth) ? 1u : 0u;
+    }
+    uint32_t total;
+    const uint32_t excl = block_exclusive_scan((ngt << 16) | neq, s_wave, &total);
+    uint32_t pg = gt_before + (excl >> 16);
+    uint32_t pe = eq_before + (excl & 0xFFFFu);
+    uint32_t err = 0;
+    if (ngt != 0u || (neq != 0u && pe < need)) {
+#pragma unroll
+        for (int j = 0; j < kSplitKeys; ++j) {
+            const uint32_t k = (j & 1) ? (kk[j >> 1] >> 16) : (kk[j >> 1] & 0xFFFFu);
+            if (j < count) {
+                if (k > kth) {
+                    if (pg < n_gt) out[pg] = first + j;
+                    else err = KVIP_STATUS_HISTOGRAM;
+                    ++pg;
+                } else if (k == kth) {
+                    if (pe < need) out[n_gt + pe] = first + j;
+                    ++pe;
+                }
+            }
+        }
+    }
+    report(p.status, err);
+}
+
 }  // namespace
 
 uint32_t validate_topk(const KvipTopkArgs* a) {
@@ -298,6 +471,7 @@ uint32_t validate_topk(const KvipTopkArgs* a) {
                     (a->rows_per_request == 1 || a->rows_per_request == 2 || a->rows_per_request == 4) &&
                     a->batch >= 1 && static_cast<int64_t>(a->batch) * a->rows_per_request <= (1 << 24) &&
                     a->key_stride >= 8 && a->key_stride % 8 == 0 && a->key_stride <= (1 << 24) &&
+                    (a->segments == nullptr || static_cast<int64_t>(a->batch) * a->rows_per_request <= 65535) &&
                     (reinterpret_cast<uintptr_t>(a->score_keys) & 15u) == 0;
     return ok ? KVIP_OK : KVIP_ERR_INVALID;
 }
@@ -305,6 +479,13 @@ uint32_t validate_topk(const KvipTopkArgs* a) {
 hipError_t launch_topk(const KvipTopkArgs& a, hipStream_t stream) {
     const dim3 grid(a.batch * a.rows_per_request);
     const dim3 block(kTopkThreads);
+    if (a.segments != nullptr && a.histogram != nullptr) {
+        const dim3 split((a.key_stride + KVIP_TOPK_SEGMENT_KEYS - 1) / KVIP_TOPK_SEGMENT_KEYS,
+                         a.batch * a.rows_per_request);
+        hipLaunchKernelGGL(topk_segment_kernel, split, dim3(kSplitThreads), 0, stream, a);
+        hipLaunchKernelGGL(topk_emit_kernel, split, dim3(kSplitThreads), 0, stream, a);
+        return hipGetLastError();
+    }
     // Rows that fit 1024*KPT keys use the register-resident select.
     if (a.key_stride <= kTopkThreads * 8) {
         hipLaunchKernelGGL(topk_regs_kernel<8>, grid, block, 0, stream, a);

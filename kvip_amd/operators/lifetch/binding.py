@@ -19,6 +19,8 @@ TOPK = 2048
 BLOCK_TOKENS = 128
 INDEX_DIM = 128
 TOKEN_BYTES = 656
+TOPK_SEGMENT_KEYS = 4096
+TOPK_SEGMENT_WORDS = 260
 MAX_CONTEXT = 1 << 24
 
 
@@ -69,6 +71,9 @@ class LIFetchBinding:
         # int16 storage holding uint16 sortable keys (reinterpret with .view on the host).
         self.score_keys = torch.zeros((self.rows, self.key_stride), dtype=torch.int16, device=dev)
         self.histogram = torch.zeros((self.rows, 256), dtype=torch.int32, device=dev)
+        # Per-segment records of the multi-workgroup TopK (written before they are read).
+        segments = (self.key_stride + TOPK_SEGMENT_KEYS - 1) // TOPK_SEGMENT_KEYS
+        self.topk_segments = torch.empty((self.rows, segments, TOPK_SEGMENT_WORDS), dtype=torch.int32, device=dev)
         self.topk = torch.full((self.rows, TOPK), -1, dtype=torch.int32, device=dev)
         self.status = torch.zeros(1, dtype=torch.int32, device=dev)
         self.keys = None
@@ -111,10 +116,13 @@ class LIFetchBinding:
             weight_dtype=self.weight_code,
         )
 
-    def topk_args(self, use_histogram=True):
+    def topk_args(self, use_histogram=True, split=True):
+        """TopK arguments; with the scoring histogram the select runs on 4096-key segments
+        (split=True) or one workgroup per row (split=False)."""
         p = abi.ptr
         return abi.TopkArgs(
             score_keys=p(self.score_keys), histogram=p(self.histogram) if use_histogram else 0,
+            segments=p(self.topk_segments) if use_histogram and split else 0,
             seq_lens=p(self.seq_lens), query_ends=p(self.query_ends), topk=p(self.topk), status=p(self.status),
             batch=self.batch, rows_per_request=self.rows_per_request, key_stride=self.key_stride,
         )

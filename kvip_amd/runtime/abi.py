@@ -9,7 +9,7 @@ import ctypes
 from pathlib import Path
 
 LIBRARY = Path(__file__).resolve().parents[1] / "_lib" / "libkvip_hip.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 KVIP_OK = 0
 KVIP_ERR_INVALID = 100000
@@ -40,7 +40,7 @@ class IndexerArgs(ctypes.Structure):
 
 class TopkArgs(ctypes.Structure):
     _fields_ = [
-        ("score_keys", _p), ("histogram", _p), ("seq_lens", _p), ("query_ends", _p), ("topk", _p),
+        ("score_keys", _p), ("histogram", _p), ("segments", _p), ("seq_lens", _p), ("query_ends", _p), ("topk", _p),
         ("status", _p),
         ("batch", _i32), ("rows_per_request", _i32), ("key_stride", _i32),
     ]

@@ -125,6 +125,17 @@ def test_topk_bit_exact_on_oracle_keys(torch_gpu, kind, ctx):
         want = ref.topk_reference(keys[r], v)
         assert np.array_equal(got[r], want), f"row {r} valid {v}"
     assert int(rot.status.item()) == 0
+    # The multi-workgroup select, fed the rows' high-byte histogram as the scoring kernel
+    # leaves it, gives the same rows and clears the histogram.
+    hist = np.stack([np.bincount(keys[r, :v] >> 8, minlength=256) for r, v in enumerate(ctx)])
+    rot.histogram.copy_(torch.from_numpy(hist.astype(np.int32)))
+    rot.topk.fill_(-5)
+    say(f"case topk split {kind} {ctx}")
+    got = run_topk(torch, rot, use_histogram=True)
+    for r, v in enumerate(ctx):
+        assert np.array_equal(got[r], ref.topk_reference(keys[r], v)), f"split row {r} valid {v}"
+    assert int(rot.status.item()) == 0
+    assert not rot.histogram.any()
 
 
 def test_topk_from_scoring_histogram_equals_standalone(torch_gpu):
