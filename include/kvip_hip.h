@@ -32,6 +32,10 @@
  *                                 op_kernel/a5_lidu_fused_batch_get_prepare_mtp.cpp)
  *   kvip_hip_lidu_workspace_bytes
  *                             <- the op's workspace sizing (op_host/a5_lidu_fused_batch_get_prepare_mtp.cpp:101, :282-288)
+ *   kvip_hip_pack_queries     <- QueryInputs.bind_positions + QueryInputs.pack
+ *                                (python/kvip/adapters/vllm/inputs.py:127-152)
+ *   kvip_hip_ingest_index     <- VllmIndexCacheStorage.ingest_prefill / ingest_decode
+ *                                (python/kvip/adapters/vllm/index_import.py:18-52)
  */
 #ifndef KVIP_HIP_H
 #define KVIP_HIP_H
@@ -236,6 +240,69 @@ typedef struct KvipLiduArgs {
     int32_t qcap;
 } KvipLiduArgs;
 
+/* Decode query packing for the LIFetch query buffers, one packed row r < rows at a time
+ * (rows = batch * 4):
+ *   positions != NULL: query_ends[r] = (positions[gather_indices[r]] + 1) * query_valid[r]
+ *   query_in  != NULL: query_out[r] = query_in[gather_indices[r]] (heads * 128 fp8 bytes),
+ *                      weights_out[r] = weights_in[...] (heads bf16), scale_out[r] = scale_in[...]
+ *                      (heads fp32); the six row arrays 16-byte aligned.
+ * A gather index outside [0, tokens) yields query_ends 0 and zero rows and sets
+ * KVIP_STATUS_BAD_TOKEN. */
+typedef struct KvipQueryPackArgs {
+    const int64_t* gather_indices;  /* [rows] source token of each packed row */
+    const int64_t* query_valid;     /* [rows] 1 = live row, 0 = padding */
+    const int64_t* positions;       /* [tokens] token positions, or NULL */
+    int32_t* query_ends;            /* [rows] out (with positions) */
+    const void* query_in;           /* [tokens, heads, 128] fp8, or NULL */
+    const void* weights_in;         /* [tokens, heads] bf16 */
+    const void* scale_in;           /* [tokens, heads] fp32 */
+    void* query_out;                /* [rows, heads, 128] */
+    void* weights_out;              /* [rows, heads] */
+    void* scale_out;                /* [rows, heads] */
+    uint32_t* status;               /* device status word, or NULL */
+    int64_t tokens;
+    int32_t rows;
+    int32_t heads;                  /* 32 or 64 */
+} KvipQueryPackArgs;
+
+/* Index-K ingestion: `count` rows of 128 bytes (+ one fp32 scale) copied from the paged
+ * source cache (source_rows rows = blocks * block_size) into target storage
+ * (target_rows rows = owners * history), row i taking source s_i and target t_i:
+ *   KVIP_INGEST_DECODE: rows of a packed decode batch, i < batch * queries_per_request:
+ *       live (query_ends[i] > 0): s = slot_mapping[gather_indices[i]],
+ *                                 t = row_owners[i / queries_per_request] * history + query_ends[i] - 1
+ *       padding:                  s = 0, t = i (distinct positions of owner 0)
+ *   KVIP_INGEST_LIST:   s = sources[i], t = target_base + targets[i]
+ *   KVIP_INGEST_PREFIX: t = target_base + i, s = block_table[i / block_size] * block_size + i % block_size
+ * Rows whose s or t falls outside the arrays are skipped and set KVIP_STATUS_BAD_TOKEN. */
+#define KVIP_INGEST_DECODE 0
+#define KVIP_INGEST_LIST 1
+#define KVIP_INGEST_PREFIX 2
+typedef struct KvipIngestArgs {
+    const uint8_t* source_keys;     /* [source_rows, 128] */
+    const float* source_scales;     /* [source_rows] */
+    uint8_t* target_keys;           /* [target_rows, 128] */
+    float* target_scales;           /* [target_rows] */
+    const int32_t* query_ends;      /* DECODE: [count] */
+    const int64_t* gather_indices;  /* DECODE: [count] */
+    const int64_t* slot_mapping;    /* DECODE: [slot_count] */
+    const int32_t* row_owners;      /* DECODE: [count / queries_per_request] */
+    const int64_t* sources;         /* LIST: [count] */
+    const int64_t* targets;         /* LIST: [count] */
+    const int32_t* block_table;     /* PREFIX: [ceil(count / block_size)] */
+    uint32_t* status;               /* device status word, or NULL */
+    int64_t source_rows;
+    int64_t target_rows;
+    int64_t count;
+    int64_t history;                /* DECODE: positions per owner */
+    int64_t target_base;            /* LIST, PREFIX */
+    int64_t slot_count;             /* DECODE: slot_mapping length */
+    int32_t mode;
+    int32_t queries_per_request;    /* DECODE */
+    int32_t block_size;             /* PREFIX */
+    int32_t reserved;
+} KvipIngestArgs;
+
 uint32_t kvip_hip_abi_version(void);
 uint32_t kvip_hip_indexer_decode(const KvipIndexerArgs* args, void* stream);
 uint32_t kvip_hip_topk(const KvipTopkArgs* args, void* stream);
@@ -248,6 +315,8 @@ uint32_t kvip_hip_lru_commit(const KvipLruArgs* args, const int32_t* destination
                              void* stream);
 uint64_t kvip_hip_lidu_workspace_bytes(int32_t batch);
 uint32_t kvip_hip_lidu(const KvipLiduArgs* args, void* stream);
+uint32_t kvip_hip_pack_queries(const KvipQueryPackArgs* args, void* stream);
+uint32_t kvip_hip_ingest_index(const KvipIngestArgs* args, void* stream);
 
 #ifdef __cplusplus
 }

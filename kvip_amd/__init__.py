@@ -7,6 +7,8 @@ there is no CPU fallback.
 from importlib import import_module
 
 __all__ = [
+    "QueryInputs",
+    "IndexCacheStorage",
     "LIFetch",
     "LIFetchBinding",
     "ContiguousFetch",
@@ -19,6 +21,8 @@ __all__ = [
 ]
 
 _EXPORTS = {
+    "QueryInputs": ("adapters.vllm.inputs", "QueryInputs"),
+    "IndexCacheStorage": ("adapters.vllm.index_import", "VllmIndexCacheStorage"),
     "LIFetch": ("operators.lifetch.forward", "LIFetchForward"),
     "LIFetchBinding": ("operators.lifetch.binding", "LIFetchBinding"),
     "ContiguousFetch": ("operators.lifetch.binding", "ContiguousFetch"),

@@ -88,6 +88,30 @@ class LiduArgs(ctypes.Structure):
     ]
 
 
+class QueryPackArgs(ctypes.Structure):
+    _fields_ = [
+        ("gather_indices", _p), ("query_valid", _p), ("positions", _p), ("query_ends", _p), ("query_in", _p),
+        ("weights_in", _p), ("scale_in", _p), ("query_out", _p), ("weights_out", _p), ("scale_out", _p),
+        ("status", _p), ("tokens", _i64), ("rows", _i32), ("heads", _i32),
+    ]
+
+
+INGEST_DECODE = 0
+INGEST_LIST = 1
+INGEST_PREFIX = 2
+
+
+class IngestArgs(ctypes.Structure):
+    _fields_ = [
+        ("source_keys", _p), ("source_scales", _p), ("target_keys", _p), ("target_scales", _p),
+        ("query_ends", _p), ("gather_indices", _p), ("slot_mapping", _p), ("row_owners", _p),
+        ("sources", _p), ("targets", _p), ("block_table", _p), ("status", _p),
+        ("source_rows", _i64), ("target_rows", _i64), ("count", _i64), ("history", _i64), ("target_base", _i64),
+        ("slot_count", _i64), ("mode", _i32), ("queries_per_request", _i32), ("block_size", _i32),
+        ("reserved", _i32),
+    ]
+
+
 # name -> (argtypes, restype); must list every function declared in include/kvip_hip.h.
 PROTOTYPES = {
     "kvip_hip_abi_version": ([], ctypes.c_uint32),
@@ -101,6 +125,8 @@ PROTOTYPES = {
     "kvip_hip_lru_commit": ([ctypes.POINTER(LruArgs), _p, _i32, _i32, _p], ctypes.c_uint32),
     "kvip_hip_lidu_workspace_bytes": ([_i32], ctypes.c_uint64),
     "kvip_hip_lidu": ([ctypes.POINTER(LiduArgs), _p], ctypes.c_uint32),
+    "kvip_hip_pack_queries": ([ctypes.POINTER(QueryPackArgs), _p], ctypes.c_uint32),
+    "kvip_hip_ingest_index": ([ctypes.POINTER(IngestArgs), _p], ctypes.c_uint32),
 }
 
 _LIB = None

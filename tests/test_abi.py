@@ -37,6 +37,8 @@ STRUCTS = {
     "KvipAbcArgs": abi.AbcArgs,
     "KvipLruArgs": abi.LruArgs,
     "KvipLiduArgs": abi.LiduArgs,
+    "KvipQueryPackArgs": abi.QueryPackArgs,
+    "KvipIngestArgs": abi.IngestArgs,
 }
 
 
