@@ -55,7 +55,7 @@ def algorithmic_bytes(wl, heads, has_qscale):
     live = np.minimum(ctx, TOPK).repeat(wl.rows_per_request)
     topk = rows * TOPK * 4
     gather = int(live.sum()) * row_bytes * 2
-    return {"indexer": score, "topk": topk, "fetch": gather}
+    return {"indexer": score, "select_fetch": topk + gather}
 
 
 def measured_traffic(kernel):
@@ -221,8 +221,9 @@ def main():
     steps_bytes = sum(step_bytes[s % 2] for s in range(args.steps))
 
     # Per-kernel durations: HIP events around each launch on the launch stream, same
-    # alternating inputs, eager launches.
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
+    # alternating inputs, eager launches (the forward's two launches: scoring, then
+    # TopK fused with the Fetch gather).
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
     torch.cuda.synchronize()
     for s in range(args.steps):
         f = sets[s % 2][3]
@@ -230,14 +231,12 @@ def main():
         e[0].record(stream)
         f.score()
         e[1].record(stream)
-        f.select()
+        f.select_fetch()
         e[2].record(stream)
-        f.fetch()
-        e[3].record(stream)
     torch.cuda.synchronize()
     times = {name: float(np.mean([ev[s][i].elapsed_time(ev[s][i + 1]) for s in range(args.steps)]))
-             for i, name in enumerate(["indexer", "topk", "fetch"])}
-    eager_ms = ev[0][0].elapsed_time(ev[-1][3]) / args.steps
+             for i, name in enumerate(["indexer", "select_fetch"])}
+    eager_ms = ev[0][0].elapsed_time(ev[-1][2]) / args.steps
     for w, r, u, f in sets:
         if int(r.status.item()) != 0:
             raise RuntimeError(f"device status {int(r.status.item())} after the timed steps")

@@ -21,6 +21,8 @@
  *   kvip_hip_fetch_gather     <- kvaf_device::KvafBatchGetDevice as called by FetchQueryGroup
  *                                (op_kernel/streaming.cpp:365-500, :445;
  *                                 patches/kvaf-ubmem-device-get.patch:41-90)
+ *   kvip_hip_select_fetch     <- ProcessTopK followed by the FetchQueryGroup gather
+ *                                (indexer_vector.h:799-973; streaming.cpp:365-500)
  *   kvip_hip_update_abc       <- kvip.update_abc (python/kvip/cache/abc.py:5-33; the NPU launch
  *                                of cache/_abc_kernel.py:9-34)
  *   kvip_hip_lru_reset/extend/commit
@@ -46,7 +48,7 @@
 extern "C" {
 #endif
 
-#define KVIP_HIP_ABI_VERSION 2u
+#define KVIP_HIP_ABI_VERSION 3u
 
 #define KVIP_TOPK 2048
 #define KVIP_BLOCK_TOKENS 128
@@ -68,6 +70,8 @@ extern "C" {
 #define KVIP_STATUS_BAD_BLOCK 1u     /* a block-table entry outside [0, num_blocks) */
 #define KVIP_STATUS_HISTOGRAM 2u     /* TopK histogram inconsistent with the row length */
 #define KVIP_STATUS_BAD_TOKEN 4u     /* a TopK token id outside the block table */
+#define KVIP_STATUS_STALLED 8u       /* a multi-workgroup select waited past its spin bound; the
+                                        segment work memory must be re-zeroed before reuse */
 
 /* Lightning-indexer scoring over a paged index-K cache.
  *
@@ -109,13 +113,14 @@ typedef struct KvipIndexerArgs {
  * valid >= 2048: the 2048 tokens that come first in the order (key desc, index asc),
  * written as the tokens with key > kth in ascending index order followed by the
  * tokens with key == kth in ascending index order. */
-#define KVIP_TOPK_SEGMENT_KEYS 4096
+#define KVIP_TOPK_SEGMENT_KEYS 2048
 #define KVIP_TOPK_SEGMENT_WORDS 260
 typedef struct KvipTopkArgs {
     const uint16_t* score_keys;  /* [rows, key_stride] */
     uint32_t* histogram;         /* [rows, 256] from kvip_hip_indexer_decode (re-zeroed here), or NULL */
-    uint32_t* segments;          /* with a histogram: work memory of rows * ceil(key_stride / 4096) * 260
-                                    words for the multi-workgroup select; NULL: one workgroup per row */
+    uint32_t* segments;          /* with a histogram: work memory of rows * ceil(key_stride / 2048) * 260
+                                    words for the multi-workgroup select, zero before the first call
+                                    (every call leaves it reusable); NULL: one workgroup per row */
     const int32_t* seq_lens;     /* [batch] */
     const int32_t* query_ends;   /* [rows] or NULL */
     int32_t* topk;               /* [rows, 2048] token ids, -1 = empty */
@@ -142,7 +147,9 @@ typedef struct KvipFetchArgs {
     int32_t num_blocks;
 } KvipFetchArgs;
 
-/* One decode round: scoring -> TopK-2048 -> Fetch gather, stream-ordered. */
+/* One decode round: scoring -> TopK-2048 -> Fetch gather, stream-ordered. With the
+ * scoring histogram and segment work memory in `topk`, TopK and Fetch run as one fused
+ * launch (kvip_hip_select_fetch). */
 typedef struct KvipLIFetchArgs {
     KvipIndexerArgs indexer;
     KvipTopkArgs topk;
@@ -308,6 +315,10 @@ uint32_t kvip_hip_indexer_decode(const KvipIndexerArgs* args, void* stream);
 uint32_t kvip_hip_topk(const KvipTopkArgs* args, void* stream);
 uint32_t kvip_hip_fetch_gather(const KvipFetchArgs* args, void* stream);
 uint32_t kvip_hip_lifetch_forward(const KvipLIFetchArgs* args, void* stream);
+/* TopK-2048 of rows scored by kvip_hip_indexer_decode fused with the Fetch gather of the
+ * selected rows: same outputs as kvip_hip_topk followed by kvip_hip_fetch_gather. Needs
+ * topk->histogram and topk->segments; fetch->topk must be topk->topk. */
+uint32_t kvip_hip_select_fetch(const KvipTopkArgs* topk, const KvipFetchArgs* fetch, void* stream);
 uint32_t kvip_hip_update_abc(const KvipAbcArgs* args, void* stream);
 uint32_t kvip_hip_lru_reset(const KvipLruArgs* args, int32_t committed, void* stream);
 uint32_t kvip_hip_lru_extend(const KvipLruArgs* args, int32_t active, int32_t committed, void* stream);

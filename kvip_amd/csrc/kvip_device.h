@@ -90,4 +90,19 @@ KVIP_DEVICE uint32_t block_exclusive_scan(uint32_t v, uint32_t* wave_sums, uint3
     return before + incl - v;
 }
 
+// Finds the bin holding the target-th largest element of a 256-bin histogram
+// (bin 255 = largest keys). Writes {bin, count strictly above the bin} to sel[0..1]
+// (sel[0] stays -1 when the histogram holds fewer than `target` elements).
+KVIP_DEVICE void select_bin(const uint32_t* hist, uint32_t target, int* sel, uint32_t* wave_sums) {
+    const int tid = threadIdx.x;
+    const uint32_t c = tid < 256 ? hist[255 - tid] : 0u;
+    uint32_t total;
+    const uint32_t excl = block_exclusive_scan(c, wave_sums, &total);
+    if (tid < 256 && c != 0u && excl < target && excl + c >= target) {
+        sel[0] = 255 - tid;
+        sel[1] = static_cast<int>(excl);
+    }
+    __syncthreads();
+}
+
 }  // namespace kvip

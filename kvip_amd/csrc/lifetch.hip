@@ -1,6 +1,8 @@
 // One decode round of the lightning indexer with fetch: scoring -> TopK-2048 ->
 // Fetch gather, enqueued back to back on one stream (no allocation, no sync, no
-// memset), so the whole round can be captured into a single hipGraph.
+// memset), so the whole round can be captured into a single hipGraph. When the TopK
+// arguments carry the scoring histogram and segment work memory, TopK and the gather
+// run as one fused launch (select_fetch.hip).
 //
 // Replaces kvip_lifetch_streaming_forward (csrc/operators/lightning_indexer_with_fetch/
 // include/api.h:7, op_host/launch.cpp:76-83), whose init -> LI -> resolve/update/fetch
@@ -14,6 +16,8 @@ uint32_t validate_fetch(const KvipFetchArgs* a);
 hipError_t launch_indexer(const KvipIndexerArgs& a, hipStream_t stream);
 hipError_t launch_topk(const KvipTopkArgs& a, hipStream_t stream);
 hipError_t launch_fetch(const KvipFetchArgs& a, hipStream_t stream);
+uint32_t validate_select_fetch(const KvipTopkArgs* t, const KvipFetchArgs* f);
+hipError_t launch_select_fetch(const KvipTopkArgs& t, const KvipFetchArgs& f, hipStream_t stream);
 }  // namespace kvip
 
 extern "C" uint32_t kvip_hip_abi_version(void) { return KVIP_HIP_ABI_VERSION; }
@@ -35,8 +39,11 @@ extern "C" uint32_t kvip_hip_lifetch_forward(const KvipLIFetchArgs* args, void* 
                          fe.batch == li.batch && fe.rows_per_request == li.rows_per_request;
     if (!chained) return KVIP_ERR_INVALID;
     const hipStream_t s = static_cast<hipStream_t>(stream);
+    // With the histogram and segment work memory, TopK and Fetch run as one launch.
+    const bool fused = kvip::validate_select_fetch(&tk, &fe) == KVIP_OK;
     hipError_t e = kvip::launch_indexer(li, s);
     if (e != hipSuccess) return static_cast<uint32_t>(e);
+    if (fused) return static_cast<uint32_t>(kvip::launch_select_fetch(tk, fe, s));
     e = kvip::launch_topk(tk, s);
     if (e != hipSuccess) return static_cast<uint32_t>(e);
     return static_cast<uint32_t>(kvip::launch_fetch(fe, s));

@@ -40,21 +40,6 @@ KVIP_DEVICE Keys8 load_keys(const uint16_t* keys, int idx0, int valid, int strid
     return r;
 }
 
-// Finds the bin holding the target-th largest element of a 256-bin histogram
-// (bin 255 = largest keys). Writes {bin, count strictly above the bin} to sel[0..1]
-// (sel[0] stays -1 when the histogram holds fewer than `target` elements).
-KVIP_DEVICE void select_bin(const uint32_t* hist, uint32_t target, int* sel, uint32_t* wave_sums) {
-    const int tid = threadIdx.x;
-    const uint32_t c = tid < 256 ? hist[255 - tid] : 0u;
-    uint32_t total;
-    const uint32_t excl = block_exclusive_scan(c, wave_sums, &total);
-    if (tid < 256 && c != 0u && excl < target && excl + c >= target) {
-        sel[0] = 255 - tid;
-        sel[1] = static_cast<int>(excl);
-    }
-    __syncthreads();
-}
-
 __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const KvipTopkArgs p) {
     __shared__ uint32_t s_hist[256];
     __shared__ uint32_t s_wave[kTopkThreads / 64];
@@ -291,7 +276,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_regs_kernel(const KvipTopkA
 }
 
 // Split select for rows scored by kvip_hip_indexer_decode (the high-byte histogram is
-// given): the row is cut into 4096-key segments, one 256-thread workgroup each, in two
+// given): the row is cut into 2048-key segments, one 256-thread workgroup each, in two
 // launches, so a batch of long rows spreads over many CUs instead of one workgroup per
 // row.
 //   topk_segment_kernel: every segment workgroup derives the high-byte bin hb from the
@@ -304,7 +289,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_regs_kernel(const KvipTopkA
 // segment 0 also holds [257] hb (-1: inconsistent histogram) and [258] keys above hb in
 // the row.
 constexpr int kSplitThreads = 256;
-constexpr int kSplitKeys = KVIP_TOPK_SEGMENT_KEYS / kSplitThreads;  // 16 per thread
+constexpr int kSplitKeys = KVIP_TOPK_SEGMENT_KEYS / kSplitThreads;  // 8 per thread
 constexpr int kSegWords = KVIP_TOPK_SEGMENT_WORDS;
 
 KVIP_DEVICE int row_valid(const KvipTopkArgs& p, int row) {

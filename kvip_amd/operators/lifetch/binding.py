@@ -19,7 +19,7 @@ TOPK = 2048
 BLOCK_TOKENS = 128
 INDEX_DIM = 128
 TOKEN_BYTES = 656
-TOPK_SEGMENT_KEYS = 4096
+TOPK_SEGMENT_KEYS = 2048
 TOPK_SEGMENT_WORDS = 260
 MAX_CONTEXT = 1 << 24
 
@@ -71,9 +71,10 @@ class LIFetchBinding:
         # int16 storage holding uint16 sortable keys (reinterpret with .view on the host).
         self.score_keys = torch.zeros((self.rows, self.key_stride), dtype=torch.int16, device=dev)
         self.histogram = torch.zeros((self.rows, 256), dtype=torch.int32, device=dev)
-        # Per-segment records of the multi-workgroup TopK (written before they are read).
+        # Per-segment records and per-row arrival counters of the multi-workgroup TopK
+        # (zero once here; every launch leaves the counters at zero).
         segments = (self.key_stride + TOPK_SEGMENT_KEYS - 1) // TOPK_SEGMENT_KEYS
-        self.topk_segments = torch.empty((self.rows, segments, TOPK_SEGMENT_WORDS), dtype=torch.int32, device=dev)
+        self.topk_segments = torch.zeros((self.rows, segments, TOPK_SEGMENT_WORDS), dtype=torch.int32, device=dev)
         self.topk = torch.full((self.rows, TOPK), -1, dtype=torch.int32, device=dev)
         self.status = torch.zeros(1, dtype=torch.int32, device=dev)
         self.keys = None

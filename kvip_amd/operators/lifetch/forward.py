@@ -49,3 +49,8 @@ class LIFetchForward:
 
     def fetch(self):
         abi.check(self.library.kvip_hip_fetch_gather(self._fetch, self._stream()), "Fetch gather")
+
+    def select_fetch(self):
+        """TopK fused with the Fetch gather (the second launch of the forward when the
+        binding carries the segment work memory)."""
+        abi.check(self.library.kvip_hip_select_fetch(self._topk, self._fetch, self._stream()), "TopK+Fetch")

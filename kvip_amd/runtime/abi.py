@@ -9,7 +9,7 @@ import ctypes
 from pathlib import Path
 
 LIBRARY = Path(__file__).resolve().parents[1] / "_lib" / "libkvip_hip.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 KVIP_OK = 0
 KVIP_ERR_INVALID = 100000
@@ -21,6 +21,7 @@ DTYPE_FP32 = 2
 STATUS_BAD_BLOCK = 1
 STATUS_HISTOGRAM = 2
 STATUS_BAD_TOKEN = 4
+STATUS_STALLED = 8
 
 _p = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -119,6 +120,7 @@ PROTOTYPES = {
     "kvip_hip_topk": ([ctypes.POINTER(TopkArgs), _p], ctypes.c_uint32),
     "kvip_hip_fetch_gather": ([ctypes.POINTER(FetchArgs), _p], ctypes.c_uint32),
     "kvip_hip_lifetch_forward": ([ctypes.POINTER(LIFetchArgs), _p], ctypes.c_uint32),
+    "kvip_hip_select_fetch": ([ctypes.POINTER(TopkArgs), ctypes.POINTER(FetchArgs), _p], ctypes.c_uint32),
     "kvip_hip_update_abc": ([ctypes.POINTER(AbcArgs), _p], ctypes.c_uint32),
     "kvip_hip_lru_reset": ([ctypes.POINTER(LruArgs), _i32, _p], ctypes.c_uint32),
     "kvip_hip_lru_extend": ([ctypes.POINTER(LruArgs), _i32, _i32, _p], ctypes.c_uint32),

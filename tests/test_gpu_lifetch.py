@@ -219,3 +219,66 @@ def test_bad_block_id_is_reported_not_faulted(torch_gpu):
     fwd()
     torch.cuda.synchronize()
     assert int(rot.status.item()) & abi.STATUS_BAD_BLOCK
+
+
+@pytest.mark.parametrize("kind,ctx", [
+    ("random", [32768, 20000, 2048, 2047, 0, 8193, 2049]),
+    ("few_levels", [16384, 30000, 4096]),
+    ("all_equal", [6144, 2048]),
+    ("one_bin", [32768, 2100]),
+])
+def test_select_fetch_matches_topk_then_gather(torch_gpu, kind, ctx):
+    """The fused TopK+Fetch launch, fed oracle keys and their high-byte histogram, gives
+    the oracle's TopK (bit-exact, order included) and its byte-exact gather; run twice
+    in a row so the second launch starts from the counters the first one left."""
+    torch = torch_gpu
+    rng = np.random.default_rng(len(ctx) * 13 + ctx[0])
+    rot = kvip_amd.LIFetchBinding(torch, batch=len(ctx), max_context=max(ctx), device="cuda")
+    blocks = rot.batch * rot.max_blocks
+    table = rng.permutation(blocks).astype(np.int32).reshape(rot.batch, rot.max_blocks)
+    kv = rng.integers(0, 256, (blocks, 128, 656), dtype=np.uint8)
+    kv_dev = torch.from_numpy(kv).to("cuda")
+    rot.block_table.copy_(torch.from_numpy(table))
+    rot.bind_index_cache(torch.zeros((blocks, 128, 128), dtype=torch.float8_e4m3fn, device="cuda"))
+    upd = kvip_amd.ContiguousFetch(torch, rot, kv_dev)
+    fwd = kvip_amd.LIFetch(rot, upd)
+    keys = np.zeros((len(ctx), rot.key_stride), np.uint16)
+    for r, v in enumerate(ctx):
+        keys[r, :v] = keys_case(kind, v, rng)
+    hist = np.stack([np.bincount(keys[r, :v] >> 8, minlength=256) for r, v in enumerate(ctx)])
+    rot.score_keys.copy_(torch.from_numpy(keys.view(np.int16)))
+    rot.seq_lens.copy_(torch.tensor(ctx, dtype=torch.int32))
+    want_topk = np.stack([ref.topk_reference(keys[r], v) for r, v in enumerate(ctx)])
+    want_rows = ref.fetch_gather(kv, table, want_topk)
+    for attempt in range(2):
+        say(f"case select_fetch {kind} {ctx} attempt {attempt}")
+        rot.histogram.copy_(torch.from_numpy(hist.astype(np.int32)))
+        rot.topk.fill_(-5)
+        upd.output.fill_(0xAB)
+        fwd.select_fetch()
+        torch.cuda.synchronize()
+        assert int(rot.status.item()) == 0
+        assert np.array_equal(rot.topk.cpu().numpy(), want_topk), attempt
+        assert np.array_equal(upd.output.cpu().numpy(), want_rows), attempt
+        assert not rot.histogram.any()
+        # Every arrival counter is back at zero.
+        assert not rot.topk_segments[:, 0, -1].any()
+
+
+def test_select_fetch_rejects_rows_beyond_32768_and_forward_falls_back(torch_gpu):
+    """Rows longer than 32768 keys are outside the fused launch (arguments rejected before
+    anything runs); the forward then runs TopK and Fetch as separate launches."""
+    torch = torch_gpu
+    wl = synthetic.decode_workload(torch, batch=2, ctx=[40000, 5000], device="cuda", seed=4)
+    rot, upd, fwd = synthetic.bind(torch, kvip_amd, wl)
+    with pytest.raises(ValueError):
+        fwd.select_fetch()
+    fwd()
+    torch.cuda.synchronize()
+    assert int(rot.status.item()) == 0
+    topk = rot.topk.cpu().numpy()
+    keys = gpu_keys(rot)
+    for r, v in enumerate(wl.ctx):
+        assert np.array_equal(topk[r], ref.topk_reference(keys[r], v))
+    assert np.array_equal(upd.output.cpu().numpy(),
+                          ref.fetch_gather(wl.kv_cache.cpu().numpy(), wl.block_table.cpu().numpy(), topk))
