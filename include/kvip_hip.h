@@ -38,6 +38,21 @@
  *                                (python/kvip/adapters/vllm/inputs.py:127-152)
  *   kvip_hip_ingest_index     <- VllmIndexCacheStorage.ingest_prefill / ingest_decode
  *                                (python/kvip/adapters/vllm/index_import.py:18-52)
+ *   kvip_hip_resident_round   <- the streaming resolver round after LI: InitializeRound
+ *                                (op_kernel/lifecycle.cpp:32-81), EmitFinalClassification /
+ *                                ClassifyTopkHalf (indexer_vector.h:679-795,
+ *                                staged_topk_classify.h:9-47), Producer + StagedQuery
+ *                                (streaming.cpp:103-204, resolver_staged_dma2.h:98-237),
+ *                                PublishQueryOutputs (streaming.cpp:66-90), the Fetch of
+ *                                FetchQueryGroup (streaming.cpp:365-500), Consumer + ApplyBatch
+ *                                (streaming.cpp:205-274, shadow_exchange_parallel.h:28-85),
+ *                                PublishDestinationResidency (common/lifetch/cache_metadata.h:54-73)
+ *   kvip_hip_resident_forward <- kvip_lifetch_streaming_forward in resident mode
+ *                                (include/api.h:7, op_host/launch.cpp:76-83)
+ *   kvip_hip_resident_workspace_bytes / kvip_hip_resident_prepare
+ *                             <- the rotation scratch allocated and reset at bind time
+ *                                (python/kvip/operators/lifetch/workspace.py:9-31,
+ *                                 binding.py:113-130)
  */
 #ifndef KVIP_HIP_H
 #define KVIP_HIP_H
@@ -310,6 +325,72 @@ typedef struct KvipIngestArgs {
     int32_t reserved;
 } KvipIngestArgs;
 
+/* Resident-cache round of one LIFetch step (hot/cold split of the TopK positions):
+ * every request b owns the Index rows [row_owners[b], 0..history) (keys, scales, KV
+ * addresses in host_pool, logical ids); position p < resident is hot, its KV row living
+ * in hot_cache[owner, p] when hot_valid[owner, p] != 0. After TopK over positions:
+ *   init     reserved_hot[b] = LRU ordinal of each candidate slot of lru_slots[b] (-1
+ *            otherwise); changes = -1; change_slots = candidates then -1; counts zero;
+ *   resolve  per request, query rows in order: hot hits (p < resident, hot_valid, not a
+ *            candidate) keep slot p; rows q >= 2 reuse row q-2's slot for the same position
+ *            at the same index; the other positions' first occurrences become misses
+ *            ranked in index order over the rows, each given the next free candidate in
+ *            ordinal order (pass 0 ordinals >= used, pass 1 < used; slots holding this
+ *            step's hits or earlier misses are skipped), then the lowest free hot slots;
+ *            slot_output = hot slot of every selected position, logical_output = its
+ *            logical id before the update; change records at (candidate ordinal or 2048 +
+ *            rank); Fetch descriptors (host_pool offset, slot) per miss;
+ *   fetch    hot_cache[owner, slot] = host_pool[offset .. offset + row_bytes) per miss;
+ *   update   per query, misses in rank order in 512-change chunks: the row of each
+ *            missed position moves to its slot, rows displaced from destinations fill
+ *            the chunk's freed positions in order (those below resident lose residency);
+ *            keys, scales, addresses and logical ids move with their rows; finally every
+ *            miss slot becomes valid.
+ * Device errors (bits of KVIP_RESIDENT_ERR_*) go to status[b]; a failed request's later
+ * phases are skipped. The workspace (kvip_hip_resident_workspace_bytes) is prepared once
+ * by kvip_hip_resident_prepare and left prepared by every round; rounds sharing it must
+ * be stream-ordered. */
+#define KVIP_RESIDENT_MAX_QUERIES 4
+#define KVIP_RESIDENT_MAX_RESIDENT 131072
+#define KVIP_RESIDENT_LRU_SLOTS 2048
+#define KVIP_RESIDENT_CHANGES (KVIP_RESIDENT_LRU_SLOTS + KVIP_RESIDENT_MAX_QUERIES * KVIP_TOPK)
+#define KVIP_RESIDENT_ERR_TOKEN 1u       /* a TopK position >= history, or a bad owner row */
+#define KVIP_RESIDENT_ERR_CANDIDATE 4u   /* a candidate outside [0, resident), or no free hot slot */
+#define KVIP_RESIDENT_ERR_SOURCE 8u      /* a Fetch source outside host_pool */
+#define KVIP_RESIDENT_ERR_UPDATE 16u     /* the changes are not a partial permutation */
+typedef struct KvipResidentArgs {
+    const int32_t* topk;          /* [batch * rows_per_request, 2048] selected positions, -1 = empty */
+    const int32_t* row_owners;    /* [batch] */
+    const int32_t* lru_slots;     /* [batch, 2048] victim candidates, oldest first */
+    int32_t* reserved_hot;        /* [batch, resident] (written by the round) */
+    int32_t* hot_valid;           /* [owners, resident] */
+    uint8_t* index_keys;          /* [owners, history, 128] */
+    float* index_scales;          /* [owners, history] */
+    int64_t* addresses;           /* [owners, history] byte offset of each row's KV in host_pool */
+    int64_t* logical_ids;         /* [owners, history] */
+    const uint8_t* host_pool;     /* device-accessible host memory (mapped pinned) */
+    uint8_t* hot_cache;           /* [owners, hot_stride, row_bytes] */
+    int32_t* logical_output;      /* [batch * rows_per_request, 2048] */
+    int32_t* slot_output;         /* [batch * rows_per_request, 2048] */
+    int32_t* changes;             /* [batch, 2048 + rows_per_request * 2048] */
+    int32_t* change_slots;        /* [batch, 2048 + rows_per_request * 2048] */
+    int32_t* miss_counts;         /* [batch, 5]: new misses of each query row, then the total */
+    int64_t* fetch_sources;       /* [batch, rows_per_request * 2048] host_pool offsets by rank */
+    int32_t* fetch_slots;         /* [batch, rows_per_request * 2048] */
+    int32_t* fetch_positions;     /* [batch, rows_per_request * 2048] missed position by rank */
+    int32_t* status;              /* [batch] KVIP_RESIDENT_ERR_* bits */
+    void* workspace;              /* kvip_hip_resident_workspace_bytes(batch, history), 16-byte aligned */
+    int64_t host_pool_bytes;
+    int32_t batch;
+    int32_t rows_per_request;     /* 1..4 */
+    int32_t owners;
+    int32_t history;              /* Index rows per owner, multiple of 128 */
+    int32_t resident;             /* hot positions per owner, 2048..131072 */
+    int32_t hot_stride;           /* hot_cache rows per owner, >= resident */
+    int32_t row_bytes;            /* KV row bytes, multiple of 16 */
+    int32_t used;                 /* candidates consumed before this step (0 without prefetch) */
+} KvipResidentArgs;
+
 uint32_t kvip_hip_abi_version(void);
 uint32_t kvip_hip_indexer_decode(const KvipIndexerArgs* args, void* stream);
 uint32_t kvip_hip_topk(const KvipTopkArgs* args, void* stream);
@@ -328,6 +409,13 @@ uint64_t kvip_hip_lidu_workspace_bytes(int32_t batch);
 uint32_t kvip_hip_lidu(const KvipLiduArgs* args, void* stream);
 uint32_t kvip_hip_pack_queries(const KvipQueryPackArgs* args, void* stream);
 uint32_t kvip_hip_ingest_index(const KvipIngestArgs* args, void* stream);
+uint64_t kvip_hip_resident_workspace_bytes(int32_t batch, int32_t history);
+uint32_t kvip_hip_resident_prepare(const KvipResidentArgs* args, void* stream);
+uint32_t kvip_hip_resident_round(const KvipResidentArgs* args, void* stream);
+/* One resident-cache LIFetch step: block_table[b][j] = row_owners[b] * (history / 128) + j,
+ * scoring of the owners' Index rows, TopK-2048, then kvip_hip_resident_round. */
+uint32_t kvip_hip_resident_forward(const KvipIndexerArgs* indexer, const KvipTopkArgs* topk,
+                                   const KvipResidentArgs* resident, void* stream);
 
 #ifdef __cplusplus
 }

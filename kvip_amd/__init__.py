@@ -12,6 +12,7 @@ __all__ = [
     "LIFetch",
     "LIFetchBinding",
     "ContiguousFetch",
+    "ResidentIndexUpdate",
     "SlotLRU",
     "update_abc",
     "lidu",
@@ -26,6 +27,7 @@ _EXPORTS = {
     "LIFetch": ("operators.lifetch.forward", "LIFetchForward"),
     "LIFetchBinding": ("operators.lifetch.binding", "LIFetchBinding"),
     "ContiguousFetch": ("operators.lifetch.binding", "ContiguousFetch"),
+    "ResidentIndexUpdate": ("operators.lifetch.resident", "ResidentIndexUpdate"),
     "SlotLRU": ("cache.lru", "SlotLRU"),
     "update_abc": ("cache.abc", "update_abc"),
     "lidu": ("operators.lidu", "lidu"),

@@ -1,0 +1,648 @@
+// Resident-cache round of the streaming LIFetch path on gfx950: hot/cold classification
+// of the final TopK positions, per-query miss resolution with LRU victim slots, Fetch of
+// the missed KV rows from mapped host memory into the hot cache, the Index-row
+// permutation and the residency publication. Four launches per round:
+//   resident_init_kernel     one workgroup per request: reserved_hot from the LRU
+//                            candidates, change records and counts cleared;
+//   resident_resolve_kernel  one 1024-thread workgroup per request, everything staged in
+//                            LDS (TopK rows, locations, protection bitmap, rank -> slot);
+//                            first occurrences are found with atomicMin on a per-request
+//                            position table kept in the workspace (reset at the end);
+//   resident_fetch_kernel    one wave per 32 misses, 16-byte nontemporal copies;
+//   resident_update_kernel   one 1024-thread workgroup per request: each 512-change chunk
+//                            is planned in LDS (membership hash sets, closure by scan),
+//                            snapshotted into registers, then written; the position <->
+//                            row maps live in the workspace and are restored to identity.
+// Every per-request loop is bounded by the request's sizes and every workgroup reaches
+// the end of its kernel (errors skip work, never wait).
+//
+// Reference (paths relative to the KVIP tree, op_kernel/ of
+// lightning_indexer_with_fetch unless noted): lifecycle.cpp:32-81 (InitializeRound),
+// staged_topk_classify.h:9-47 and resolver_staged_dma2.h:9-22 (classification),
+// resolver_staged_dma2.h:98-237 (StagedQuery), streaming.cpp:16-22, :66-90 (events,
+// outputs), :205-274 and shadow_exchange_parallel.h:28-85 (Consumer, ApplyBatch,
+// CommitMetadata), common/lifetch/cache_metadata.h:54-73 (residency publication).
+#include "kvip_device.h"
+
+namespace kvip {
+uint32_t validate_indexer(const KvipIndexerArgs* a);
+uint32_t validate_topk(const KvipTopkArgs* a);
+hipError_t launch_indexer(const KvipIndexerArgs& a, hipStream_t stream);
+hipError_t launch_topk(const KvipTopkArgs& a, hipStream_t stream);
+
+namespace {
+
+constexpr int kRsThreads = 1024;
+constexpr int kMaxQ = KVIP_RESIDENT_MAX_QUERIES;
+constexpr int kLru = KVIP_RESIDENT_LRU_SLOTS;
+constexpr int kMaxWords = KVIP_RESIDENT_MAX_RESIDENT / 32;
+constexpr int kChanges = KVIP_RESIDENT_CHANGES;
+constexpr int kChunk = 512;
+constexpr int kSetSize = 2048;               // membership hash set buckets (power of two)
+constexpr uint32_t kNoFirst = 0xFFFFFFFFu;
+constexpr uint32_t kEmpty = 0xFFFFFFFFu;
+static_assert(kTopK == 2 * kRsThreads, "two TopK entries per thread");
+static_assert(kLru == 2 * kRsThreads, "two candidates per thread");
+
+struct Workspace {
+    uint32_t* first;   // [batch, history] lowest index of each position in the current query
+    int32_t* rank;     // [batch, history] miss rank of each position, -1 = none
+    int32_t* row_at;   // [batch, history] row now at each position (identity between rounds)
+    int32_t* pos_of;   // [batch, history] position of each row (identity between rounds)
+};
+
+KVIP_DEVICE Workspace workspace_of(const KvipResidentArgs& p) {
+    const size_t n = static_cast<size_t>(p.batch) * p.history;
+    uint32_t* base = static_cast<uint32_t*>(p.workspace);
+    return {base, reinterpret_cast<int32_t*>(base + n), reinterpret_cast<int32_t*>(base + 2 * n),
+            reinterpret_cast<int32_t*>(base + 3 * n)};
+}
+
+template <typename T>
+KVIP_DEVICE T load_agent(const T* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename T>
+KVIP_DEVICE void store_agent(T* p, T v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+KVIP_DEVICE bool owner_ok(const KvipResidentArgs& p, int o) { return o >= 0 && o < p.owners; }
+
+// Workspace preparation: first = none, rank = none, maps = identity.
+__global__ void resident_prepare_kernel(const KvipResidentArgs p) {
+    const Workspace ws = workspace_of(p);
+    const size_t n = static_cast<size_t>(p.batch) * p.history;
+    for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+         i += static_cast<size_t>(gridDim.x) * blockDim.x) {
+        const int pos = static_cast<int>(i % static_cast<size_t>(p.history));
+        ws.first[i] = kNoFirst;
+        ws.rank[i] = -1;
+        ws.row_at[i] = pos;
+        ws.pos_of[i] = pos;
+    }
+}
+
+// Round initialisation of request b.
+__global__ __launch_bounds__(kRsThreads) void resident_init_kernel(const KvipResidentArgs p) {
+    const int b = blockIdx.x;
+    const int tid = threadIdx.x;
+    int32_t* reserved = p.reserved_hot + static_cast<size_t>(b) * p.resident;
+    for (int s = tid; s < p.resident; s += kRsThreads) reserved[s] = -1;
+    const int nchg = kLru + p.rows_per_request * kTopK;
+    const int32_t* lru = p.lru_slots + static_cast<size_t>(b) * kLru;
+    for (int i = tid; i < nchg; i += kRsThreads) {
+        p.changes[static_cast<size_t>(b) * nchg + i] = -1;
+        p.change_slots[static_cast<size_t>(b) * nchg + i] = i < kLru ? lru[i] : -1;
+    }
+    if (tid < 5) p.miss_counts[b * 5 + tid] = 0;
+    if (tid == 0) p.status[b] = 0;
+    __syncthreads();
+    for (int i = tid; i < kLru; i += kRsThreads) {
+        const int s = lru[i];
+        if (s >= 0 && s < p.resident) reserved[s] = i;
+    }
+}
+
+__global__ __launch_bounds__(kRsThreads) void resident_resolve_kernel(const KvipResidentArgs p) {
+    __shared__ int32_t s_sel[kMaxQ * kTopK];
+    __shared__ int32_t s_loc[kMaxQ * kTopK];
+    __shared__ int32_t s_slots[kMaxQ * kTopK];   // slot of each miss rank
+    __shared__ uint32_t s_bitmap[kMaxWords];     // protected or allocated hot slots
+    __shared__ uint32_t s_wave[kRsThreads / 64];
+    __shared__ uint32_t s_err;
+
+    const int b = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int Q = p.rows_per_request;
+    const int R = p.resident;
+    const int H = p.history;
+    const int words = (R + 31) / 32;
+    const int o = p.row_owners[b];
+    const Workspace ws = workspace_of(p);
+    uint32_t* first = ws.first + static_cast<size_t>(b) * H;
+    int32_t* rank_of = ws.rank + static_cast<size_t>(b) * H;
+    const int32_t* reserved = p.reserved_hot + static_cast<size_t>(b) * R;
+    const int32_t* lru = p.lru_slots + static_cast<size_t>(b) * kLru;
+    const int nchg = kLru + Q * kTopK;
+
+    for (int i = tid; i < words; i += kRsThreads) s_bitmap[i] = 0u;
+    if (tid == 0) s_err = owner_ok(p, o) ? 0u : KVIP_RESIDENT_ERR_TOKEN;
+    __syncthreads();
+    const bool good_owner = owner_ok(p, o);
+    const int32_t* hot_valid = p.hot_valid + static_cast<size_t>(good_owner ? o : 0) * R;
+
+    // Classification of every query row: hot hits keep their position as slot.
+    for (int e = tid; e < Q * kTopK; e += kRsThreads) {
+        const int t = p.topk[static_cast<size_t>(b) * Q * kTopK + e];
+        s_sel[e] = t;
+        int loc = -1;
+        if (t >= H) {
+            atomicOr(&s_err, KVIP_RESIDENT_ERR_TOKEN);
+        } else if (good_owner && t >= 0 && t < R && hot_valid[t] != 0 && reserved[t] < 0) {
+            loc = t;
+            atomicOr(&s_bitmap[t >> 5], 1u << (t & 31));
+        }
+        s_loc[e] = loc;
+    }
+    __syncthreads();
+
+    int old = 0;  // misses ranked by earlier query rows (uniform)
+    for (int q = 0; q < Q; ++q) {
+        if (s_err != 0u) break;  // uniform: read after a barrier
+        const int base = q * kTopK;
+        int tok[2];
+        bool shortcut[2], unresolved[2], fresh[2];
+        // (a) first occurrence of every unresolved position of this row.
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int i = 2 * tid + k;
+            const int t = s_sel[base + i];
+            tok[k] = t;
+            shortcut[k] = q >= 2 && t == s_sel[base - 2 * kTopK + i];
+            unresolved[k] = !shortcut[k] && t >= 0 && t < H && s_loc[base + i] < 0 && load_agent(&rank_of[t]) < 0;
+            if (unresolved[k]) atomicMin(&first[t], static_cast<uint32_t>(i));
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        // (b) new misses in index order -> ranks.
+        uint32_t nnew = 0;
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            fresh[k] = unresolved[k] && load_agent(&first[tok[k]]) == static_cast<uint32_t>(2 * tid + k);
+            nnew += fresh[k] ? 1u : 0u;
+        }
+        uint32_t need_u;
+        uint32_t r = static_cast<uint32_t>(old) + block_exclusive_scan(nnew, s_wave, &need_u);
+        const int need = static_cast<int>(need_u);
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            if (fresh[k]) store_agent(&rank_of[tok[k]], static_cast<int32_t>(r++));
+        }
+        // (c) slots: free candidates in ordinal order, pass 0 = ordinals >= used.
+        int allocated = 0;
+        if (need > 0) {
+            for (int pass = 0; pass < 2 && allocated < need; ++pass) {
+                bool ok[2];
+                int cand[2];
+                uint32_t avail = 0;
+#pragma unroll
+                for (int k = 0; k < 2; ++k) {
+                    const int ord = 2 * tid + k;
+                    const int s = lru[ord];
+                    cand[k] = s;
+                    ok[k] = false;
+                    if ((ord >= p.used) == (pass == 0)) {
+                        if (s < 0 || s >= R) {
+                            atomicOr(&s_err, KVIP_RESIDENT_ERR_CANDIDATE);
+                        } else {
+                            ok[k] = ((s_bitmap[s >> 5] >> (s & 31)) & 1u) == 0u;
+                        }
+                    }
+                    avail += ok[k] ? 1u : 0u;
+                }
+                uint32_t n_avail;
+                uint32_t rank = block_exclusive_scan(avail, s_wave, &n_avail);
+                const int take = min(static_cast<int>(n_avail), need - allocated);
+#pragma unroll
+                for (int k = 0; k < 2; ++k) {
+                    if (ok[k]) {
+                        if (rank < static_cast<uint32_t>(take)) s_slots[old + allocated + rank] = cand[k];
+                        ++rank;
+                    }
+                }
+                __syncthreads();
+                for (int j = tid; j < take; j += kRsThreads) {
+                    const int s = s_slots[old + allocated + j];
+                    atomicOr(&s_bitmap[s >> 5], 1u << (s & 31));
+                }
+                allocated += take;
+                __syncthreads();
+            }
+            if (allocated < need && s_err == 0u) {
+                // Fallback: every known slot of every row is protected, then the free hot
+                // slots in ascending order.
+                for (int e = tid; e < Q * kTopK; e += kRsThreads) {
+                    const int s = s_loc[e];
+                    if (s >= 0 && s < R) atomicOr(&s_bitmap[s >> 5], 1u << (s & 31));
+                }
+                __syncthreads();
+                const int per = (words + kRsThreads - 1) / kRsThreads;
+                const int w0 = min(tid * per, words);
+                const int w1 = min(w0 + per, words);
+                uint32_t free_bits = 0;
+                for (int w = w0; w < w1; ++w) {
+                    const int bits = min(32, R - 32 * w);
+                    const uint32_t live = bits == 32 ? 0xFFFFFFFFu : ((1u << bits) - 1u);
+                    free_bits += __popc(~s_bitmap[w] & live);
+                }
+                uint32_t n_free;
+                uint32_t rank = block_exclusive_scan(free_bits, s_wave, &n_free);
+                const int want = need - allocated;
+                if (n_free < static_cast<uint32_t>(want)) {
+                    if (tid == 0) atomicOr(&s_err, KVIP_RESIDENT_ERR_CANDIDATE);
+                } else {
+                    for (int w = w0; w < w1 && rank < static_cast<uint32_t>(want); ++w) {
+                        const int bits = min(32, R - 32 * w);
+                        const uint32_t live = bits == 32 ? 0xFFFFFFFFu : ((1u << bits) - 1u);
+                        uint32_t m = ~s_bitmap[w] & live;
+                        while (m != 0u && rank < static_cast<uint32_t>(want)) {
+                            const int bit = __ffs(m) - 1;
+                            s_slots[old + allocated + rank] = 32 * w + bit;
+                            ++rank;
+                            m &= m - 1u;
+                        }
+                    }
+                }
+                __syncthreads();
+                if (s_err == 0u) {
+                    for (int j = tid; j < want; j += kRsThreads) {
+                        const int s = s_slots[old + allocated + j];
+                        atomicOr(&s_bitmap[s >> 5], 1u << (s & 31));
+                    }
+                    allocated = need;
+                }
+                __syncthreads();
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (s_err != 0u) break;
+        // (d) locations of the row, change records and Fetch descriptors of its misses.
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int i = 2 * tid + k;
+            const int t = tok[k];
+            if (shortcut[k]) {
+                s_loc[base + i] = s_loc[base - 2 * kTopK + i];
+            } else if (t >= 0 && t < H && s_loc[base + i] < 0) {
+                s_loc[base + i] = s_slots[load_agent(&rank_of[t])];
+            }
+            if (fresh[k]) {
+                const int rk = load_agent(&rank_of[t]);
+                const int s = s_slots[rk];
+                const int ord = reserved[s];
+                const int rec = ord >= 0 ? ord : kLru + rk;
+                p.change_slots[static_cast<size_t>(b) * nchg + rec] = s;
+                p.changes[static_cast<size_t>(b) * nchg + rec] = t;
+                const size_t d = static_cast<size_t>(b) * Q * kTopK + rk;
+                const int64_t off = p.addresses[static_cast<size_t>(o) * H + t];
+                // Every source is checked here, before anything is fetched.
+                if (off < 0 || off > p.host_pool_bytes - p.row_bytes || (off & 15) != 0) {
+                    atomicOr(&s_err, KVIP_RESIDENT_ERR_SOURCE);
+                }
+                p.fetch_slots[d] = s;
+                p.fetch_positions[d] = t;
+                p.fetch_sources[d] = off;
+            }
+        }
+        if (tid == 0) p.miss_counts[b * 5 + q] = need;
+        old += need;
+        __syncthreads();
+    }
+
+    // Outputs of every row (-1 throughout for a failed request) and the total.
+    const bool failed = s_err != 0u;
+    for (int e = tid; e < Q * kTopK; e += kRsThreads) {
+        const size_t at = static_cast<size_t>(b) * Q * kTopK + e;
+        const int t = s_sel[e];
+        const bool live = !failed && t >= 0 && t < H;
+        p.slot_output[at] = live ? s_loc[e] : -1;
+        p.logical_output[at] = live ? static_cast<int32_t>(p.logical_ids[static_cast<size_t>(o) * H + t]) : -1;
+    }
+    if (tid == 0) {
+        p.miss_counts[b * 5 + 4] = failed ? 0 : old;
+        p.status[b] = static_cast<int32_t>(s_err);
+    }
+    // Workspace back to its prepared state for the positions this request touched.
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    for (int e = tid; e < Q * kTopK; e += kRsThreads) {
+        const int t = s_sel[e];
+        if (t >= 0 && t < H) {
+            store_agent(&first[t], kNoFirst);
+            store_agent(&rank_of[t], -1);
+        }
+    }
+}
+
+// Fetch of the missed rows: wave w of workgroup (x, b) moves ranks [32*(4x+w), +32).
+constexpr int kFetchRows = 32;
+template <int PIECES>
+__global__ __launch_bounds__(256) void resident_fetch_kernel(const KvipResidentArgs p) {
+    const int b = blockIdx.y;
+    const int lane = threadIdx.x & 63;
+    const int r0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * kFetchRows;
+    if (p.status[b] != 0) return;
+    const int total = p.miss_counts[b * 5 + 4];
+    if (r0 >= total) return;
+    const int o = p.row_owners[b];
+    const int pieces = PIECES > 0 ? PIECES : p.row_bytes / 16;
+    const int rows = min(kFetchRows, total - r0);
+    int64_t src = -1, dst = -1;
+    uint32_t err = 0;
+    if (lane < rows) {
+        const size_t d = static_cast<size_t>(b) * p.rows_per_request * kTopK + r0 + lane;
+        const int64_t off = p.fetch_sources[d];
+        const int slot = p.fetch_slots[d];
+        if (off >= 0 && off <= p.host_pool_bytes - p.row_bytes && (off & 15) == 0) {
+            src = off;
+            dst = (static_cast<int64_t>(o) * p.hot_stride + slot) * p.row_bytes;
+        } else {
+            err = KVIP_RESIDENT_ERR_SOURCE;
+        }
+    }
+    const int n = rows * pieces;
+    if constexpr (PIECES > 0) {
+        constexpr int kIters = (kFetchRows * PIECES + 63) / 64;
+        v4i val[kIters];
+#pragma unroll
+        for (int it = 0; it < kIters; ++it) {
+            const int idx = it * 64 + lane;
+            const int r = idx / PIECES;
+            const int piece = idx - r * PIECES;
+            const int64_t s = __shfl(src, min(r, kFetchRows - 1));
+            val[it] = v4i{0, 0, 0, 0};
+            if (idx < n && s >= 0) val[it] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(p.host_pool + s + piece * 16));
+        }
+#pragma unroll
+        for (int it = 0; it < kIters; ++it) {
+            const int idx = it * 64 + lane;
+            const int r = idx / PIECES;
+            const int piece = idx - r * PIECES;
+            const int64_t d = __shfl(dst, min(r, kFetchRows - 1));
+            if (idx < n && d >= 0) *reinterpret_cast<v4i*>(p.hot_cache + d + piece * 16) = val[it];
+        }
+    } else {
+        const int iters = (kFetchRows * pieces + 63) / 64;
+        for (int it = 0; it < iters; ++it) {
+            const int idx = it * 64 + lane;
+            const int r = idx / pieces;
+            const int piece = idx - r * pieces;
+            const int64_t s = __shfl(src, min(r, kFetchRows - 1));
+            const int64_t d = __shfl(dst, min(r, kFetchRows - 1));
+            if (idx < n && s >= 0 && d >= 0) {
+                *reinterpret_cast<v4i*>(p.hot_cache + d + piece * 16) =
+                    *reinterpret_cast<const v4i*>(p.host_pool + s + piece * 16);
+            }
+        }
+    }
+    if (err != 0u) atomicOr(&p.status[b], static_cast<int32_t>(err));
+}
+
+KVIP_DEVICE uint32_t set_hash(uint32_t k) { return (k * 0x9E3779B9u) >> 21; }  // 11 bits: kSetSize
+
+// Inserts k; false when it is already present (or the set is full).
+KVIP_DEVICE bool set_insert(uint32_t* set, uint32_t k) {
+    uint32_t h = set_hash(k);
+    for (int i = 0; i < kSetSize; ++i) {
+        const uint32_t prev = atomicCAS(&set[h], kEmpty, k);
+        if (prev == kEmpty) return true;
+        if (prev == k) return false;
+        h = (h + 1) & (kSetSize - 1);
+    }
+    return false;
+}
+
+KVIP_DEVICE bool set_contains(const uint32_t* set, uint32_t k) {
+    uint32_t h = set_hash(k);
+    for (int i = 0; i < kSetSize; ++i) {
+        const uint32_t v = set[h];
+        if (v == k) return true;
+        if (v == kEmpty) return false;
+        h = (h + 1) & (kSetSize - 1);
+    }
+    return false;
+}
+
+// Index update of request b, then residency of its miss slots.
+constexpr int kMaxLog = 2 * kMaxQ * kTopK;  // destinations written this round
+__global__ __launch_bounds__(kRsThreads) void resident_update_kernel(const KvipResidentArgs p) {
+    __shared__ uint32_t s_src_set[kSetSize];
+    __shared__ uint32_t s_dst_set[kSetSize];
+    __shared__ int32_t s_ps[2 * kChunk];
+    __shared__ int32_t s_pd[2 * kChunk];
+    __shared__ int32_t s_log[kMaxLog];
+    __shared__ uint32_t s_wave[kRsThreads / 64];
+    __shared__ uint32_t s_err;
+    __shared__ int s_nlog;
+
+    const int b = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int Q = p.rows_per_request;
+    const int R = p.resident;
+    const int H = p.history;
+    if (p.status[b] != 0) return;  // uniform
+    const int o = p.row_owners[b];
+    const Workspace ws = workspace_of(p);
+    int32_t* row_at = ws.row_at + static_cast<size_t>(b) * H;
+    int32_t* pos_of = ws.pos_of + static_cast<size_t>(b) * H;
+    uint8_t* keys = p.index_keys + static_cast<size_t>(o) * H * kIndexDim;
+    float* scales = p.index_scales + static_cast<size_t>(o) * H;
+    int64_t* addresses = p.addresses + static_cast<size_t>(o) * H;
+    int64_t* logical = p.logical_ids + static_cast<size_t>(o) * H;
+    int32_t* hot_valid = p.hot_valid + static_cast<size_t>(o) * R;
+    const size_t dbase = static_cast<size_t>(b) * Q * kTopK;
+    if (tid == 0) {
+        s_err = 0u;
+        s_nlog = 0;
+    }
+    __syncthreads();
+
+    int r0 = 0;
+    for (int q = 0; q < Q; ++q) {
+        const int count = p.miss_counts[b * 5 + q];
+        for (int c0 = 0; c0 < count; c0 += kChunk) {
+            if (s_err != 0u) break;  // uniform
+            const int n = min(kChunk, count - c0);
+            for (int i = tid; i < kSetSize; i += kRsThreads) {
+                s_src_set[i] = kEmpty;
+                s_dst_set[i] = kEmpty;
+            }
+            __syncthreads();
+            int src = -1, dst = -1;
+            if (tid < n) {
+                const int orig = p.fetch_positions[dbase + r0 + c0 + tid];
+                dst = p.fetch_slots[dbase + r0 + c0 + tid];
+                const bool in_range = orig >= 0 && orig < H && dst >= 0 && dst < R;
+                src = in_range ? pos_of[orig] : -1;
+                if (!in_range || !set_insert(s_src_set, static_cast<uint32_t>(src)) ||
+                    !set_insert(s_dst_set, static_cast<uint32_t>(dst))) {
+                    atomicOr(&s_err, KVIP_RESIDENT_ERR_UPDATE);
+                }
+            }
+            __syncthreads();
+            if (s_err != 0u) break;
+            // Closure: displaced destination rows fill the freed source positions in order.
+            const bool out = tid < n && !set_contains(s_src_set, static_cast<uint32_t>(dst));
+            const bool freed = tid < n && !set_contains(s_dst_set, static_cast<uint32_t>(src));
+            uint32_t totals;
+            const uint32_t pre = block_exclusive_scan((out ? 1u : 0u) | ((freed ? 1u : 0u) << 16), s_wave, &totals);
+            if (tid < n) {
+                s_ps[tid] = src;
+                s_pd[tid] = dst;
+            }
+            if (out) s_ps[kChunk + (pre & 0xFFFFu)] = dst;
+            if (freed) s_pd[kChunk + (pre >> 16)] = src;
+            __syncthreads();
+            const int extras = static_cast<int>(totals & 0xFFFFu);
+            const int moves = n + extras;
+            // Snapshot every moving row, then write (a permutation of the moved positions).
+            const int m = tid;
+            const int j = m < n ? m : kChunk + m - n;
+            int ps = 0, pd = 0, row = 0;
+            v4i kv[kIndexDim / 16];
+            float sc = 0.f;
+            int64_t ad = 0, lg = 0;
+            if (m < moves) {
+                ps = s_ps[j];
+                pd = s_pd[j];
+                const v4i* kr = reinterpret_cast<const v4i*>(keys + static_cast<size_t>(ps) * kIndexDim);
+#pragma unroll
+                for (int v = 0; v < kIndexDim / 16; ++v) kv[v] = kr[v];
+                sc = scales[ps];
+                ad = addresses[ps];
+                lg = logical[ps];
+                row = row_at[ps];
+            }
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+            if (m < moves) {
+                v4i* kw = reinterpret_cast<v4i*>(keys + static_cast<size_t>(pd) * kIndexDim);
+#pragma unroll
+                for (int v = 0; v < kIndexDim / 16; ++v) kw[v] = kv[v];
+                scales[pd] = sc;
+                addresses[pd] = ad;
+                logical[pd] = lg;
+                row_at[pd] = row;
+                pos_of[row] = pd;
+                if (m >= n && pd < R) hot_valid[pd] = 0;  // freed hot position: its KV did not move
+                const int at = atomicAdd(&s_nlog, 1);
+                if (at < kMaxLog) s_log[at] = pd;
+            }
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+        }
+        r0 += count;
+    }
+    // Residency of every fetched slot (after the freed positions were invalidated).
+    const int total = p.miss_counts[b * 5 + 4];
+    if (s_err == 0u) {
+        for (int i = tid; i < total; i += kRsThreads) hot_valid[p.fetch_slots[dbase + i]] = 1;
+    }
+    // Maps back to identity: read every logged position's row, then reset both maps.
+    const int nlog = min(s_nlog, kMaxLog);
+    int rows[kMaxLog / kRsThreads];
+#pragma unroll
+    for (int k = 0; k < kMaxLog / kRsThreads; ++k) {
+        const int i = tid + k * kRsThreads;
+        rows[k] = i < nlog ? row_at[s_log[i]] : -1;
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < kMaxLog / kRsThreads; ++k) {
+        const int i = tid + k * kRsThreads;
+        if (i < nlog) {
+            row_at[s_log[i]] = s_log[i];
+            pos_of[rows[k]] = rows[k];
+        }
+    }
+    if (tid == 0 && s_err != 0u) atomicOr(&p.status[b], static_cast<int32_t>(s_err));
+}
+
+__global__ void owner_table_kernel(int32_t* table, const int32_t* owners, int batch, int max_blocks,
+                                   int blocks_per_owner) {
+    const int b = blockIdx.y;
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (b < batch && j < max_blocks) {
+        const int o = owners[b];
+        table[static_cast<size_t>(b) * max_blocks + j] = j < blocks_per_owner ? o * blocks_per_owner + j : 0;
+    }
+}
+
+bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+}  // namespace
+
+uint32_t validate_resident(const KvipResidentArgs* a) {
+    if (a == nullptr) return KVIP_ERR_INVALID;
+    const bool ptrs = a->topk && a->row_owners && a->lru_slots && a->reserved_hot && a->hot_valid && a->index_keys &&
+                      a->index_scales && a->addresses && a->logical_ids && a->host_pool && a->hot_cache &&
+                      a->logical_output && a->slot_output && a->changes && a->change_slots && a->miss_counts &&
+                      a->fetch_sources && a->fetch_slots && a->fetch_positions && a->status && a->workspace;
+    if (!ptrs) return KVIP_ERR_INVALID;
+    const bool ok = a->batch >= 1 && a->batch <= 65535 && a->rows_per_request >= 1 &&
+                    a->rows_per_request <= kMaxQ && a->owners >= 1 && a->history >= 128 && a->history % 128 == 0 &&
+                    a->history <= (1 << 24) && a->resident >= kLru && a->resident <= KVIP_RESIDENT_MAX_RESIDENT &&
+                    a->resident <= a->history && a->hot_stride >= a->resident && a->row_bytes >= 16 &&
+                    a->row_bytes % 16 == 0 && a->used >= 0 && a->used <= kLru && a->host_pool_bytes >= a->row_bytes &&
+                    aligned(a->index_keys, 16) && aligned(a->host_pool, 16) && aligned(a->hot_cache, 16) &&
+                    aligned(a->workspace, 16);
+    return ok ? KVIP_OK : KVIP_ERR_INVALID;
+}
+
+hipError_t launch_resident_round(const KvipResidentArgs& a, hipStream_t s) {
+    hipLaunchKernelGGL(resident_init_kernel, dim3(a.batch), dim3(kRsThreads), 0, s, a);
+    hipLaunchKernelGGL(resident_resolve_kernel, dim3(a.batch), dim3(kRsThreads), 0, s, a);
+    const dim3 fgrid((a.rows_per_request * kTopK + 4 * kFetchRows - 1) / (4 * kFetchRows), a.batch);
+    if (a.row_bytes == KVIP_KV_ROW_BYTES) {
+        hipLaunchKernelGGL(resident_fetch_kernel<KVIP_KV_ROW_BYTES / 16>, fgrid, dim3(256), 0, s, a);
+    } else {
+        hipLaunchKernelGGL(resident_fetch_kernel<0>, fgrid, dim3(256), 0, s, a);
+    }
+    hipLaunchKernelGGL(resident_update_kernel, dim3(a.batch), dim3(kRsThreads), 0, s, a);
+    return hipGetLastError();
+}
+
+}  // namespace kvip
+
+extern "C" uint64_t kvip_hip_resident_workspace_bytes(int32_t batch, int32_t history) {
+    if (batch < 1 || history < 1) return 0;
+    return 16ull * static_cast<uint64_t>(batch) * static_cast<uint64_t>(history);
+}
+
+extern "C" uint32_t kvip_hip_resident_prepare(const KvipResidentArgs* args, void* stream) {
+    const uint32_t rc = kvip::validate_resident(args);
+    if (rc != KVIP_OK) return rc;
+    hipLaunchKernelGGL(kvip::resident_prepare_kernel, dim3(1024), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       *args);
+    return static_cast<uint32_t>(hipGetLastError());
+}
+
+extern "C" uint32_t kvip_hip_resident_round(const KvipResidentArgs* args, void* stream) {
+    const uint32_t rc = kvip::validate_resident(args);
+    if (rc != KVIP_OK) return rc;
+    return static_cast<uint32_t>(kvip::launch_resident_round(*args, static_cast<hipStream_t>(stream)));
+}
+
+extern "C" uint32_t kvip_hip_resident_forward(const KvipIndexerArgs* indexer, const KvipTopkArgs* topk,
+                                              const KvipResidentArgs* resident, void* stream) {
+    if (indexer == nullptr || topk == nullptr || resident == nullptr) return KVIP_ERR_INVALID;
+    if (kvip::validate_indexer(indexer) != KVIP_OK || kvip::validate_topk(topk) != KVIP_OK ||
+        kvip::validate_resident(resident) != KVIP_OK) {
+        return KVIP_ERR_INVALID;
+    }
+    const KvipIndexerArgs& li = *indexer;
+    const KvipResidentArgs& ra = *resident;
+    const int blocks_per_owner = ra.history / kvip::kBlockTokens;
+    // Scoring reads the owners' Index rows through the block table; TopK feeds the round.
+    const bool chained = topk->score_keys == li.score_keys && topk->batch == li.batch &&
+                         topk->rows_per_request == li.rows_per_request && topk->key_stride == li.key_stride &&
+                         li.batch == ra.batch && li.rows_per_request == ra.rows_per_request &&
+                         topk->topk == ra.topk && li.keys == ra.index_keys && li.key_scale == ra.index_scales &&
+                         li.key_block_stride == static_cast<int64_t>(kvip::kBlockTokens) * kvip::kIndexDim &&
+                         li.scale_block_stride == kvip::kBlockTokens && li.max_blocks >= blocks_per_owner &&
+                         li.num_blocks == ra.owners * blocks_per_owner && li.qk_dtype == KVIP_DTYPE_FP8_E4M3;
+    if (!chained) return KVIP_ERR_INVALID;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(kvip::owner_table_kernel, dim3((li.max_blocks + 255) / 256, li.batch), dim3(256), 0, s,
+                       const_cast<int32_t*>(li.block_table), ra.row_owners, li.batch, li.max_blocks, blocks_per_owner);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return static_cast<uint32_t>(e);
+    e = kvip::launch_indexer(li, s);
+    if (e != hipSuccess) return static_cast<uint32_t>(e);
+    e = kvip::launch_topk(*topk, s);
+    if (e != hipSuccess) return static_cast<uint32_t>(e);
+    return static_cast<uint32_t>(kvip::launch_resident_round(ra, s));
+}

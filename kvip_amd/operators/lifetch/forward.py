@@ -13,20 +13,32 @@ import ctypes
 
 from kvip_amd.runtime import abi
 from kvip_amd.operators.lifetch.binding import ContiguousFetch, LIFetchBinding
+from kvip_amd.operators.lifetch.resident import ResidentIndexUpdate
 
 
 class LIFetchForward:
+    """`update` is a ContiguousFetch (selected KV rows gathered into one buffer) or a
+    ResidentIndexUpdate (hot-cache round: resolve, Fetch of the misses from host memory,
+    Index update)."""
+
     def __init__(self, rotating, update):
         if not isinstance(rotating, LIFetchBinding):
             raise ValueError("LIFetch rotating must be a kvip_amd LIFetchBinding")
-        if not isinstance(update, ContiguousFetch):
-            raise ValueError("LIFetch update must be a kvip_amd ContiguousFetch")
+        if not isinstance(update, (ContiguousFetch, ResidentIndexUpdate)):
+            raise ValueError("LIFetch update must be a kvip_amd ContiguousFetch or ResidentIndexUpdate")
         if update.rotating is not rotating:
             raise ValueError("Fetch destination was built for another LIFetch binding")
         if rotating.device != update.device:
             raise ValueError("Fetch and Index update must use the same device")
         self.rotating, self.update, self.torch = rotating, update, rotating.torch
         self.library = abi.load_library()
+        self.resident = isinstance(update, ResidentIndexUpdate)
+        if self.resident:
+            self.indexer_args, self.topk_args = rotating.indexer_args(), rotating.topk_args()
+            self.resident_args = update.args
+            self._refs = (ctypes.byref(self.indexer_args), ctypes.byref(self.topk_args),
+                          ctypes.byref(self.resident_args))
+            return
         self.args = abi.LIFetchArgs(rotating.indexer_args(), rotating.topk_args(), update.fetch_args())
         self._args_ref = ctypes.byref(self.args)
         # Stage-wise argument blocks for score()/select()/fetch().
@@ -38,6 +50,9 @@ class LIFetchForward:
         return abi.stream_handle(self.torch, self.rotating.device)
 
     def __call__(self):
+        if self.resident:
+            abi.check(self.library.kvip_hip_resident_forward(*self._refs, self._stream()), "resident LIFetch forward")
+            return
         abi.check(self.library.kvip_hip_lifetch_forward(self._args_ref, self._stream()), "LIFetch forward")
 
     # Individual stages (same kernels as the fused forward).

@@ -1,0 +1,114 @@
+"""Resident-cache `update` argument of ``kvip_amd.LIFetch``: the hot/cold LIFetch round.
+
+`ResidentIndexUpdate` mirrors the reference's DirectIndexUpdate
+(python/kvip/operators/lifetch/index_update.py:28-102): it binds the stable per-owner
+Index storage (keys [owners, history, 128] fp8, scales [owners, history] float32, KV
+addresses and logical ids [owners, history] int64), the request -> owner rows and the
+service outputs (logical and slot TopK, int32 [2, rows, 1, 2048]). Next to them it binds
+what the reference keeps behind KVAF: the hot KV cache [owners, hot_stride, row_bytes]
+(position p < resident of an owner is hot slot p) and the host KV pool, a
+device-accessible (pinned) host tensor in which `addresses` are byte offsets.
+
+The forward enqueues, on the current stream and without host synchronisation: the
+owner block table, LI scoring of the owners' Index rows, TopK-2048 per query row, and the
+round of kvip_hip_resident_round (init, resolve, Fetch from the host pool, Index update,
+residency). Per-step inputs are `rotating.lru_slots` ([batch, 2048] victim candidates,
+oldest first, e.g. ``SlotLRU.slots``) plus the query buffers of the binding. Device
+errors land in `status` ([batch] int32, KVIP_RESIDENT_ERR_* bits).
+"""
+from __future__ import annotations
+
+import ctypes
+
+from kvip_amd.runtime import abi
+from kvip_amd.operators.lifetch.binding import BLOCK_TOKENS, INDEX_DIM, TOPK
+
+LRU_SLOTS = abi.RESIDENT_LRU_SLOTS
+
+
+class ResidentIndexUpdate:
+    def __init__(self, torch, *, keys, scales, addresses, logical_ids, row_owners, rotating, hot_valid, hot_cache,
+                 host_pool, resident, status=None, outputs=None, used=0):
+        self.torch, self.rotating, self.device = torch, rotating, rotating.device
+        if keys.dim() != 3 or keys.shape[2] != INDEX_DIM or keys.dtype != torch.float8_e4m3fn or not keys.is_contiguous():
+            raise ValueError("Index keys must be contiguous float8_e4m3fn [owners, history, 128]")
+        owners, history = int(keys.shape[0]), int(keys.shape[1])
+        if history % BLOCK_TOKENS:
+            raise ValueError("Index history must be a multiple of 128 positions")
+        for name, t, dtype in (("scales", scales, torch.float32), ("addresses", addresses, torch.int64),
+                               ("logical_ids", logical_ids, torch.int64)):
+            if tuple(t.shape) != (owners, history) or t.dtype != dtype or not t.is_contiguous():
+                raise ValueError(f"Index {name} must be contiguous {dtype} [owners, history]")
+        if row_owners.dtype != torch.int32 or tuple(row_owners.shape) != (rotating.batch,):
+            raise ValueError("row_owners must be int32 [batch]")
+        if not abi.RESIDENT_LRU_SLOTS <= resident <= min(history, abi.RESIDENT_MAX_RESIDENT):
+            raise ValueError(f"resident must be in 2048..min(history, {abi.RESIDENT_MAX_RESIDENT})")
+        if tuple(hot_valid.shape) != (owners, resident) or hot_valid.dtype != torch.int32:
+            raise ValueError("hot_valid must be int32 [owners, resident]")
+        if (hot_cache.dim() != 3 or hot_cache.shape[0] != owners or hot_cache.shape[1] < resident or
+                hot_cache.dtype != torch.uint8 or not hot_cache.is_contiguous() or hot_cache.shape[2] % 16):
+            raise ValueError("hot cache must be contiguous uint8 [owners, >= resident, row_bytes % 16 == 0]")
+        if host_pool.dtype != torch.uint8 or host_pool.device.type != "cpu" or not host_pool.is_pinned():
+            raise ValueError("host pool must be a pinned uint8 CPU tensor (device-mapped host memory)")
+        if rotating.rows_per_request > abi.RESIDENT_MAX_QUERIES or rotating.qk_name != "fp8":
+            raise ValueError("resident LIFetch supports fp8 Index keys and up to 4 query rows per request")
+        if rotating.max_blocks * BLOCK_TOKENS < history:
+            raise ValueError("LIFetch binding max_context must cover the Index history")
+        if not 0 <= used <= LRU_SLOTS:
+            raise ValueError("used must be in 0..2048")
+        dev = self.device
+        if any(t.device != dev for t in (keys, scales, addresses, logical_ids, row_owners, hot_valid, hot_cache)):
+            raise ValueError("Index storage, hot cache and the LIFetch binding must share one device")
+        self.keys, self.scales, self.addresses, self.logical_ids = keys, scales, addresses, logical_ids
+        self.row_owners, self.hot_valid, self.hot_cache, self.host_pool = row_owners, hot_valid, hot_cache, host_pool
+        self.owners, self.history, self.resident, self.used = owners, history, resident, used
+        rows, q = rotating.rows, rotating.rows_per_request
+        self.status = torch.zeros(rotating.batch, dtype=torch.int32, device=dev) if status is None else status
+        if outputs is None:
+            outputs = torch.full((2, rows, 1, TOPK), -1, dtype=torch.int32, device=dev)
+        if tuple(outputs.shape) != (2, rows, 1, TOPK) or outputs.dtype != torch.int32 or not outputs.is_contiguous():
+            raise ValueError("Service outputs must be contiguous int32 [2, rows, 1, 2048]")
+        self.outputs = outputs
+        self.logical_output, self.slot_output = outputs.unbind(0)
+        b = rotating.batch
+        # Round state (the reference's rotation scratch, workspace.py:9-31).
+        self.lru_slots = rotating.lru_slots = torch.full((b, LRU_SLOTS), -1, dtype=torch.int32, device=dev)
+        self.reserved_hot = torch.full((b, resident), -1, dtype=torch.int32, device=dev)
+        nchg = LRU_SLOTS + q * TOPK
+        self.changes = torch.full((b, nchg), -1, dtype=torch.int32, device=dev)
+        self.change_slots = torch.full((b, nchg), -1, dtype=torch.int32, device=dev)
+        self.miss_counts = torch.zeros((b, 5), dtype=torch.int32, device=dev)
+        self.fetch_sources = torch.zeros((b, q * TOPK), dtype=torch.int64, device=dev)
+        self.fetch_slots = torch.zeros((b, q * TOPK), dtype=torch.int32, device=dev)
+        self.fetch_positions = torch.zeros((b, q * TOPK), dtype=torch.int32, device=dev)
+        lib = abi.load_library()
+        nbytes = int(lib.kvip_hip_resident_workspace_bytes(b, history))
+        self.workspace = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        # LI reads the owners' Index rows as 128-position blocks.
+        rotating.bind_index_cache(keys.view(owners * history // BLOCK_TOKENS, BLOCK_TOKENS, INDEX_DIM),
+                                  scales.view(owners * history // BLOCK_TOKENS, BLOCK_TOKENS))
+        if rotating.query_ends is None:
+            rotating.seq_lens.fill_(history)
+        self.args = self.resident_args()
+        abi.check(lib.kvip_hip_resident_prepare(ctypes.byref(self.args), abi.stream_handle(torch, dev)),
+                  "resident workspace")
+
+    def set_candidates(self, lru_slots):
+        """Victim candidates for the next step ([batch, 2048] int32, oldest first)."""
+        self.lru_slots.copy_(lru_slots)
+
+    def resident_args(self):
+        p = abi.ptr
+        r = self.rotating
+        return abi.ResidentArgs(
+            topk=p(r.topk), row_owners=p(self.row_owners), lru_slots=p(self.lru_slots),
+            reserved_hot=p(self.reserved_hot), hot_valid=p(self.hot_valid), index_keys=p(self.keys),
+            index_scales=p(self.scales), addresses=p(self.addresses), logical_ids=p(self.logical_ids),
+            host_pool=p(self.host_pool), hot_cache=p(self.hot_cache), logical_output=p(self.logical_output),
+            slot_output=p(self.slot_output), changes=p(self.changes), change_slots=p(self.change_slots),
+            miss_counts=p(self.miss_counts), fetch_sources=p(self.fetch_sources), fetch_slots=p(self.fetch_slots),
+            fetch_positions=p(self.fetch_positions), status=p(self.status), workspace=p(self.workspace),
+            host_pool_bytes=self.host_pool.numel(), batch=r.batch, rows_per_request=r.rows_per_request,
+            owners=self.owners, history=self.history, resident=self.resident, hot_stride=int(self.hot_cache.shape[1]),
+            row_bytes=int(self.hot_cache.shape[2]), used=self.used,
+        )

@@ -113,6 +113,27 @@ class IngestArgs(ctypes.Structure):
     ]
 
 
+RESIDENT_MAX_QUERIES = 4
+RESIDENT_MAX_RESIDENT = 131072
+RESIDENT_LRU_SLOTS = 2048
+RESIDENT_ERR_TOKEN = 1
+RESIDENT_ERR_CANDIDATE = 4
+RESIDENT_ERR_SOURCE = 8
+RESIDENT_ERR_UPDATE = 16
+
+
+class ResidentArgs(ctypes.Structure):
+    _fields_ = [
+        ("topk", _p), ("row_owners", _p), ("lru_slots", _p), ("reserved_hot", _p), ("hot_valid", _p),
+        ("index_keys", _p), ("index_scales", _p), ("addresses", _p), ("logical_ids", _p), ("host_pool", _p),
+        ("hot_cache", _p), ("logical_output", _p), ("slot_output", _p), ("changes", _p), ("change_slots", _p),
+        ("miss_counts", _p), ("fetch_sources", _p), ("fetch_slots", _p), ("fetch_positions", _p), ("status", _p),
+        ("workspace", _p), ("host_pool_bytes", _i64),
+        ("batch", _i32), ("rows_per_request", _i32), ("owners", _i32), ("history", _i32), ("resident", _i32),
+        ("hot_stride", _i32), ("row_bytes", _i32), ("used", _i32),
+    ]
+
+
 # name -> (argtypes, restype); must list every function declared in include/kvip_hip.h.
 PROTOTYPES = {
     "kvip_hip_abi_version": ([], ctypes.c_uint32),
@@ -129,6 +150,11 @@ PROTOTYPES = {
     "kvip_hip_lidu": ([ctypes.POINTER(LiduArgs), _p], ctypes.c_uint32),
     "kvip_hip_pack_queries": ([ctypes.POINTER(QueryPackArgs), _p], ctypes.c_uint32),
     "kvip_hip_ingest_index": ([ctypes.POINTER(IngestArgs), _p], ctypes.c_uint32),
+    "kvip_hip_resident_workspace_bytes": ([_i32, _i32], ctypes.c_uint64),
+    "kvip_hip_resident_prepare": ([ctypes.POINTER(ResidentArgs), _p], ctypes.c_uint32),
+    "kvip_hip_resident_round": ([ctypes.POINTER(ResidentArgs), _p], ctypes.c_uint32),
+    "kvip_hip_resident_forward": ([ctypes.POINTER(IndexerArgs), ctypes.POINTER(TopkArgs), ctypes.POINTER(ResidentArgs),
+                                   _p], ctypes.c_uint32),
 }
 
 _LIB = None

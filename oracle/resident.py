@@ -1,0 +1,257 @@
+"""CPU restatement of the resident-cache round of the streaming LIFetch resolver:
+hot/cold classification of the final TopK, per-query miss resolution with LRU victim
+allocation, Fetch descriptors, the Index-row permutation and the round's residency
+publication. TEST INFRASTRUCTURE ONLY (see oracle/__init__.py).
+
+Positions. Each request owns `history` Index rows (one per position). Position p <
+`resident` is hot: its KV row lives in hot-cache slot p when hot_valid[p] != 0. TopK
+selects positions; the Index update moves every fetched token's row to its new hot slot.
+
+Follows (paths relative to the KVIP reference tree,
+csrc/operators/lightning_indexer_with_fetch/op_kernel/ unless noted):
+  classify   staged_topk_classify.h:9-36 (ClassifyTopkHalf), resolver_staged_dma2.h:9-22
+             (StagedKnownSlot), :34-77 (StagedInitialize: Q3/Q4 same-position shortcut,
+             protection bitmap of every query's hot hits)
+  resolve    resolver_staged_dma2.h:98-237 (StagedQuery): first-occurrence dedup per
+             query, ranks continuing over queries, LRU candidates in ordinal order (pass 0
+             ordinals >= used, pass 1 < used) skipping protected slots, fallback scan of the
+             free hot slots in ascending order (lidu/op_kernel/hot_slot_selection.h:7-137
+             with scan start 0), change records (record = reserved ordinal or 2048 + rank)
+  events     streaming.cpp:16-22 (PublishQ: source = token position, destination = slot,
+             in rank order per query), :205-274 (Consumer: batches in query order)
+  init       lifecycle.cpp:32-81 (InitializeRound: changes cleared, candidate prefix of
+             the change slots = the LRU candidates); reserved_hot = each candidate slot's
+             LRU ordinal, as the reference harness derives it from the candidates
+             (tests/operators/lifetch/support/execution.py:1557-1568)
+  update     shadow_exchange_parallel.h:28-78 (ApplyBatch: 512-change chunks, closure of
+             displaced rows into freed positions, freed hot positions invalidated),
+             :79 (CommitMetadata: addresses / logical ids follow their rows)
+  publish    common/lifetch/cache_metadata.h:54-73 (PublishDestinationResidency: every
+             Fetch destination becomes valid)
+  outputs    streaming.cpp:66-90 (PublishQueryOutputs) with the harness check
+             tests/operators/lifetch/support/execution.py:2109-2130 (logical output =
+             pre-update logical ids of the TopK positions, slot output = locations)
+
+Scope of this restatement: no speculative prefetch (`used` candidates consumed by an
+earlier window are supported by the two allocation passes, but no prefetch mapping is
+consulted) and no ABC tail bounds (tail tokens are ordinary positions).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from oracle.lidu import ring_select
+
+TOPK = 2048
+LRU_SLOTS = 2048
+CHUNK = 512
+EMPTY = -1
+
+ERR_TOKEN = 1          # a TopK position >= history
+ERR_CANDIDATE = 4      # an LRU candidate >= resident, or too few free hot slots
+ERR_UPDATE = 16        # an Index change that is not a valid partial permutation
+
+
+def classify(selected, history, resident, hot_valid, reserved):
+    """Hot hits of every query row of one request (StagedKnownSlot without prefetch
+    mapping). selected [Q, 2048] positions (-1 empty). Returns (loc [Q, 2048] with the hit
+    slot or -1, protection bitmap as a bool array [resident], error bits). Rows q >= 2
+    copy loc from row q - 2 where they select the same position at the same index."""
+    q_rows = selected.shape[0]
+    loc = np.full(selected.shape, EMPTY, np.int64)
+    protect = np.zeros(resident, bool)
+    err = 0
+    for q in range(q_rows):
+        for i in range(TOPK):
+            t = int(selected[q, i])
+            if q >= 2 and t == int(selected[q - 2, i]):
+                loc[q, i] = loc[q - 2, i]
+                continue
+            if t < 0:
+                continue
+            if t >= history:
+                err |= ERR_TOKEN
+                continue
+            if t < resident and hot_valid[t] != 0 and reserved[t] < 0:
+                loc[q, i] = t
+                protect[t] = True
+    return loc, protect, err
+
+
+def resolve(selected, history, resident, hot_valid, reserved, lru, used=0):
+    """Per-query miss resolution of one request (StagedQuery). Returns a dict with
+    loc [Q, 2048] (hot slot of every selected position, -1 for empty entries), slots
+    [misses] (slot of each miss rank), tokens [misses] (position of each miss rank),
+    added [Q] (new misses per query), changes / change_slots [2048 + Q*2048] records and
+    the error bits. Stops (like the reference) at the first query that fails."""
+    q_rows = selected.shape[0]
+    loc, protect, err = classify(selected, history, resident, hot_valid, reserved)
+    bitmap = protect.copy()
+    rank_of = {}
+    slots, tokens, added_per_q = [], [], []
+    # Round initialisation (lifecycle.cpp:58-71): no changes; the candidate prefix of
+    # change_slots holds the LRU candidates.
+    changes = np.full(LRU_SLOTS + q_rows * TOPK, EMPTY, np.int64)
+    change_slots = np.full(LRU_SLOTS + q_rows * TOPK, EMPTY, np.int64)
+    change_slots[:LRU_SLOTS] = lru[:LRU_SLOTS]
+    for q in range(q_rows):
+        if err:
+            break
+        # Unresolved entries, the shortcut rows excluded (they copy q - 2 at the end).
+        shortcut = np.zeros(TOPK, bool)
+        if q >= 2:
+            shortcut = selected[q] == selected[q - 2]
+        first = {}
+        for i in range(TOPK):
+            t = int(selected[q, i])
+            if t < 0 or t >= history or shortcut[i] or loc[q, i] >= 0:
+                continue
+            if t in rank_of:
+                continue
+            first.setdefault(t, i)
+        new = sorted(first.items(), key=lambda kv: kv[1])  # in index order
+        old = len(slots)
+        for n, (t, i) in enumerate(new):
+            rank_of[t] = old + n
+            tokens.append(t)
+        need = len(new)
+        got = []
+        if need:
+            # Every candidate of a pass is checked (a candidate outside the hot range
+            # fails the request); the free ones are taken in ordinal order.
+            for ordinals in (range(used, LRU_SLOTS), range(0, used)):
+                free = []
+                for o in ordinals:
+                    s = int(lru[o])
+                    if s >= resident or s < 0:
+                        err |= ERR_CANDIDATE
+                    elif not bitmap[s]:
+                        free.append(s)
+                got += free[:need - len(got)]
+                for s in got:
+                    bitmap[s] = True
+                if len(got) == need:
+                    break
+        if len(got) < need:
+            # Fallback: every known hot slot of every query is protected, then the free
+            # hot slots in ascending order.
+            fb = bitmap.copy()
+            for s in loc.reshape(-1):
+                if 0 <= s < resident:
+                    fb[s] = True
+            words = np.zeros((resident + 31) // 32, np.uint32)
+            for s in np.nonzero(fb)[0]:
+                words[s // 32] |= np.uint32(1 << (s % 32))
+            extra = ring_select(words, resident, 0, need - len(got))
+            if len(extra) < need - len(got):
+                err |= ERR_CANDIDATE
+            for s in extra:
+                bitmap[s] = True
+            got += list(extra)
+            bitmap = bitmap | fb
+        if err:
+            break
+        slots += got
+        for i in range(TOPK):
+            t = int(selected[q, i])
+            if shortcut[i]:
+                loc[q, i] = loc[q - 2, i]
+            elif 0 <= t < history and loc[q, i] < 0:
+                loc[q, i] = slots[rank_of[t]]
+        for n in range(need):
+            r = old + n
+            s = slots[r]
+            record = int(reserved[s]) if reserved[s] >= 0 else LRU_SLOTS + r
+            change_slots[record] = s
+            changes[record] = tokens[r]
+        added_per_q.append(need)
+    return dict(loc=loc, slots=np.array(slots, np.int64), tokens=np.array(tokens, np.int64),
+                added=np.array(added_per_q, np.int64), changes=changes, change_slots=change_slots, error=err)
+
+
+def apply_changes(batches, history, resident, keys, scales, addresses, logical, hot_valid):
+    """Index-row permutation of one request (ApplyBatch + CommitMetadata), in place.
+
+    batches: list (one per query, in order) of [(orig_position, destination_slot)] in
+    rank order. Row r of the tables is the row at position r before the round; a change
+    moves the row of orig_position (wherever earlier changes of the round put it) to the
+    destination; inside each 512-change chunk, rows displaced from destinations that are
+    not themselves sources fill the freed source positions in order, and freed hot
+    positions lose their residency. Returns the error bits (0 = applied)."""
+    row_at = np.arange(history)
+    pos_of = np.arange(history)
+    keys0, scales0 = keys.copy(), scales.copy()
+    addresses0, logical0 = addresses.copy(), logical.copy()
+    for batch in batches:
+        for c0 in range(0, len(batch), CHUNK):
+            chunk = batch[c0:c0 + CHUNK]
+            srcs, dsts = [], []
+            for orig, dst in chunk:
+                if not (0 <= orig < history) or not (0 <= dst < resident):
+                    return ERR_UPDATE
+                srcs.append(int(pos_of[orig]))
+                dsts.append(int(dst))
+            if len(set(srcs)) != len(srcs) or len(set(dsts)) != len(dsts):
+                return ERR_UPDATE
+            sset, dset = set(srcs), set(dsts)
+            outs = [d for d in dsts if d not in sset]
+            freed = [s for s in srcs if s not in dset]
+            moves = list(zip(srcs, dsts)) + list(zip(outs, freed))
+            snap_k = {s: keys[s].copy() for s, _ in moves}
+            snap_s = {s: scales[s] for s, _ in moves}
+            snap_row = {s: int(row_at[s]) for s, _ in moves}
+            for s, d in moves:
+                keys[d] = snap_k[s]
+                scales[d] = snap_s[s]
+                row_at[d] = snap_row[s]
+                pos_of[snap_row[s]] = d
+            for d in freed:
+                if d < resident:
+                    hot_valid[d] = 0
+    changed = np.nonzero(row_at != np.arange(history))[0]
+    addresses[changed] = addresses0[row_at[changed]]
+    logical[changed] = logical0[row_at[changed]]
+    del keys0, scales0
+    return 0
+
+
+def resident_round(selected, history, resident, keys, scales, addresses, logical, hot_valid, reserved, lru,
+                   hot_cache, host_pool, used=0):
+    """One request's full round after TopK, in place on its tables: resolve, outputs,
+    Fetch (hot_cache[slot] = host_pool[addresses[token]]), Index update, residency
+    publication. Returns (logical_output [Q, 2048], slot_output [Q, 2048], resolve dict,
+    error bits)."""
+    res = resolve(selected, history, resident, hot_valid, reserved, lru, used)
+    q_rows = selected.shape[0]
+    logical_out = np.full(selected.shape, EMPTY, np.int64)
+    for q in range(q_rows):
+        for i in range(TOPK):
+            t = int(selected[q, i])
+            if 0 <= t < history:
+                logical_out[q, i] = logical[t]
+    if res["error"]:
+        return logical_out, res["loc"], res, res["error"]
+    row_bytes = hot_cache.shape[1]
+    for t, s in zip(res["tokens"], res["slots"]):
+        a = int(addresses[t])
+        hot_cache[s] = host_pool[a:a + row_bytes]
+    batches, r = [], 0
+    for n in res["added"]:
+        batches.append([(int(res["tokens"][r + k]), int(res["slots"][r + k])) for k in range(n)])
+        r += n
+    err = apply_changes(batches, history, resident, keys, scales, addresses, logical, hot_valid)
+    if err:
+        return logical_out, res["loc"], res, err
+    for s in res["slots"]:
+        hot_valid[s] = 1
+    return logical_out, res["loc"], res, 0
+
+
+def reserved_from_candidates(lru, resident):
+    """reserved_hot of one request: the LRU ordinal of every candidate slot, -1 for the
+    other hot slots (tests/operators/lifetch/support/execution.py:1557-1568)."""
+    reserved = np.full(resident, EMPTY, np.int64)
+    for i, s in enumerate(lru[:LRU_SLOTS]):
+        if 0 <= s < resident:
+            reserved[int(s)] = i
+    return reserved

@@ -39,6 +39,7 @@ STRUCTS = {
     "KvipLiduArgs": abi.LiduArgs,
     "KvipQueryPackArgs": abi.QueryPackArgs,
     "KvipIngestArgs": abi.IngestArgs,
+    "KvipResidentArgs": abi.ResidentArgs,
 }
 
 

@@ -1,0 +1,283 @@
+"""GPU parity of the resident-cache LIFetch round (kvip_hip_resident_round /
+kvip_hip_resident_forward) against oracle/resident.py, through the C ABI.
+
+Bars: every output and every table the round touches is bit-exact against the oracle
+(slot and logical outputs, miss counts, change records, reserved_hot, hot_valid, the
+permuted Index keys / scales / addresses / logical ids, the hot KV cache), over several
+consecutive rounds so that each round starts from the state the previous one left; the
+reference's stateful known answer (reads 2048, 0, 4096, 2048) through the full forward
+with LI and TopK on the device; errors reported in status without touching the tables."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import kvip_amd
+from kvip_amd.runtime import abi
+from oracle import cache as lru_ref
+from oracle import indexer as li_ref
+from oracle import resident as ref
+
+pytestmark = pytest.mark.gpu
+TOPK = 2048
+ROW = 656
+
+
+def say(*args):
+    print(*args, flush=True)
+
+
+class Setup:
+    """Owners' Index storage with identity KV rows in a pinned host pool, the hot cache
+    holding positions 0..resident-1, and a resident-mode LIFetch binding."""
+
+    def __init__(self, torch, *, batch, owners, history, resident, q_rows, seed, heads=64, invalid=0.0,
+                 row_owners=None):
+        rng = np.random.default_rng(seed)
+        self.torch, self.rng = torch, rng
+        self.batch, self.owners, self.history, self.resident, self.q = batch, owners, history, resident, q_rows
+        dev = "cuda"
+        keys = rng.integers(0, 256, (owners, history, 128), dtype=np.uint8)
+        keys &= 0x77  # finite fp8 e4m3 values
+        self.h_keys = keys
+        self.h_scales = rng.uniform(0.5, 2.0, (owners, history)).astype(np.float32)
+        tokens = np.arange(owners * history).reshape(owners, history)
+        self.h_addresses = (tokens * ROW).astype(np.int64)
+        self.h_logical = np.broadcast_to(np.arange(history), (owners, history)).astype(np.int64).copy()
+        pool = li_ref.identity_rows(tokens.reshape(-1), ROW)
+        self.h_pool = pool.reshape(-1)
+        self.h_hot = np.zeros((owners, resident, ROW), np.uint8)
+        for o in range(owners):
+            self.h_hot[o] = pool[o * history:o * history + resident]
+        self.h_valid = (rng.random((owners, resident)) >= invalid).astype(np.int32)
+        owners_of = np.arange(batch) if row_owners is None else np.asarray(row_owners)
+        self.h_owners = owners_of.astype(np.int32)
+        t = torch
+        self.keys = t.from_numpy(keys).to(dev).view(t.float8_e4m3fn)
+        self.scales = t.from_numpy(self.h_scales).to(dev)
+        self.addresses = t.from_numpy(self.h_addresses).to(dev)
+        self.logical = t.from_numpy(self.h_logical).to(dev)
+        self.pool = t.empty(self.h_pool.size, dtype=t.uint8, pin_memory=True)
+        self.pool.copy_(t.from_numpy(self.h_pool))
+        self.hot = t.from_numpy(self.h_hot).to(dev)
+        self.valid = t.from_numpy(self.h_valid).to(dev)
+        self.row_owners = t.from_numpy(self.h_owners).to(dev)
+        self.rot = kvip_amd.LIFetchBinding(t, batch=batch, max_context=history, device=dev, heads=heads,
+                                           rows_per_request=q_rows, qk_dtype="fp8", query_ends=True)
+        self.rot.seq_lens.fill_(history)
+        self.rot.query_ends.fill_(history)
+        self.upd = kvip_amd.ResidentIndexUpdate(
+            t, keys=self.keys, scales=self.scales, addresses=self.addresses, logical_ids=self.logical,
+            row_owners=self.row_owners, rotating=self.rot, hot_valid=self.valid, hot_cache=self.hot,
+            host_pool=self.pool, resident=resident)
+        self.lib = abi.load_library()
+
+    def run_round(self, selected, lru):
+        """Device round on the given TopK rows [batch*q, 2048] and candidates [batch, 2048]."""
+        t = self.torch
+        self.rot.topk.copy_(t.from_numpy(selected.astype(np.int32)))
+        self.upd.set_candidates(t.from_numpy(lru.astype(np.int32)).to("cuda"))
+        rc = self.lib.kvip_hip_resident_round(ctypes.byref(self.upd.args), abi.stream_handle(t, self.rot.device))
+        abi.check(rc, "resident round")
+        t.cuda.synchronize()
+
+    def oracle_round(self, selected, lru):
+        """Oracle on the host copies, request by request (each owner once per round)."""
+        outs = []
+        for b in range(self.batch):
+            o = int(self.h_owners[b])
+            sel = selected[b * self.q:(b + 1) * self.q]
+            reserved = ref.reserved_from_candidates(lru[b], self.resident)
+            keys = self.h_keys[o].copy()
+            lout, sout, res, err = ref.resident_round(
+                sel, self.history, self.resident, keys, self.h_scales[o], self.h_addresses[o], self.h_logical[o],
+                self.h_valid[o], reserved, lru[b], self.h_hot[o], self.h_pool)
+            self.h_keys[o] = keys
+            outs.append((lout, sout, res, err, reserved))
+        return outs
+
+    def compare(self, outs):
+        t = self.torch
+        lo = self.upd.logical_output.cpu().numpy().reshape(self.batch, self.q, TOPK)
+        so = self.upd.slot_output.cpu().numpy().reshape(self.batch, self.q, TOPK)
+        counts = self.upd.miss_counts.cpu().numpy()
+        status = self.upd.status.cpu().numpy()
+        changes = self.upd.changes.cpu().numpy()
+        cslots = self.upd.change_slots.cpu().numpy()
+        reserved = self.upd.reserved_hot.cpu().numpy()
+        for b, (lout, sout, res, err, rsv) in enumerate(outs):
+            assert status[b] == err, (b, status[b], err)
+            assert np.array_equal(reserved[b], rsv), b
+            if err:
+                continue
+            assert np.array_equal(lo[b], lout), b
+            assert np.array_equal(so[b], sout), b
+            added = list(res["added"]) + [0] * (4 - len(res["added"]))
+            assert counts[b].tolist() == added + [int(res["added"].sum())], b
+            assert np.array_equal(changes[b], res["changes"]), b
+            assert np.array_equal(cslots[b], res["change_slots"]), b
+        assert np.array_equal(self.keys.view(t.uint8).cpu().numpy(), self.h_keys)
+        assert np.array_equal(self.scales.cpu().numpy(), self.h_scales)
+        assert np.array_equal(self.addresses.cpu().numpy(), self.h_addresses)
+        assert np.array_equal(self.logical.cpu().numpy(), self.h_logical)
+        assert np.array_equal(self.valid.cpu().numpy(), self.h_valid)
+        assert np.array_equal(self.hot.cpu().numpy(), self.h_hot)
+
+
+def mtp_selection(rng, q_rows, history, resident, hot_frac, n=None, hot_pool=None):
+    """Rows of one request sharing most of their selection (decode + MTP)."""
+    n = int(rng.integers(1500, TOPK + 1)) if n is None else n
+    hot_src = np.arange(resident) if hot_pool is None else hot_pool
+    hot = rng.choice(hot_src, int(n * hot_frac), replace=False)
+    cold = rng.choice(np.arange(resident, history), n - len(hot), replace=False)
+    base = rng.permutation(np.concatenate([hot, cold]))
+    out = np.full((q_rows, TOPK), -1, np.int64)
+    for q in range(q_rows):
+        row = base.copy()
+        swap = rng.random(n) < 0.1
+        row[swap] = rng.choice(np.setdiff1d(np.arange(history), base), int(swap.sum()), replace=False)
+        out[q, :n] = rng.permutation(row)
+    return out
+
+
+@pytest.mark.parametrize("batch,owners,q_rows,history,resident,seed", [
+    (2, 2, 1, 8192, 4096, 1),
+    (3, 4, 4, 16384, 8192, 2),
+    (4, 4, 2, 12288, 2048, 3),
+])
+def test_resident_round_matches_oracle_over_rounds(torch_gpu, batch, owners, q_rows, history, resident, seed):
+    torch = torch_gpu
+    say(f"case resident round b={batch} o={owners} q={q_rows} h={history} r={resident} seed={seed}")
+    owners_of = np.random.default_rng(seed).permutation(owners)[:batch]
+    st = Setup(torch, batch=batch, owners=owners, history=history, resident=resident, q_rows=q_rows, seed=seed,
+               invalid=0.05, row_owners=owners_of)
+    rng = st.rng
+    policies = []
+    for b in range(batch):
+        p = lru_ref.SlotLRU()
+        p.resize(resident, resident)
+        policies.append(p)
+    for rnd in range(3):
+        say(f"  round {rnd}")
+        selected = np.concatenate([mtp_selection(rng, q_rows, history, resident, 0.6) for _ in range(batch)])
+        lru = np.stack([p.slots.astype(np.int64) for p in policies])
+        outs = st.oracle_round(selected, lru)
+        st.run_round(selected, lru)
+        st.compare(outs)
+        for b, p in enumerate(policies):
+            s = outs[b][1]
+            p.commit(s[s >= 0])
+
+
+def test_resident_forward_stateful_known_answer(torch_gpu):
+    """correctness.py:170-228 through the whole forward on the device (LI, TopK, round),
+    the device SlotLRU supplying candidates: reads 2048, 0, 4096, 2048 per request."""
+    torch = torch_gpu
+    batch, history, resident, heads = 2, 12288, 4096, 32
+    st = Setup(torch, batch=batch, owners=batch, history=history, resident=resident, q_rows=4, seed=7, heads=heads)
+    keys = np.zeros((batch, history, 128), np.uint8)
+    for feature, begin in enumerate((4096, 6144, 8192)):
+        keys[:, begin:begin + 2048, feature] = 0x38  # exactly 1 in e4m3
+    st.keys.view(torch.uint8).copy_(torch.from_numpy(keys))
+    st.valid.fill_(1)
+    rot, upd = st.rot, st.upd
+    rot.weights.fill_(1.0)
+    rot.query_ends.copy_(torch.arange(history - 3, history + 1, dtype=torch.int32).repeat(batch))
+    fwd = kvip_amd.LIFetch(rot, upd)
+    lrus = [kvip_amd.SlotLRU("cuda") for _ in range(batch)]
+    for p in lrus:
+        p.resize(resident, resident)
+    reads = []
+    for number in range(1, 5):
+        features = (1, 2, 1, 2) if number == 3 else (0, 0, 0, 0)
+        query = torch.zeros((batch, 4, heads, 128), dtype=torch.float32)
+        for q, feature in enumerate(features):
+            query[:, q, :, feature] = 1.0
+        rot.query.copy_(query.view(batch * 4, heads, 128).to(torch.float8_e4m3fn))
+        upd.set_candidates(torch.cat([p.slots for p in lrus]))
+        say(f"  stateful round {number}")
+        fwd()
+        torch.cuda.synchronize()
+        assert not upd.status.any(), upd.status.cpu().tolist()
+        counts = upd.miss_counts.cpu().numpy()
+        reads.append(counts[:, 4].tolist())
+        slots = upd.slot_output.view(batch, -1)
+        for b, p in enumerate(lrus):
+            p.commit(slots[b][slots[b] >= 0].contiguous())
+        logical = st.logical.cpu().numpy()
+        valid = st.valid.cpu().numpy()
+        expected = set(range(6144, 10240)) if number == 3 else set(range(4096, 6144))
+        for b in range(batch):
+            hot = set(logical[b, :resident][valid[b] != 0].tolist())
+            assert expected <= hot, (number, b)
+            if number == 3:
+                assert not hot & set(range(4096, 6144))
+            # Every selected slot holds its token's KV (identity rows of owner b).
+            lo = upd.logical_output.view(batch, -1)[b].cpu().numpy()
+            so = slots[b].cpu().numpy()
+            pool = st.h_pool.reshape(-1, ROW)
+            hotc = st.hot[b].cpu().numpy()
+            assert np.array_equal(hotc[so], pool[b * history + lo])
+    assert reads == [[2048, 2048], [0, 0], [4096, 4096], [2048, 2048]]
+
+
+def test_resident_errors_are_reported_and_leave_tables(torch_gpu):
+    torch = torch_gpu
+    st = Setup(torch, batch=2, owners=2, history=8192, resident=4096, q_rows=1, seed=9)
+    rng = st.rng
+    selected = np.concatenate([mtp_selection(rng, 1, 8192, 4096, 0.5) for _ in range(2)])
+    lru = np.stack([np.arange(2048), np.arange(2048, 4096)])
+    lru[1, 5] = 9999  # outside the hot range: request 1 fails, request 0 runs
+    before = [x.clone() for x in (st.keys, st.logical, st.valid, st.hot)]
+    st.run_round(selected, lru)
+    status = st.upd.status.cpu().numpy()
+    assert status[0] == 0 and status[1] & abi.RESIDENT_ERR_CANDIDATE
+    assert (st.upd.slot_output[1].cpu() == -1).all()
+    assert torch.equal(st.logical[1], before[1][1]) and torch.equal(st.hot[1], before[3][1])
+    # A KV address outside the host pool fails the request before anything is fetched.
+    st2 = Setup(torch, batch=1, owners=1, history=8192, resident=4096, q_rows=1, seed=10)
+    st2.addresses[0, 5000] = st2.pool.numel()
+    sel = np.full((1, TOPK), -1, np.int64)
+    sel[0, :3] = [5000, 6000, 7000]
+    hot_before = st2.hot.clone()
+    st2.run_round(sel, np.arange(2048)[None, :])
+    assert st2.upd.status.cpu().numpy()[0] & abi.RESIDENT_ERR_SOURCE
+    assert torch.equal(st2.hot, hot_before)
+
+
+def test_resident_forward_graph_replay(torch_gpu):
+    """The resident forward captured once and replayed: each replay equals the same step
+    run eagerly on a copy of the state (tables and outputs)."""
+    torch = torch_gpu
+    st = Setup(torch, batch=2, owners=2, history=8192, resident=4096, q_rows=2, seed=12)
+    rot, upd = st.rot, st.upd
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(5)
+    rot.query.copy_(torch.randn(rot.query.shape, generator=gen, device="cuda").clamp(-8, 8).to(torch.float8_e4m3fn))
+    rot.weights.copy_(torch.randn(rot.weights.shape, generator=gen, device="cuda") / 8)
+    upd.set_candidates(torch.stack([torch.arange(2048), torch.arange(2048, 4096)]).int().cuda())
+    fwd = kvip_amd.LIFetch(rot, upd)
+    state = (st.keys, st.scales, st.addresses, st.logical, st.valid, st.hot)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fwd()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        fwd()
+    for step in range(3):
+        start = [x.clone() for x in state]
+        graph.replay()
+        torch.cuda.synchronize()
+        got = [x.clone() for x in state] + [upd.outputs.clone(), upd.miss_counts.clone()]
+        for x, s in zip(state, start):
+            x.copy_(s)
+        upd.outputs.fill_(-9)
+        fwd()
+        torch.cuda.synchronize()
+        want = [x for x in state] + [upd.outputs, upd.miss_counts]
+        for g, w in zip(got, want):
+            assert torch.equal(g, w), step
+        assert not upd.status.any()
