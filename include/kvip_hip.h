@@ -47,6 +47,11 @@
  *                                FetchQueryGroup (streaming.cpp:365-500), Consumer + ApplyBatch
  *                                (streaming.cpp:205-274, shadow_exchange_parallel.h:28-85),
  *                                PublishDestinationResidency (common/lifetch/cache_metadata.h:54-73)
+ *   kvip_hip_resident_prefix  <- ProcessResidentTopK + SaveResident (indexer_vector.h:100-105,
+ *                                :162-234), ClassifyScore / ClassifyResidentScores
+ *                                (indexer_score.h:784-792, :1018-1048), GatherVictimScores
+ *                                (common/lifetch/victim_ops.h:3-12), the cold-tile hit bits
+ *                                (indexer_vector.h:584-593, :626-638)
  *   kvip_hip_resident_forward <- kvip_lifetch_streaming_forward in resident mode
  *                                (include/api.h:7, op_host/launch.cpp:76-83)
  *   kvip_hip_resident_workspace_bytes / kvip_hip_resident_prepare
@@ -123,7 +128,8 @@ typedef struct KvipIndexerArgs {
     int32_t weight_dtype;        /* KVIP_DTYPE_FP32 or KVIP_DTYPE_BF16 */
 } KvipIndexerArgs;
 
-/* Exact TopK-2048 of sortable uint16 keys per query row.
+/* Exact TopK-2048 of sortable uint16 keys per query row, over the row's valid
+ * positions valid = min(seq_lens[b], query_ends[r], limit if limit > 0).
  * valid < 2048: out = [0, 1, ..., valid-1, -1, ...].
  * valid >= 2048: the 2048 tokens that come first in the order (key desc, index asc),
  * written as the tokens with key > kth in ascending index order followed by the
@@ -143,6 +149,7 @@ typedef struct KvipTopkArgs {
     int32_t batch;
     int32_t rows_per_request;
     int32_t key_stride;          /* multiple of 8 */
+    int32_t limit;               /* > 0: only positions below limit take part (the resident prefix) */
 } KvipTopkArgs;
 
 /* Gather of the selected KV rows from a paged KV cache into a contiguous buffer:
@@ -391,6 +398,30 @@ typedef struct KvipResidentArgs {
     int32_t used;                 /* candidates consumed before this step (0 without prefetch) */
 } KvipResidentArgs;
 
+/* Resident-prefix classification of one step (the resident TopK, its threshold and the
+ * hit bits the speculative prefetch reads): for query row r with valid positions
+ * v = min(seq_lens[b], query_ends[r]) and prefix p = min(v, resident), given prefix_topk =
+ * the TopK-2048 of positions [0, p) (kvip_hip_topk with limit = resident):
+ *   thresholds[r]   = the smallest key of that selection when p >= 2048, else 0;
+ *   victim_hits[r]  bit i (word i / 32) = lru_slots[b][i] in [0, p) and its key > threshold;
+ *   cold_hits[r]    bit j (word j / 32) = position resident + j < v and its key > threshold. */
+typedef struct KvipPrefixClassifyArgs {
+    const uint16_t* score_keys;   /* [rows, key_stride] */
+    const int32_t* prefix_topk;   /* [rows, 2048] */
+    const int32_t* seq_lens;      /* [batch] */
+    const int32_t* query_ends;    /* [rows], or NULL */
+    const int32_t* lru_slots;     /* [batch, 2048] */
+    uint16_t* thresholds;         /* [rows] */
+    uint32_t* victim_hits;        /* [rows, 64] */
+    uint32_t* cold_hits;          /* [rows, cold_words] */
+    int32_t batch;
+    int32_t rows_per_request;
+    int32_t key_stride;
+    int32_t resident;
+    int32_t cold_words;           /* >= ceil((key_stride - resident) / 32) */
+    int32_t reserved;
+} KvipPrefixClassifyArgs;
+
 uint32_t kvip_hip_abi_version(void);
 uint32_t kvip_hip_indexer_decode(const KvipIndexerArgs* args, void* stream);
 uint32_t kvip_hip_topk(const KvipTopkArgs* args, void* stream);
@@ -409,6 +440,9 @@ uint64_t kvip_hip_lidu_workspace_bytes(int32_t batch);
 uint32_t kvip_hip_lidu(const KvipLiduArgs* args, void* stream);
 uint32_t kvip_hip_pack_queries(const KvipQueryPackArgs* args, void* stream);
 uint32_t kvip_hip_ingest_index(const KvipIngestArgs* args, void* stream);
+/* Resident TopK (kvip_hip_topk of `topk`, whose limit must equal cls->resident and whose
+ * output must be cls->prefix_topk) followed by the prefix classification. */
+uint32_t kvip_hip_resident_prefix(const KvipTopkArgs* topk, const KvipPrefixClassifyArgs* cls, void* stream);
 uint64_t kvip_hip_resident_workspace_bytes(int32_t batch, int32_t history);
 uint32_t kvip_hip_resident_prepare(const KvipResidentArgs* args, void* stream);
 uint32_t kvip_hip_resident_round(const KvipResidentArgs* args, void* stream);

@@ -13,6 +13,7 @@ __all__ = [
     "LIFetchBinding",
     "ContiguousFetch",
     "ResidentIndexUpdate",
+    "ResidentPrefix",
     "SlotLRU",
     "update_abc",
     "lidu",
@@ -28,6 +29,7 @@ _EXPORTS = {
     "LIFetchBinding": ("operators.lifetch.binding", "LIFetchBinding"),
     "ContiguousFetch": ("operators.lifetch.binding", "ContiguousFetch"),
     "ResidentIndexUpdate": ("operators.lifetch.resident", "ResidentIndexUpdate"),
+    "ResidentPrefix": ("operators.lifetch.resident", "ResidentPrefix"),
     "SlotLRU": ("cache.lru", "SlotLRU"),
     "update_abc": ("cache.abc", "update_abc"),
     "lidu": ("operators.lidu", "lidu"),

@@ -105,4 +105,13 @@ KVIP_DEVICE void select_bin(const uint32_t* hist, uint32_t target, int* sel, uin
     __syncthreads();
 }
 
+// Valid positions of TopK row `row`: min(seq_lens[b], query_ends[row], limit when > 0),
+// clamped to [0, key_stride].
+KVIP_DEVICE int topk_row_valid(const KvipTopkArgs& p, int row) {
+    int valid = max(p.seq_lens[row / p.rows_per_request], 0);
+    if (p.query_ends != nullptr) valid = min(valid, p.query_ends[row]);
+    if (p.limit > 0) valid = min(valid, p.limit);
+    return min(max(valid, 0), p.key_stride);
+}
+
 }  // namespace kvip

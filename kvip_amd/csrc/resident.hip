@@ -646,3 +646,82 @@ extern "C" uint32_t kvip_hip_resident_forward(const KvipIndexerArgs* indexer, co
     if (e != hipSuccess) return static_cast<uint32_t>(e);
     return static_cast<uint32_t>(kvip::launch_resident_round(ra, s));
 }
+
+namespace kvip {
+namespace {
+
+constexpr int kPcThreads = 256;
+
+__global__ __launch_bounds__(kPcThreads) void prefix_classify_kernel(const KvipPrefixClassifyArgs p) {
+    __shared__ uint32_t s_min[kPcThreads / 64];
+    const int row = blockIdx.x;
+    const int b = row / p.rows_per_request;
+    const int tid = threadIdx.x;
+    int valid = max(p.seq_lens[b], 0);
+    if (p.query_ends != nullptr) valid = min(valid, p.query_ends[row]);
+    valid = min(max(valid, 0), p.key_stride);
+    const int pv = min(valid, p.resident);
+    const uint16_t* keys = p.score_keys + static_cast<size_t>(row) * p.key_stride;
+    // Threshold: smallest key of a full prefix selection.
+    uint32_t m = 0xFFFFu;
+    if (pv >= kTopK) {
+        const int32_t* sel = p.prefix_topk + static_cast<size_t>(row) * kTopK;
+        for (int i = tid; i < kTopK; i += kPcThreads) {
+            const int t = sel[i];
+            if (t >= 0 && t < pv) m = min(m, static_cast<uint32_t>(keys[t]));
+        }
+    }
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) m = min(m, static_cast<uint32_t>(__shfl_xor(static_cast<int>(m), d)));
+    if ((tid & 63) == 0) s_min[tid >> 6] = m;
+    __syncthreads();
+    uint32_t thr = 0u;
+    if (pv >= kTopK) {
+        thr = s_min[0];
+        for (int w = 1; w < kPcThreads / 64; ++w) thr = min(thr, s_min[w]);
+    }
+    if (tid == 0) p.thresholds[row] = static_cast<uint16_t>(thr);
+    // Victim bits: one word (32 candidates) per thread.
+    if (tid < kTopK / 32) {
+        const int32_t* lru = p.lru_slots + static_cast<size_t>(b) * kTopK;
+        uint32_t word = 0u;
+        for (int k = 0; k < 32; ++k) {
+            const int s = lru[tid * 32 + k];
+            const bool hit = s >= 0 && s < pv && static_cast<uint32_t>(keys[s]) > thr;
+            word |= (hit ? 1u : 0u) << k;
+        }
+        p.victim_hits[static_cast<size_t>(row) * (kTopK / 32) + tid] = word;
+    }
+    // Cold bits: position resident + 32 w + k.
+    for (int w = tid; w < p.cold_words; w += kPcThreads) {
+        uint32_t word = 0u;
+        for (int k = 0; k < 32; ++k) {
+            const int pos = p.resident + 32 * w + k;
+            const bool hit = pos < valid && static_cast<uint32_t>(keys[pos]) > thr;
+            word |= (hit ? 1u : 0u) << k;
+        }
+        p.cold_hits[static_cast<size_t>(row) * p.cold_words + w] = word;
+    }
+}
+
+}  // namespace
+}  // namespace kvip
+
+extern "C" uint32_t kvip_hip_resident_prefix(const KvipTopkArgs* topk, const KvipPrefixClassifyArgs* cls, void* stream) {
+    if (topk == nullptr || cls == nullptr || kvip::validate_topk(topk) != KVIP_OK) return KVIP_ERR_INVALID;
+    const KvipPrefixClassifyArgs& c = *cls;
+    const bool ok = c.score_keys && c.prefix_topk && c.seq_lens && c.lru_slots && c.thresholds && c.victim_hits &&
+                    c.cold_hits && c.batch == topk->batch && c.rows_per_request == topk->rows_per_request &&
+                    c.key_stride == topk->key_stride && c.score_keys == topk->score_keys &&
+                    c.prefix_topk == topk->topk && c.seq_lens == topk->seq_lens && c.query_ends == topk->query_ends &&
+                    topk->limit == c.resident && c.resident >= 1 && c.resident <= c.key_stride &&
+                    static_cast<int64_t>(c.cold_words) * 32 >= static_cast<int64_t>(c.key_stride) - c.resident &&
+                    c.cold_words >= 0;
+    if (!ok) return KVIP_ERR_INVALID;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    hipError_t e = kvip::launch_topk(*topk, s);
+    if (e != hipSuccess) return static_cast<uint32_t>(e);
+    hipLaunchKernelGGL(kvip::prefix_classify_kernel, dim3(c.batch * c.rows_per_request), dim3(kvip::kPcThreads), 0, s,
+                       c);
+    return static_cast<uint32_t>(hipGetLastError());
+}

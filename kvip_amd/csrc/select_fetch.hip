@@ -40,11 +40,7 @@ constexpr int kTicketWord = KVIP_TOPK_SEGMENT_WORDS - 1;  // of the row's first 
 constexpr int kMaxFusedKeys = kSgThreads * 32;     // 32768
 static_assert(kPartRows % (kSgWaves * kGatherRows) == 0, "whole gather passes");
 
-KVIP_DEVICE int sg_row_valid(const KvipTopkArgs& p, int row) {
-    int valid = max(p.seq_lens[row / p.rows_per_request], 0);
-    if (p.query_ends != nullptr) valid = min(valid, p.query_ends[row]);
-    return min(max(valid, 0), p.key_stride);
-}
+KVIP_DEVICE int sg_row_valid(const KvipTopkArgs& p, int row) { return topk_row_valid(p, row); }
 
 // Byte offset of the KV row of `token` of request b in the paged cache, or -1 for an
 // empty entry or an id outside the block table / cache (reported in err).
@@ -276,7 +272,7 @@ hipError_t launch_pieces(const KvipTopkArgs& t, const KvipFetchArgs& f, hipStrea
 uint32_t validate_select_fetch(const KvipTopkArgs* t, const KvipFetchArgs* f) {
     if (validate_topk(t) != KVIP_OK || validate_fetch(f) != KVIP_OK) return KVIP_ERR_INVALID;
     const int64_t rows = static_cast<int64_t>(t->batch) * t->rows_per_request;
-    const bool ok = t->histogram != nullptr && t->segments != nullptr && rows <= 65535 &&
+    const bool ok = t->histogram != nullptr && t->segments != nullptr && rows <= 65535 && t->limit == 0 &&
                     t->key_stride <= kMaxFusedKeys && f->topk == t->topk && f->batch == t->batch &&
                     f->rows_per_request == t->rows_per_request &&
                     (reinterpret_cast<uintptr_t>(t->segments) & 3u) == 0;

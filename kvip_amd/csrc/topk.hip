@@ -48,9 +48,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const KvipTopkArgs p
     const int tid = threadIdx.x;
     const int row = blockIdx.x;
     const int b = row / p.rows_per_request;
-    int valid = max(p.seq_lens[b], 0);
-    if (p.query_ends != nullptr) valid = min(valid, p.query_ends[row]);
-    valid = min(max(valid, 0), p.key_stride);
+    const int valid = topk_row_valid(p, row);
     int32_t* out = p.topk + static_cast<size_t>(row) * kTopK;
     const uint16_t* keys = p.score_keys + static_cast<size_t>(row) * p.key_stride;
     uint32_t* ghist = p.histogram != nullptr ? p.histogram + static_cast<size_t>(row) * 256 : nullptr;
@@ -164,9 +162,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_regs_kernel(const KvipTopkA
     const int tid = threadIdx.x;
     const int row = blockIdx.x;
     const int b = row / p.rows_per_request;
-    int valid = max(p.seq_lens[b], 0);
-    if (p.query_ends != nullptr) valid = min(valid, p.query_ends[row]);
-    valid = min(max(valid, 0), min(p.key_stride, kTopkThreads * KPT));
+    const int valid = min(topk_row_valid(p, row), kTopkThreads * KPT);
     int32_t* out = p.topk + static_cast<size_t>(row) * kTopK;
     const uint16_t* keys = p.score_keys + static_cast<size_t>(row) * p.key_stride;
     uint32_t* ghist = p.histogram != nullptr ? p.histogram + static_cast<size_t>(row) * 256 : nullptr;
@@ -292,11 +288,7 @@ constexpr int kSplitThreads = 256;
 constexpr int kSplitKeys = KVIP_TOPK_SEGMENT_KEYS / kSplitThreads;  // 8 per thread
 constexpr int kSegWords = KVIP_TOPK_SEGMENT_WORDS;
 
-KVIP_DEVICE int row_valid(const KvipTopkArgs& p, int row) {
-    int valid = max(p.seq_lens[row / p.rows_per_request], 0);
-    if (p.query_ends != nullptr) valid = min(valid, p.query_ends[row]);
-    return min(max(valid, 0), p.key_stride);
-}
+KVIP_DEVICE int row_valid(const KvipTopkArgs& p, int row) { return topk_row_valid(p, row); }
 
 KVIP_DEVICE void load_segment(const uint16_t* keys, int first, int stride, uint32_t* kk) {
 #pragma unroll
@@ -456,6 +448,7 @@ uint32_t validate_topk(const KvipTopkArgs* a) {
                     (a->rows_per_request == 1 || a->rows_per_request == 2 || a->rows_per_request == 4) &&
                     a->batch >= 1 && static_cast<int64_t>(a->batch) * a->rows_per_request <= (1 << 24) &&
                     a->key_stride >= 8 && a->key_stride % 8 == 0 && a->key_stride <= (1 << 24) &&
+                    a->limit >= 0 && (a->limit == 0 || a->histogram == nullptr) &&
                     (a->segments == nullptr || static_cast<int64_t>(a->batch) * a->rows_per_request <= 65535) &&
                     (reinterpret_cast<uintptr_t>(a->score_keys) & 15u) == 0;
     return ok ? KVIP_OK : KVIP_ERR_INVALID;

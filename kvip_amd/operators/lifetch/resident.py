@@ -112,3 +112,45 @@ class ResidentIndexUpdate:
             owners=self.owners, history=self.history, resident=self.resident, hot_stride=int(self.hot_cache.shape[1]),
             row_bytes=int(self.hot_cache.shape[2]), used=self.used,
         )
+
+
+class ResidentPrefix:
+    """Resident TopK of a scored step and its hit bits (what the reference's speculative
+    prefetch reads; ProcessResidentTopK + SaveResident, op_kernel/indexer/
+    indexer_vector.h:100-105, :162-234): `prefix_topk` [rows, 2048] = TopK-2048 of positions
+    [0, resident), `thresholds` [rows] (uint16 keys in int16 storage) = the smallest key of
+    a full prefix selection, `victim_hits` [rows, 64] bit i = LRU candidate i scores above
+    the threshold, `cold_hits` [rows, words] bit j = position resident + j does. Call after
+    scoring (``LIFetch.score()``) and before the next one."""
+
+    def __init__(self, torch, rotating, lru_slots, resident):
+        if not 1 <= resident <= rotating.key_stride:
+            raise ValueError("resident must be in 1..key_stride")
+        if lru_slots.dtype != torch.int32 or tuple(lru_slots.shape) != (rotating.batch, LRU_SLOTS):
+            raise ValueError("lru_slots must be int32 [batch, 2048]")
+        dev = rotating.device
+        self.torch, self.rotating, self.resident, self.lru_slots = torch, rotating, resident, lru_slots
+        rows = rotating.rows
+        self.cold_words = (rotating.key_stride - resident + 31) // 32
+        self.prefix_topk = torch.full((rows, TOPK), -1, dtype=torch.int32, device=dev)
+        self.thresholds = torch.zeros(rows, dtype=torch.int16, device=dev)
+        self.victim_hits = torch.zeros((rows, TOPK // 32), dtype=torch.int32, device=dev)
+        self.cold_hits = torch.zeros((rows, max(self.cold_words, 1)), dtype=torch.int32, device=dev)
+        p = abi.ptr
+        r = rotating
+        self.topk_args = abi.TopkArgs(score_keys=p(r.score_keys), histogram=0, segments=0, seq_lens=p(r.seq_lens),
+                                      query_ends=p(r.query_ends), topk=p(self.prefix_topk), status=p(r.status),
+                                      batch=r.batch, rows_per_request=r.rows_per_request, key_stride=r.key_stride,
+                                      limit=resident)
+        self.args = abi.PrefixClassifyArgs(
+            score_keys=p(r.score_keys), prefix_topk=p(self.prefix_topk), seq_lens=p(r.seq_lens),
+            query_ends=p(r.query_ends), lru_slots=p(lru_slots), thresholds=p(self.thresholds),
+            victim_hits=p(self.victim_hits), cold_hits=p(self.cold_hits), batch=r.batch,
+            rows_per_request=r.rows_per_request, key_stride=r.key_stride, resident=resident,
+            cold_words=self.cold_words)
+        self.library = abi.load_library()
+
+    def __call__(self):
+        abi.check(self.library.kvip_hip_resident_prefix(ctypes.byref(self.topk_args), ctypes.byref(self.args),
+                                                        abi.stream_handle(self.torch, self.rotating.device)),
+                  "resident prefix")

@@ -43,7 +43,7 @@ class TopkArgs(ctypes.Structure):
     _fields_ = [
         ("score_keys", _p), ("histogram", _p), ("segments", _p), ("seq_lens", _p), ("query_ends", _p), ("topk", _p),
         ("status", _p),
-        ("batch", _i32), ("rows_per_request", _i32), ("key_stride", _i32),
+        ("batch", _i32), ("rows_per_request", _i32), ("key_stride", _i32), ("limit", _i32),
     ]
 
 
@@ -134,6 +134,15 @@ class ResidentArgs(ctypes.Structure):
     ]
 
 
+class PrefixClassifyArgs(ctypes.Structure):
+    _fields_ = [
+        ("score_keys", _p), ("prefix_topk", _p), ("seq_lens", _p), ("query_ends", _p), ("lru_slots", _p),
+        ("thresholds", _p), ("victim_hits", _p), ("cold_hits", _p),
+        ("batch", _i32), ("rows_per_request", _i32), ("key_stride", _i32), ("resident", _i32), ("cold_words", _i32),
+        ("reserved", _i32),
+    ]
+
+
 # name -> (argtypes, restype); must list every function declared in include/kvip_hip.h.
 PROTOTYPES = {
     "kvip_hip_abi_version": ([], ctypes.c_uint32),
@@ -150,6 +159,8 @@ PROTOTYPES = {
     "kvip_hip_lidu": ([ctypes.POINTER(LiduArgs), _p], ctypes.c_uint32),
     "kvip_hip_pack_queries": ([ctypes.POINTER(QueryPackArgs), _p], ctypes.c_uint32),
     "kvip_hip_ingest_index": ([ctypes.POINTER(IngestArgs), _p], ctypes.c_uint32),
+    "kvip_hip_resident_prefix": ([ctypes.POINTER(TopkArgs), ctypes.POINTER(PrefixClassifyArgs), _p],
+                                 ctypes.c_uint32),
     "kvip_hip_resident_workspace_bytes": ([_i32, _i32], ctypes.c_uint64),
     "kvip_hip_resident_prepare": ([ctypes.POINTER(ResidentArgs), _p], ctypes.c_uint32),
     "kvip_hip_resident_round": ([ctypes.POINTER(ResidentArgs), _p], ctypes.c_uint32),

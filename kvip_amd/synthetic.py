@@ -193,3 +193,58 @@ def lidu_workload(torch, device, *, seed=2026, batch=16, queries=4, budget=16384
              "resident_block_table", "logical_seq_lengths", "profile_enabled")
     args = [dev[k] for k in order] + list(outs.values()) + [layer_id, num_layers, pool, (cand + 127) // 128]
     return dev, outs, args
+
+
+def resident_workload(torch, kvip, device, *, seed=2026, batch=16, history=131072, resident=16384, q_rows=1,
+                      heads=64):
+    """BASELINE config 4 shape for the resident-cache round: `batch` requests, each owning
+    `history` Index rows (fp8 keys ~ random finite codes, scales U(0.5, 2)) and a hot
+    cache of `resident` slots holding positions 0..resident-1; every row's KV lives in a
+    pinned host pool (contents irrelevant to timing). Returns (rotating, update,
+    forward)."""
+    g = torch.Generator(device=device).manual_seed(seed)
+    owners = batch
+    keys = (torch.randint(0, 256, (owners, history, 128), generator=g, device=device, dtype=torch.uint8) & 0x77)
+    keys = keys.view(torch.float8_e4m3fn)
+    scales = torch.rand((owners, history), generator=g, device=device) * 1.5 + 0.5
+    addresses = (torch.arange(owners * history, device=device, dtype=torch.int64) * 656).view(owners, history)
+    logical = torch.arange(history, device=device, dtype=torch.int64).repeat(owners, 1)
+    pool = torch.empty(owners * history * 656, dtype=torch.uint8, pin_memory=True)
+    hot = torch.zeros((owners, resident, 656), dtype=torch.uint8, device=device)
+    valid = torch.ones((owners, resident), dtype=torch.int32, device=device)
+    rot = kvip.LIFetchBinding(torch, batch=batch, max_context=history, device=device, heads=heads,
+                              rows_per_request=q_rows, qk_dtype="fp8", query_ends=True)
+    rot.query.copy_(saturating_fp8(torch, torch.randn(rot.query.shape, generator=g, device=device)))
+    rot.weights.copy_(torch.randn(rot.weights.shape, generator=g, device=device) / 8)
+    rot.seq_lens.fill_(history)
+    rot.query_ends.fill_(history)
+    upd = kvip.ResidentIndexUpdate(torch, keys=keys, scales=scales, addresses=addresses, logical_ids=logical,
+                                   row_owners=torch.arange(batch, dtype=torch.int32, device=device), rotating=rot,
+                                   hot_valid=valid, hot_cache=hot, host_pool=pool, resident=resident)
+    return rot, upd, kvip.LIFetch(rot, upd)
+
+
+def resident_selections(torch, rng, *, steps, batch, q_rows, history, resident, hot_share=0.8, zipf=1.1):
+    """TopK rows for `steps` rounds: `hot_share` of every row drawn from the hot positions
+    with Zipf(`zipf`) popularity over a fixed random ranking (so consecutive steps revisit
+    the same positions), the rest uniform over the cold positions; rows of one request
+    share 90 % of their positions. Returns int32 [steps, batch * q_rows, 2048]."""
+    out = np.full((steps, batch * q_rows, 2048), -1, np.int32)
+    rank = rng.permutation(resident)
+    weights = 1.0 / np.arange(1, resident + 1) ** zipf
+    weights /= weights.sum()
+    n_hot = int(2048 * hot_share)
+    for s in range(steps):
+        for b in range(batch):
+            hot = rank[rng.choice(resident, n_hot, replace=False, p=weights)]
+            cold = rng.choice(np.arange(resident, history), 2048 - n_hot, replace=False)
+            base = np.concatenate([hot, cold])
+            for q in range(q_rows):
+                row = base.copy()
+                if q:
+                    swap = rng.random(2048) < 0.1
+                    fresh = rng.choice(np.arange(resident, history), int(swap.sum()) * 2, replace=False)
+                    fresh = np.setdiff1d(fresh, base)[:int(swap.sum())]
+                    row[np.nonzero(swap)[0][:len(fresh)]] = fresh
+                out[s, b * q_rows + q] = rng.permutation(row)
+    return out

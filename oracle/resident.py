@@ -255,3 +255,29 @@ def reserved_from_candidates(lru, resident):
         if 0 <= s < resident:
             reserved[int(s)] = i
     return reserved
+
+
+def prefix_classify(keys, valid, resident, lru, cold_words):
+    """Resident TopK of one query row and its hit bits (ProcessResidentTopK + SaveResident,
+    indexer_vector.h:100-105, :162-234; ClassifyScore / ClassifyResidentScores,
+    indexer_score.h:784-792, :1018-1048; cold-tile classification, indexer_vector.h:584-593).
+
+    keys: uint16 sortable keys of the row; valid: its valid positions. Returns
+    (prefix TopK [2048] of positions [0, min(valid, resident)), threshold = the smallest
+    selected key when the prefix selection is full (0 otherwise), victim bits [64] uint32
+    (candidate lru[i] inside the prefix with key > threshold), cold bits [cold_words]
+    uint32 (position resident + j < valid with key > threshold))."""
+    from oracle.indexer import topk_reference
+
+    pv = min(valid, resident)
+    sel = topk_reference(keys, pv)
+    thr = int(keys[sel].min()) if pv >= TOPK else 0
+    victim = np.zeros(TOPK // 32, np.uint32)
+    for i, s in enumerate(lru[:TOPK]):
+        if 0 <= s < pv and int(keys[s]) > thr:
+            victim[i // 32] |= np.uint32(1 << (i % 32))
+    cold = np.zeros(cold_words, np.uint32)
+    for j in range(max(0, valid - resident)):
+        if int(keys[resident + j]) > thr:
+            cold[j // 32] |= np.uint32(1 << (j % 32))
+    return sel, thr, victim, cold

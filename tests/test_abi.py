@@ -40,6 +40,7 @@ STRUCTS = {
     "KvipQueryPackArgs": abi.QueryPackArgs,
     "KvipIngestArgs": abi.IngestArgs,
     "KvipResidentArgs": abi.ResidentArgs,
+    "KvipPrefixClassifyArgs": abi.PrefixClassifyArgs,
 }
 
 

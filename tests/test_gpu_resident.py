@@ -281,3 +281,32 @@ def test_resident_forward_graph_replay(torch_gpu):
         for g, w in zip(got, want):
             assert torch.equal(g, w), step
         assert not upd.status.any()
+
+
+def test_resident_prefix_matches_oracle(torch_gpu):
+    """Resident TopK, threshold and hit bits on the device keys of a scored step equal the
+    oracle's on the same keys (bit-exact), including short and query-bounded rows."""
+    torch = torch_gpu
+    from kvip_amd import synthetic
+
+    ctx = [20000, 9000, 3000, 1500]
+    wl = synthetic.decode_workload(torch, batch=2, ctx=ctx[:2], device="cuda", seed=21, rows_per_request=2)
+    ends = [20000, 19990, 9000, 1500]
+    rot, upd, fwd = synthetic.bind(torch, kvip_amd, wl, query_ends=ends)
+    fwd.score()
+    resident = 4096
+    rng = np.random.default_rng(21)
+    lru = np.stack([rng.permutation(resident)[:2048] for _ in range(2)]).astype(np.int32)
+    lru[0, :2] = [resident + 3, -1]
+    pre = kvip_amd.ResidentPrefix(torch, rot, torch.from_numpy(lru).cuda(), resident)
+    say("case resident prefix")
+    pre()
+    torch.cuda.synchronize()
+    keys = rot.score_keys.cpu().numpy().view(np.uint16)
+    for r in range(rot.rows):
+        valid = min(int(wl.ctx[r // 2]), ends[r])
+        sel, thr, victim, cold = ref.prefix_classify(keys[r], valid, resident, lru[r // 2], pre.cold_words)
+        assert np.array_equal(pre.prefix_topk[r].cpu().numpy(), sel), r
+        assert int(pre.thresholds[r].item()) & 0xFFFF == thr, r
+        assert np.array_equal(pre.victim_hits[r].cpu().numpy().view(np.uint32), victim), r
+        assert np.array_equal(pre.cold_hits[r, :pre.cold_words].cpu().numpy().view(np.uint32), cold), r

@@ -271,3 +271,25 @@ def test_random_multi_round_invariants(seed):
             selected[q, :n] = rng.permutation(row)
         lout, sout, res = run_round(st, selected, policy.slots.astype(np.int64).copy())
         policy.commit(sout[sout >= 0])
+
+
+def test_prefix_classify_closed_forms():
+    """Threshold = the resident selection's kth key (the smallest selected key, the TopK's
+    own cut), hits = strict comparisons against it (ClassifyScore uses CMPMODE::GT)."""
+    rng = np.random.default_rng(4)
+    resident, valid, key_stride = 4096, 10000, 10240
+    keys = rng.integers(0x8000, 0x8400, key_stride).astype(np.uint16)
+    lru = rng.permutation(resident)[:2048]
+    lru[:3] = [resident + 5, 9999, -1]  # outside the prefix: never hits
+    sel, thr, victim, cold = ref.prefix_classify(keys, valid, resident, lru, (key_stride - resident + 31) // 32)
+    assert np.array_equal(sel, li_ref.topk_reference(keys, resident))
+    assert thr == np.sort(keys[:resident])[::-1][2047]
+    bits = np.unpackbits(victim.view(np.uint8), bitorder="little")
+    want = np.array([0 <= s < resident and keys[s] > thr for s in lru])
+    assert np.array_equal(bits.astype(bool), want)
+    cbits = np.unpackbits(cold.view(np.uint8), bitorder="little")[:key_stride - resident].astype(bool)
+    wantc = (keys[resident:] > thr) & (np.arange(resident, key_stride) < valid)
+    assert np.array_equal(cbits, wantc)
+    # A short prefix selects everything below it and has threshold 0.
+    sel, thr, _, _ = ref.prefix_classify(keys, 1000, resident, lru, 200)
+    assert thr == 0 and np.array_equal(sel[:1000], np.arange(1000)) and (sel[1000:] == -1).all()
