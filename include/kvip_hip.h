@@ -16,6 +16,10 @@
  *   kvip_hip_indexer_decode   <- v9_li / QuantLightningIndexerKernel scoring
  *                                (op_host/launch.cpp:16; op_kernel/indexer.cpp:23-86;
  *                                 op_kernel/indexer/indexer_score.h:384-426)
+ *   kvip_hip_indexer_prefill  <- the native prefill LI the vLLM selector runs for prefill rows
+ *                                (python/kvip/adapters/vllm/selector.py:126-154 ->
+ *                                 torch_npu.npu_quant_lightning_indexer, TND / sparse_mode 3,
+ *                                 tests/operators/lifetch/support/execution.py:126-145)
  *   kvip_hip_topk             <- LITopk<uint16_t> inside QLIVector::ProcessTopK
  *                                (op_kernel/indexer/indexer_vector.h:799-973; topk.h:122-197)
  *   kvip_hip_fetch_gather     <- kvaf_device::KvafBatchGetDevice as called by FetchQueryGroup
@@ -127,6 +131,40 @@ typedef struct KvipIndexerArgs {
     int32_t qk_dtype;            /* KVIP_DTYPE_FP8_E4M3 or KVIP_DTYPE_BF16 */
     int32_t weight_dtype;        /* KVIP_DTYPE_FP32 or KVIP_DTYPE_BF16 */
 } KvipIndexerArgs;
+
+/* Prefill and mixed-batch lightning-indexer scoring over packed query rows (TND layout):
+ * sequence s owns query rows [cu_seqlens_q[s], cu_seqlens_q[s+1]) and key positions
+ * [0, seq_lens_k[s]) of block_table[s]; local row j of sequence s (q_len rows) sees the
+ * positions t < vis = clamp(seq_lens_k[s] - q_len + j + 1, 0, seq_lens_k[s]) (right-down
+ * causal). Keys and the high-byte histogram are those of kvip_hip_indexer_decode for each
+ * (row, t < vis); row_valid[r] = vis is written for TopK (kvip_hip_topk with batch = rows,
+ * rows_per_request = 1, seq_lens = row_valid). fp8 Q/K only; 32 or 64 heads; at most 1024
+ * sequences. */
+#define KVIP_PREFILL_MAX_SEQUENCES 1024
+typedef struct KvipPrefillArgs {
+    const void* query;           /* [rows, heads, 128] fp8 e4m3 */
+    const void* weights;         /* [rows, heads] fp32 or bf16 (weight_dtype) */
+    const float* query_scale;    /* [rows, heads], or NULL for 1.0 */
+    const void* keys;            /* paged index-K, as KvipIndexerArgs */
+    const float* key_scale;      /* per-token scales, as KvipIndexerArgs, or NULL */
+    const int32_t* block_table;  /* [sequences, max_blocks] */
+    const int32_t* cu_seqlens_q; /* [sequences + 1] cumulative query rows, cu[0] = 0 */
+    const int32_t* seq_lens_k;   /* [sequences] key positions of each sequence */
+    uint16_t* score_keys;        /* [rows, key_stride] */
+    uint32_t* histogram;         /* [rows, 256], zero before the launch */
+    int32_t* row_valid;          /* [rows] out */
+    uint32_t* status;            /* device status word, or NULL */
+    int64_t key_block_stride;    /* bytes between index-K blocks (multiple of 16, >= 16 KiB) */
+    int64_t scale_block_stride;  /* floats between key-scale blocks */
+    int32_t sequences;
+    int32_t rows;                /* = cu_seqlens_q[sequences] */
+    int32_t heads;               /* 32 or 64 */
+    int32_t max_blocks;
+    int32_t num_blocks;
+    int32_t key_stride;          /* multiple of 8, >= max_blocks * 128 */
+    int32_t qk_dtype;            /* KVIP_DTYPE_FP8_E4M3 */
+    int32_t weight_dtype;        /* KVIP_DTYPE_FP32 or KVIP_DTYPE_BF16 */
+} KvipPrefillArgs;
 
 /* Exact TopK-2048 of sortable uint16 keys per query row, over the row's valid
  * positions valid = min(seq_lens[b], query_ends[r], limit if limit > 0).
@@ -426,6 +464,7 @@ uint32_t kvip_hip_abi_version(void);
 uint32_t kvip_hip_indexer_decode(const KvipIndexerArgs* args, void* stream);
 uint32_t kvip_hip_topk(const KvipTopkArgs* args, void* stream);
 uint32_t kvip_hip_fetch_gather(const KvipFetchArgs* args, void* stream);
+uint32_t kvip_hip_indexer_prefill(const KvipPrefillArgs* args, void* stream);
 uint32_t kvip_hip_lifetch_forward(const KvipLIFetchArgs* args, void* stream);
 /* TopK-2048 of rows scored by kvip_hip_indexer_decode fused with the Fetch gather of the
  * selected rows: same outputs as kvip_hip_topk followed by kvip_hip_fetch_gather. Needs

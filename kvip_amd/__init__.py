@@ -14,6 +14,8 @@ __all__ = [
     "ContiguousFetch",
     "ResidentIndexUpdate",
     "ResidentPrefix",
+    "PrefillIndexer",
+    "quant_lightning_indexer",
     "SlotLRU",
     "update_abc",
     "lidu",
@@ -30,6 +32,8 @@ _EXPORTS = {
     "ContiguousFetch": ("operators.lifetch.binding", "ContiguousFetch"),
     "ResidentIndexUpdate": ("operators.lifetch.resident", "ResidentIndexUpdate"),
     "ResidentPrefix": ("operators.lifetch.resident", "ResidentPrefix"),
+    "PrefillIndexer": ("operators.prefill", "PrefillIndexer"),
+    "quant_lightning_indexer": ("operators.prefill", "quant_lightning_indexer"),
     "SlotLRU": ("cache.lru", "SlotLRU"),
     "update_abc": ("cache.abc", "update_abc"),
     "lidu": ("operators.lidu", "lidu"),

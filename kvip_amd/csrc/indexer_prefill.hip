@@ -1,0 +1,307 @@
+// Prefill (and mixed-batch) lightning-indexer scoring on gfx950 MFMA: packed query rows of
+// several sequences against their paged index-K under a right-down causal mask.
+//
+// Work unit = (query block, context segment): 8 consecutive query rows of one sequence
+// against 4096 key positions. The workgroup's 4 waves own 2 query rows each and keep their
+// Q fragments and per-lane head weights (w'_h = w_h * qscale_h for the 32 heads a lane
+// reduces) in registers. The segment streams through LDS in 256-token chunks, double
+// buffered: every wave issues direct-to-LDS 16-byte loads (global_load_lds_dwordx4) for a
+// quarter of the next chunk, with the XOR swizzle applied on the global side so that the
+// fragment reads (lane n of a 32-token tile reads row n) hit distinct bank groups. Each
+// chunk tile (32 tokens) is one B fragment set read once from LDS and reused by the wave's
+// 2 rows x 2 head tiles x 2 K slices = 8 MFMAs (v_mfma_scale_f32_32x32x64_f8f6f4). The
+// epilogue is the decode kernel's: ReLU, head weights, head reduction, key scale, bf16
+// half-away rounding, sortable key; keys go through a per-wave LDS strip to coalesced
+// stores, and a per-workgroup 256-bin histogram of the key high byte (two 16-bit counters
+// per word) is added to the row histograms at the end.
+//
+// Reference: the native prefill LI (torch_npu.npu_quant_lightning_indexer, TND layout,
+// sparse_mode 3) that the vLLM selector runs for prefill rows (python/kvip/adapters/vllm/
+// selector.py:126-154); the score formula is the decode one (op_kernel/indexer/
+// indexer_cube.h:161-322, indexer_score.h:384-426, score_common.h:66-97).
+#include "indexer_tile.h"
+
+namespace kvip {
+namespace {
+
+constexpr int kPfWaves = 4;
+constexpr int kPfThreads = kPfWaves * 64;
+constexpr int kPfRowsPerWave = 2;
+constexpr int kPfBlockRows = kPfWaves * kPfRowsPerWave;     // 8 query rows per workgroup
+constexpr int kPfChunk = 256;                               // tokens per LDS chunk
+constexpr int kPfTiles = kPfChunk / 32;
+constexpr int kPfSegment = 4096;                            // key positions per workgroup
+constexpr int kPfChunks = kPfSegment / kPfChunk;
+constexpr int kPfPages = kPfSegment / kBlockTokens;         // 32
+constexpr int kPfMaxSeq = KVIP_PREFILL_MAX_SEQUENCES;
+#define LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
+
+template <bool W_BF16>
+KVIP_DEVICE float pf_weight(const KvipPrefillArgs& p, size_t idx) {
+    float w;
+    if constexpr (W_BF16) {
+        w = bf16_to_float(static_cast<const uint16_t*>(p.weights)[idx]);
+    } else {
+        w = static_cast<const float*>(p.weights)[idx];
+    }
+    return w * (p.query_scale != nullptr ? p.query_scale[idx] : 1.0f);
+}
+
+template <int HEADS, bool W_BF16>
+__global__ __launch_bounds__(kPfThreads, 2) void indexer_prefill_kernel(const KvipPrefillArgs p) {
+    constexpr int MT = HEADS / 32;
+    constexpr int NV = Mma<1>::NV;                 // 4 x 16 bytes of a 128-byte fp8 row
+    __shared__ __align__(16) uint8_t s_k[2][kPfChunk * kIndexDim];
+    __shared__ __align__(16) float s_ks[2][kPfChunk];
+    __shared__ __align__(16) uint16_t s_keys[kPfWaves][kPfRowsPerWave][kPfChunk];
+    __shared__ uint32_t s_hist[kPfBlockRows][128];  // two 16-bit counters per word
+    __shared__ int s_prefix[kPfMaxSeq + 1];
+    __shared__ uint32_t s_scan[kPfWaves];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int n = lane & 31;
+    const int g = lane >> 5;
+
+    // Query blocks per sequence -> prefix sums; this workgroup's sequence and rows.
+    int running = 0;
+    for (int base = 0; base < p.sequences; base += kPfThreads) {
+        const int s = base + tid;
+        const int c = s < p.sequences ? (p.cu_seqlens_q[s + 1] - p.cu_seqlens_q[s] + kPfBlockRows - 1) / kPfBlockRows : 0;
+        uint32_t total;
+        const uint32_t excl = block_exclusive_scan(static_cast<uint32_t>(max(c, 0)), s_scan, &total);
+        if (s < p.sequences) s_prefix[s] = running + static_cast<int>(excl);
+        running += static_cast<int>(total);
+    }
+    if (tid == 0) s_prefix[p.sequences] = running;
+    for (int i = tid; i < kPfBlockRows * 128; i += kPfThreads) (&s_hist[0][0])[i] = 0u;
+    __syncthreads();
+    const int block = blockIdx.x;
+    if (block >= s_prefix[p.sequences]) return;  // uniform
+    int lo = 0, hi = p.sequences - 1;            // largest s with s_prefix[s] <= block
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (s_prefix[mid] <= block) lo = mid; else hi = mid - 1;
+    }
+    const int seq = lo;
+    const int q0 = p.cu_seqlens_q[seq];
+    const int q_len = p.cu_seqlens_q[seq + 1] - q0;
+    const int k_len = min(max(p.seq_lens_k[seq], 0), p.max_blocks * kBlockTokens);
+    const int j0 = (block - s_prefix[seq]) * kPfBlockRows;
+
+    // The wave's two rows: visibility (right-down causal) and row_valid.
+    int vis[kPfRowsPerWave];
+    int rowi[kPfRowsPerWave];
+#pragma unroll
+    for (int q = 0; q < kPfRowsPerWave; ++q) {
+        const int j = j0 + wave * kPfRowsPerWave + q;
+        const bool live = j < q_len;
+        rowi[q] = q0 + min(j, q_len - 1);
+        vis[q] = live ? min(max(k_len - q_len + j + 1, 0), k_len) : 0;
+        if (live && blockIdx.y == 0 && lane == 0) p.row_valid[q0 + j] = vis[q];
+    }
+    const int last = min(j0 + kPfBlockRows, q_len) - 1;
+    const int vis_max = min(max(k_len - q_len + last + 1, 0), k_len);
+    const int seg0 = blockIdx.y * kPfSegment;
+    const int seg_end = min(seg0 + kPfSegment, vis_max);
+    if (seg0 >= seg_end) return;  // uniform: nothing visible in this segment
+    const int nchunks = (seg_end - seg0 + kPfChunk - 1) / kPfChunk;
+
+    // Q fragments and head weights of the wave's rows.
+    v4i qa[kPfRowsPerWave][MT][NV];
+    float wr[kPfRowsPerWave][MT * 16];
+#pragma unroll
+    for (int q = 0; q < kPfRowsPerWave; ++q) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            const v4i* src = reinterpret_cast<const v4i*>(static_cast<const uint8_t*>(p.query) +
+                                                          (static_cast<size_t>(rowi[q]) * HEADS + mt * 32 + n) * kIndexDim +
+                                                          g * (kIndexDim / 2));
+#pragma unroll
+            for (int v = 0; v < NV; ++v) qa[q][mt][v] = src[v];
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    wr[q][mt * 16 + r4 * 4 + j] =
+                        pf_weight<W_BF16>(p, static_cast<size_t>(rowi[q]) * HEADS + mt * 32 + r4 * 8 + g * 4 + j);
+                }
+            }
+        }
+    }
+
+    // Page ids of the segment (lane i < 32 holds page seg0/128 + i, clamped to the
+    // sequence's last page; out-of-range ids read block 0 with zero key scale).
+    const int pages_k = (k_len + kBlockTokens - 1) / kBlockTokens;
+    int my_page = 0;
+    float my_ok = 0.0f;
+    uint32_t err = 0;
+    if (lane < kPfPages) {
+        const int pi = min(seg0 / kBlockTokens + lane, max(pages_k - 1, 0));
+        const int id = p.block_table[static_cast<size_t>(seq) * p.max_blocks + pi];
+        const bool ok = static_cast<unsigned>(id) < static_cast<unsigned>(p.num_blocks);
+        my_page = ok ? id : 0;
+        my_ok = ok ? 1.0f : 0.0f;
+        if (!ok) err |= KVIP_STATUS_BAD_BLOCK;
+    }
+    const uint8_t* kbase = static_cast<const uint8_t*>(p.keys);
+
+    // Wave w stages rows [64w, 64w + 64) of a chunk: 8 direct-to-LDS loads of 8 rows each.
+    auto stage = [&](int c, int buf) {
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+            const int row = wave * 64 + v * 8 + (lane >> 3);
+            const int piece = (lane & 7) ^ swizzle<1>(row);
+            const int pg = __builtin_amdgcn_readlane(my_page, c * 2 + (wave >> 1));
+            const uint8_t* src = kbase + static_cast<size_t>(pg) * p.key_block_stride +
+                                 (row & (kBlockTokens - 1)) * kIndexDim + piece * 16;
+            __builtin_amdgcn_global_load_lds(src, LDS_PTR(&s_k[buf][(wave * 64 + v * 8) * kIndexDim]), 16, 0, 0);
+        }
+        if (wave == 0) {
+            if (p.key_scale != nullptr) {
+                const int row = lane * 4;  // 4 consecutive scales of one page
+                // readlane takes a wave-uniform lane index: read both pages, pick per half-wave.
+                const int pg0 = __builtin_amdgcn_readlane(my_page, c * 2);
+                const int pg1 = __builtin_amdgcn_readlane(my_page, c * 2 + 1);
+                const int pg = lane < 32 ? pg0 : pg1;
+                const float* src = p.key_scale + static_cast<size_t>(pg) * p.scale_block_stride + (row & 127);
+                __builtin_amdgcn_global_load_lds(src, LDS_PTR(&s_ks[buf][0]), 16, 0, 0);
+            } else {
+#pragma unroll
+                for (int k = 0; k < 4; ++k) s_ks[buf][lane * 4 + k] = 1.0f;
+            }
+        }
+    };
+
+    stage(0, 0);
+    for (int c = 0; c < nchunks; ++c) {
+        const int buf = c & 1;
+        __builtin_amdgcn_s_waitcnt(0);  // chunk c landed (and the previous flush stores done)
+        __syncthreads();                // visible to every wave; buffer c+1 free again
+        if (c + 1 < nchunks) stage(c + 1, buf ^ 1);
+        const int cstart = seg0 + c * kPfChunk;
+        const float page_ok0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_ok), c * 2));
+        const float page_ok1 =
+            __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_ok), c * 2 + 1));
+#pragma unroll 1
+        for (int k = 0; k < kPfTiles; ++k) {
+            const int t0 = cstart + k * 32;
+            if (t0 >= vis[0] && t0 >= vis[1]) break;  // uniform per wave: later tiles are masked too
+            const int r = k * 32 + n;
+            v4i kb[NV];
+#pragma unroll
+            for (int u = 0; u < NV; ++u) {
+                const int j = g * NV + u;
+                kb[u] = *reinterpret_cast<const v4i*>(&s_k[buf][r * kIndexDim + ((j ^ swizzle<1>(r)) * 16)]);
+            }
+            const float ks = s_ks[buf][r] * (k < kPfTiles / 2 ? page_ok0 : page_ok1);
+#pragma unroll
+            for (int q = 0; q < kPfRowsPerWave; ++q) {
+                if (t0 >= vis[q]) continue;  // uniform
+                v16f acc[MT];
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    acc[mt] = v16f{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+                }
+#pragma unroll
+                for (int s = 0; s < Mma<1>::STEPS; ++s) {
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt) Mma<1>::step(s, qa[q][mt], kb, acc[mt]);
+                }
+                float pj[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+                    for (int r4 = 0; r4 < 4; ++r4) {
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            const float relu = __int_as_float(max(__float_as_int(acc[mt][r4 * 4 + j]), 0));
+                            pj[j] = fmaf(relu, wr[q][mt * 16 + r4 * 4 + j], pj[j]);
+                        }
+                    }
+                }
+                float part = (pj[0] + pj[1]) + (pj[2] + pj[3]);
+                const auto swapped =
+                    __builtin_amdgcn_permlane32_swap(__float_as_int(part), __float_as_int(part), false, false);
+                part += __int_as_float(g == 0 ? swapped[1] : swapped[0]);
+                const uint32_t key = sortable_key(bf16_bits_half_away(part * ks));
+                if (g == 0) {
+                    s_keys[wave][q][k * 32 + n] = static_cast<uint16_t>(key);
+                    if (t0 + n < vis[q]) {
+                        const uint32_t bin = key >> 8;
+                        atomicAdd(&s_hist[wave * kPfRowsPerWave + q][bin >> 1], 1u << (16 * (bin & 1)));
+                    }
+                }
+            }
+        }
+        // Flush the chunk's keys of the wave's rows (8-byte stores, inside the row stride).
+#pragma unroll
+        for (int q = 0; q < kPfRowsPerWave; ++q) {
+            if (cstart >= vis[q]) continue;  // uniform
+            const int o = lane * 4;
+            if (cstart + o + 4 <= p.key_stride) {
+                *reinterpret_cast<uint2*>(p.score_keys + static_cast<size_t>(rowi[q]) * p.key_stride + cstart + o) =
+                    *reinterpret_cast<const uint2*>(&s_keys[wave][q][o]);
+            }
+        }
+    }
+    __syncthreads();
+    // Histogram of the workgroup's rows.
+    for (int i = tid; i < kPfBlockRows * 256; i += kPfThreads) {
+        const int rq = i >> 8;
+        const int bin = i & 255;
+        const int j = j0 + rq;
+        const uint32_t c = (s_hist[rq][bin >> 1] >> (16 * (bin & 1))) & 0xFFFFu;
+        if (j < q_len && c != 0u) atomicAdd(&p.histogram[static_cast<size_t>(q0 + j) * 256 + bin], c);
+    }
+    report(p.status, err);
+}
+
+template <int HEADS>
+hipError_t launch_heads(const KvipPrefillArgs& a, hipStream_t stream) {
+    const int blocks = a.rows / kPfBlockRows + a.sequences;  // bound on the per-sequence blocks
+    const dim3 grid(blocks, (a.max_blocks * kBlockTokens + kPfSegment - 1) / kPfSegment);
+    if (a.weight_dtype == KVIP_DTYPE_BF16) {
+        hipLaunchKernelGGL((indexer_prefill_kernel<HEADS, true>), grid, dim3(kPfThreads), 0, stream, a);
+    } else {
+        hipLaunchKernelGGL((indexer_prefill_kernel<HEADS, false>), grid, dim3(kPfThreads), 0, stream, a);
+    }
+    return hipGetLastError();
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+
+uint32_t validate_prefill(const KvipPrefillArgs* a) {
+    if (a == nullptr) return KVIP_ERR_INVALID;
+    const bool ok =
+        a->query != nullptr && a->weights != nullptr && a->keys != nullptr && a->block_table != nullptr &&
+        a->cu_seqlens_q != nullptr && a->seq_lens_k != nullptr && a->score_keys != nullptr &&
+        a->histogram != nullptr && a->row_valid != nullptr && a->qk_dtype == KVIP_DTYPE_FP8_E4M3 &&
+        (a->weight_dtype == KVIP_DTYPE_FP32 || a->weight_dtype == KVIP_DTYPE_BF16) &&
+        (a->heads == 32 || a->heads == 64) && a->sequences >= 1 && a->sequences <= kPfMaxSeq && a->rows >= 1 &&
+        a->rows <= (1 << 24) && a->max_blocks >= 1 && a->num_blocks >= 1 &&
+        a->max_blocks <= (1 << 24) / kBlockTokens &&
+        static_cast<int64_t>(a->key_stride) >= static_cast<int64_t>(a->max_blocks) * kBlockTokens &&
+        a->key_stride % 8 == 0 && a->key_block_stride % 16 == 0 &&
+        a->key_block_stride >= static_cast<int64_t>(kBlockTokens) * kIndexDim &&
+        (a->key_scale == nullptr || (a->scale_block_stride >= kBlockTokens && a->scale_block_stride % 4 == 0 &&
+                                     (reinterpret_cast<uintptr_t>(a->key_scale) & 15u) == 0)) &&
+        aligned16(a->query) && aligned16(a->keys) && aligned16(a->score_keys) &&
+        static_cast<int64_t>(a->rows / kPfBlockRows + a->sequences) <= 0x7FFFFFFF;
+    return ok ? KVIP_OK : KVIP_ERR_INVALID;
+}
+
+hipError_t launch_prefill(const KvipPrefillArgs& a, hipStream_t stream) {
+    return a.heads == 64 ? launch_heads<64>(a, stream) : launch_heads<32>(a, stream);
+}
+
+}  // namespace kvip
+
+extern "C" uint32_t kvip_hip_indexer_prefill(const KvipPrefillArgs* args, void* stream) {
+    const uint32_t rc = kvip::validate_prefill(args);
+    if (rc != KVIP_OK) return rc;
+    return static_cast<uint32_t>(kvip::launch_prefill(*args, static_cast<hipStream_t>(stream)));
+}

@@ -39,6 +39,17 @@ class IndexerArgs(ctypes.Structure):
     ]
 
 
+class PrefillArgs(ctypes.Structure):
+    _fields_ = [
+        ("query", _p), ("weights", _p), ("query_scale", _p), ("keys", _p), ("key_scale", _p), ("block_table", _p),
+        ("cu_seqlens_q", _p), ("seq_lens_k", _p), ("score_keys", _p), ("histogram", _p), ("row_valid", _p),
+        ("status", _p),
+        ("key_block_stride", _i64), ("scale_block_stride", _i64),
+        ("sequences", _i32), ("rows", _i32), ("heads", _i32), ("max_blocks", _i32), ("num_blocks", _i32),
+        ("key_stride", _i32), ("qk_dtype", _i32), ("weight_dtype", _i32),
+    ]
+
+
 class TopkArgs(ctypes.Structure):
     _fields_ = [
         ("score_keys", _p), ("histogram", _p), ("segments", _p), ("seq_lens", _p), ("query_ends", _p), ("topk", _p),
@@ -147,6 +158,7 @@ class PrefixClassifyArgs(ctypes.Structure):
 PROTOTYPES = {
     "kvip_hip_abi_version": ([], ctypes.c_uint32),
     "kvip_hip_indexer_decode": ([ctypes.POINTER(IndexerArgs), _p], ctypes.c_uint32),
+    "kvip_hip_indexer_prefill": ([ctypes.POINTER(PrefillArgs), _p], ctypes.c_uint32),
     "kvip_hip_topk": ([ctypes.POINTER(TopkArgs), _p], ctypes.c_uint32),
     "kvip_hip_fetch_gather": ([ctypes.POINTER(FetchArgs), _p], ctypes.c_uint32),
     "kvip_hip_lifetch_forward": ([ctypes.POINTER(LIFetchArgs), _p], ctypes.c_uint32),

@@ -79,6 +79,23 @@ def score_values(keys):
 # ----------------------------------------------------------------------------
 # LI score
 # ----------------------------------------------------------------------------
+def identical_share(got_keys, want_keys, valid, floor=3e-2):
+    """Share of bit-identical keys among the valid keys whose oracle |score| is at least
+    `floor` of the row's largest |score|. A checker's statistic, not part of the
+    algorithm: the device's fp8 dot products are not correctly rounded fp32, so scores that
+    cancel to near zero (where a bf16 ulp is far below that absolute error) may differ in
+    their last bits; every key is held to the score tolerance separately."""
+    same = total = 0
+    for r, v in enumerate(valid):
+        if v == 0:
+            continue
+        w = np.abs(score_values(want_keys[r, :v]).astype(np.float64))
+        keep = w >= floor * w.max()
+        same += int(np.sum(got_keys[r, :v][keep] == want_keys[r, :v][keep]))
+        total += int(keep.sum())
+    return same / max(total, 1)
+
+
 def _fma32(a, b, c):
     """float32 a*b + c rounded once; emulated in float64 (a*b is exact there, the add
     can double-round in rare last-bit cases)."""
@@ -155,6 +172,41 @@ def decode_keys_paged(query, weights, query_scale, keys, key_scale, block_table,
         qs = None if query_scale is None else query_scale[r]
         out[r, :v] = li_keys(query[r], k, weights[r], qs, ks)
     return out, valid
+
+
+def prefill_visible(cu_seqlens_q, seq_lens_k):
+    """Visible key positions of every packed query row under the right-down causal mask
+    (sparse_mode 3 of the native indexer the reference's selector calls for prefill rows,
+    python/kvip/adapters/vllm/selector.py:126-154): local row j of a sequence with q_len
+    rows and k_len keys sees positions t < clamp(k_len - q_len + j + 1, 0, k_len)."""
+    out = []
+    for s in range(len(seq_lens_k)):
+        q_len = int(cu_seqlens_q[s + 1] - cu_seqlens_q[s])
+        k_len = int(seq_lens_k[s])
+        for j in range(q_len):
+            out.append(max(0, min(k_len - q_len + j + 1, k_len)))
+    return np.array(out, np.int64)
+
+
+def prefill_keys_paged(query, weights, query_scale, keys, key_scale, block_table, cu_seqlens_q, seq_lens_k,
+                       key_stride):
+    """Keys of packed prefill rows: row r of sequence s scores positions [0, vis(r)) of
+    that sequence's paged keys with the decode formula (li_keys). Returns (keys
+    [rows, key_stride] uint16 with zeros past vis, vis [rows])."""
+    vis = prefill_visible(cu_seqlens_q, seq_lens_k)
+    out = np.zeros((len(vis), key_stride), np.uint16)
+    for s in range(len(seq_lens_k)):
+        k_len = int(seq_lens_k[s])
+        tokens = np.arange(k_len)
+        k = paged_rows(keys, block_table[s], tokens)
+        ks = None if key_scale is None else paged_rows(key_scale, block_table[s], tokens)
+        for r in range(int(cu_seqlens_q[s]), int(cu_seqlens_q[s + 1])):
+            v = int(vis[r])
+            if v == 0:
+                continue
+            qs = None if query_scale is None else query_scale[r]
+            out[r, :v] = li_keys(query[r], k[:v], weights[r], qs, None if ks is None else ks[:v])
+    return out, vis
 
 
 # ----------------------------------------------------------------------------

@@ -31,6 +31,7 @@ def test_library_exports_every_declared_symbol():
 
 STRUCTS = {
     "KvipIndexerArgs": abi.IndexerArgs,
+    "KvipPrefillArgs": abi.PrefillArgs,
     "KvipTopkArgs": abi.TopkArgs,
     "KvipFetchArgs": abi.FetchArgs,
     "KvipLIFetchArgs": abi.LIFetchArgs,

@@ -175,3 +175,32 @@ def test_fetch_gather_known_answer():
     assert np.array_equal(out[1, 0], kv[1, 127]) and np.array_equal(out[1, 2], kv[2, 0])
     rows = ref.identity_rows(np.arange(4096))
     assert len({r.tobytes() for r in rows}) == 4096
+
+
+def test_prefill_visibility_closed_form():
+    """Right-down causal: the last row of a sequence sees every key, rows above it one
+    fewer each; a sequence with more queries than keys starts with empty rows."""
+    from oracle.indexer import prefill_visible
+
+    vis = prefill_visible(np.array([0, 4, 7]), np.array([10, 2]))
+    assert vis.tolist() == [7, 8, 9, 10, 0, 1, 2]
+
+
+def test_prefill_keys_equal_per_row_decode_keys():
+    """Each prefill row scores the same keys as a decode row bounded at its visibility."""
+    from oracle import indexer as ref
+
+    rng = np.random.default_rng(8)
+    heads, blocks = 8, 6
+    keys = ref.fp8_e4m3_decode(rng.integers(0, 256, (blocks, 128, 128), dtype=np.uint8) & 0x77)
+    key_scale = rng.uniform(0.5, 2, (blocks, 128)).astype(np.float32)
+    query = ref.fp8_e4m3_decode(rng.integers(0, 256, (5, heads, 128), dtype=np.uint8) & 0x77)
+    weights = rng.standard_normal((5, heads)).astype(np.float32) / 8
+    table = np.array([[3, 1, 5], [0, 2, 4]], np.int32)
+    cu, kl = np.array([0, 3, 5]), np.array([300, 257])
+    got, vis = ref.prefill_keys_paged(query, weights, None, keys, key_scale, table, cu, kl, 384)
+    for r, v in enumerate(vis):
+        s = 0 if r < 3 else 1
+        want, _ = ref.decode_keys_paged(query[r:r + 1], weights[r:r + 1], None, keys, key_scale, table[s:s + 1],
+                                        [kl[s]], query_ends=[v], key_stride=384)
+        assert np.array_equal(got[r], want[0]), r
