@@ -26,7 +26,7 @@ namespace {
 
 constexpr int kPfWaves = 4;
 constexpr int kPfThreads = kPfWaves * 64;
-constexpr int kPfRowsPerWave = 2;
+constexpr int kPfRowsPerWave = 2;                           // one row per lane half at the finish
 constexpr int kPfBlockRows = kPfWaves * kPfRowsPerWave;     // 8 query rows per workgroup
 constexpr int kPfChunk = 256;                               // tokens per LDS chunk
 constexpr int kPfTiles = kPfChunk / 32;
@@ -35,6 +35,60 @@ constexpr int kPfChunks = kPfSegment / kPfChunk;
 constexpr int kPfPages = kPfSegment / kBlockTokens;         // 32
 constexpr int kPfMaxSeq = KVIP_PREFILL_MAX_SEQUENCES;
 #define LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
+typedef int v2i __attribute__((ext_vector_type(2)));
+
+// LDS piece swizzle of a staged 128-byte K row: piece j of row r sits at slot j ^ (r & 7).
+// A fragment read (lane n reads piece j of row n) then touches 8 distinct 16-byte slots
+// in every group of 8 consecutive lanes, i.e. all 32 banks once per 128-byte phase.
+KVIP_DEVICE int pf_swizzle(int row) { return row & 7; }
+
+// LDS accesses inside the chunk loop are inline asm. The compiler's wait insertion cannot
+// tell an LDS read from the in-flight direct-to-LDS loads of the next chunk, and would
+// wait for those loads (vmcnt(0)) before every read, which serialises the double buffer.
+// Reads are issued and waited for in one asm block, so their registers are valid when it
+// ends; the chunk barrier waits for this wave's direct-to-LDS loads explicitly.
+KVIP_DEVICE uint32_t lds_addr(const void* p) {
+    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(LDS_PTR(p)));
+}
+
+// The four 16-byte K fragment pieces of a tile row and the row's key scale.
+KVIP_DEVICE void lds_read_tile(uint32_t a0, uint32_t a1, uint32_t a2, uint32_t a3, uint32_t as, v4i (&kb)[4],
+                               float& ks) {
+    asm volatile(
+        "ds_read_b128 %0, %5\n"
+        "ds_read_b128 %1, %6\n"
+        "ds_read_b128 %2, %7\n"
+        "ds_read_b128 %3, %8\n"
+        "ds_read_b32 %4, %9\n"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(kb[0]), "=&v"(kb[1]), "=&v"(kb[2]), "=&v"(kb[3]), "=&v"(ks)
+        : "v"(a0), "v"(a1), "v"(a2), "v"(a3), "v"(as));
+}
+
+KVIP_DEVICE v2i lds_read_b64(uint32_t a) {
+    v2i v;
+    asm volatile("ds_read_b64 %0, %1\ns_waitcnt lgkmcnt(0)" : "=&v"(v) : "v"(a));
+    return v;
+}
+
+KVIP_DEVICE void lds_write_b16(uint32_t a, uint32_t v) { asm volatile("ds_write_b16 %0, %1" : : "v"(a), "v"(v)); }
+
+KVIP_DEVICE void lds_add_u32(uint32_t a, uint32_t v) { asm volatile("ds_add_u32 %0, %1" : : "v"(a), "v"(v)); }
+
+// Workgroup barrier after this wave's LDS operations and all but its `stores` most recent
+// vector-memory operations (the key stores issued after the chunk's direct-to-LDS loads;
+// vector memory operations complete in issue order) have completed.
+KVIP_DEVICE void chunk_barrier(int stores) {
+    if (stores >= 2) {
+        asm volatile("s_waitcnt vmcnt(2) lgkmcnt(0)" : : : "memory");
+    } else if (stores == 1) {
+        asm volatile("s_waitcnt vmcnt(1) lgkmcnt(0)" : : : "memory");
+    } else {
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" : : : "memory");
+    }
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" : : : "memory");
+}
 
 template <bool W_BF16>
 KVIP_DEVICE float pf_weight(const KvipPrefillArgs& p, size_t idx) {
@@ -51,6 +105,7 @@ template <int HEADS, bool W_BF16>
 __global__ __launch_bounds__(kPfThreads, 2) void indexer_prefill_kernel(const KvipPrefillArgs p) {
     constexpr int MT = HEADS / 32;
     constexpr int NV = Mma<1>::NV;                 // 4 x 16 bytes of a 128-byte fp8 row
+    static_assert(kPfRowsPerWave == 2, "the finish maps row q to lane half q");
     __shared__ __align__(16) uint8_t s_k[2][kPfChunk * kIndexDim];
     __shared__ __align__(16) float s_ks[2][kPfChunk];
     __shared__ __align__(16) uint16_t s_keys[kPfWaves][kPfRowsPerWave][kPfChunk];
@@ -60,7 +115,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void indexer_prefill_kernel(const Kv
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: row data stays scalar
     const int n = lane & 31;
     const int g = lane >> 5;
 
@@ -152,33 +207,45 @@ __global__ __launch_bounds__(kPfThreads, 2) void indexer_prefill_kernel(const Kv
 #pragma unroll
         for (int v = 0; v < 8; ++v) {
             const int row = wave * 64 + v * 8 + (lane >> 3);
-            const int piece = (lane & 7) ^ swizzle<1>(row);
+            const int piece = (lane & 7) ^ pf_swizzle(row);
             const int pg = __builtin_amdgcn_readlane(my_page, c * 2 + (wave >> 1));
             const uint8_t* src = kbase + static_cast<size_t>(pg) * p.key_block_stride +
                                  (row & (kBlockTokens - 1)) * kIndexDim + piece * 16;
             __builtin_amdgcn_global_load_lds(src, LDS_PTR(&s_k[buf][(wave * 64 + v * 8) * kIndexDim]), 16, 0, 0);
         }
-        if (wave == 0) {
-            if (p.key_scale != nullptr) {
-                const int row = lane * 4;  // 4 consecutive scales of one page
-                // readlane takes a wave-uniform lane index: read both pages, pick per half-wave.
-                const int pg0 = __builtin_amdgcn_readlane(my_page, c * 2);
-                const int pg1 = __builtin_amdgcn_readlane(my_page, c * 2 + 1);
-                const int pg = lane < 32 ? pg0 : pg1;
-                const float* src = p.key_scale + static_cast<size_t>(pg) * p.scale_block_stride + (row & 127);
-                __builtin_amdgcn_global_load_lds(src, LDS_PTR(&s_ks[buf][0]), 16, 0, 0);
-            } else {
-#pragma unroll
-                for (int k = 0; k < 4; ++k) s_ks[buf][lane * 4 + k] = 1.0f;
-            }
+        if (wave == 0 && p.key_scale != nullptr) {
+            const int row = lane * 4;  // 4 consecutive scales of one page
+            // readlane takes a wave-uniform lane index: read both pages, pick per half-wave.
+            const int pg0 = __builtin_amdgcn_readlane(my_page, c * 2);
+            const int pg1 = __builtin_amdgcn_readlane(my_page, c * 2 + 1);
+            const int pg = lane < 32 ? pg0 : pg1;
+            const float* src = p.key_scale + static_cast<size_t>(pg) * p.scale_block_stride + (row & 127);
+            __builtin_amdgcn_global_load_lds(src, LDS_PTR(&s_ks[buf][0]), 16, 0, 0);
         }
     };
+    if (p.key_scale == nullptr) {  // unit key scales, written once before the loop
+        for (int i = tid; i < 2 * kPfChunk; i += kPfThreads) (&s_ks[0][0])[i] = 1.0f;
+        __syncthreads();
+    }
+
+    const int vis_mine = g == 0 ? vis[0] : vis[1];          // this lane half's row
+    const int hist_row = wave * kPfRowsPerWave + g;
+    // Per-lane LDS addresses: the tile row's four swizzled K pieces (the swizzle of row
+    // k*32 + n does not depend on k), its key scale, and the key strip slots.
+    uint32_t ka[NV];
+#pragma unroll
+    for (int u = 0; u < NV; ++u) ka[u] = lds_addr(&s_k[0][n * kIndexDim + (((g * NV + u) ^ pf_swizzle(n)) * 16)]);
+    const uint32_t ksa = lds_addr(&s_ks[0][n]);
+    const uint32_t keya = lds_addr(&s_keys[wave][g][n]);
+    const uint32_t hista = lds_addr(&s_hist[hist_row][0]);
+    constexpr uint32_t kKBuf = kPfChunk * kIndexDim;   // bytes between the two K buffers
+    constexpr uint32_t kSBuf = kPfChunk * 4;           // bytes between the two scale buffers
 
     stage(0, 0);
+    int stores = 0;  // key stores this wave issued after the latest staging loads
     for (int c = 0; c < nchunks; ++c) {
         const int buf = c & 1;
-        __builtin_amdgcn_s_waitcnt(0);  // chunk c landed (and the previous flush stores done)
-        __syncthreads();                // visible to every wave; buffer c+1 free again
+        chunk_barrier(stores);  // chunk c landed and is visible; buffer c+1 is free again
         if (c + 1 < nchunks) stage(c + 1, buf ^ 1);
         const int cstart = seg0 + c * kPfChunk;
         const float page_ok0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_ok), c * 2));
@@ -188,65 +255,83 @@ __global__ __launch_bounds__(kPfThreads, 2) void indexer_prefill_kernel(const Kv
         for (int k = 0; k < kPfTiles; ++k) {
             const int t0 = cstart + k * 32;
             if (t0 >= vis[0] && t0 >= vis[1]) break;  // uniform per wave: later tiles are masked too
-            const int r = k * 32 + n;
             v4i kb[NV];
+            float ks_raw;
+            const uint32_t toff = buf * kKBuf + k * 32 * kIndexDim;
+            lds_read_tile(ka[0] + toff, ka[1] + toff, ka[2] + toff, ka[3] + toff, ksa + buf * kSBuf + k * 128, kb,
+                          ks_raw);
+            const float ks = ks_raw * (k < kPfTiles / 2 ? page_ok0 : page_ok1);
+            // Units u = (row q = u / MT, head tile mt = u % MT), two dependent K-slice MFMAs
+            // each. Unit u+1's MFMAs are issued between the 32 VALU ops (ReLU, weight FMA) of
+            // unit u's epilogue so that the matrix core and the VALU work side by side.
+            constexpr int U = kPfRowsPerWave * MT;
+            float pj[kPfRowsPerWave][4];
 #pragma unroll
-            for (int u = 0; u < NV; ++u) {
-                const int j = g * NV + u;
-                kb[u] = *reinterpret_cast<const v4i*>(&s_k[buf][r * kIndexDim + ((j ^ swizzle<1>(r)) * 16)]);
+            for (int q = 0; q < kPfRowsPerWave; ++q) pj[q][0] = pj[q][1] = pj[q][2] = pj[q][3] = 0.f;
+            v16f acc[2];
+            acc[0] = v16f{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            Mma<1>::step(0, qa[0][0], kb, acc[0]);
+            Mma<1>::step(1, qa[0][0], kb, acc[0]);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int q = u / MT, mt = u % MT;
+                v16f& cur = acc[u & 1];
+                v16f& nxt = acc[(u + 1) & 1];
+                if (u + 1 < U) {
+                    nxt = v16f{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+                    Mma<1>::step(0, qa[(u + 1) / MT][(u + 1) % MT], kb, nxt);
+                    Mma<1>::step(1, qa[(u + 1) / MT][(u + 1) % MT], kb, nxt);
+                }
+#pragma unroll
+                for (int r4 = 0; r4 < 4; ++r4) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const float relu = __int_as_float(max(__float_as_int(cur[r4 * 4 + j]), 0));
+                        pj[q][j] = fmaf(relu, wr[q][mt * 16 + r4 * 4 + j], pj[q][j]);
+                    }
+                }
+                if (u + 1 < U) {
+                    // 1 MFMA, 16 VALU, 1 MFMA, 16 VALU; nothing crosses into the next unit.
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
             }
-            const float ks = s_ks[buf][r] * (k < kPfTiles / 2 ? page_ok0 : page_ok1);
-#pragma unroll
-            for (int q = 0; q < kPfRowsPerWave; ++q) {
-                if (t0 >= vis[q]) continue;  // uniform
-                v16f acc[MT];
-#pragma unroll
-                for (int mt = 0; mt < MT; ++mt) {
-                    acc[mt] = v16f{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-                }
-#pragma unroll
-                for (int s = 0; s < Mma<1>::STEPS; ++s) {
-#pragma unroll
-                    for (int mt = 0; mt < MT; ++mt) Mma<1>::step(s, qa[q][mt], kb, acc[mt]);
-                }
-                float pj[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int mt = 0; mt < MT; ++mt) {
-#pragma unroll
-                    for (int r4 = 0; r4 < 4; ++r4) {
-#pragma unroll
-                        for (int j = 0; j < 4; ++j) {
-                            const float relu = __int_as_float(max(__float_as_int(acc[mt][r4 * 4 + j]), 0));
-                            pj[j] = fmaf(relu, wr[q][mt * 16 + r4 * 4 + j], pj[j]);
-                        }
-                    }
-                }
-                float part = (pj[0] + pj[1]) + (pj[2] + pj[3]);
-                const auto swapped =
-                    __builtin_amdgcn_permlane32_swap(__float_as_int(part), __float_as_int(part), false, false);
-                part += __int_as_float(g == 0 ? swapped[1] : swapped[0]);
-                const uint32_t key = sortable_key(bf16_bits_half_away(part * ks));
-                if (g == 0) {
-                    s_keys[wave][q][k * 32 + n] = static_cast<uint16_t>(key);
-                    if (t0 + n < vis[q]) {
-                        const uint32_t bin = key >> 8;
-                        atomicAdd(&s_hist[wave * kPfRowsPerWave + q][bin >> 1], 1u << (16 * (bin & 1)));
-                    }
-                }
+            // Both rows finish together: after the swap, lanes 0-31 hold row 0's total for
+            // token n and lanes 32-63 row 1's (each the sum of the two lane halves' heads).
+            const float part0 = (pj[0][0] + pj[0][1]) + (pj[0][2] + pj[0][3]);
+            const float part1 = (pj[1][0] + pj[1][1]) + (pj[1][2] + pj[1][3]);
+            const float mine = g == 0 ? part0 : part1;
+            const float other = g == 0 ? part1 : part0;
+            const auto swapped =
+                __builtin_amdgcn_permlane32_swap(__float_as_int(other), __float_as_int(other), false, false);
+            const float total = mine + __int_as_float(g == 0 ? swapped[1] : swapped[0]);
+            const uint32_t key = sortable_key(bf16_bits_half_away(total * ks));
+            lds_write_b16(keya + k * 64, key);
+            if (t0 + n < vis_mine) {
+                const uint32_t bin = key >> 8;
+                lds_add_u32(hista + (bin >> 1) * 4, 1u << (16 * (bin & 1)));
             }
         }
         // Flush the chunk's keys of the wave's rows (8-byte stores, inside the row stride).
+        // Lane 0's store is always in range (cstart < key_stride, both multiples of 8), so
+        // each live row issues exactly one store instruction.
+        stores = 0;
 #pragma unroll
         for (int q = 0; q < kPfRowsPerWave; ++q) {
             if (cstart >= vis[q]) continue;  // uniform
             const int o = lane * 4;
+            const v2i v = lds_read_b64(lds_addr(&s_keys[wave][q][o]));
             if (cstart + o + 4 <= p.key_stride) {
-                *reinterpret_cast<uint2*>(p.score_keys + static_cast<size_t>(rowi[q]) * p.key_stride + cstart + o) =
-                    *reinterpret_cast<const uint2*>(&s_keys[wave][q][o]);
+                *reinterpret_cast<v2i*>(p.score_keys + static_cast<size_t>(rowi[q]) * p.key_stride + cstart + o) = v;
             }
+            ++stores;
         }
     }
-    __syncthreads();
+    chunk_barrier(0);
     // Histogram of the workgroup's rows.
     for (int i = tid; i < kPfBlockRows * 256; i += kPfThreads) {
         const int rq = i >> 8;

@@ -54,6 +54,13 @@ class PrefillIndexer:
         [blocks, 128] float32 or None; cu_seqlens_q [sequences + 1] int32 (device);
         seq_lens_k [sequences] int32; block_table [sequences, max_blocks] int32. Returns the
         TopK view [rows, 2048] int32 (positions within each row's sequence)."""
+        self.bind(query, weights, query_scale, key, key_scale, cu_seqlens_q, seq_lens_k, block_table)
+        self.score()
+        return self.select()
+
+    def bind(self, query, weights, query_scale, key, key_scale, cu_seqlens_q, seq_lens_k, block_table):
+        """Validate one call's tensors (same meaning as __call__) and keep their launch
+        arguments; `score()` and `select()` then enqueue the two launches."""
         t = self.torch
         rows, sequences = int(query.shape[0]), int(seq_lens_k.shape[0])
         if not 1 <= rows <= self.max_rows or not 1 <= sequences <= self.max_sequences:
@@ -89,13 +96,23 @@ class PrefillIndexer:
             else key_scale.stride(0), sequences=sequences, rows=rows, heads=self.heads,
             max_blocks=int(block_table.shape[1]), num_blocks=int(key.shape[0]), key_stride=self.key_stride,
             qk_dtype=abi.DTYPE_FP8_E4M3, weight_dtype=self.weight_code)
-        stream = abi.stream_handle(t, self.device)
-        abi.check(self.library.kvip_hip_indexer_prefill(ctypes.byref(args), stream), "prefill LI")
         topk = abi.TopkArgs(score_keys=p(self.score_keys), histogram=p(self.histogram), segments=0,
                             seq_lens=p(self.row_valid), query_ends=0, topk=p(self.topk), status=p(self.status),
                             batch=rows, rows_per_request=1, key_stride=self.key_stride)
-        abi.check(self.library.kvip_hip_topk(ctypes.byref(topk), stream), "prefill TopK")
-        return self.topk[:rows]
+        # The bound tensors stay referenced for as long as their pointers are kept.
+        self._bound = (query, weights, query_scale, key, key_scale, cu_seqlens_q, seq_lens_k, block_table)
+        self._args, self._topk_args, self._rows = args, topk, rows
+
+    def score(self):
+        """Scoring launch: score keys, per-row visible lengths and high-byte histograms."""
+        abi.check(self.library.kvip_hip_indexer_prefill(ctypes.byref(self._args),
+                                                        abi.stream_handle(self.torch, self.device)), "prefill LI")
+
+    def select(self):
+        """TopK-2048 launch over the scored rows (consumes and re-zeroes the histograms)."""
+        abi.check(self.library.kvip_hip_topk(ctypes.byref(self._topk_args),
+                                             abi.stream_handle(self.torch, self.device)), "prefill TopK")
+        return self.topk[:self._rows]
 
 
 def quant_lightning_indexer(query, key, weights, query_dequant_scale, key_dequant_scale, actual_seq_lengths_query,

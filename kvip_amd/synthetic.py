@@ -9,6 +9,10 @@ Configurations:
   c1: batch 4, ctx 4096, bf16 Q/K ~N(0,1), fp32 weights ~N(0,1)/8, no scales.
   c2: batch 64, ctx ~U{8192..32768}, fp8 e4m3 Q/K from N(0,1) (saturating cast),
       per-token key scale ~U(0.5, 2), fp32 weights ~N(0,1)/8, KV rows of 656 bytes.
+  c3 (`prefill_workload`): one sequence, 4096 query rows against 65536 context tokens,
+      right-down causal (row i sees 61440 + i + 1 tokens), fp8 Q/K from N(0,1), per-row
+      query scales ~U(0.5, 1.5) and per-token key scales ~U(0.5, 2), fp32 weights
+      ~N(0,1)/8; the new rows' index-K sit at the sequence's last 4096 paged slots.
 """
 from __future__ import annotations
 
@@ -103,6 +107,34 @@ def config_workload(torch, name, device, seed=2026):
         return decode_workload(torch, batch=64, ctx_low=8192, ctx_high=32768, device=device, qk="fp8",
                                key_scale=True, seed=seed, max_context=32768)
     raise ValueError(f"unknown decode configuration {name!r}")
+
+
+def prefill_workload(torch, device, *, seed=2026, q_len=4096, k_len=65536, heads=64):
+    """Config-3 prefill chunk on the device: dict of the PrefillIndexer inputs plus the
+    slot_mapping [q_len] int64 and target positions [q_len] int64 of the new rows."""
+    rng = np.random.default_rng(seed)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    dev = torch.device(device)
+    blocks = (k_len + BLOCK_TOKENS - 1) // BLOCK_TOKENS
+    table = rng.permutation(blocks).astype(np.int32)[None, :]
+
+    def normal(shape):
+        return torch.randn(shape, generator=gen, device=dev, dtype=torch.float32)
+
+    keys = saturating_fp8(torch, normal((blocks, BLOCK_TOKENS, INDEX_DIM)))
+    query = saturating_fp8(torch, normal((q_len, heads, INDEX_DIM)))
+    weights = normal((q_len, heads)) / 8
+    query_scale = torch.rand((q_len, heads), generator=gen, device=dev, dtype=torch.float32) + 0.5
+    key_scale = torch.rand((blocks, BLOCK_TOKENS), generator=gen, device=dev, dtype=torch.float32) * 1.5 + 0.5
+    positions = np.arange(k_len - q_len, k_len, dtype=np.int64)
+    slots = table[0, positions // BLOCK_TOKENS].astype(np.int64) * BLOCK_TOKENS + positions % BLOCK_TOKENS
+    return dict(query=query, weights=weights, query_scale=query_scale, keys=keys, key_scale=key_scale,
+                block_table=torch.from_numpy(table).to(dev), cu_seqlens_q=torch.tensor([0, q_len], dtype=torch.int32,
+                                                                                       device=dev),
+                seq_lens_k=torch.tensor([k_len], dtype=torch.int32, device=dev),
+                slot_mapping=torch.from_numpy(slots).to(dev), positions=torch.from_numpy(positions).to(dev),
+                q_len=q_len, k_len=k_len, heads=heads)
 
 
 def bind(torch, kvip, wl, *, query_ends=None):
