@@ -27,6 +27,11 @@
 #include "indexer_tile.h"
 
 namespace kvip {
+
+// fp8 decode with one row per request: the LDS-ring kernel (indexer_ring.hip).
+bool ring_eligible(const KvipIndexerArgs& a);
+hipError_t launch_indexer_ring(const KvipIndexerArgs& a, hipStream_t stream);
+
 namespace {
 
 constexpr int kLiWaves = 4;
@@ -441,6 +446,7 @@ int stream_grid(K kernel) {
 
 template <int ELEM, int HEADS, int RPR, bool W_BF16>
 hipError_t launch_kernel(const KvipIndexerArgs& a, hipStream_t stream) {
+    if (ring_eligible(a)) return launch_indexer_ring(a, stream);
     if (a.batch <= kStreamMaxBatch) {
         auto kernel = indexer_stream_kernel<ELEM, HEADS, RPR, W_BF16>;
         const int grid = stream_grid(kernel);

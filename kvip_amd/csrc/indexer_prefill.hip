@@ -20,6 +20,7 @@
 // selector.py:126-154); the score formula is the decode one (op_kernel/indexer/
 // indexer_cube.h:161-322, indexer_score.h:384-426, score_common.h:66-97).
 #include "indexer_tile.h"
+#include "lds_async.h"
 
 namespace kvip {
 namespace {
@@ -34,61 +35,10 @@ constexpr int kPfSegment = 4096;                            // key positions per
 constexpr int kPfChunks = kPfSegment / kPfChunk;
 constexpr int kPfPages = kPfSegment / kBlockTokens;         // 32
 constexpr int kPfMaxSeq = KVIP_PREFILL_MAX_SEQUENCES;
-#define LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
-typedef int v2i __attribute__((ext_vector_type(2)));
-
 // LDS piece swizzle of a staged 128-byte K row: piece j of row r sits at slot j ^ (r & 7).
 // A fragment read (lane n reads piece j of row n) then touches 8 distinct 16-byte slots
 // in every group of 8 consecutive lanes, i.e. all 32 banks once per 128-byte phase.
 KVIP_DEVICE int pf_swizzle(int row) { return row & 7; }
-
-// LDS accesses inside the chunk loop are inline asm. The compiler's wait insertion cannot
-// tell an LDS read from the in-flight direct-to-LDS loads of the next chunk, and would
-// wait for those loads (vmcnt(0)) before every read, which serialises the double buffer.
-// Reads are issued and waited for in one asm block, so their registers are valid when it
-// ends; the chunk barrier waits for this wave's direct-to-LDS loads explicitly.
-KVIP_DEVICE uint32_t lds_addr(const void* p) {
-    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(LDS_PTR(p)));
-}
-
-// The four 16-byte K fragment pieces of a tile row and the row's key scale.
-KVIP_DEVICE void lds_read_tile(uint32_t a0, uint32_t a1, uint32_t a2, uint32_t a3, uint32_t as, v4i (&kb)[4],
-                               float& ks) {
-    asm volatile(
-        "ds_read_b128 %0, %5\n"
-        "ds_read_b128 %1, %6\n"
-        "ds_read_b128 %2, %7\n"
-        "ds_read_b128 %3, %8\n"
-        "ds_read_b32 %4, %9\n"
-        "s_waitcnt lgkmcnt(0)"
-        : "=&v"(kb[0]), "=&v"(kb[1]), "=&v"(kb[2]), "=&v"(kb[3]), "=&v"(ks)
-        : "v"(a0), "v"(a1), "v"(a2), "v"(a3), "v"(as));
-}
-
-KVIP_DEVICE v2i lds_read_b64(uint32_t a) {
-    v2i v;
-    asm volatile("ds_read_b64 %0, %1\ns_waitcnt lgkmcnt(0)" : "=&v"(v) : "v"(a));
-    return v;
-}
-
-KVIP_DEVICE void lds_write_b16(uint32_t a, uint32_t v) { asm volatile("ds_write_b16 %0, %1" : : "v"(a), "v"(v)); }
-
-KVIP_DEVICE void lds_add_u32(uint32_t a, uint32_t v) { asm volatile("ds_add_u32 %0, %1" : : "v"(a), "v"(v)); }
-
-// Workgroup barrier after this wave's LDS operations and all but its `stores` most recent
-// vector-memory operations (the key stores issued after the chunk's direct-to-LDS loads;
-// vector memory operations complete in issue order) have completed.
-KVIP_DEVICE void chunk_barrier(int stores) {
-    if (stores >= 2) {
-        asm volatile("s_waitcnt vmcnt(2) lgkmcnt(0)" : : : "memory");
-    } else if (stores == 1) {
-        asm volatile("s_waitcnt vmcnt(1) lgkmcnt(0)" : : : "memory");
-    } else {
-        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" : : : "memory");
-    }
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" : : : "memory");
-}
 
 template <bool W_BF16>
 KVIP_DEVICE float pf_weight(const KvipPrefillArgs& p, size_t idx) {
@@ -245,7 +195,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void indexer_prefill_kernel(const Kv
     int stores = 0;  // key stores this wave issued after the latest staging loads
     for (int c = 0; c < nchunks; ++c) {
         const int buf = c & 1;
-        chunk_barrier(stores);  // chunk c landed and is visible; buffer c+1 is free again
+        lds_barrier(stores);  // chunk c landed and is visible; buffer c+1 is free again
         if (c + 1 < nchunks) stage(c + 1, buf ^ 1);
         const int cstart = seg0 + c * kPfChunk;
         const float page_ok0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_ok), c * 2));
@@ -331,7 +281,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void indexer_prefill_kernel(const Kv
             ++stores;
         }
     }
-    chunk_barrier(0);
+    lds_barrier(0);
     // Histogram of the workgroup's rows.
     for (int i = tid; i < kPfBlockRows * 256; i += kPfThreads) {
         const int rq = i >> 8;

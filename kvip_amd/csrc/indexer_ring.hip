@@ -1,0 +1,359 @@
+// Decode lightning-indexer scoring for fp8 Q/K with one query row per request (the plain
+// decode step): a streaming kernel that feeds MFMA straight from a per-wave LDS ring.
+//
+// Work split: the (request, 32-token tile) pairs of the batch are flattened and every
+// wave of a grid that fills the GPU once takes one balanced, contiguous range of them.
+// Each wave owns a 4-slot LDS ring (4 KiB of K rows + 128 bytes of key scales per slot):
+// direct-to-LDS loads (global_load_lds_dwordx4) bring tile i+3 while tile i is scored.
+// The loads apply the fragment swizzle on the global side (LDS row r, 16-byte slot s
+// holds piece s ^ (r & 7) of token r's row), so the MFMA B fragments are read straight
+// from the ring, bank-conflict free, with no transposition and no barrier (the ring is
+// private to the wave). The wave waits for its own loads with an exact vmcnt: every
+// iteration issues the same vector memory instructions (tiles past the range end repeat
+// its last tile into their own slot).
+//
+// Q fragments and per-lane head weights (w'_h = w_h * qscale_h) of the current request
+// stay in registers and are reloaded when the range crosses a request boundary. Scoring
+// is the decode formula: fp8 MFMA (v_mfma_scale_f32_32x32x64_f8f6f4), ReLU, head
+// weights, head reduction, key scale, bf16 half-away rounding, sortable key. Tiles are
+// finished in pairs: after each tile's per-lane-half head reduction a v_permlane32_swap
+// leaves tile A's token totals in lanes 0-31 and tile B's in lanes 32-63, so scaling,
+// rounding, the key store and the histogram update run once for two tiles. The 256-bin
+// high-byte histogram of each request is kept per wave in LDS (two buffers, for the at
+// most two requests a pair can touch) and added to the global rows when the request's
+// last tile of the range has been counted.
+//
+// Reference: QLIMatmul::ComputeMm1 (op_kernel/indexer/indexer_cube.h:161-322),
+// MulWeightAndReduceSum (indexer_score.h:384-426, loop :60-103, finalize :105-140),
+// FloatToSortableKey (score_common.h:66-97).
+#include "indexer_tile.h"
+#include "lds_async.h"
+
+namespace kvip {
+namespace {
+
+constexpr int kRgWaves = 4;
+constexpr int kRgThreads = kRgWaves * 64;
+constexpr int kRgSlots = 4;                          // ring slots per wave
+constexpr int kRgTileBytes = 32 * kIndexDim;         // 32 fp8 rows
+constexpr int kRgSlotBytes = kRgTileBytes + 32 * 4;  // + 32 key scales
+constexpr int kRgPass = 64;                          // tiles described per pass (one per lane)
+constexpr int kRgMaxBatch = 512;
+// Vector memory instructions per tile load: 4 K pieces + 1 key-scale piece.
+constexpr int kRgOps = 5;
+// s_waitcnt immediate (gfx9 encoding) for vmcnt(0), expcnt and lgkmcnt unconstrained.
+constexpr int kVmcntZero = 0x0F70;
+constexpr int kVmcnt15 = 0x0F7F;  // vmcnt(15)
+
+// Stands in for a missing key-scale array (stride 0): 128 unit scales.
+__device__ __align__(16) float kRingUnitScale[kBlockTokens] = {
+    1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f,
+    1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f,
+    1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f,
+    1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f,
+    1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f,
+    1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f,
+    1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f,
+    1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f};
+
+// Weights w'_h = w_h * qscale_h of heads [h, h + 4) of row `row` (h a multiple of 4).
+template <int HEADS, bool W_BF16>
+KVIP_DEVICE v4f rg_weights4(const KvipIndexerArgs& p, int row, int h, bool qscale) {
+    const size_t idx = static_cast<size_t>(row) * HEADS + h;
+    v4f w;
+    if constexpr (W_BF16) {
+        const v2i raw = *reinterpret_cast<const v2i*>(static_cast<const uint16_t*>(p.weights) + idx);
+        w = v4f{__uint_as_float(static_cast<uint32_t>(raw[0]) << 16),
+                __uint_as_float(static_cast<uint32_t>(raw[0]) & 0xFFFF0000u),
+                __uint_as_float(static_cast<uint32_t>(raw[1]) << 16),
+                __uint_as_float(static_cast<uint32_t>(raw[1]) & 0xFFFF0000u)};
+    } else {
+        w = *reinterpret_cast<const v4f*>(static_cast<const float*>(p.weights) + idx);
+    }
+    if (qscale) w *= *reinterpret_cast<const v4f*>(p.query_scale + idx);
+    return w;
+}
+
+// Visible tokens of request b's single query row.
+KVIP_DEVICE int rg_valid(const KvipIndexerArgs& p, int b) {
+    int v = max(p.seq_lens[b], 0);
+    if (p.query_ends != nullptr) v = min(v, p.query_ends[b]);
+    return min(max(v, 0), p.max_blocks * kBlockTokens);
+}
+
+template <int HEADS, bool W_BF16>
+__global__ __launch_bounds__(kRgThreads, 2) void indexer_ring_kernel(const KvipIndexerArgs p) {
+    constexpr int MT = HEADS / 32;
+    __shared__ __align__(16) uint8_t s_ring[kRgWaves][kRgSlots][kRgSlotBytes];
+    __shared__ __align__(16) uint32_t s_hist[kRgWaves][2][256];
+    __shared__ int s_prefix[kRgMaxBatch + 1];
+    __shared__ uint32_t s_scan[kRgWaves];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n = lane & 31;
+    const int g = lane >> 5;
+
+    // Tile counts per request -> prefix sums (whole workgroup, before any ring load).
+    int running = 0;
+    for (int base = 0; base < p.batch; base += kRgThreads) {
+        const int b = base + tid;
+        const int c = b < p.batch ? (rg_valid(p, b) + 31) / 32 : 0;
+        uint32_t total;
+        const uint32_t excl = block_exclusive_scan(static_cast<uint32_t>(c), s_scan, &total);
+        if (b < p.batch) s_prefix[b] = running + static_cast<int>(excl);
+        running += static_cast<int>(total);
+    }
+    if (tid == 0) s_prefix[p.batch] = running;
+    for (int i = tid; i < kRgWaves * 2 * 256; i += kRgThreads) (&s_hist[0][0][0])[i] = 0u;
+    __syncthreads();
+
+    // This wave's balanced share [t, t_end) of the flattened tile list.
+    const int total_tiles = s_prefix[p.batch];
+    const int64_t nw = static_cast<int64_t>(gridDim.x) * kRgWaves;
+    const int64_t w = static_cast<int64_t>(blockIdx.x) * kRgWaves + wave;
+    int t = static_cast<int>(total_tiles * w / nw);
+    const int t_end = static_cast<int>(total_tiles * (w + 1) / nw);
+    if (t >= t_end) return;  // no barrier follows: waves run independently from here
+
+    uint8_t* ring = &s_ring[wave][0][0];
+    const uint32_t ring_lds = lds_addr(ring);
+    // Fragment reads (slot 0): lane (n, g) reads pieces g*4 + u of row n.
+    uint32_t ka[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) ka[u] = ring_lds + n * kIndexDim + (((g * 4 + u) ^ (n & 7)) * 16);
+    const uint32_t ksa = ring_lds + kRgTileBytes + n * 4;
+    const uint32_t hist_lds = lds_addr(&s_hist[wave][0][0]);
+    // Ring loads: in the v-th 1 KiB of a slot, lane L fills LDS row 8v + L/8, slot L%8, with
+    // piece (L%8) ^ (L/8) of that token's row (rows 8v + L/8 have swizzle L/8).
+    const int src_lane = (lane >> 3) * kIndexDim + (((lane & 7) ^ (lane >> 3)) * 16);
+    const uint8_t* kbase = static_cast<const uint8_t*>(p.keys);
+    const float* kscale = p.key_scale != nullptr ? p.key_scale : kRingUnitScale;
+    const int64_t kscale_stride = p.key_scale != nullptr ? p.scale_block_stride : 0;
+    uint32_t err = 0;
+
+    v4i qa[MT][4];
+    float wr[MT * 16];
+    int qb = -1;  // request whose Q fragments and weights are loaded
+    const bool qscale = p.query_scale != nullptr;
+    auto load_q = [&](int b) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            const v4i* src = reinterpret_cast<const v4i*>(static_cast<const uint8_t*>(p.query) +
+                                                          (static_cast<size_t>(b) * HEADS + mt * 32 + n) * kIndexDim +
+                                                          g * (kIndexDim / 2));
+#pragma unroll
+            for (int v = 0; v < 4; ++v) qa[mt][v] = src[v];
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4) {
+                const v4f w4 = rg_weights4<HEADS, W_BF16>(p, b, mt * 32 + r4 * 8 + g * 4, qscale);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) wr[mt * 16 + r4 * 4 + j] = w4[j];
+            }
+        }
+    };
+
+    // The run's histogram (one request) in LDS, added to the global row at the run's end.
+    auto flush = [&](int req) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t a = hist_lds + (k * 64 + lane) * 4;
+            const uint32_t c = lds_read_b32(a);
+            if (c != 0u) {
+                atomicAdd(&p.histogram[static_cast<size_t>(req) * 256 + k * 64 + lane], c);
+                lds_write_b32(a, 0u);
+            }
+        }
+    };
+
+    while (t < t_end) {
+        const int cnt = min(t_end - t, kRgPass);
+        // Lane i describes tile t + i: request, tile within the request, page, validity.
+        int d_b = 0, d_k = 0, d_page = 0, d_valid = 0;
+        float d_ok = 0.0f;
+        if (lane < cnt) {
+            const int tt = t + lane;
+            int lo = 0, hi = p.batch - 1;  // largest b with s_prefix[b] <= tt
+            while (lo < hi) {
+                const int mid = (lo + hi + 1) >> 1;
+                if (s_prefix[mid] <= tt) lo = mid; else hi = mid - 1;
+            }
+            d_b = lo;
+            d_k = tt - s_prefix[lo];
+            const int id = p.block_table[static_cast<size_t>(d_b) * p.max_blocks + (d_k >> 2)];
+            const bool ok = static_cast<unsigned>(id) < static_cast<unsigned>(p.num_blocks);
+            d_page = ok ? id : 0;
+            d_ok = ok ? 1.0f : 0.0f;
+            if (!ok) err |= KVIP_STATUS_BAD_BLOCK;
+            d_valid = rg_valid(p, d_b);
+        }
+        // Tiles whose request differs from the next tile's end a run (lane cnt - 1 always).
+        const int next_b = __shfl_down(d_b, 1);
+        const uint64_t run_ends = __ballot(lane < cnt && (lane == cnt - 1 || next_b != d_b));
+
+        auto issue = [&](int j) {
+            const int jj = min(j, cnt - 1);
+            const int page = __builtin_amdgcn_readlane(d_page, jj);
+            const int k = __builtin_amdgcn_readlane(d_k, jj);
+            uint8_t* dst = ring + (j & (kRgSlots - 1)) * kRgSlotBytes;
+            const uint8_t* src = kbase + static_cast<size_t>(page) * p.key_block_stride + (k & 3) * kRgTileBytes + src_lane;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                __builtin_amdgcn_global_load_lds(src + v * 1024, LDS_PTR(dst + v * 1024), 16, 0, 0);
+            }
+            if (lane < 8) {
+                const float* ssrc = kscale + static_cast<size_t>(page) * kscale_stride + (k & 3) * 32 + lane * 4;
+                __builtin_amdgcn_global_load_lds(ssrc, LDS_PTR(dst + kRgTileBytes), 16, 0, 0);
+            }
+        };
+
+        // Scores tile i with the current Q and stores its keys (one store instruction).
+        auto score = [&](int i) {
+            const uint32_t so = (i & (kRgSlots - 1)) * kRgSlotBytes;
+            v4i kb[4];
+            float ks_raw;
+            lds_read_tile(ka[0] + so, ka[1] + so, ka[2] + so, ka[3] + so, ksa + so, kb, ks_raw);
+            float pj[4] = {0.f, 0.f, 0.f, 0.f};
+            v16f acc[2];
+            acc[0] = v16f{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            Mma<1>::step(0, qa[0], kb, acc[0]);
+            Mma<1>::step(1, qa[0], kb, acc[0]);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                v16f& cur = acc[mt & 1];
+                if (mt + 1 < MT) {
+                    v16f& nxt = acc[(mt + 1) & 1];
+                    nxt = v16f{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+                    Mma<1>::step(0, qa[mt + 1], kb, nxt);
+                    Mma<1>::step(1, qa[mt + 1], kb, nxt);
+                }
+#pragma unroll
+                for (int r4 = 0; r4 < 4; ++r4) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        // ReLU as an integer max: negative floats (sign bit set) map to +0.
+                        const float relu = __int_as_float(max(__float_as_int(cur[r4 * 4 + j]), 0));
+                        pj[j] = fmaf(relu, wr[mt * 16 + r4 * 4 + j], pj[j]);
+                    }
+                }
+                if (mt + 1 < MT) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+            float part = (pj[0] + pj[1]) + (pj[2] + pj[3]);
+            // Add the other lane half's heads (v_permlane32_swap: lane l <-> lane l ^ 32).
+            const auto swapped =
+                __builtin_amdgcn_permlane32_swap(__float_as_int(part), __float_as_int(part), false, false);
+            part += __int_as_float(g == 0 ? swapped[1] : swapped[0]);
+            const float ks = ks_raw * __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, d_ok), i));
+            const uint32_t key = sortable_key(bf16_bits_half_away(part * ks));
+            const int b = __builtin_amdgcn_readlane(d_b, i);
+            const int tok = __builtin_amdgcn_readlane(d_k, i) * 32 + n;
+            if (g == 0) {  // lanes 0-31: one store instruction per tile
+                p.score_keys[static_cast<size_t>(b) * p.key_stride + tok] = static_cast<uint16_t>(key);
+                if (tok < __builtin_amdgcn_readlane(d_valid, i)) lds_add_u32(hist_lds + (key >> 8) * 4, 1u);
+            }
+        };
+
+        // Q of the pass's first request is loaded ahead of the ring loads and waited for
+        // with them in flight (loads complete in order: at most the 15 ring-load
+        // instructions issued after it may remain).
+        const int b_first = __builtin_amdgcn_readlane(d_b, 0);
+        if (b_first != qb) {
+            load_q(b_first);
+            qb = b_first;
+        }
+        issue(0);
+        issue(1);
+        issue(2);
+        __builtin_amdgcn_s_waitcnt(kVmcnt15);
+        // Pipeline: loads of tiles i+1..i+3 stay in flight while tile i is scored. The
+        // vmcnt of each wait counts the vector memory instructions issued after tile i's
+        // loads (3 tile loads of kRgOps instructions plus the key stores in between);
+        // a Q reload or histogram flush in between only makes a wait longer.
+        int i = 0;
+        while (i < cnt) {  // runs of one request
+            const int b = __builtin_amdgcn_readlane(d_b, i);
+            if (b != qb) {
+                load_q(b);
+                qb = b;
+                __builtin_amdgcn_s_waitcnt(kVmcntZero);  // after the ring loads in flight
+            }
+            const uint64_t later = run_ends >> i;
+            const int run_end = i + static_cast<int>(__builtin_ctzll(later)) + 1;
+            for (; i < run_end; ++i) {
+                issue(i + 3);
+                if (i >= 3) {
+                    wait_vmcnt<3 * kRgOps + 3>();
+                } else if (i == 2) {
+                    wait_vmcnt<3 * kRgOps + 2>();
+                } else if (i == 1) {
+                    wait_vmcnt<3 * kRgOps + 1>();
+                } else {
+                    wait_vmcnt<3 * kRgOps>();
+                }
+                score(i);
+            }
+            flush(b);
+        }
+        wait_vmcnt<0>();  // repeated tail loads land before the ring is reused
+        t += cnt;
+    }
+    report(p.status, err);
+}
+
+// Workgroups per CU the kernel keeps resident times the CU count.
+template <typename K>
+int ring_grid(K kernel) {
+    static int grid = 0;
+    if (grid == 0) {
+        int dev = 0, cus = 0, per_cu = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kRgThreads, 0) != hipSuccess) {
+            return 0;
+        }
+        grid = max(1, cus * max(per_cu, 1));
+    }
+    return grid;
+}
+
+template <int HEADS, bool W_BF16>
+hipError_t launch_ring_kernel(const KvipIndexerArgs& a, hipStream_t stream) {
+    auto kernel = indexer_ring_kernel<HEADS, W_BF16>;
+    const int grid = ring_grid(kernel);
+    if (grid == 0) return hipErrorInvalidDevice;
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(kRgThreads), 0, stream, a);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+// fp8, one row per request, batch within the LDS prefix table, 16-byte aligned key-scale
+// rows (direct-to-LDS loads move 16 bytes per lane) and 16-byte (8-byte for bf16) aligned
+// weight and query-scale rows (vector loads of 4 heads).
+bool ring_eligible(const KvipIndexerArgs& a) {
+    const uintptr_t wal = a.weight_dtype == KVIP_DTYPE_BF16 ? 7u : 15u;
+    return a.qk_dtype == KVIP_DTYPE_FP8_E4M3 && a.rows_per_request == 1 && a.batch <= kRgMaxBatch &&
+           (reinterpret_cast<uintptr_t>(a.weights) & wal) == 0 &&
+           (a.query_scale == nullptr || (reinterpret_cast<uintptr_t>(a.query_scale) & 15u) == 0) &&
+           (a.key_scale == nullptr ||
+            ((reinterpret_cast<uintptr_t>(a.key_scale) & 15u) == 0 && a.scale_block_stride % 4 == 0));
+}
+
+hipError_t launch_indexer_ring(const KvipIndexerArgs& a, hipStream_t stream) {
+    if (a.heads == 64) {
+        return a.weight_dtype == KVIP_DTYPE_BF16 ? launch_ring_kernel<64, true>(a, stream)
+                                                 : launch_ring_kernel<64, false>(a, stream);
+    }
+    return a.weight_dtype == KVIP_DTYPE_BF16 ? launch_ring_kernel<32, true>(a, stream)
+                                             : launch_ring_kernel<32, false>(a, stream);
+}
+
+}  // namespace kvip
