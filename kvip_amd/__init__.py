@@ -16,6 +16,7 @@ __all__ = [
     "ResidentPrefix",
     "PrefillIndexer",
     "quant_lightning_indexer",
+    "MixedRound",
     "SlotLRU",
     "update_abc",
     "lidu",
@@ -34,6 +35,7 @@ _EXPORTS = {
     "ResidentPrefix": ("operators.lifetch.resident", "ResidentPrefix"),
     "PrefillIndexer": ("operators.prefill", "PrefillIndexer"),
     "quant_lightning_indexer": ("operators.prefill", "quant_lightning_indexer"),
+    "MixedRound": ("operators.mixed", "MixedRound"),
     "SlotLRU": ("cache.lru", "SlotLRU"),
     "update_abc": ("cache.abc", "update_abc"),
     "lidu": ("operators.lidu", "lidu"),

@@ -1,0 +1,79 @@
+"""One continuous-batching round over decode requests and packed prefill chunks.
+
+The reference's vLLM selector runs a mixed batch as: Index ingest of the round's new tokens
+(python/kvip/adapters/vllm/selector.py:102-106 -> index_import.py:17-56), the fused LIFetch
+forward for the decode rows (:110-112) and the native prefill indexer for each prefill
+chunk (:126-154). `MixedRound` enqueues the same three stages on the current stream with
+buffers bound once, so the whole round is one hipGraph:
+
+  1. one list-mode `kvip_hip_ingest_index` launch copies every new token's index-K row and
+     scale from the paged cache (`sources`: cache row = block * 128 + offset) to its Index
+     storage row (`targets`: owner * history + position);
+  2. the decode forward (`kvip_amd.LIFetch` over a `ResidentIndexUpdate`, or a
+     `ContiguousFetch`): LI over the owners' Index rows, TopK, resolver, Fetch, Index update
+     and outputs;
+  3. the prefill indexer bound with `PrefillIndexer.bind`: LI over the paged cache for the
+     packed chunks (cumulative query lengths) and TopK-2048 per row.
+
+The caller fills the per-round inputs in place before a launch or replay: decode Q /
+weights / lengths, the prefill buffers it bound, and `sources` / `targets` of the new
+tokens. Device errors land in the status words of the three stages.
+"""
+from __future__ import annotations
+
+import ctypes
+
+from kvip_amd.runtime import abi
+
+INDEX_DIM = 128
+
+
+class MixedRound:
+    def __init__(self, torch, *, decode, prefill, storage_keys, storage_scales, cache_keys, cache_scales,
+                 new_tokens, status=None):
+        """decode: a LIFetch forward; prefill: a PrefillIndexer after `bind(...)`;
+        storage_keys [owners, history, 128] (fp8 or uint8) and storage_scales
+        [owners, history] float32: the persistent Index rows; cache_keys
+        [blocks, 128, 128] and cache_scales [blocks, 128]: the paged index-K cache the new
+        tokens are read from; new_tokens: rows ingested per round."""
+        if getattr(prefill, "_args", None) is None:
+            raise ValueError("bind the prefill indexer before building the round")
+        if storage_keys.dim() != 3 or storage_keys.shape[2] != INDEX_DIM or storage_keys.element_size() != 1:
+            raise ValueError("Index storage keys must be 1-byte [owners, history, 128]")
+        if not storage_keys.is_contiguous() or storage_scales.dtype != torch.float32 or not storage_scales.is_contiguous():
+            raise ValueError("Index storage must be contiguous with float32 scales")
+        if tuple(storage_scales.shape) != tuple(storage_keys.shape[:2]):
+            raise ValueError("Index storage scales must be [owners, history]")
+        if cache_keys.dim() != 3 or tuple(cache_keys.shape[1:]) != (128, INDEX_DIM) or cache_keys.element_size() != 1:
+            raise ValueError("paged index-K cache must be 1-byte [blocks, 128, 128]")
+        if not cache_keys.is_contiguous() or cache_scales.dtype != torch.float32 or not cache_scales.is_contiguous():
+            raise ValueError("paged index-K cache and its scales must be contiguous (scales float32)")
+        if tuple(cache_scales.shape) != tuple(cache_keys.shape[:2]):
+            raise ValueError("paged key scales must be [blocks, 128]")
+        if new_tokens < 1:
+            raise ValueError("a round ingests at least one new token")
+        dev = storage_keys.device
+        self.torch, self.decode, self.prefill, self.device = torch, decode, prefill, dev
+        self.storage_keys, self.storage_scales = storage_keys, storage_scales
+        self.cache_keys, self.cache_scales = cache_keys, cache_scales
+        self.sources = torch.zeros(new_tokens, dtype=torch.int64, device=dev)
+        self.targets = torch.zeros(new_tokens, dtype=torch.int64, device=dev)
+        self.status = torch.zeros(1, dtype=torch.int32, device=dev) if status is None else status
+        p = abi.ptr
+        self.ingest_args = abi.IngestArgs(
+            source_keys=p(cache_keys), source_scales=p(cache_scales), target_keys=p(storage_keys),
+            target_scales=p(storage_scales), sources=p(self.sources), targets=p(self.targets),
+            status=p(self.status), source_rows=cache_keys.shape[0] * 128,
+            target_rows=storage_keys.shape[0] * storage_keys.shape[1], count=new_tokens, target_base=0,
+            mode=abi.INGEST_LIST)
+        self.library = abi.load_library()
+
+    def ingest(self):
+        abi.check(self.library.kvip_hip_ingest_index(ctypes.byref(self.ingest_args),
+                                                     abi.stream_handle(self.torch, self.device)), "mixed ingest")
+
+    def __call__(self):
+        self.ingest()
+        self.decode()
+        self.prefill.score()
+        return self.prefill.select()

@@ -137,6 +137,97 @@ def prefill_workload(torch, device, *, seed=2026, q_len=4096, k_len=65536, heads
                 q_len=q_len, k_len=k_len, heads=heads)
 
 
+def mixed_workload(torch, kvip, device, *, seed=2026, decode_ctx=None, history=65536, resident=16384,
+                   prefill=((2048, 8192), (1536, 1536)), heads=64):
+    """BASELINE config 5 round: decode requests (one row each, contexts `decode_ctx`, default
+    32 requests ~U[4096, 65536]) on the resident cache (owner Index rows of `history`
+    positions, `resident` hot slots, misses from a pinned host pool) plus prefill chunks
+    (q_len, k_len) packed TND-style against a paged index-K cache; every new token (the
+    last position of each decode request, the chunks' rows) is ingested into the Index
+    storage. Returns a SimpleNamespace with the bound `round` (a kvip.MixedRound) and its
+    parts; inputs are seeded and already resident on the device."""
+    from types import SimpleNamespace
+
+    rng = np.random.default_rng(seed)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    dev = torch.device(device)
+    if decode_ctx is None:
+        decode_ctx = rng.integers(4096, history + 1, size=32)
+    decode_ctx = np.asarray(decode_ctx, dtype=np.int64)
+    nd, npf = len(decode_ctx), len(prefill)
+    owners = nd + npf
+
+    def normal(shape):
+        return torch.randn(shape, generator=gen, device=dev, dtype=torch.float32)
+
+    # Persistent Index storage (fp8 codes with the NaN bit pattern masked out) and KV rows.
+    keys = (torch.randint(0, 256, (owners, history, 128), generator=gen, device=dev, dtype=torch.uint8) & 0x77)
+    keys = keys.view(torch.float8_e4m3fn)
+    scales = torch.rand((owners, history), generator=gen, device=dev) * 1.5 + 0.5
+    addresses = (torch.arange(owners * history, device=dev, dtype=torch.int64) * 656).view(owners, history)
+    logical = torch.arange(history, device=dev, dtype=torch.int64).repeat(owners, 1)
+    pool = torch.empty(owners * history * 656, dtype=torch.uint8, pin_memory=True)
+    hot = torch.zeros((owners, resident, 656), dtype=torch.uint8, device=dev)
+    valid = torch.ones((owners, resident), dtype=torch.int32, device=dev)
+    # Paged index-K cache: the prefill sequences' pages, then one page per 128 decode tokens.
+    pf_blocks = [(k + BLOCK_TOKENS - 1) // BLOCK_TOKENS for _, k in prefill]
+    dec_blocks = (nd + BLOCK_TOKENS - 1) // BLOCK_TOKENS
+    nblocks = sum(pf_blocks) + dec_blocks
+    perm = rng.permutation(nblocks).astype(np.int32)
+    cache_keys = saturating_fp8(torch, normal((nblocks, BLOCK_TOKENS, INDEX_DIM)))
+    cache_scales = torch.rand((nblocks, BLOCK_TOKENS), generator=gen, device=dev) * 1.5 + 0.5
+    max_pf_blocks = max(pf_blocks)
+    pf_table = np.zeros((npf, max_pf_blocks), np.int32)
+    at = 0
+    for s, nb in enumerate(pf_blocks):
+        pf_table[s, :nb] = perm[at:at + nb]
+        at += nb
+    dec_pages = perm[at:at + dec_blocks]
+    # New tokens: decode request b's token at position ctx_b - 1, then the chunks' rows.
+    sources, targets = [], []
+    for b, c in enumerate(decode_ctx):
+        sources.append(int(dec_pages[b // BLOCK_TOKENS]) * BLOCK_TOKENS + b % BLOCK_TOKENS)
+        targets.append(b * history + int(c) - 1)
+    for s, (q_len, k_len) in enumerate(prefill):
+        pos = np.arange(k_len - q_len, k_len)
+        sources += list(pf_table[s, pos // BLOCK_TOKENS].astype(np.int64) * BLOCK_TOKENS + pos % BLOCK_TOKENS)
+        targets += list((nd + s) * history + pos)
+    # Decode binding on the resident cache.
+    rot = kvip.LIFetchBinding(torch, batch=nd, max_context=history, device=dev, heads=heads, rows_per_request=1,
+                              qk_dtype="fp8", query_ends=True)
+    rot.query.copy_(saturating_fp8(torch, normal(tuple(rot.query.shape))))
+    rot.weights.copy_(normal(tuple(rot.weights.shape)) / 8)
+    ctx_t = torch.from_numpy(decode_ctx.astype(np.int32)).to(dev)
+    rot.seq_lens.copy_(ctx_t)
+    rot.query_ends.copy_(ctx_t)
+    upd = kvip.ResidentIndexUpdate(torch, keys=keys, scales=scales, addresses=addresses, logical_ids=logical,
+                                   row_owners=torch.arange(nd, dtype=torch.int32, device=dev), rotating=rot,
+                                   hot_valid=valid, hot_cache=hot, host_pool=pool, resident=resident)
+    upd.set_candidates(torch.arange(2048, dtype=torch.int32, device=dev).repeat(nd, 1))
+    # Prefill chunks.
+    rows = sum(q for q, _ in prefill)
+    pf_query = saturating_fp8(torch, normal((rows, heads, INDEX_DIM)))
+    pf_weights = normal((rows, heads)) / 8
+    pf_qscale = torch.rand((rows, heads), generator=gen, device=dev) + 0.5
+    cu = torch.tensor(np.concatenate([[0], np.cumsum([q for q, _ in prefill])]), dtype=torch.int32, device=dev)
+    kl = torch.tensor([k for _, k in prefill], dtype=torch.int32, device=dev)
+    table = torch.from_numpy(pf_table).to(dev)
+    pidx = kvip.PrefillIndexer(torch, max_rows=rows, max_context=max_pf_blocks * BLOCK_TOKENS, max_sequences=npf,
+                               device=dev, heads=heads)
+    pidx.bind(pf_query, pf_weights, pf_qscale, cache_keys, cache_scales, cu, kl, table)
+    forward = kvip.LIFetch(rot, upd)
+    rnd = kvip.MixedRound(torch, decode=forward, prefill=pidx, storage_keys=keys, storage_scales=scales,
+                          cache_keys=cache_keys, cache_scales=cache_scales, new_tokens=len(sources))
+    rnd.sources.copy_(torch.tensor(sources, dtype=torch.int64))
+    rnd.targets.copy_(torch.tensor(targets, dtype=torch.int64))
+    return SimpleNamespace(round=rnd, rot=rot, update=upd, forward=forward, prefill=pidx, keys=keys, scales=scales,
+                           addresses=addresses, logical=logical, hot=hot, valid=valid, pool=pool,
+                           cache_keys=cache_keys, cache_scales=cache_scales, pf_query=pf_query, pf_weights=pf_weights,
+                           pf_qscale=pf_qscale, cu=cu, kl=kl, table=table, decode_ctx=decode_ctx, chunks=prefill,
+                           history=history, resident=resident, sources=sources, targets=targets)
+
+
 def bind(torch, kvip, wl, *, query_ends=None):
     """LIFetchBinding + ContiguousFetch + LIFetch forward for a workload."""
     heads = int(wl.query.shape[1])
