@@ -72,7 +72,7 @@
 extern "C" {
 #endif
 
-#define KVIP_HIP_ABI_VERSION 3u
+#define KVIP_HIP_ABI_VERSION 5u
 
 #define KVIP_TOPK 2048
 #define KVIP_BLOCK_TOKENS 128
@@ -209,11 +209,24 @@ typedef struct KvipFetchArgs {
 
 /* One decode round: scoring -> TopK-2048 -> Fetch gather, stream-ordered. With the
  * scoring histogram and segment work memory in `topk`, TopK and Fetch run as one fused
- * launch (kvip_hip_select_fetch). */
+ * launch (kvip_hip_select_fetch). With `round_work` (KVIP_ROUND_WORK_WORDS(rows) words,
+ * 128-byte aligned, zero before the first launch; every launch leaves it zero), fp8 Q/K,
+ * one row per request, at most KVIP_ROUND_MAX_ROWS requests and 656-byte KV rows, the
+ * whole round is one persistent launch in which each request's selection overlaps the
+ * scoring of later requests and the gathers of earlier ones (score keys are then written
+ * only for rows of at least 2048 tokens, and the histogram is not used). Layout: per XCD a
+ * line of counters, per request a completion line, per publication slot a line, per
+ * request a 256-bin histogram. Launches that share one work memory must not overlap. */
+#define KVIP_ROUND_MAX_ROWS 256
+#define KVIP_ROUND_MAX_XCDS 16
+#define KVIP_ROUND_LINE_WORDS 32
+#define KVIP_ROUND_WORK_WORDS(rows) \
+    (KVIP_ROUND_MAX_XCDS * KVIP_ROUND_LINE_WORDS + (2 * KVIP_ROUND_LINE_WORDS + 256) * (rows))
 typedef struct KvipLIFetchArgs {
     KvipIndexerArgs indexer;
     KvipTopkArgs topk;
     KvipFetchArgs fetch;
+    uint32_t* round_work;        /* single-launch round work memory, or NULL */
 } KvipLIFetchArgs;
 
 /* ABC ring maps: token_to_slot / slot_to_token are int32 [layers, pool, tokens];
@@ -466,6 +479,15 @@ uint32_t kvip_hip_topk(const KvipTopkArgs* args, void* stream);
 uint32_t kvip_hip_fetch_gather(const KvipFetchArgs* args, void* stream);
 uint32_t kvip_hip_indexer_prefill(const KvipPrefillArgs* args, void* stream);
 uint32_t kvip_hip_lifetch_forward(const KvipLIFetchArgs* args, void* stream);
+/* The launch plan kvip_hip_lifetch_forward takes for these arguments (no launch, no device
+ * access): KVIP_LIFETCH_PLAN_ROUND (one persistent launch), _SELECT_FETCH (scoring, then
+ * TopK fused with the gather) or _THREE (scoring, TopK, gather); KVIP_ERR_INVALID when the
+ * forward would reject them. A host query with no counterpart in the reference, for
+ * callers and tests that need to know which kernels a round runs. */
+#define KVIP_LIFETCH_PLAN_THREE 0u
+#define KVIP_LIFETCH_PLAN_SELECT_FETCH 1u
+#define KVIP_LIFETCH_PLAN_ROUND 2u
+uint32_t kvip_hip_lifetch_plan(const KvipLIFetchArgs* args);
 /* TopK-2048 of rows scored by kvip_hip_indexer_decode fused with the Fetch gather of the
  * selected rows: same outputs as kvip_hip_topk followed by kvip_hip_fetch_gather. Needs
  * topk->histogram and topk->segments; fetch->topk must be topk->topk. */

@@ -59,6 +59,14 @@ KVIP_DEVICE void lds_write_b32(uint32_t a, uint32_t v) { asm volatile("ds_write_
 
 KVIP_DEVICE void lds_add_u32(uint32_t a, uint32_t v) { asm volatile("ds_add_u32 %0, %1" : : "v"(a), "v"(v)); }
 
+KVIP_DEVICE v4i lds_read_b128(uint32_t a) {
+    v4i v;
+    asm volatile("ds_read_b128 %0, %1\ns_waitcnt lgkmcnt(0)" : "=&v"(v) : "v"(a));
+    return v;
+}
+
+KVIP_DEVICE void lds_write_b128(uint32_t a, v4i v) { asm volatile("ds_write_b128 %0, %1" : : "v"(a), "v"(v)); }
+
 // Waits until at most N vector memory instructions of this wave are outstanding (N is a
 // compile-time count, 0..63).
 template <int N>

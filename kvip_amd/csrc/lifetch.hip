@@ -2,7 +2,8 @@
 // Fetch gather, enqueued back to back on one stream (no allocation, no sync, no
 // memset), so the whole round can be captured into a single hipGraph. When the TopK
 // arguments carry the scoring histogram and segment work memory, TopK and the gather
-// run as one fused launch (select_fetch.hip).
+// run as one fused launch (select_fetch.hip); with the round work memory the whole round
+// is one persistent launch (round_fused.hip).
 //
 // Replaces kvip_lifetch_streaming_forward (csrc/operators/lightning_indexer_with_fetch/
 // include/api.h:7, op_host/launch.cpp:76-83), whose init -> LI -> resolve/update/fetch
@@ -18,11 +19,17 @@ hipError_t launch_topk(const KvipTopkArgs& a, hipStream_t stream);
 hipError_t launch_fetch(const KvipFetchArgs& a, hipStream_t stream);
 uint32_t validate_select_fetch(const KvipTopkArgs* t, const KvipFetchArgs* f);
 hipError_t launch_select_fetch(const KvipTopkArgs& t, const KvipFetchArgs& f, hipStream_t stream);
+bool round_fused_eligible(const KvipIndexerArgs& a, const KvipTopkArgs& t, const KvipFetchArgs& f,
+                          const uint32_t* work);
+hipError_t launch_round_fused(const KvipIndexerArgs& a, const KvipFetchArgs& f, uint32_t* work, hipStream_t stream);
 }  // namespace kvip
 
 extern "C" uint32_t kvip_hip_abi_version(void) { return KVIP_HIP_ABI_VERSION; }
 
-extern "C" uint32_t kvip_hip_lifetch_forward(const KvipLIFetchArgs* args, void* stream) {
+namespace {
+// Validates the chained arguments and picks the launch plan (KVIP_LIFETCH_PLAN_*), or
+// returns KVIP_ERR_INVALID.
+uint32_t lifetch_plan(const KvipLIFetchArgs* args) {
     if (args == nullptr) return KVIP_ERR_INVALID;
     const KvipIndexerArgs& li = args->indexer;
     const KvipTopkArgs& tk = args->topk;
@@ -38,12 +45,29 @@ extern "C" uint32_t kvip_hip_lifetch_forward(const KvipLIFetchArgs* args, void* 
                          tk.rows_per_request == li.rows_per_request && fe.topk == tk.topk &&
                          fe.batch == li.batch && fe.rows_per_request == li.rows_per_request;
     if (!chained) return KVIP_ERR_INVALID;
+    // With the round work memory the whole round is one persistent launch; with the
+    // histogram and segment work memory, TopK and Fetch run as one launch.
+    if (args->round_work != nullptr && kvip::round_fused_eligible(li, tk, fe, args->round_work)) {
+        return KVIP_LIFETCH_PLAN_ROUND;
+    }
+    if (kvip::validate_select_fetch(&tk, &fe) == KVIP_OK) return KVIP_LIFETCH_PLAN_SELECT_FETCH;
+    return KVIP_LIFETCH_PLAN_THREE;
+}
+}  // namespace
+
+extern "C" uint32_t kvip_hip_lifetch_plan(const KvipLIFetchArgs* args) { return lifetch_plan(args); }
+
+extern "C" uint32_t kvip_hip_lifetch_forward(const KvipLIFetchArgs* args, void* stream) {
+    const uint32_t plan = lifetch_plan(args);
+    if (plan == KVIP_ERR_INVALID) return plan;
     const hipStream_t s = static_cast<hipStream_t>(stream);
-    // With the histogram and segment work memory, TopK and Fetch run as one launch.
-    const bool fused = kvip::validate_select_fetch(&tk, &fe) == KVIP_OK;
+    const KvipIndexerArgs& li = args->indexer;
+    const KvipTopkArgs& tk = args->topk;
+    const KvipFetchArgs& fe = args->fetch;
+    if (plan == KVIP_LIFETCH_PLAN_ROUND) return static_cast<uint32_t>(kvip::launch_round_fused(li, fe, args->round_work, s));
     hipError_t e = kvip::launch_indexer(li, s);
     if (e != hipSuccess) return static_cast<uint32_t>(e);
-    if (fused) return static_cast<uint32_t>(kvip::launch_select_fetch(tk, fe, s));
+    if (plan == KVIP_LIFETCH_PLAN_SELECT_FETCH) return static_cast<uint32_t>(kvip::launch_select_fetch(tk, fe, s));
     e = kvip::launch_topk(tk, s);
     if (e != hipSuccess) return static_cast<uint32_t>(e);
     return static_cast<uint32_t>(kvip::launch_fetch(fe, s));

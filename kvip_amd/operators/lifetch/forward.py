@@ -21,7 +21,10 @@ class LIFetchForward:
     ResidentIndexUpdate (hot-cache round: resolve, Fetch of the misses from host memory,
     Index update)."""
 
-    def __init__(self, rotating, update):
+    def __init__(self, rotating, update, *, fused=True):
+        """fused: hand the round work memory to the contiguous-Fetch forward, which then
+        runs the round as one persistent launch where it applies (fp8, one row per
+        request); False keeps the scoring and TopK+Fetch launches."""
         if not isinstance(rotating, LIFetchBinding):
             raise ValueError("LIFetch rotating must be a kvip_amd LIFetchBinding")
         if not isinstance(update, (ContiguousFetch, ResidentIndexUpdate)):
@@ -39,7 +42,8 @@ class LIFetchForward:
             self._refs = (ctypes.byref(self.indexer_args), ctypes.byref(self.topk_args),
                           ctypes.byref(self.resident_args))
             return
-        self.args = abi.LIFetchArgs(rotating.indexer_args(), rotating.topk_args(), update.fetch_args())
+        self.args = abi.LIFetchArgs(rotating.indexer_args(), rotating.topk_args(), update.fetch_args(),
+                                    abi.ptr(rotating.round_work) if fused else 0)
         self._args_ref = ctypes.byref(self.args)
         # Stage-wise argument blocks for score()/select()/fetch().
         self._indexer = ctypes.byref(self.args.indexer)
@@ -48,6 +52,18 @@ class LIFetchForward:
 
     def _stream(self):
         return abi.stream_handle(self.torch, self.rotating.device)
+
+    @property
+    def plan(self):
+        """The launch plan of a contiguous-Fetch forward: "round" (one persistent launch),
+        "select_fetch" (scoring, then TopK fused with the gather) or "three" (scoring, TopK,
+        gather); "resident" for the resident-cache forward."""
+        if self.resident:
+            return "resident"
+        code = self.library.kvip_hip_lifetch_plan(self._args_ref)
+        if code not in abi.LIFETCH_PLANS:
+            raise RuntimeError(f"LIFetch forward arguments rejected (code {code})")
+        return abi.LIFETCH_PLANS[code]
 
     def __call__(self):
         if self.resident:

@@ -9,7 +9,7 @@ import ctypes
 from pathlib import Path
 
 LIBRARY = Path(__file__).resolve().parents[1] / "_lib" / "libkvip_hip.so"
-ABI_VERSION = 3
+ABI_VERSION = 5
 
 KVIP_OK = 0
 KVIP_ERR_INVALID = 100000
@@ -68,7 +68,17 @@ class FetchArgs(ctypes.Structure):
 
 
 class LIFetchArgs(ctypes.Structure):
-    _fields_ = [("indexer", IndexerArgs), ("topk", TopkArgs), ("fetch", FetchArgs)]
+    _fields_ = [("indexer", IndexerArgs), ("topk", TopkArgs), ("fetch", FetchArgs), ("round_work", _p)]
+
+
+ROUND_MAX_ROWS = 256
+ROUND_MAX_XCDS = 16
+ROUND_LINE_WORDS = 32
+
+
+def round_work_words(rows):
+    """Words of the single-launch round work memory (KVIP_ROUND_WORK_WORDS)."""
+    return ROUND_MAX_XCDS * ROUND_LINE_WORDS + (2 * ROUND_LINE_WORDS + 256) * rows
 
 
 class AbcArgs(ctypes.Structure):
@@ -107,6 +117,9 @@ class QueryPackArgs(ctypes.Structure):
         ("status", _p), ("tokens", _i64), ("rows", _i32), ("heads", _i32),
     ]
 
+
+# kvip_hip_lifetch_plan results.
+LIFETCH_PLANS = {0: "three", 1: "select_fetch", 2: "round"}
 
 INGEST_DECODE = 0
 INGEST_LIST = 1
@@ -162,6 +175,7 @@ PROTOTYPES = {
     "kvip_hip_topk": ([ctypes.POINTER(TopkArgs), _p], ctypes.c_uint32),
     "kvip_hip_fetch_gather": ([ctypes.POINTER(FetchArgs), _p], ctypes.c_uint32),
     "kvip_hip_lifetch_forward": ([ctypes.POINTER(LIFetchArgs), _p], ctypes.c_uint32),
+    "kvip_hip_lifetch_plan": ([ctypes.POINTER(LIFetchArgs)], ctypes.c_uint32),
     "kvip_hip_select_fetch": ([ctypes.POINTER(TopkArgs), ctypes.POINTER(FetchArgs), _p], ctypes.c_uint32),
     "kvip_hip_update_abc": ([ctypes.POINTER(AbcArgs), _p], ctypes.c_uint32),
     "kvip_hip_lru_reset": ([ctypes.POINTER(LruArgs), _i32, _p], ctypes.c_uint32),
