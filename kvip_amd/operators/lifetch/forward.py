@@ -21,10 +21,10 @@ class LIFetchForward:
     ResidentIndexUpdate (hot-cache round: resolve, Fetch of the misses from host memory,
     Index update)."""
 
-    def __init__(self, rotating, update, *, fused=True):
+    def __init__(self, rotating, update, *, fused=False):
         """fused: hand the round work memory to the contiguous-Fetch forward, which then
         runs the round as one persistent launch where it applies (fp8, one row per
-        request); False keeps the scoring and TopK+Fetch launches."""
+        request); False (the default) keeps the scoring and TopK+Fetch launches."""
         if not isinstance(rotating, LIFetchBinding):
             raise ValueError("LIFetch rotating must be a kvip_amd LIFetchBinding")
         if not isinstance(update, (ContiguousFetch, ResidentIndexUpdate)):

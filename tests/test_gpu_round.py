@@ -31,7 +31,8 @@ def pair(torch, ctx, heads, wdt, kscale, qscale, ends, seed):
     wl = synthetic.decode_workload(torch, batch=len(ctx), ctx=ctx, device="cuda", heads=heads, qk="fp8",
                                    weight_dtype=torch.float32 if wdt == "f32" else torch.bfloat16,
                                    key_scale=kscale, query_scale=qscale, seed=seed, max_context=32768)
-    rot, upd, fused = synthetic.bind(torch, kvip_amd, wl, query_ends=ends)
+    rot, upd, _ = synthetic.bind(torch, kvip_amd, wl, query_ends=ends)
+    fused = kvip_amd.LIFetch(rot, upd, fused=True)
     two = kvip_amd.LIFetch(rot, upd, fused=False)
     assert fused.plan == "round" and two.plan == "select_fetch"
     return wl, rot, upd, fused, two
