@@ -15,13 +15,13 @@
 // Q fragments and per-lane head weights (w'_h = w_h * qscale_h) of the current request
 // stay in registers and are reloaded when the range crosses a request boundary. Scoring
 // is the decode formula: fp8 MFMA (v_mfma_scale_f32_32x32x64_f8f6f4), ReLU, head
-// weights, head reduction, key scale, bf16 half-away rounding, sortable key. Tiles are
-// finished in pairs: after each tile's per-lane-half head reduction a v_permlane32_swap
-// leaves tile A's token totals in lanes 0-31 and tile B's in lanes 32-63, so scaling,
-// rounding, the key store and the histogram update run once for two tiles. The 256-bin
-// high-byte histogram of each request is kept per wave in LDS (two buffers, for the at
-// most two requests a pair can touch) and added to the global rows when the request's
-// last tile of the range has been counted.
+// weights, head reduction, key scale, bf16 half-away rounding, sortable key. Each lane
+// half holds half of the heads of the tile's 32 tokens; after the per-lane-half head
+// reduction a v_permlane32_swap adds the other half's heads, and lanes 0-31 scale, round,
+// store the tile's keys and count them. The 256-bin high-byte histogram of the current
+// request is kept per wave in LDS (one buffer: a run covers one request) and added to the
+// global row at the run's end. LDS per workgroup stays under 80 KB so that two scoring
+// workgroups leave room on a CU for a 1024-thread TopK workgroup of another row group.
 //
 // Reference: QLIMatmul::ComputeMm1 (op_kernel/indexer/indexer_cube.h:161-322),
 // MulWeightAndReduceSum (indexer_score.h:384-426, loop :60-103, finalize :105-140),
@@ -85,7 +85,7 @@ template <int HEADS, bool W_BF16>
 __global__ __launch_bounds__(kRgThreads, 2) void indexer_ring_kernel(const KvipIndexerArgs p) {
     constexpr int MT = HEADS / 32;
     __shared__ __align__(16) uint8_t s_ring[kRgWaves][kRgSlots][kRgSlotBytes];
-    __shared__ __align__(16) uint32_t s_hist[kRgWaves][2][256];
+    __shared__ __align__(16) uint32_t s_hist[kRgWaves][256];
     __shared__ int s_prefix[kRgMaxBatch + 1];
     __shared__ uint32_t s_scan[kRgWaves];
 
@@ -106,7 +106,7 @@ __global__ __launch_bounds__(kRgThreads, 2) void indexer_ring_kernel(const KvipI
         running += static_cast<int>(total);
     }
     if (tid == 0) s_prefix[p.batch] = running;
-    for (int i = tid; i < kRgWaves * 2 * 256; i += kRgThreads) (&s_hist[0][0][0])[i] = 0u;
+    for (int i = tid; i < kRgWaves * 256; i += kRgThreads) (&s_hist[0][0])[i] = 0u;
     __syncthreads();
 
     // This wave's balanced share [t, t_end) of the flattened tile list.
@@ -124,7 +124,7 @@ __global__ __launch_bounds__(kRgThreads, 2) void indexer_ring_kernel(const KvipI
 #pragma unroll
     for (int u = 0; u < 4; ++u) ka[u] = ring_lds + n * kIndexDim + (((g * 4 + u) ^ (n & 7)) * 16);
     const uint32_t ksa = ring_lds + kRgTileBytes + n * 4;
-    const uint32_t hist_lds = lds_addr(&s_hist[wave][0][0]);
+    const uint32_t hist_lds = lds_addr(&s_hist[wave][0]);
     // Ring loads: in the v-th 1 KiB of a slot, lane L fills LDS row 8v + L/8, slot L%8, with
     // piece (L%8) ^ (L/8) of that token's row (rows 8v + L/8 have swizzle L/8).
     const int src_lane = (lane >> 3) * kIndexDim + (((lane & 7) ^ (lane >> 3)) * 16);

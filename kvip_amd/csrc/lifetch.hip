@@ -1,9 +1,11 @@
 // One decode round of the lightning indexer with fetch: scoring -> TopK-2048 ->
 // Fetch gather, enqueued back to back on one stream (no allocation, no sync, no
-// memset), so the whole round can be captured into a single hipGraph. When the TopK
-// arguments carry the scoring histogram and segment work memory, TopK and the gather
-// run as one fused launch (select_fetch.hip); with the round work memory the whole round
-// is one persistent launch (round_fused.hip).
+// memset), so the whole round can be captured into a single hipGraph. With the round
+// work memory the round is two launches: XCD-local scoring in which each request is
+// selected by the workgroup that finishes scoring it (score_select.hip), then the gather,
+// which also checks that launch (fetch_gather.hip). Without it, when the TopK arguments
+// carry the scoring histogram and segment work memory, TopK and the gather run as one
+// fused launch after the scoring launch (select_fetch.hip).
 //
 // Replaces kvip_lifetch_streaming_forward (csrc/operators/lightning_indexer_with_fetch/
 // include/api.h:7, op_host/launch.cpp:76-83), whose init -> LI -> resolve/update/fetch
@@ -19,9 +21,9 @@ hipError_t launch_topk(const KvipTopkArgs& a, hipStream_t stream);
 hipError_t launch_fetch(const KvipFetchArgs& a, hipStream_t stream);
 uint32_t validate_select_fetch(const KvipTopkArgs* t, const KvipFetchArgs* f);
 hipError_t launch_select_fetch(const KvipTopkArgs& t, const KvipFetchArgs& f, hipStream_t stream);
-bool round_fused_eligible(const KvipIndexerArgs& a, const KvipTopkArgs& t, const KvipFetchArgs& f,
-                          const uint32_t* work);
-hipError_t launch_round_fused(const KvipIndexerArgs& a, const KvipFetchArgs& f, uint32_t* work, hipStream_t stream);
+bool score_select_eligible(const KvipIndexerArgs& a, const KvipTopkArgs& t, const uint32_t* work);
+hipError_t launch_score_select(const KvipIndexerArgs& a, const KvipTopkArgs& t, uint32_t* work, hipStream_t stream);
+hipError_t launch_fetch_checked(const KvipFetchArgs& a, const RoundCheck& rc, hipStream_t stream);
 }  // namespace kvip
 
 extern "C" uint32_t kvip_hip_abi_version(void) { return KVIP_HIP_ABI_VERSION; }
@@ -45,9 +47,9 @@ uint32_t lifetch_plan(const KvipLIFetchArgs* args) {
                          tk.rows_per_request == li.rows_per_request && fe.topk == tk.topk &&
                          fe.batch == li.batch && fe.rows_per_request == li.rows_per_request;
     if (!chained) return KVIP_ERR_INVALID;
-    // With the round work memory the whole round is one persistent launch; with the
-    // histogram and segment work memory, TopK and Fetch run as one launch.
-    if (args->round_work != nullptr && kvip::round_fused_eligible(li, tk, fe, args->round_work)) {
+    // With the round work memory: scoring with in-launch selection, then the gather; with
+    // the histogram and segment work memory, TopK and Fetch run as one launch.
+    if (args->round_work != nullptr && kvip::score_select_eligible(li, tk, args->round_work)) {
         return KVIP_LIFETCH_PLAN_ROUND;
     }
     if (kvip::validate_select_fetch(&tk, &fe) == KVIP_OK) return KVIP_LIFETCH_PLAN_SELECT_FETCH;
@@ -64,7 +66,12 @@ extern "C" uint32_t kvip_hip_lifetch_forward(const KvipLIFetchArgs* args, void* 
     const KvipIndexerArgs& li = args->indexer;
     const KvipTopkArgs& tk = args->topk;
     const KvipFetchArgs& fe = args->fetch;
-    if (plan == KVIP_LIFETCH_PLAN_ROUND) return static_cast<uint32_t>(kvip::launch_round_fused(li, fe, args->round_work, s));
+    if (plan == KVIP_LIFETCH_PLAN_ROUND) {
+        const hipError_t e = kvip::launch_score_select(li, tk, args->round_work, s);
+        if (e != hipSuccess) return static_cast<uint32_t>(e);
+        const kvip::RoundCheck rc{args->round_work, tk.histogram, li.batch * li.rows_per_request};
+        return static_cast<uint32_t>(kvip::launch_fetch_checked(fe, rc, s));
+    }
     hipError_t e = kvip::launch_indexer(li, s);
     if (e != hipSuccess) return static_cast<uint32_t>(e);
     if (plan == KVIP_LIFETCH_PLAN_SELECT_FETCH) return static_cast<uint32_t>(kvip::launch_select_fetch(tk, fe, s));

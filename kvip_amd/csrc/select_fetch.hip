@@ -8,9 +8,9 @@
 //      2048th largest key;
 //   2. a low-byte histogram of the keys in bin hb gives the kth key and n_gt (keys above
 //      it);
-//   3. one workgroup scan of (keys > kth, keys == kth) counts in token order places every
-//      selected token: keys > kth at [0, n_gt) in token order, then the first 2048 - n_gt
-//      keys == kth in token order;
+//   3. per-32-key bitmasks of (keys > kth, keys == kth), their popcounts scanned over the
+//      workgroup in token order, place every selected token: keys > kth at [0, n_gt) in
+//      token order, then the first 2048 - n_gt keys == kth in token order (select_row.h);
 //   4. the tokens whose positions fall in this workgroup's quarter go to an LDS list
 //      indexed by position, are written to the TopK output and their KV rows gathered
 //      into output[row, position, :].
@@ -24,6 +24,7 @@
 // the Fetch gather (FetchQueryGroup, op_kernel/streaming.cpp:365-500; KV row layout
 // tests/operators/lifetch/support/workloads.py:493-515).
 #include "kvip_device.h"
+#include "select_row.h"
 
 namespace kvip {
 uint32_t validate_topk(const KvipTopkArgs* a);
@@ -104,81 +105,11 @@ KVIP_DEVICE void gather_pass(const KvipFetchArgs& f, int b, uint8_t* out_rows, c
     }
 }
 
-// Steps 2-4 for one row: low-byte histogram of the keys in bin hb -> kth; scan of
-// (> kth, == kth) counts in token order; the tokens whose positions fall in
-// [pos0, pos0 + 512) go to s_tok. The `dead` keys of this thread past the row's end read
-// as 0, the smallest key: they can only matter when hb == 0 (bin 0 of the low-byte
-// histogram) or kth == 0 (equal-key count), where their count is taken back out; in
-// token order they follow every live key, so their equal-key positions are never below
-// `need` and nothing past the row is emitted. Called by the whole workgroup.
-template <int KPT>
-KVIP_DEVICE void select_part(uint32_t (&kk)[KPT / 2], int dead, int hb, uint32_t gt_hi, int first, int pos0,
-                             int part, int tid, uint32_t* s_hist, int* s_sel, uint32_t* s_wave, int32_t* s_tok,
-                             uint32_t& err) {
-    auto key_at = [&](int j) -> uint32_t { return (j & 1) ? (kk[j >> 1] >> 16) : (kk[j >> 1] & 0xFFFFu); };
-    if (hb >= 0) {
-#pragma unroll
-        for (int j = 0; j < KPT; ++j) {
-            const uint32_t k = key_at(j);
-            if (static_cast<int>(k >> 8) == hb) atomicAdd(&s_hist[k & 0xFFu], 1u);
-        }
-        if (hb == 0 && dead > 0) atomicSub(&s_hist[0], static_cast<uint32_t>(dead));
-    }
-    __syncthreads();
-    select_bin(s_hist, kTopK - gt_hi, s_sel + 2, s_wave);
-    const int lo = hb >= 0 ? s_sel[2] : -1;
-    if (lo < 0) {
-        if (part == 0 && tid == 0) err |= KVIP_STATUS_HISTOGRAM;
-        return;
-    }
-    const uint32_t kth = (static_cast<uint32_t>(hb) << 8) | static_cast<uint32_t>(lo);
-    const uint32_t n_gt = gt_hi + static_cast<uint32_t>(s_sel[3]);
-    const uint32_t need = kTopK - n_gt;
-    // Positions from one scan of (gt, eq) counts packed as gt << 16 | eq (per-thread
-    // counts <= 32, row totals <= 32768: no carry between the halves).
-    uint32_t ngt = 0, neq = 0;
-#pragma unroll
-    for (int j = 0; j < KPT; ++j) {
-        const uint32_t k = key_at(j);
-        ngt += k > kth ? 1u : 0u;
-        neq += k == kth ? 1u : 0u;
-    }
-    if (kth == 0u) neq -= static_cast<uint32_t>(dead);
-    uint32_t total;
-    const uint32_t excl = block_exclusive_scan((ngt << 16) | neq, s_wave, &total);
-    if (part == 0 && tid == 0 && (total >> 16) != n_gt) err |= KVIP_STATUS_HISTOGRAM;
-    uint32_t pg = excl >> 16;
-    uint32_t pe = excl & 0xFFFFu;
-    const uint32_t lo_pos = static_cast<uint32_t>(pos0);
-    const uint32_t hi_pos = lo_pos + kPartRows;
-    const bool gt_mine = ngt != 0u && pg < hi_pos && pg + ngt > lo_pos;
-    const bool eq_mine = neq != 0u && pe < need && n_gt + pe < hi_pos && n_gt + min(pe + neq, need) > lo_pos;
-    if (gt_mine || eq_mine) {
-        // Opaque to the compiler: the compares are redone here instead of keeping the
-        // counting loop's 2*KPT lane masks alive across the scan (scalar-register spills).
-#pragma unroll
-        for (int i = 0; i < KPT / 2; ++i) asm volatile("" : "+v"(kk[i]));
-#pragma unroll
-        for (int j = 0; j < KPT; ++j) {
-            const uint32_t k = key_at(j);
-            const bool gt = k > kth;
-            const bool eq = k == kth;
-            // pg < n_gt whenever the histogram matches the keys.
-            const bool sel = gt ? pg < n_gt : (eq && pe < need);
-            const uint32_t rel = (gt ? pg : n_gt + pe) - lo_pos;
-            pg += gt ? 1u : 0u;
-            pe += eq ? 1u : 0u;
-            if (sel && rel < static_cast<uint32_t>(kPartRows)) s_tok[rel] = first + j;
-        }
-    }
-}
-
 template <int KPT, int PIECES>
 __global__ __launch_bounds__(kSgThreads) void select_gather_kernel(const KvipTopkArgs p, const KvipFetchArgs f) {
     constexpr int W = KPT / 2;  // packed key registers per thread
-    __shared__ uint32_t s_hist[256];
+    __shared__ __align__(16) uint32_t s_hist[256];
     __shared__ uint32_t s_wave[kSgWaves];
-    __shared__ int s_sel[4];
     __shared__ int s_last;
     __shared__ __align__(16) int32_t s_tok[kPartRows];
 
@@ -215,20 +146,23 @@ __global__ __launch_bounds__(kSgThreads) void select_gather_kernel(const KvipTop
                 kk[4 * v + w] = static_cast<uint32_t>(x[w]) & static_cast<uint32_t>((1ull << (16 * live)) - 1ull);
             }
         }
-        if (tid < 256) s_hist[tid] = hist_g[tid];
-        if (tid == 0) {
-            s_sel[0] = -1;
-            s_sel[2] = -1;
-        }
-        __syncthreads();
-        select_bin(s_hist, kTopK, s_sel, s_wave);
-        const int hb = s_sel[0];
-        const uint32_t gt_hi = static_cast<uint32_t>(s_sel[1]);
+        // Every wave reads the whole high-byte histogram (4 bins per lane) and finds the bin
+        // of the 2048th largest key on its own.
+        const v4i hv = *reinterpret_cast<const v4i*>(hist_g + lane_id() * 4);
         if (tid < 256) s_hist[tid] = 0u;
         for (int i = tid; i < kPartRows; i += kSgThreads) s_tok[i] = -1;  // positions nobody claims stay empty
+        const uint32_t h[4] = {static_cast<uint32_t>(hv[0]), static_cast<uint32_t>(hv[1]),
+                               static_cast<uint32_t>(hv[2]), static_cast<uint32_t>(hv[3])};
+        int hb;
+        uint32_t gt_hi;
+        wave_select_bin(h, kTopK, hb, gt_hi);
         __syncthreads();
-
-        select_part<KPT>(kk, KPT - count, hb, gt_hi, first, pos0, part, tid, s_hist, s_sel, s_wave, s_tok, err);
+        // Steps 2-4: the tokens whose positions fall in this part's quarter go to s_tok.
+        const RowSelection sel = select_row<KPT>(kk, count, first, hb, gt_hi, s_hist, s_wave, [&](int pos, int tok) {
+            const uint32_t rel = static_cast<uint32_t>(pos - pos0);
+            if (rel < static_cast<uint32_t>(kPartRows)) s_tok[rel] = tok;
+        });
+        if (part == 0 && tid == 0 && !sel.ok) err |= KVIP_STATUS_HISTOGRAM;
     }
     __syncthreads();
     // TopK output of this part (coalesced), then the gather.

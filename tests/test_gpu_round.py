@@ -1,6 +1,7 @@
-"""GPU parity of the single-launch decode round (round_fused.hip, through
-kvip_hip_lifetch_forward with the round work memory) against the two-launch round
-(scoring, then TopK fused with the gather) on the same inputs.
+"""GPU parity of the XCD-local decode round (score_select.hip: scoring with each request
+selected by the workgroup that finishes it, then the checked gather; through
+kvip_hip_lifetch_forward with the round work memory) against the scoring + fused
+TopK/gather round on the same inputs.
 
 Bars: TopK ids and every gathered byte bit-exact; the device status clear; the work memory
 left zero after every launch (two eager launches in a row and graph replays agree); the
@@ -39,7 +40,7 @@ def pair(torch, ctx, heads, wdt, kscale, qscale, ends, seed):
 
 
 @pytest.mark.parametrize("name,ctx,heads,wdt,kscale,qscale,ends", CASES, ids=[c[0] for c in CASES])
-def test_round_fused_matches_two_launch_round(torch_gpu, name, ctx, heads, wdt, kscale, qscale, ends):
+def test_round_matches_two_launch_round(torch_gpu, name, ctx, heads, wdt, kscale, qscale, ends):
     torch = torch_gpu
     say(f"case round {name}")
     wl, rot, upd, fused, two = pair(torch, ctx, heads, wdt, kscale, qscale, ends, seed=31)
@@ -64,7 +65,7 @@ def test_round_fused_matches_two_launch_round(torch_gpu, name, ctx, heads, wdt, 
                 assert torch.equal(rot.score_keys[r, :v], want_keys[r, :v]), (launch, r)
 
 
-def test_round_fused_graph_replay(torch_gpu):
+def test_round_graph_replay(torch_gpu):
     torch = torch_gpu
     ctx = [32768, 20000, 2048, 2047, 0, 8193, 2049, 26000]
     say("case round graph replay")
@@ -90,3 +91,29 @@ def test_round_fused_graph_replay(torch_gpu):
         assert torch.equal(g_topk, rot.topk), step
         assert torch.equal(g_out, upd.output), step
         assert int(rot.status.item()) == 0, step
+
+
+def test_round_config2_shape(torch_gpu):
+    """BASELINE config 2 (64 requests, ctx U[8192, 32768], fp8, key scales): the round plan
+    against the two-launch plan, both input seeds of the benchmark."""
+    torch = torch_gpu
+    for seed in (2026, 2027):
+        say(f"case round config2 seed {seed}")
+        wl = synthetic.config_workload(torch, "c2", "cuda", seed=seed)
+        rot, upd, _ = synthetic.bind(torch, kvip_amd, wl)
+        fused = kvip_amd.LIFetch(rot, upd, fused=True)
+        two = kvip_amd.LIFetch(rot, upd, fused=False)
+        assert fused.plan == "round"
+        two()
+        torch.cuda.synchronize()
+        want_topk, want_out = rot.topk.clone(), upd.output.clone()
+        for launch in range(2):
+            rot.topk.fill_(-7)
+            upd.output.fill_(0x5A)
+            fused()
+            torch.cuda.synchronize()
+            assert int(rot.status.item()) == 0, launch
+            assert torch.equal(rot.topk, want_topk), launch
+            assert torch.equal(upd.output, want_out), launch
+            assert not rot.round_work.any(), launch
+            assert not rot.histogram.any(), launch
