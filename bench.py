@@ -59,7 +59,7 @@ def algorithmic_bytes(wl, heads, has_qscale):
     live = np.minimum(ctx, TOPK).repeat(wl.rows_per_request)
     topk = rows * TOPK * 4
     gather = int(live.sum()) * row_bytes * 2
-    return {"indexer": score, "select_fetch": topk + gather}
+    return {"indexer": score, "topk": topk, "fetch": gather}
 
 
 def measured_traffic(kernel):
@@ -391,12 +391,12 @@ def main():
     steps_bytes = sum(step_bytes[s % 2] for s in range(args.steps))
 
     # Per-kernel durations: HIP events on the launch stream around back-to-back graph
-    # replays (no host gap between launches), same alternating inputs. With the "round"
-    # plan the step is one launch, timed by the full graphs. The two-launch plan (scoring,
-    # then TopK fused with the gather) is timed beside it on the same inputs: its scoring
-    # launch alone from score-only graphs, TopK+gather as its full round minus scoring.
+    # replays (no host gap between launches), same alternating inputs: scoring from
+    # score-only graphs, TopK as score+TopK graphs minus scoring, the gather as the full
+    # three-launch round minus score+TopK. The XCD-local round (scoring with in-launch
+    # selection, then the gather) is timed beside it on the same inputs.
     plan = fwd.plan
-    twos = [kvip_amd.LIFetch(r, u, fused=False) for w, r, u, f in sets]
+    threes = [kvip_amd.LIFetch(r, u, fused=False) for w, r, u, f in sets]
     rounds = [kvip_amd.LIFetch(r, u, fused=True) for w, r, u, f in sets]
 
     def capture(calls):
@@ -420,20 +420,18 @@ def main():
         return e0.elapsed_time(e1) / args.steps
 
     with torch.cuda.stream(side):
-        for t in twos + rounds:
+        for t in threes + rounds:
             t()
     stream.wait_stream(side)
     torch.cuda.synchronize()
     full_ms = replay_ms(graphs)
-    score_ms = replay_ms(capture([t.score for t in twos]))
+    score_ms = replay_ms(capture([t.score for t in threes]))
     for w, r, u, f in sets:
         r.histogram.zero_()  # score-only replays keep adding to the histograms
-    two_ms = replay_ms(capture(twos))
-    times = {"indexer": score_ms, "select_fetch": two_ms - score_ms}
-    mean_bytes["round_fused"] = mean_bytes["indexer"] + mean_bytes["select_fetch"]
+    st_ms = replay_ms(capture([lambda t=t: (t.score(), t.select()) for t in threes]))
+    three_ms = replay_ms(capture(threes))
+    times = {"indexer": score_ms, "topk": st_ms - score_ms, "fetch": three_ms - st_ms}
     round_ms = replay_ms(capture(rounds)) if rounds[0].plan == "round" else None
-    if round_ms is not None:
-        times["round_fused"] = round_ms
     for w, r, u, f in sets:
         if int(r.status.item()) != 0:
             raise RuntimeError(f"device status {int(r.status.item())} after the timed steps")
@@ -446,9 +444,8 @@ def main():
         torch.cuda.synchronize()
 
     rows = rot.rows
-    # The dominant kernel of the step's plan: the one persistent launch, or the larger of
-    # the two launches.
-    dominant = "round_fused" if plan == "round" else max(("indexer", "select_fetch"), key=times.get)
+    # The dominant kernel of the default three-launch round: the longest launch.
+    dominant = max(times, key=times.get)
     achieved = mean_bytes[dominant] / (times[dominant] * 1e-3) / 1e9
     result = {
         "metric": "decode queries/sec LI+TopK+Fetch, B=64 ctx 32k; achieved HBM GB/s vs peak",
@@ -473,8 +470,8 @@ def main():
         "step_bytes": step_bytes,
         "plan": plan,
         "graph_ms_per_step": round(full_ms, 4),
-        "two_launch_graph_ms_per_step": round(two_ms, 4),
-        "single_launch_graph_ms_per_step": None if round_ms is None else round(round_ms, 4),
+        "three_launch_graph_ms_per_step": round(three_ms, 4),
+        "xcd_round_graph_ms_per_step": None if round_ms is None else round(round_ms, 4),
         "kernels": {k: {"ms": round(v, 5), "bytes": int(mean_bytes[k]),
                         "gbs": round(mean_bytes[k] / (v * 1e-3) / 1e9, 1)} for k, v in times.items()},
         "roofline": {"kernel": dominant, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,

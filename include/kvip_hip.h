@@ -210,13 +210,16 @@ typedef struct KvipFetchArgs {
 /* One decode round: scoring -> TopK-2048 -> Fetch gather, stream-ordered. With the
  * scoring histogram and segment work memory in `topk`, TopK and Fetch run as one fused
  * launch (kvip_hip_select_fetch). With `round_work` (KVIP_ROUND_WORK_WORDS(rows) words,
- * 128-byte aligned, zero before the first launch; every launch leaves it zero), fp8 Q/K,
- * one row per request, at most KVIP_ROUND_MAX_ROWS requests and 656-byte KV rows, the
- * whole round is one persistent launch in which each request's selection overlaps the
- * scoring of later requests and the gathers of earlier ones (score keys are then written
- * only for rows of at least 2048 tokens, and the histogram is not used). Layout: per XCD a
- * line of counters, per request a completion line, per publication slot a line, per
- * request a 256-bin histogram. Launches that share one work memory must not overlap. */
+ * 128-byte aligned, zero before the first launch; every round leaves it zero), fp8 Q/K,
+ * one row per request, at most KVIP_ROUND_MAX_ROWS requests, key rows of at most 32768
+ * keys on 128-byte boundaries and the scoring histogram, the round is two launches: scoring
+ * with the requests dealt to XCDs, each request selected inside that launch by the
+ * workgroup that finishes scoring it, then the gather, which also checks the first launch
+ * (KVIP_STATUS_STALLED if a request went unselected or the dispatcher did not deal
+ * workgroups round-robin over the XCDs) and zeroes the work memory. Score keys are then
+ * written only for rows of at least 2048 tokens. Layout: 16 lines of per-XCD masks, a
+ * completion line per request, one word per request. Rounds that share one work memory
+ * must not overlap. */
 #define KVIP_ROUND_MAX_ROWS 256
 #define KVIP_ROUND_MAX_XCDS 16
 #define KVIP_ROUND_LINE_WORDS 32
@@ -226,7 +229,7 @@ typedef struct KvipLIFetchArgs {
     KvipIndexerArgs indexer;
     KvipTopkArgs topk;
     KvipFetchArgs fetch;
-    uint32_t* round_work;        /* single-launch round work memory, or NULL */
+    uint32_t* round_work;        /* XCD-local round work memory, or NULL */
 } KvipLIFetchArgs;
 
 /* ABC ring maps: token_to_slot / slot_to_token are int32 [layers, pool, tokens];
@@ -480,13 +483,14 @@ uint32_t kvip_hip_fetch_gather(const KvipFetchArgs* args, void* stream);
 uint32_t kvip_hip_indexer_prefill(const KvipPrefillArgs* args, void* stream);
 uint32_t kvip_hip_lifetch_forward(const KvipLIFetchArgs* args, void* stream);
 /* The launch plan kvip_hip_lifetch_forward takes for these arguments (no launch, no device
- * access): KVIP_LIFETCH_PLAN_ROUND (one persistent launch), _SELECT_FETCH (scoring, then
- * TopK fused with the gather) or _THREE (scoring, TopK, gather); KVIP_ERR_INVALID when the
- * forward would reject them. A host query with no counterpart in the reference, for
- * callers and tests that need to know which kernels a round runs. */
+ * access): KVIP_LIFETCH_PLAN_ROUND (with the round work memory: XCD-local scoring with
+ * in-launch selection, then the checked gather) or _THREE (scoring, TopK, gather; rows of
+ * at most KVIP_TOPK_REGS_MAX_KEYS keys use the register-resident TopK);
+ * KVIP_ERR_INVALID when the forward would reject them. A host query with no counterpart in
+ * the reference, for callers and tests that need to know which kernels a round runs. */
 #define KVIP_LIFETCH_PLAN_THREE 0u
-#define KVIP_LIFETCH_PLAN_SELECT_FETCH 1u
 #define KVIP_LIFETCH_PLAN_ROUND 2u
+#define KVIP_TOPK_REGS_MAX_KEYS 65536
 uint32_t kvip_hip_lifetch_plan(const KvipLIFetchArgs* args);
 /* TopK-2048 of rows scored by kvip_hip_indexer_decode fused with the Fetch gather of the
  * selected rows: same outputs as kvip_hip_topk followed by kvip_hip_fetch_gather. Needs

@@ -1,11 +1,14 @@
 // One decode round of the lightning indexer with fetch: scoring -> TopK-2048 ->
 // Fetch gather, enqueued back to back on one stream (no allocation, no sync, no
-// memset), so the whole round can be captured into a single hipGraph. With the round
-// work memory the round is two launches: XCD-local scoring in which each request is
-// selected by the workgroup that finishes scoring it (score_select.hip), then the gather,
-// which also checks that launch (fetch_gather.hip). Without it, when the TopK arguments
-// carry the scoring histogram and segment work memory, TopK and the gather run as one
-// fused launch after the scoring launch (select_fetch.hip).
+// memset), so the whole round can be captured into a single hipGraph. The default plan is
+// three launches: scoring (indexer_ring.hip), TopK with the row's keys in registers
+// (topk.hip; rows above 65536 keys take the multi-workgroup split select) and the
+// gather (fetch_gather.hip). Measured at BASELINE config 2 this beats TopK fused with the
+// gather (select_fetch.hip, still exported as kvip_hip_select_fetch): the separate gather
+// launch is balanced by the hardware dispatcher, while the fused one waits for its
+// slowest workgroup. With the round work memory the round is two launches: XCD-local
+// scoring in which each request is selected by the workgroup that finishes scoring it
+// (score_select.hip), then the gather, which also checks that launch.
 //
 // Replaces kvip_lifetch_streaming_forward (csrc/operators/lightning_indexer_with_fetch/
 // include/api.h:7, op_host/launch.cpp:76-83), whose init -> LI -> resolve/update/fetch
@@ -19,8 +22,6 @@ uint32_t validate_fetch(const KvipFetchArgs* a);
 hipError_t launch_indexer(const KvipIndexerArgs& a, hipStream_t stream);
 hipError_t launch_topk(const KvipTopkArgs& a, hipStream_t stream);
 hipError_t launch_fetch(const KvipFetchArgs& a, hipStream_t stream);
-uint32_t validate_select_fetch(const KvipTopkArgs* t, const KvipFetchArgs* f);
-hipError_t launch_select_fetch(const KvipTopkArgs& t, const KvipFetchArgs& f, hipStream_t stream);
 bool score_select_eligible(const KvipIndexerArgs& a, const KvipTopkArgs& t, const uint32_t* work);
 hipError_t launch_score_select(const KvipIndexerArgs& a, const KvipTopkArgs& t, uint32_t* work, hipStream_t stream);
 hipError_t launch_fetch_checked(const KvipFetchArgs& a, const RoundCheck& rc, hipStream_t stream);
@@ -47,12 +48,10 @@ uint32_t lifetch_plan(const KvipLIFetchArgs* args) {
                          tk.rows_per_request == li.rows_per_request && fe.topk == tk.topk &&
                          fe.batch == li.batch && fe.rows_per_request == li.rows_per_request;
     if (!chained) return KVIP_ERR_INVALID;
-    // With the round work memory: scoring with in-launch selection, then the gather; with
-    // the histogram and segment work memory, TopK and Fetch run as one launch.
+    // With the round work memory: scoring with in-launch selection, then the gather.
     if (args->round_work != nullptr && kvip::score_select_eligible(li, tk, args->round_work)) {
         return KVIP_LIFETCH_PLAN_ROUND;
     }
-    if (kvip::validate_select_fetch(&tk, &fe) == KVIP_OK) return KVIP_LIFETCH_PLAN_SELECT_FETCH;
     return KVIP_LIFETCH_PLAN_THREE;
 }
 }  // namespace
@@ -74,8 +73,11 @@ extern "C" uint32_t kvip_hip_lifetch_forward(const KvipLIFetchArgs* args, void* 
     }
     hipError_t e = kvip::launch_indexer(li, s);
     if (e != hipSuccess) return static_cast<uint32_t>(e);
-    if (plan == KVIP_LIFETCH_PLAN_SELECT_FETCH) return static_cast<uint32_t>(kvip::launch_select_fetch(tk, fe, s));
-    e = kvip::launch_topk(tk, s);
+    // Rows that fit the register-resident TopK take it even when the split select's work
+    // memory is given.
+    KvipTopkArgs t = tk;
+    if (t.histogram != nullptr && t.key_stride <= KVIP_TOPK_REGS_MAX_KEYS) t.segments = nullptr;
+    e = kvip::launch_topk(t, s);
     if (e != hipSuccess) return static_cast<uint32_t>(e);
     return static_cast<uint32_t>(kvip::launch_fetch(fe, s));
 }

@@ -13,6 +13,7 @@
 // (op_kernel/indexer/indexer_vector.h:849-873, :943-957): valid <= 0 -> all -1,
 // valid < 2048 -> [0..valid-1, -1...].
 #include "kvip_device.h"
+#include "select_row.h"
 
 namespace kvip {
 namespace {
@@ -20,6 +21,7 @@ namespace {
 constexpr int kTopkThreads = 1024;
 constexpr int kKeysPerThread = 8;
 constexpr int kTileKeys = kTopkThreads * kKeysPerThread;
+static_assert(KVIP_TOPK_REGS_MAX_KEYS == kTopkThreads * 64, "largest register-resident row");
 
 struct Keys8 {
     uint32_t k[kKeysPerThread];
@@ -149,19 +151,20 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const KvipTopkArgs p
 
 
 // Register-resident variant for rows of at most 1024*KPT keys (KPT <= 64): thread t holds keys
-// [t*KPT, (t+1)*KPT) (packed two per register), loaded in one batch, so the whole
-// select costs one round of key loads, two LDS histograms and one workgroup scan.
+// [t*KPT, (t+1)*KPT) (packed two per register), loaded in one batch; the high-byte bin
+// comes from the scoring histogram (each wave reads it) or a histogram built here, and
+// the rest is select_row.h (low-byte histogram, bitmask counts, one workgroup scan,
+// emission of the selected keys only).
 template <int KPT>
 __global__ __launch_bounds__(kTopkThreads) void topk_regs_kernel(const KvipTopkArgs p) {
     constexpr int W = KPT / 2;  // packed registers per thread
-    __shared__ uint32_t s_hist[256];
+    __shared__ __align__(16) uint32_t s_hist[256];
     __shared__ uint32_t s_wave[kTopkThreads / 64];
-    __shared__ int s_sel[4];
     __shared__ __align__(16) int32_t s_out[kTopK];
 
     const int tid = threadIdx.x;
+    const int lane = tid & 63;
     const int row = blockIdx.x;
-    const int b = row / p.rows_per_request;
     const int valid = min(topk_row_valid(p, row), kTopkThreads * KPT);
     int32_t* out = p.topk + static_cast<size_t>(row) * kTopK;
     const uint16_t* keys = p.score_keys + static_cast<size_t>(row) * p.key_stride;
@@ -173,11 +176,11 @@ __global__ __launch_bounds__(kTopkThreads) void topk_regs_kernel(const KvipTopkA
         return;
     }
 
-    // Keys of this thread; positions >= valid read as 0 and are masked by `count`.
+    // Keys of this thread; positions >= valid are excluded by `count`. Every vector load
+    // is unconditional: its start is clamped into the row (the row stride is a multiple
+    // of 8 keys).
     const int first = tid * KPT;
     const int count = max(0, min(KPT, valid - first));
-    // Every vector load is unconditional: its start is clamped into the row (the row
-    // stride is a multiple of 8 keys), and keys past `valid` are masked by `count`.
     uint32_t kk[W];
 #pragma unroll
     for (int v = 0; v < W / 4; ++v) {
@@ -188,87 +191,39 @@ __global__ __launch_bounds__(kTopkThreads) void topk_regs_kernel(const KvipTopkA
         kk[4 * v + 2] = x[2];
         kk[4 * v + 3] = x[3];
     }
-    auto key_at = [&](int j) -> uint32_t { return (j & 1) ? (kk[j >> 1] >> 16) : (kk[j >> 1] & 0xFFFFu); };
 
-    // Level 1: high byte.
-    if (tid < 256) s_hist[tid] = ghist != nullptr ? ghist[tid] : 0u;
-    if (tid == 0) {
-        s_sel[0] = -1;
-        s_sel[2] = -1;
-    }
-    __syncthreads();
+    // High-byte bin of the 2048th largest key.
+    v4i hv;
     if (ghist != nullptr) {
-        if (tid < 256) ghist[tid] = 0u;  // ready for the next scoring launch
+        hv = *reinterpret_cast<const v4i*>(ghist + lane * 4);  // every wave reads all 256 bins
     } else {
-#pragma unroll
-        for (int j = 0; j < KPT; ++j) wave_hist_add(s_hist, key_at(j) >> 8, j < count);
-    }
-    __syncthreads();
-    select_bin(s_hist, kTopK, s_sel, s_wave);
-    const int hb = s_sel[0];
-    const uint32_t gt_hi = static_cast<uint32_t>(s_sel[1]);
-    if (hb < 0) {
-        for (int i = tid; i < kTopK; i += kTopkThreads) out[i] = -1;
-        if (tid == 0) report(p.status, KVIP_STATUS_HISTOGRAM);
-        return;
-    }
-
-    // Level 2: low byte among keys whose high byte is hb.
-    if (tid < 256) s_hist[tid] = 0u;
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < KPT; ++j) {
-        const uint32_t k = key_at(j);
-        if (j < count && static_cast<int>(k >> 8) == hb) atomicAdd(&s_hist[k & 0xFFu], 1u);
-    }
-    __syncthreads();
-    select_bin(s_hist, kTopK - gt_hi, s_sel + 2, s_wave);
-    if (s_sel[2] < 0) {
-        for (int i = tid; i < kTopK; i += kTopkThreads) out[i] = -1;
-        if (tid == 0) report(p.status, KVIP_STATUS_HISTOGRAM);
-        return;
-    }
-    const uint32_t kth = (static_cast<uint32_t>(hb) << 8) | static_cast<uint32_t>(s_sel[2]);
-    const uint32_t n_gt = gt_hi + static_cast<uint32_t>(s_sel[3]);
-    const uint32_t need = kTopK - n_gt;
-
-    // Level 3: one scan of (gt, eq) counts packed as gt << 20 | eq (gt < 2048, eq < 2^20).
-    uint32_t ngt = 0, neq = 0;
-#pragma unroll
-    for (int j = 0; j < KPT; ++j) {
-        const uint32_t k = key_at(j);
-        const bool in = j < count;
-        ngt += (in && k > kth) ? 1u : 0u;
-        neq += (in && k == kth) ? 1u : 0u;
-    }
-    uint32_t total;
-    const uint32_t excl = block_exclusive_scan((ngt << 20) | neq, s_wave, &total);
-    uint32_t pg = excl >> 20;
-    uint32_t pe = excl & 0xFFFFFu;
-    uint32_t err = 0;
-    // The row is assembled in LDS and written with one coalesced 8-byte store per thread.
-    reinterpret_cast<int2*>(s_out)[tid] = int2{-1, -1};
-    __syncthreads();
-    if (ngt != 0u || (neq != 0u && pe < need)) {
+        if (tid < 256) s_hist[tid] = 0u;
+        __syncthreads();
 #pragma unroll
         for (int j = 0; j < KPT; ++j) {
-            const uint32_t k = key_at(j);
-            if (j < count) {
-                if (k > kth) {
-                    if (pg < n_gt) s_out[pg] = first + j;
-                    else err = KVIP_STATUS_HISTOGRAM;
-                    ++pg;
-                } else if (k == kth) {
-                    if (pe < need) s_out[n_gt + pe] = first + j;
-                    ++pe;
-                }
-            }
+            const uint32_t k = (j & 1) ? (kk[j >> 1] >> 16) : (kk[j >> 1] & 0xFFFFu);
+            wave_hist_add(s_hist, k >> 8, j < count);
         }
+        __syncthreads();
+        hv = *reinterpret_cast<const v4i*>(s_hist + lane * 4);
+        __syncthreads();  // every wave has its copy before the bins are cleared below
     }
+    const uint32_t h[4] = {static_cast<uint32_t>(hv[0]), static_cast<uint32_t>(hv[1]), static_cast<uint32_t>(hv[2]),
+                           static_cast<uint32_t>(hv[3])};
+    int hb;
+    uint32_t gt_hi;
+    wave_select_bin(h, kTopK, hb, gt_hi);
+    if (tid < 256) s_hist[tid] = 0u;
+    reinterpret_cast<int2*>(s_out)[tid] = int2{-1, -1};
+    __syncthreads();
+    if (ghist != nullptr && tid < 256) ghist[tid] = 0u;  // read by every wave: ready for the next scoring launch
+
+    const RowSelection sel =
+        select_row<KPT>(kk, count, first, hb, gt_hi, s_hist, s_wave, [&](int pos, int tok) { s_out[pos] = tok; });
     __syncthreads();
     static_assert(kTopK == 2 * kTopkThreads, "one int2 per thread");
     reinterpret_cast<int2*>(out)[tid] = reinterpret_cast<const int2*>(s_out)[tid];
-    report(p.status, err);
+    if (tid == 0 && !sel.ok) report(p.status, KVIP_STATUS_HISTOGRAM);
 }
 
 // Split select for rows scored by kvip_hip_indexer_decode (the high-byte histogram is

@@ -23,8 +23,9 @@ class LIFetchForward:
 
     def __init__(self, rotating, update, *, fused=False):
         """fused: hand the round work memory to the contiguous-Fetch forward, which then
-        runs the round as one persistent launch where it applies (fp8, one row per
-        request); False (the default) keeps the scoring and TopK+Fetch launches."""
+        runs the XCD-local round where it applies (fp8, one row per request: scoring with
+        each request selected inside that launch, then the gather); False (the default)
+        keeps three launches: scoring, TopK, gather."""
         if not isinstance(rotating, LIFetchBinding):
             raise ValueError("LIFetch rotating must be a kvip_amd LIFetchBinding")
         if not isinstance(update, (ContiguousFetch, ResidentIndexUpdate)):
@@ -49,15 +50,21 @@ class LIFetchForward:
         self._indexer = ctypes.byref(self.args.indexer)
         self._topk = ctypes.byref(self.args.topk)
         self._fetch = ctypes.byref(self.args.fetch)
+        # The forward's TopK: rows that fit the register-resident select take it even when
+        # the split select's work memory is bound.
+        self.topk_args = abi.TopkArgs.from_buffer_copy(self.args.topk)
+        if self.topk_args.histogram and self.topk_args.key_stride <= abi.TOPK_REGS_MAX_KEYS:
+            self.topk_args.segments = 0
+        self._topk_fwd = ctypes.byref(self.topk_args)
 
     def _stream(self):
         return abi.stream_handle(self.torch, self.rotating.device)
 
     @property
     def plan(self):
-        """The launch plan of a contiguous-Fetch forward: "round" (one persistent launch),
-        "select_fetch" (scoring, then TopK fused with the gather) or "three" (scoring, TopK,
-        gather); "resident" for the resident-cache forward."""
+        """The launch plan of a contiguous-Fetch forward: "round" (XCD-local scoring with
+        in-launch selection, then the gather) or "three" (scoring, TopK, gather);
+        "resident" for the resident-cache forward."""
         if self.resident:
             return "resident"
         code = self.library.kvip_hip_lifetch_plan(self._args_ref)
@@ -76,12 +83,13 @@ class LIFetchForward:
         abi.check(self.library.kvip_hip_indexer_decode(self._indexer, self._stream()), "LI scoring")
 
     def select(self):
-        abi.check(self.library.kvip_hip_topk(self._topk, self._stream()), "TopK")
+        abi.check(self.library.kvip_hip_topk(self._topk_fwd, self._stream()), "TopK")
 
     def fetch(self):
         abi.check(self.library.kvip_hip_fetch_gather(self._fetch, self._stream()), "Fetch gather")
 
     def select_fetch(self):
-        """TopK fused with the Fetch gather (the second launch of the forward when the
-        binding carries the segment work memory)."""
+        """TopK fused with the Fetch gather in one launch (kvip_hip_select_fetch; needs the
+        binding's segment work memory and rows of at most 32768 keys). Not part of the
+        default forward, whose separate gather launch measured faster."""
         abi.check(self.library.kvip_hip_select_fetch(self._topk, self._fetch, self._stream()), "TopK+Fetch")

@@ -77,7 +77,7 @@ ROUND_LINE_WORDS = 32
 
 
 def round_work_words(rows):
-    """Words of the single-launch round work memory (KVIP_ROUND_WORK_WORDS)."""
+    """Words of the XCD-local round work memory (KVIP_ROUND_WORK_WORDS)."""
     return ROUND_MAX_XCDS * ROUND_LINE_WORDS + (2 * ROUND_LINE_WORDS + 256) * rows
 
 
@@ -119,7 +119,8 @@ class QueryPackArgs(ctypes.Structure):
 
 
 # kvip_hip_lifetch_plan results.
-LIFETCH_PLANS = {0: "three", 1: "select_fetch", 2: "round"}
+LIFETCH_PLANS = {0: "three", 2: "round"}
+TOPK_REGS_MAX_KEYS = 65536  # KVIP_TOPK_REGS_MAX_KEYS
 
 INGEST_DECODE = 0
 INGEST_LIST = 1

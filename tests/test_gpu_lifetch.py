@@ -268,7 +268,7 @@ def test_select_fetch_matches_topk_then_gather(torch_gpu, kind, ctx):
 
 def test_select_fetch_rejects_rows_beyond_32768_and_forward_falls_back(torch_gpu):
     """Rows longer than 32768 keys are outside the fused launch (arguments rejected before
-    anything runs); the forward then runs TopK and Fetch as separate launches."""
+    anything runs); the forward, which runs TopK and Fetch as separate launches, takes them."""
     torch = torch_gpu
     wl = synthetic.decode_workload(torch, batch=2, ctx=[40000, 5000], device="cuda", seed=4)
     rot, upd, fwd = synthetic.bind(torch, kvip_amd, wl)

@@ -1,7 +1,7 @@
 """GPU parity of the XCD-local decode round (score_select.hip: scoring with each request
 selected by the workgroup that finishes it, then the checked gather; through
-kvip_hip_lifetch_forward with the round work memory) against the scoring + fused
-TopK/gather round on the same inputs.
+kvip_hip_lifetch_forward with the round work memory) against the default three-launch
+round (scoring, TopK, gather) on the same inputs.
 
 Bars: TopK ids and every gathered byte bit-exact; the device status clear; the work memory
 left zero after every launch (two eager launches in a row and graph replays agree); the
@@ -35,7 +35,7 @@ def pair(torch, ctx, heads, wdt, kscale, qscale, ends, seed):
     rot, upd, _ = synthetic.bind(torch, kvip_amd, wl, query_ends=ends)
     fused = kvip_amd.LIFetch(rot, upd, fused=True)
     two = kvip_amd.LIFetch(rot, upd, fused=False)
-    assert fused.plan == "round" and two.plan == "select_fetch"
+    assert fused.plan == "round" and two.plan == "three"
     return wl, rot, upd, fused, two
 
 
