@@ -213,6 +213,10 @@ __global__ __launch_bounds__(kTopkThreads) void topk_regs_kernel(const KvipTopkA
     int hb;
     uint32_t gt_hi;
     wave_select_bin(h, kTopK, hb, gt_hi);
+    // The scoring histogram counts every visible key once: a total other than `valid`
+    // means the scoring launch skipped or repeated tiles.
+    const uint32_t hist_total = __shfl(wave_inclusive_scan(h[0] + h[1] + h[2] + h[3]), 63);
+    const bool counted = hist_total == static_cast<uint32_t>(valid);
     if (tid < 256) s_hist[tid] = 0u;
     reinterpret_cast<int2*>(s_out)[tid] = int2{-1, -1};
     __syncthreads();
@@ -223,7 +227,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_regs_kernel(const KvipTopkA
     __syncthreads();
     static_assert(kTopK == 2 * kTopkThreads, "one int2 per thread");
     reinterpret_cast<int2*>(out)[tid] = reinterpret_cast<const int2*>(s_out)[tid];
-    if (tid == 0 && !sel.ok) report(p.status, KVIP_STATUS_HISTOGRAM);
+    if (tid == 0 && !(sel.ok && counted)) report(p.status, KVIP_STATUS_HISTOGRAM);
 }
 
 // Split select for rows scored by kvip_hip_indexer_decode (the high-byte histogram is
