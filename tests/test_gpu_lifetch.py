@@ -84,9 +84,9 @@ def test_indexer_scores_match_oracle(torch_gpu, name, qk, heads, wdt, kscale, qs
         assert np.array_equal(hist[r], np.bincount(gpu_keys(rot)[r, :v] >> 8, minlength=256)), r
 
 
-def run_topk(torch, rot, use_histogram):
+def run_topk(torch, rot, use_histogram, split=True):
     lib = abi.load_library()
-    args = rot.topk_args(use_histogram)
+    args = rot.topk_args(use_histogram, split=split)
     rc = lib.kvip_hip_topk(ctypes.byref(args), abi.stream_handle(torch, rot.device))
     abi.check(rc, "topk")
     torch.cuda.synchronize()
@@ -137,6 +137,32 @@ def test_topk_bit_exact_on_oracle_keys(torch_gpu, kind, ctx):
         assert np.array_equal(got[r], ref.topk_reference(keys[r], v)), f"split row {r} valid {v}"
     assert int(rot.status.item()) == 0
     assert not rot.histogram.any()
+    # The forward's select: keys in registers, the high-byte bin from the same histogram.
+    rot.histogram.copy_(torch.from_numpy(hist.astype(np.int32)))
+    rot.topk.fill_(-5)
+    say(f"case topk registers+histogram {kind} {ctx}")
+    got = run_topk(torch, rot, use_histogram=True, split=False)
+    for r, v in enumerate(ctx):
+        assert np.array_equal(got[r], ref.topk_reference(keys[r], v)), f"register row {r} valid {v}"
+    assert int(rot.status.item()) == 0
+    assert not rot.histogram.any()
+
+
+def test_topk_reports_a_histogram_that_misses_keys(torch_gpu):
+    """A scoring histogram whose total differs from the row's visible keys (a skipped or
+    repeated tile) is reported in the status word instead of passing silently."""
+    torch = torch_gpu
+    rng = np.random.default_rng(17)
+    rot = kvip_amd.LIFetchBinding(torch, batch=1, max_context=8192, device="cuda")
+    keys = np.zeros((1, rot.key_stride), np.uint16)
+    keys[0, :8192] = keys_case("random", 8192, rng)
+    rot.score_keys.copy_(torch.from_numpy(keys.view(np.int16)))
+    rot.seq_lens.copy_(torch.tensor([8192], dtype=torch.int32))
+    hist = np.bincount(keys[0, :8192] >> 8, minlength=256)
+    hist[int(np.argmax(hist))] -= 32  # one 32-token tile missing from the counts
+    rot.histogram.copy_(torch.from_numpy(hist[None, :].astype(np.int32)))
+    run_topk(torch, rot, use_histogram=True, split=False)
+    assert int(rot.status.item()) & abi.STATUS_HISTOGRAM
 
 
 def test_topk_from_scoring_histogram_equals_standalone(torch_gpu):
@@ -182,6 +208,38 @@ def test_forward_end_to_end_against_oracle_scores(torch_gpu):
         assert np.array_equal(topk[r], ref.topk_reference(gpu_keys(rot)[r], v))
     out = upd.output.cpu().numpy()
     assert np.array_equal(out, ref.fetch_gather(wl.kv_cache.cpu().numpy(), wl.block_table.cpu().numpy(), topk))
+
+
+def test_forward_mtp_rows_against_oracle(torch_gpu):
+    """Four query rows per request (decode + 3 MTP rows) with per-row visible bounds: the
+    forward's scores, TopK (bit-exact on the GPU's keys, inside the oracle's cutoff band) and
+    gather."""
+    torch = torch_gpu
+    ctx = [9000, 4100, 2200, 12000]
+    wl = synthetic.decode_workload(torch, batch=4, ctx=ctx, device="cuda", rows_per_request=4, seed=44)
+    ends = []
+    for c in ctx:
+        ends += [c - 3, c - 2, c - 1, c]
+    ends[6] = 0          # a padding row
+    ends[9] = 2047       # a row below 2048 visible tokens
+    rot, upd, fwd = synthetic.bind(torch, kvip_amd, wl, query_ends=ends)
+    assert fwd.plan == "three"
+    fwd()
+    torch.cuda.synchronize()
+    assert int(rot.status.item()) == 0
+    want, valid = oracle_keys(torch, wl, rot)
+    keys = gpu_keys(rot)
+    assert_scores_close(keys, want, valid, 3e-2)
+    topk = rot.topk.cpu().numpy()
+    for r, v in enumerate(valid):
+        assert np.array_equal(topk[r], ref.topk_reference(keys[r], v)), r
+        if v >= 2048:
+            assert ref.validate_topk_band(topk[r], ref.score_values(want[r, :v])), r
+    assert (topk[6] == -1).all()
+    assert np.array_equal(topk[9, :2047], np.arange(2047)) and topk[9, 2047] == -1
+    table = wl.block_table.cpu().numpy()
+    assert np.array_equal(upd.output.cpu().numpy(), ref.fetch_gather(wl.kv_cache.cpu().numpy(), table, topk,
+                                                                     rows_per_request=4))
 
 
 def test_graph_replay_matches_eager(torch_gpu):
