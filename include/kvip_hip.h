@@ -72,7 +72,7 @@
 extern "C" {
 #endif
 
-#define KVIP_HIP_ABI_VERSION 5u
+#define KVIP_HIP_ABI_VERSION 6u
 
 #define KVIP_TOPK 2048
 #define KVIP_BLOCK_TOKENS 128
@@ -450,6 +450,14 @@ typedef struct KvipResidentArgs {
     int32_t hot_stride;           /* hot_cache rows per owner, >= resident */
     int32_t row_bytes;            /* KV row bytes, multiple of 16 */
     int32_t used;                 /* candidates consumed before this step (0 without prefetch) */
+    /* Token-order (TND) outputs, both null or both set (then rows_per_request == 4): output
+     * row t < batch * 4 holds query row unpack_indices[t] when output_valid[t] != 0, and -1
+     * throughout when output_valid[t] == 0; query rows that no output row names are not
+     * published. Null: output row r is query row r. (QueryInputs' unpack indices and output
+     * validity, python/kvip/operators/lifetch/index_update.py:18-21; publication
+     * op_kernel/streaming.cpp:31-44, :66-89.) */
+    const int64_t* unpack_indices;  /* [batch * 4] */
+    const int64_t* output_valid;    /* [batch * 4] */
 } KvipResidentArgs;
 
 /* Resident-prefix classification of one step (the resident TopK, its threshold and the

@@ -17,6 +17,9 @@ __all__ = [
     "PrefillIndexer",
     "quant_lightning_indexer",
     "MixedRound",
+    "VllmIndexSelector",
+    "PagedIndexer",
+    "RequestPlan",
     "SlotLRU",
     "update_abc",
     "lidu",
@@ -36,6 +39,9 @@ _EXPORTS = {
     "PrefillIndexer": ("operators.prefill", "PrefillIndexer"),
     "quant_lightning_indexer": ("operators.prefill", "quant_lightning_indexer"),
     "MixedRound": ("operators.mixed", "MixedRound"),
+    "VllmIndexSelector": ("adapters.vllm.selector", "VllmIndexSelector"),
+    "PagedIndexer": ("adapters.vllm.selector", "PagedIndexer"),
+    "RequestPlan": ("adapters.vllm.selector", "RequestPlan"),
     "SlotLRU": ("cache.lru", "SlotLRU"),
     "update_abc": ("cache.abc", "update_abc"),
     "lidu": ("operators.lidu", "lidu"),

@@ -1,1 +1,1 @@
-"""vLLM adapter: decode query packing and Index-K ingestion on the device."""
+"""vLLM adapter: decode query packing, Index-K ingestion and the indexer selector."""

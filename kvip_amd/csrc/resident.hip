@@ -111,6 +111,7 @@ __global__ __launch_bounds__(kRsThreads) void resident_resolve_kernel(const Kvip
     __shared__ uint32_t s_bitmap[kMaxWords];     // protected or allocated hot slots
     __shared__ uint32_t s_wave[kRsThreads / 64];
     __shared__ uint32_t s_err;
+    __shared__ int s_dest[kMaxQ];  // token-order output row of each query row
 
     const int b = blockIdx.x;
     const int tid = threadIdx.x;
@@ -128,6 +129,7 @@ __global__ __launch_bounds__(kRsThreads) void resident_resolve_kernel(const Kvip
 
     for (int i = tid; i < words; i += kRsThreads) s_bitmap[i] = 0u;
     if (tid == 0) s_err = owner_ok(p, o) ? 0u : KVIP_RESIDENT_ERR_TOKEN;
+    if (tid < kMaxQ) s_dest[tid] = -1;
     __syncthreads();
     const bool good_owner = owner_ok(p, o);
     const int32_t* hot_valid = p.hot_valid + static_cast<size_t>(good_owner ? o : 0) * R;
@@ -301,10 +303,35 @@ __global__ __launch_bounds__(kRsThreads) void resident_resolve_kernel(const Kvip
         __syncthreads();
     }
 
-    // Outputs of every row (-1 throughout for a failed request) and the total.
+    // Outputs of every row (-1 throughout for a failed request) and the total. In token
+    // order, output row s_dest[q] holds query row q (-1: no output row names it) and this
+    // request's four output rows that hold no query are filled with -1.
     const bool failed = s_err != 0u;
+    const bool tnd = p.unpack_indices != nullptr;
+    if (tnd) {
+        const int rows = p.batch * kMaxQ;
+        for (int r = tid; r < rows; r += kRsThreads) {
+            const bool active = p.output_valid[r] != 0;
+            const int64_t src = active ? p.unpack_indices[r] : -1;
+            if (active && src >= static_cast<int64_t>(b) * kMaxQ && src < static_cast<int64_t>(b + 1) * kMaxQ) {
+                s_dest[src - static_cast<int64_t>(b) * kMaxQ] = r;
+            }
+        }
+        for (int e = tid; e < kMaxQ * kTopK; e += kRsThreads) {
+            const int r = b * kMaxQ + e / kTopK;
+            if (p.output_valid[r] == 0) {
+                const size_t at = static_cast<size_t>(r) * kTopK + e % kTopK;
+                p.slot_output[at] = -1;
+                p.logical_output[at] = -1;
+            }
+        }
+        __syncthreads();
+    }
     for (int e = tid; e < Q * kTopK; e += kRsThreads) {
-        const size_t at = static_cast<size_t>(b) * Q * kTopK + e;
+        const int q = e / kTopK;
+        const int dest = tnd ? s_dest[q] : b * Q + q;
+        if (dest < 0) continue;
+        const size_t at = static_cast<size_t>(dest) * kTopK + e % kTopK;
         const int t = s_sel[e];
         const bool live = !failed && t >= 0 && t < H;
         p.slot_output[at] = live ? s_loc[e] : -1;
@@ -578,7 +605,8 @@ uint32_t validate_resident(const KvipResidentArgs* a) {
                     a->resident <= a->history && a->hot_stride >= a->resident && a->row_bytes >= 16 &&
                     a->row_bytes % 16 == 0 && a->used >= 0 && a->used <= kLru && a->host_pool_bytes >= a->row_bytes &&
                     aligned(a->index_keys, 16) && aligned(a->host_pool, 16) && aligned(a->hot_cache, 16) &&
-                    aligned(a->workspace, 16);
+                    aligned(a->workspace, 16) && (a->unpack_indices == nullptr) == (a->output_valid == nullptr) &&
+                    (a->unpack_indices == nullptr || a->rows_per_request == kMaxQ);
     return ok ? KVIP_OK : KVIP_ERR_INVALID;
 }
 

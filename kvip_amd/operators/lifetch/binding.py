@@ -81,6 +81,7 @@ class LIFetchBinding:
         self.round_work = torch.zeros(abi.round_work_words(self.rows), dtype=torch.int32, device=dev)
         self.keys = None
         self.key_scale = None
+        self.query_inputs = None
 
     def bind_index_cache(self, keys, key_scale=None):
         """Bind the paged index-K cache: keys [num_blocks, 128, 128] (Q/K dtype) with
@@ -97,6 +98,27 @@ class LIFetchBinding:
             if key_scale.shape[0] != keys.shape[0] or key_scale.stride(1) != 1 or key_scale.device != self.device:
                 raise ValueError("key scales must match the index-K blocks and be contiguous per block")
         self.keys, self.key_scale = keys, key_scale
+        return self
+
+    def bind_query_inputs(self, inputs):
+        """Read the packed decode queries of a vLLM-adapter QueryInputs in place of this
+        binding's own buffers: query, weights, query scales and query ends become the
+        inputs' tensors, which the adapter's `pack` and `bind_positions` fill every step
+        (the reference binds the same persistent buffers as LI arguments 0, 2, 3 and its
+        query ends, adapters/vllm/binding.py:65-85, selector.py:76-82). Needs fp8
+        queries, bf16 weights, four rows per request and the inputs' batch and heads; call
+        before the forward and the Index update are built. Requests then see
+        min(seq_lens, query_ends) positions: seq_lens is set to the whole context."""
+        if self.rows_per_request != 4 or self.batch != inputs.batch or self.heads != inputs.index_heads:
+            raise ValueError("QueryInputs need a binding of four rows per request with their batch and heads")
+        if self.qk_name != "fp8" or self.weight_code != abi.DTYPE_BF16 or self.query_ends is None:
+            raise ValueError("QueryInputs need fp8 queries, bf16 weights and query ends")
+        if self.query_scale is None or inputs.device != self.device:
+            raise ValueError("QueryInputs need query scales on the binding's device")
+        self.query, self.weights, self.query_scale = inputs.query, inputs.weights, inputs.scale
+        self.query_ends = inputs.query_ends
+        self.seq_lens.fill_(self.key_stride)
+        self.query_inputs = inputs
         return self
 
     @property

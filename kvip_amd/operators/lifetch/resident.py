@@ -7,7 +7,10 @@ addresses and logical ids [owners, history] int64), the request -> owner rows an
 service outputs (logical and slot TopK, int32 [2, rows, 1, 2048]). Next to them it binds
 what the reference keeps behind KVAF: the hot KV cache [owners, hot_stride, row_bytes]
 (position p < resident of an owner is hot slot p) and the host KV pool, a
-device-accessible (pinned) host tensor in which `addresses` are byte offsets.
+device-accessible (pinned) host tensor in which `addresses` are byte offsets. With
+`query_inputs` (a vLLM-adapter QueryInputs, four query rows per request) the outputs are
+published in token order like the reference's (index_update.py:18-21, 85-99): output row
+t holds the query row unpack_indices[t] when output_valid[t], else -1 throughout.
 
 The forward enqueues, on the current stream and without host synchronisation: the
 owner block table, LI scoring of the owners' Index rows, TopK-2048 per query row, and the
@@ -28,7 +31,7 @@ LRU_SLOTS = abi.RESIDENT_LRU_SLOTS
 
 class ResidentIndexUpdate:
     def __init__(self, torch, *, keys, scales, addresses, logical_ids, row_owners, rotating, hot_valid, hot_cache,
-                 host_pool, resident, status=None, outputs=None, used=0):
+                 host_pool, resident, status=None, outputs=None, used=0, query_inputs=None):
         self.torch, self.rotating, self.device = torch, rotating, rotating.device
         if keys.dim() != 3 or keys.shape[2] != INDEX_DIM or keys.dtype != torch.float8_e4m3fn or not keys.is_contiguous():
             raise ValueError("Index keys must be contiguous float8_e4m3fn [owners, history, 128]")
@@ -56,11 +59,15 @@ class ResidentIndexUpdate:
             raise ValueError("LIFetch binding max_context must cover the Index history")
         if not 0 <= used <= LRU_SLOTS:
             raise ValueError("used must be in 0..2048")
+        if query_inputs is not None and (rotating.rows_per_request != 4 or query_inputs.batch != rotating.batch or
+                                         query_inputs.device != rotating.device):
+            raise ValueError("token-order outputs need the binding's batch, four query rows and device")
         dev = self.device
         if any(t.device != dev for t in (keys, scales, addresses, logical_ids, row_owners, hot_valid, hot_cache)):
             raise ValueError("Index storage, hot cache and the LIFetch binding must share one device")
         self.keys, self.scales, self.addresses, self.logical_ids = keys, scales, addresses, logical_ids
         self.row_owners, self.hot_valid, self.hot_cache, self.host_pool = row_owners, hot_valid, hot_cache, host_pool
+        self.query_inputs = query_inputs
         self.owners, self.history, self.resident, self.used = owners, history, resident, used
         rows, q = rotating.rows, rotating.rows_per_request
         self.status = torch.zeros(rotating.batch, dtype=torch.int32, device=dev) if status is None else status
@@ -111,6 +118,8 @@ class ResidentIndexUpdate:
             host_pool_bytes=self.host_pool.numel(), batch=r.batch, rows_per_request=r.rows_per_request,
             owners=self.owners, history=self.history, resident=self.resident, hot_stride=int(self.hot_cache.shape[1]),
             row_bytes=int(self.hot_cache.shape[2]), used=self.used,
+            unpack_indices=p(self.query_inputs.unpack_indices) if self.query_inputs is not None else 0,
+            output_valid=p(self.query_inputs.output_valid) if self.query_inputs is not None else 0,
         )
 
 

@@ -6,6 +6,10 @@ bind_positions   - QueryInputs.bind_positions (:127-133)
 pack             - QueryInputs.pack (:135-152), a byte gather
 ingest_decode    - VllmIndexCacheStorage.ingest_decode (adapters/vllm/index_import.py:39-52)
 ingest_prefill   - VllmIndexCacheStorage.ingest_prefill (:18-37)
+publish_outputs  - token-order (TND) publication of the Index update's outputs
+                   (operators/lifetch/index_update.py:18-21; op_kernel/streaming.cpp:31-44,
+                   :66-89); pinned by the inverse-of-gather property in
+                   tests/test_oracle_adapters.py
 Pinned by the known answers of tests/adapters/test_inputs.py (tests/test_oracle_adapters.py).
 """
 from __future__ import annotations
@@ -73,3 +77,13 @@ def ingest_prefill(keys, scales, source_keys, source_scales, block_table, block_
         for j in range(begin, stop):
             keys[owner, positions[j]] = source_keys[slot_mapping[j]]
             scales[owner, positions[j]] = source_scales[slot_mapping[j]]
+
+
+def publish_outputs(meta, rows):
+    """rows [batch*4, ...] in query-row (slot) order -> token order: output row t holds
+    query row unpack[t] when output_valid[t], else -1 throughout."""
+    out = np.full_like(rows, -1)
+    for t in range(meta.shape[1]):
+        if meta[3, t]:
+            out[t] = rows[int(meta[2, t])]
+    return out

@@ -107,3 +107,54 @@ def test_committed_candidates():
     cands = np.array([9, 1, 7, 3, 0, 12], np.int32)
     assert committed_candidates(cands, 100, 16) is cands
     assert committed_candidates(cands, 5, 16).tolist() == [1, 3, 0, 2, 4, 9]
+
+
+def test_token_order_publication_round_trips_pack():
+    """publish_outputs undoes pack: a row computed from each packed query, published in
+    token order, comes back to the token that query came from (decode-only batches, where
+    the gather indices are the tokens themselves), and every other output row is -1."""
+    rng = np.random.default_rng(11)
+    for trial in range(20):
+        batch = int(rng.integers(1, 9))
+        counts = [int(c) for c in rng.integers(0, 5, batch)]
+        meta = ref.prepare_metadata(batch, counts)
+        tokens = sum(counts)
+        token_rows = rng.integers(0, 1 << 30, (max(tokens, 1), 7))
+        packed = np.full((batch * 4, 7), -5, np.int64)
+        valid = meta[1] != 0
+        packed[valid] = token_rows[meta[0][valid]]
+        out = ref.publish_outputs(meta, packed)
+        assert np.array_equal(out[:tokens], token_rows[:tokens]), trial
+        assert (out[tokens:] == -1).all(), trial
+
+
+def test_token_order_publication_kat():
+    # Counts [1, 4] of a batch of 3 (the known answer of test_inputs.py:30-41): tokens
+    # 0..4 come from query rows 0, 4, 5, 6, 7; output rows 5..11 hold no token.
+    meta = ref.prepare_metadata(3, [1, 4])
+    rows = np.arange(12)[:, None] * 10 + np.arange(3)[None, :]
+    out = ref.publish_outputs(meta, rows)
+    assert out[:5, 0].tolist() == [0, 40, 50, 60, 70]
+    assert (out[5:] == -1).all()
+
+
+def test_binding_reads_query_inputs_on_cpu():
+    """LIFetchBinding.bind_query_inputs swaps in the packed buffers of QueryInputs and
+    refuses bindings whose shape or dtypes differ (host logic only)."""
+    torch = pytest.importorskip("torch")
+    import kvip_amd
+
+    inputs = kvip_amd.QueryInputs(torch, 3, "cpu", pin_memory=False, history=512)
+    rot = kvip_amd.LIFetchBinding(torch, batch=3, max_context=512, device="cpu", rows_per_request=4,
+                                  weight_dtype=torch.bfloat16, query_ends=True).bind_query_inputs(inputs)
+    for mine, theirs in ((rot.query, inputs.query), (rot.weights, inputs.weights), (rot.query_scale, inputs.scale),
+                         (rot.query_ends, inputs.query_ends)):
+        assert mine.data_ptr() == theirs.data_ptr()
+    assert rot.seq_lens.tolist() == [512] * 3
+    for kwargs in (dict(rows_per_request=1), dict(weight_dtype=torch.float32), dict(query_ends=False),
+                   dict(heads=32), dict(batch=2)):
+        args = dict(batch=3, max_context=512, device="cpu", rows_per_request=4, weight_dtype=torch.bfloat16,
+                    query_ends=True)
+        args.update(kwargs)
+        with pytest.raises(ValueError):
+            kvip_amd.LIFetchBinding(torch, **args).bind_query_inputs(inputs)
