@@ -42,6 +42,7 @@ def parse():
     p.add_argument("--no-resident", action="store_true", help="skip the resident-cache round timing leg")
     p.add_argument("--no-prefill", action="store_true", help="skip the config-3 prefill timing leg")
     p.add_argument("--no-mixed", action="store_true", help="skip the config-5 mixed-round timing leg")
+    p.add_argument("--no-sfa", action="store_true", help="skip the sparse-attention consumer timing leg")
     p.add_argument("--copy-calibration", action="store_true",
                    help="also run a plain 1 GiB device copy (for rocprof FETCH/WRITE_SIZE scaling)")
     return p.parse_args()
@@ -64,15 +65,16 @@ def algorithmic_bytes(wl, heads, has_qscale):
 
 def measured_traffic(kernel):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
-    summary, when it was taken on the current library sources; otherwise None."""
-    from kvip_amd.runtime.build import source_digest
+    summary, when it was taken on the current sources of the measured kernels (the files it
+    lists); otherwise None."""
+    from kvip_amd.runtime.build import files_digest
 
     path = ROOT / "profiles" / "decode_c2_traffic.json"
     try:
         data = json.loads(path.read_text())
     except (OSError, ValueError):
         return None
-    if data.get("source_digest") != source_digest():
+    if not data.get("sources") or data.get("source_digest") != files_digest(data["sources"]):
         return None
     return data.get("traffic_bytes", {}).get(kernel)
 
@@ -286,6 +288,57 @@ def prefill_leg(torch, kvip_amd, device, seed, iters=5):
             "index_update_gbs": round(update_bytes / (t["index_update"] * 1e-6) / 1e9, 1), "iters": iters}
 
 
+def sfa_leg(torch, kvip_amd, device, seed, iters=20):
+    """The consumer of the selected rows: sparse attention of 64 decode rows over their
+    2048 selected 656-byte KV rows (kvip_hip_sparse_attention), 16 heads (MLA heads per GPU
+    at 8-way tensor parallelism) and 128 heads, on the gathered buffer of a contiguous Fetch
+    (indices 0..2047) and on a resident hot cache (2048 random slots of 16384 per request).
+    Each call is one launch; 10 calls are captured in a hipGraph and replayed."""
+    from kvip_amd.operators.sfa import SparseAttention
+
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    rows, out = 64, {}
+    for layout, per_row in (("gathered", TOPK), ("hot_cache", 16384)):
+        blocks = rows * per_row // 128
+        kv = torch.randint(0, 256, (blocks, 128, 656), generator=gen, device=device, dtype=torch.uint8) & 0x77
+        table = (torch.arange(rows, dtype=torch.int32, device=device)[:, None] * (per_row // 128) +
+                 torch.arange(per_row // 128, dtype=torch.int32, device=device)[None, :]).contiguous()
+        if per_row == TOPK:
+            idx = torch.arange(TOPK, dtype=torch.int32, device=device).repeat(rows, 1)
+        else:
+            idx = torch.argsort(torch.rand((rows, per_row), generator=gen, device=device), dim=1)[:, :TOPK]
+            idx = idx.to(torch.int32).contiguous()
+        for heads in (16, 128):
+            q = (torch.rand((rows, heads, 576), generator=gen, device=device) * 0.4 - 0.2).to(torch.bfloat16)
+            op = SparseAttention(torch, rows=rows, heads=heads, device=device).bind(q, kv, table, idx)
+            op()
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                for _ in range(10):
+                    op()
+            graph.replay()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            stream = torch.cuda.current_stream()
+            e0.record(stream)
+            for _ in range(iters):
+                graph.replay()
+            e1.record(stream)
+            e1.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / (iters * 10)
+            if op.status.any():
+                raise RuntimeError(f"sparse attention: device status {op.status.cpu().tolist()}")
+            nbytes = rows * TOPK * (656 + 4) + rows * heads * (576 * 2 + 512 * 4)
+            out[f"{layout}_h{heads}"] = {"us": round(us, 2), "bytes": nbytes,
+                                         "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
+                                         "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    out["workload"] = ("sparse attention of 64 rows x 2048 selected 656-byte KV rows (bf16 query [heads, 576], "
+                       "fp32 out [heads, 512]); bytes = KV rows + indices + query + output, each once")
+    return out
+
+
 def mixed_leg(torch, kvip_amd, device, seed, iters=20):
     """one continuous-batching round captured as a single hipGraph and
     replayed back to back: Index ingest of all new tokens (32 decode + 2048 + 1536 prefill
@@ -486,6 +539,8 @@ def main():
         result["prefill"] = prefill_leg(torch, kvip_amd, device, args.seed)
     if not args.no_mixed:
         result["mixed"] = mixed_leg(torch, kvip_amd, device, args.seed)
+    if not args.no_sfa:
+        result["sfa"] = sfa_leg(torch, kvip_amd, device, args.seed)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(torch, wl, rot, args.cpu_seconds)
     print(json.dumps(result), flush=True)

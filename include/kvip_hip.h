@@ -460,6 +460,34 @@ typedef struct KvipResidentArgs {
     const int64_t* output_valid;    /* [batch * 4] */
 } KvipResidentArgs;
 
+/* Sparse attention over the selected KV rows (the consumer of the LIFetch outputs: the
+ * service's sparse flash attention, tests/operators/lifetch/support/correctness.py:261-339;
+ * row format workloads.py:493-515). A 656-byte row is 512 fp8 e4m3 nope features, 64 bf16
+ * rope features and 4 fp32 scales (scale k covers nope features 128k..128k+127):
+ * key = [nope * scale, rope] (576), value = nope * scale (512). For query row r (request
+ * b = r / rows_per_request) and head h, over j with indices[r][j] >= 0 (position t lives in
+ * block block_table[b][t / 128], row t % 128, of kv_cache):
+ *   s_j = scale * <query[r][h], key_j>, p_j = exp(s_j - max s),
+ *   output[r][h] = sum_j bf16(p_j) * value_j / sum_j p_j   (0 when no index is valid).
+ * Bad positions or blocks set KVIP_STATUS_BAD_TOKEN / _BAD_BLOCK and count as absent. */
+typedef struct KvipSparseAttnArgs {
+    const uint16_t* query;        /* [rows, heads, 576] bf16, 16-byte aligned */
+    const uint8_t* kv_cache;      /* [num_blocks] blocks of 128 rows, 16-byte aligned */
+    const int32_t* block_table;   /* [rows / rows_per_request, max_blocks] */
+    const int32_t* indices;       /* [rows, 2048] positions, -1 = none */
+    float* output;                /* [rows, heads, 512] */
+    uint32_t* status;             /* optional */
+    int64_t kv_block_stride;      /* bytes between blocks, >= 128 * row_stride */
+    int32_t row_stride;           /* bytes between rows, >= 656, multiple of 16 */
+    int32_t rows;
+    int32_t rows_per_request;
+    int32_t heads;                /* 1..128 */
+    int32_t max_blocks;
+    int32_t num_blocks;
+    float scale;                  /* softmax scale, e.g. 576^-0.5 */
+    int32_t reserved;
+} KvipSparseAttnArgs;
+
 /* Resident-prefix classification of one step (the resident TopK, its threshold and the
  * hit bits the speculative prefetch reads): for query row r with valid positions
  * v = min(seq_lens[b], query_ends[r]) and prefix p = min(v, resident), given prefix_topk =
@@ -523,6 +551,9 @@ uint32_t kvip_hip_resident_round(const KvipResidentArgs* args, void* stream);
  * scoring of the owners' Index rows, TopK-2048, then kvip_hip_resident_round. */
 uint32_t kvip_hip_resident_forward(const KvipIndexerArgs* indexer, const KvipTopkArgs* topk,
                                    const KvipResidentArgs* resident, void* stream);
+/* Sparse attention of the selected rows (no reference entry point: the consumer the
+ * reference's tests run on its outputs, correctness.py:261-339). */
+uint32_t kvip_hip_sparse_attention(const KvipSparseAttnArgs* args, void* stream);
 
 #ifdef __cplusplus
 }

@@ -17,6 +17,8 @@ __all__ = [
     "PrefillIndexer",
     "quant_lightning_indexer",
     "MixedRound",
+    "SparseAttention",
+    "sparse_attention",
     "VllmIndexSelector",
     "PagedIndexer",
     "RequestPlan",
@@ -39,6 +41,8 @@ _EXPORTS = {
     "PrefillIndexer": ("operators.prefill", "PrefillIndexer"),
     "quant_lightning_indexer": ("operators.prefill", "quant_lightning_indexer"),
     "MixedRound": ("operators.mixed", "MixedRound"),
+    "SparseAttention": ("operators.sfa", "SparseAttention"),
+    "sparse_attention": ("operators.sfa", "sparse_attention"),
     "VllmIndexSelector": ("adapters.vllm.selector", "VllmIndexSelector"),
     "PagedIndexer": ("adapters.vllm.selector", "PagedIndexer"),
     "RequestPlan": ("adapters.vllm.selector", "RequestPlan"),

@@ -168,9 +168,18 @@ class PrefixClassifyArgs(ctypes.Structure):
     ]
 
 
+class SparseAttnArgs(ctypes.Structure):
+    _fields_ = [
+        ("query", _p), ("kv_cache", _p), ("block_table", _p), ("indices", _p), ("output", _p), ("status", _p),
+        ("kv_block_stride", _i64), ("row_stride", _i32), ("rows", _i32), ("rows_per_request", _i32),
+        ("heads", _i32), ("max_blocks", _i32), ("num_blocks", _i32), ("scale", ctypes.c_float), ("reserved", _i32),
+    ]
+
+
 # name -> (argtypes, restype); must list every function declared in include/kvip_hip.h.
 PROTOTYPES = {
     "kvip_hip_abi_version": ([], ctypes.c_uint32),
+    "kvip_hip_sparse_attention": ([ctypes.POINTER(SparseAttnArgs), _p], ctypes.c_uint32),
     "kvip_hip_indexer_decode": ([ctypes.POINTER(IndexerArgs), _p], ctypes.c_uint32),
     "kvip_hip_indexer_prefill": ([ctypes.POINTER(PrefillArgs), _p], ctypes.c_uint32),
     "kvip_hip_topk": ([ctypes.POINTER(TopkArgs), _p], ctypes.c_uint32),

@@ -58,6 +58,18 @@ def source_digest() -> str:
     return digest.hexdigest()
 
 
+def files_digest(paths) -> str:
+    """Digest of the named files (paths relative to the repository root) and the compile
+    flags: identifies the sources a measurement of particular kernels was taken on."""
+    digest = hashlib.sha256()
+    for rel in sorted(paths):
+        path = ROOT / rel
+        digest.update(rel.encode())
+        digest.update(path.read_bytes() if path.is_file() else b"<missing>")
+    digest.update(" ".join(HIPCC_FLAGS).encode())
+    return digest.hexdigest()
+
+
 def build_libraries(force: bool = True, verbose: bool = False) -> Path:
     """Compile every HIP source into kvip_amd/_lib/libkvip_hip.so.
 
