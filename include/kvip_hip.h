@@ -72,7 +72,7 @@
 extern "C" {
 #endif
 
-#define KVIP_HIP_ABI_VERSION 6u
+#define KVIP_HIP_ABI_VERSION 7u
 
 #define KVIP_TOPK 2048
 #define KVIP_BLOCK_TOKENS 128
@@ -477,6 +477,8 @@ typedef struct KvipSparseAttnArgs {
     const int32_t* indices;       /* [rows, 2048] positions, -1 = none */
     float* output;                /* [rows, heads, 512] */
     uint32_t* status;             /* optional */
+    float* workspace;             /* kvip_hip_sparse_attention_workspace_bytes(rows, heads) bytes
+                                     (null allowed when that is 0); partials of the index splits */
     int64_t kv_block_stride;      /* bytes between blocks, >= 128 * row_stride */
     int32_t row_stride;           /* bytes between rows, >= 656, multiple of 16 */
     int32_t rows;
@@ -554,6 +556,7 @@ uint32_t kvip_hip_resident_forward(const KvipIndexerArgs* indexer, const KvipTop
 /* Sparse attention of the selected rows (no reference entry point: the consumer the
  * reference's tests run on its outputs, correctness.py:261-339). */
 uint32_t kvip_hip_sparse_attention(const KvipSparseAttnArgs* args, void* stream);
+uint64_t kvip_hip_sparse_attention_workspace_bytes(int32_t rows, int32_t heads);
 
 #ifdef __cplusplus
 }

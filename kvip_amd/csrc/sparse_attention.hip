@@ -11,12 +11,15 @@
 // i.e. softmax attention with bf16 probabilities in the value product (the reference rounds
 // the normalised probabilities to bf16; here the unnormalised ones, divided once at the end).
 //
-// One workgroup per (query row, group of 16 heads) streams the row's indices in tiles of 64
-// tokens: the rows are gathered and dequantised to bf16 in LDS, the logits of the tile come
-// from bf16 MFMA (v_mfma_f32_16x16x32_bf16: 16 heads x 16 tokens x 32 features), an online
-// softmax keeps the running maximum and sum per head, and the value product is a second MFMA
-// (16 heads x 16 features x 32 tokens) accumulated in registers. HBM traffic is one read of
-// each selected row; everything else stays on chip.
+// One workgroup per (query row, group of 16 heads, split of the 2048 indices) streams its
+// indices in tiles of 64 tokens: the rows are gathered (all loads of a tile in flight at once)
+// and dequantised to bf16 in LDS with the hardware conversions (v_cvt_pk_f32_fp8, OCP e4m3 on
+// gfx950, and v_cvt_pk_bf16_f32), the logits of the tile come from bf16 MFMA
+// (v_mfma_f32_16x16x32_bf16: 16 heads x 16 tokens x 32 features), an online softmax keeps the
+// running maximum and sum per head, and the value product is a second MFMA (16 heads x 16
+// features x 32 tokens) accumulated in registers. Splits (up to 8, enough workgroups to fill
+// the chip) leave (max, sum, unnormalised output) per head in the workspace and a second
+// launch merges them. HBM traffic is one read of each selected row plus the partials.
 #include "kvip_device.h"
 
 namespace kvip {
@@ -24,6 +27,8 @@ namespace {
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
 typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef __attribute__((ext_vector_type(2))) float f32x2;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
 
 constexpr int kSaThreads = 256;
 constexpr int kSaTile = 64;                 // tokens per tile
@@ -33,17 +38,29 @@ constexpr int kValueDim = 512;
 constexpr int kPieces = KVIP_KV_ROW_BYTES / 16;  // 41 pieces of a row, the last holds the scales
 constexpr int kPitch = kKeyDim + 8;         // bf16 per LDS key row (16 bytes of padding)
 constexpr int kPPitch = kSaTile + 8;        // bf16 per LDS probability row
+constexpr int kStageIters = (kSaTile * (kPieces - 1) + kSaThreads - 1) / kSaThreads;
+constexpr int kPartial = 2 * kSaHeads + kSaHeads * kValueDim;  // floats per split: max, sum, output
+constexpr int kMaxSplits = 8;
+
+// Index splits per (row, head group): doubled up to 8 while the launch has fewer than 512
+// workgroups.
+__host__ __device__ inline int sa_splits(int rows, int groups) {
+    int s = 1;
+    while (s < kMaxSplits && static_cast<int64_t>(rows) * groups * s < 512) s *= 2;
+    return s;
+}
+
+KVIP_DEVICE uint32_t pack_bf16(float a, float b) {  // hardware round to nearest even
+    const bf16x2 v = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
+    uint32_t u;
+    __builtin_memcpy(&u, &v, 4);
+    return u;
+}
 
 KVIP_DEVICE uint16_t bf16_bits(float f) {  // round to nearest even (finite inputs)
     uint32_t u = __float_as_uint(f);
     u += 0x7FFFu + ((u >> 16) & 1u);
     return static_cast<uint16_t>(u >> 16);
-}
-
-KVIP_DEVICE float fp8_value(uint32_t b) {  // OCP e4m3 (finite codes)
-    const uint32_t e = (b >> 3) & 15u, m = b & 7u;
-    const float mag = e == 0u ? static_cast<float>(m) * 0x1p-9f : __uint_as_float(((e + 120u) << 23) | (m << 20));
-    return (b & 128u) ? -mag : mag;
 }
 
 KVIP_DEVICE bf16x8 as_bf16x8(v4i v) {
@@ -58,12 +75,16 @@ __global__ __launch_bounds__(kSaThreads) void sparse_attention_kernel(const Kvip
     __shared__ float s_red[4][kSaHeads];
     __shared__ int64_t s_src[kSaTile];
 
-    // XCD-aware order: the head groups of a query row share blockIdx % 8, so they run on one
-    // XCD, whose L2 then serves that row's KV rows to every group after the first read.
+    // XCD-aware order: the workgroups of a query row (head groups x splits) share
+    // blockIdx % 8, so they run on one XCD, whose L2 then serves the row's KV rows and query to
+    // every head group after the first read.
     const int groups = (p.heads + kSaHeads - 1) / kSaHeads;
-    const int chunk = blockIdx.x / (8 * groups), within = blockIdx.x % (8 * groups);
+    const int splits = sa_splits(p.rows, groups);
+    const int units = groups * splits;
+    const int chunk = blockIdx.x / (8 * units), within = blockIdx.x % (8 * units);
     const int r = chunk * 8 + within % 8;
-    const int h0 = (within / 8) * kSaHeads;
+    const int unit = within / 8, hg = unit % groups, sp = unit / groups;
+    const int h0 = hg * kSaHeads;
     if (r >= p.rows) return;
     const int b = r / p.rows_per_request;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -93,7 +114,8 @@ __global__ __launch_bounds__(kSaThreads) void sparse_attention_kernel(const Kvip
     const int* idx_row = p.indices + static_cast<size_t>(r) * kTopK;
     const int capacity = p.max_blocks * kBlockTokens;
 
-    for (int t0 = 0; t0 < kTopK; t0 += kSaTile) {
+    const int span = kTopK / splits;
+    for (int t0 = sp * span; t0 < (sp + 1) * span; t0 += kSaTile) {
         // Source rows of the tile.
         if (tid < kSaTile) {
             const int t = idx_row[t0 + tid];
@@ -111,33 +133,53 @@ __global__ __launch_bounds__(kSaThreads) void sparse_attention_kernel(const Kvip
             s_src[tid] = src;
         }
         __syncthreads();
-        // Gather + dequantise: pieces 0..31 are 16 nope bytes, 32..39 8 rope values.
-        for (int q = tid; q < kSaTile * (kPieces - 1); q += kSaThreads) {
-            const int i = q / (kPieces - 1), pc = q - i * (kPieces - 1);
-            const int64_t src = s_src[i];
-            uint16_t* dst = s_k + i * kPitch;
-            if (pc < 32) {
-                uint32_t out[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
-                if (src >= 0) {
-                    const uint8_t* row = p.kv_cache + src;
-                    const v4i raw = *reinterpret_cast<const v4i*>(row + pc * 16);
-                    const float sc = *reinterpret_cast<const float*>(row + 512 + 128 + (pc >> 3) * 4);
+        // Gather + dequantise: pieces 0..31 are 16 nope bytes, 32..39 8 rope values; the loads
+        // of half a tile are issued before their conversions (a whole tile's would cost the
+        // registers of a second wave per SIMD).
 #pragma unroll
-                    for (int k = 0; k < 8; ++k) {
-                        const uint32_t word = static_cast<uint32_t>(raw[k >> 1]);
-                        const uint32_t lo = (word >> ((k & 1) * 16)) & 0xFFu, hi = (word >> ((k & 1) * 16 + 8)) & 0xFFu;
-                        out[k] = bf16_bits(fp8_value(lo) * sc) | (static_cast<uint32_t>(bf16_bits(fp8_value(hi) * sc)) << 16);
+        for (int half = 0; half < 2; ++half) {
+            constexpr int kHalf = (kStageIters + 1) / 2;
+            v4i raw[kHalf];
+            float sc[kHalf];
+#pragma unroll
+            for (int j = 0; j < kHalf; ++j) {
+                const int q = (half * kHalf + j) * kSaThreads + tid;
+                raw[j] = v4i{0, 0, 0, 0};
+                sc[j] = 0.f;
+                if (half * kHalf + j < kStageIters && q < kSaTile * (kPieces - 1)) {
+                    const int i = q / (kPieces - 1), pc = q - i * (kPieces - 1);
+                    const int64_t src = s_src[i];
+                    if (src >= 0) {
+                        const uint8_t* row = p.kv_cache + src;
+                        raw[j] = *reinterpret_cast<const v4i*>(row + (pc < 32 ? pc * 16 : 512 + (pc - 32) * 16));
+                        if (pc < 32) sc[j] = *reinterpret_cast<const float*>(row + 640 + (pc >> 3) * 4);
                     }
                 }
-                v4i* d = reinterpret_cast<v4i*>(dst + pc * 16);
-                d[0] = v4i{static_cast<int>(out[0]), static_cast<int>(out[1]), static_cast<int>(out[2]),
-                           static_cast<int>(out[3])};
-                d[1] = v4i{static_cast<int>(out[4]), static_cast<int>(out[5]), static_cast<int>(out[6]),
-                           static_cast<int>(out[7])};
-            } else {
-                const v4i v = src >= 0 ? *reinterpret_cast<const v4i*>(p.kv_cache + src + 512 + (pc - 32) * 16)
-                                       : v4i{0, 0, 0, 0};
-                *reinterpret_cast<v4i*>(dst + 512 + (pc - 32) * 8) = v;
+            }
+#pragma unroll
+            for (int j = 0; j < kHalf; ++j) {
+                const int q = (half * kHalf + j) * kSaThreads + tid;
+                if (half * kHalf + j < kStageIters && q < kSaTile * (kPieces - 1)) {
+                    const int i = q / (kPieces - 1), pc = q - i * (kPieces - 1);
+                    uint16_t* dst = s_k + i * kPitch;
+                    if (pc < 32) {
+                        uint32_t out[8];
+#pragma unroll
+                        for (int k = 0; k < 4; ++k) {
+                            const f32x2 a = __builtin_amdgcn_cvt_pk_f32_fp8(raw[j][k], false);
+                            const f32x2 c = __builtin_amdgcn_cvt_pk_f32_fp8(raw[j][k], true);
+                            out[2 * k] = pack_bf16(a[0] * sc[j], a[1] * sc[j]);
+                            out[2 * k + 1] = pack_bf16(c[0] * sc[j], c[1] * sc[j]);
+                        }
+                        v4i* d = reinterpret_cast<v4i*>(dst + pc * 16);
+                        d[0] = v4i{static_cast<int>(out[0]), static_cast<int>(out[1]), static_cast<int>(out[2]),
+                                   static_cast<int>(out[3])};
+                        d[1] = v4i{static_cast<int>(out[4]), static_cast<int>(out[5]), static_cast<int>(out[6]),
+                                   static_cast<int>(out[7])};
+                    } else {
+                        *reinterpret_cast<v4i*>(dst + 512 + (pc - 32) * 8) = raw[j];
+                    }
+                }
             }
         }
         __syncthreads();
@@ -223,6 +265,24 @@ __global__ __launch_bounds__(kSaThreads) void sparse_attention_kernel(const Kvip
         const int h = lg * 4 + i;
         l_tot[i] = s_red[0][h] + s_red[1][h] + s_red[2][h] + s_red[3][h];
     }
+    if (splits > 1) {  // partial of this split: max and sum per head, unnormalised output
+        float* ws = p.workspace + ((static_cast<size_t>(r) * groups + hg) * splits + sp) * kPartial;
+        if (w == 0 && lr == 0) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                ws[lg * 4 + i] = m_run[i];
+                ws[kSaHeads + lg * 4 + i] = l_tot[i];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float* o = ws + 2 * kSaHeads + (lg * 4 + i) * kValueDim + w * 128 + lr;
+#pragma unroll
+            for (int t = 0; t < 8; ++t) o[t * 16] = acc[t][i];
+        }
+        report(p.status, err);
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int h = h0 + lg * 4 + i;
@@ -235,7 +295,45 @@ __global__ __launch_bounds__(kSaThreads) void sparse_attention_kernel(const Kvip
     report(p.status, err);
 }
 
+// Merge of the splits: workgroup (row, head group, 64-feature chunk).
+__global__ __launch_bounds__(kSaThreads) void sparse_attention_merge_kernel(const KvipSparseAttnArgs p) {
+    __shared__ float s_w[kMaxSplits][kSaHeads];
+    __shared__ float s_inv[kSaHeads];
+    const int groups = (p.heads + kSaHeads - 1) / kSaHeads;
+    const int splits = sa_splits(p.rows, groups);
+    const int unit = blockIdx.x / 8, part = blockIdx.x % 8;
+    const int r = unit / groups, h0 = (unit % groups) * kSaHeads;
+    const float* ws = p.workspace + static_cast<size_t>(unit) * splits * kPartial;
+    const int tid = threadIdx.x;
+    if (tid < kSaHeads) {
+        float m = -INFINITY;
+        for (int s = 0; s < splits; ++s) m = fmaxf(m, ws[s * kPartial + tid]);
+        float l = 0.f;
+        for (int s = 0; s < splits; ++s) {
+            const float wgt = m == -INFINITY ? 0.f : __expf(ws[s * kPartial + tid] - m);
+            s_w[s][tid] = wgt;
+            l += wgt * ws[s * kPartial + kSaHeads + tid];
+        }
+        s_inv[tid] = l > 0.f ? 1.f / l : 0.f;
+    }
+    __syncthreads();
+    for (int o = tid; o < kSaHeads * 64; o += kSaThreads) {
+        const int h = o / 64, col = part * 64 + o % 64;
+        if (h0 + h >= p.heads) continue;
+        float v = 0.f;
+        for (int s = 0; s < splits; ++s) v += s_w[s][h] * ws[s * kPartial + 2 * kSaHeads + h * kValueDim + col];
+        p.output[(static_cast<size_t>(r) * p.heads + h0 + h) * kValueDim + col] = v * s_inv[h];
+    }
+}
+
 }  // namespace
+
+uint64_t sparse_attention_workspace_bytes(int rows, int heads) {
+    if (rows < 1 || heads < 1) return 0;
+    const int groups = (heads + kSaHeads - 1) / kSaHeads;
+    const int splits = sa_splits(rows, groups);
+    return splits > 1 ? static_cast<uint64_t>(rows) * groups * splits * kPartial * sizeof(float) : 0;
+}
 
 uint32_t validate_sparse_attention(const KvipSparseAttnArgs* a) {
     if (a == nullptr) return KVIP_ERR_INVALID;
@@ -246,7 +344,8 @@ uint32_t validate_sparse_attention(const KvipSparseAttnArgs* a) {
                     a->kv_block_stride % 16 == 0 &&
                     a->kv_block_stride >= static_cast<int64_t>(kBlockTokens) * a->row_stride &&
                     (reinterpret_cast<uintptr_t>(a->kv_cache) & 15u) == 0 &&
-                    (reinterpret_cast<uintptr_t>(a->query) & 15u) == 0 && a->rows <= 65535 * 64;
+                    (reinterpret_cast<uintptr_t>(a->query) & 15u) == 0 && a->rows <= 65535 * 64 &&
+                    (a->workspace != nullptr || sparse_attention_workspace_bytes(a->rows, a->heads) == 0);
     return ok ? KVIP_OK : KVIP_ERR_INVALID;
 }
 
@@ -256,8 +355,17 @@ extern "C" uint32_t kvip_hip_sparse_attention(const KvipSparseAttnArgs* args, vo
     const uint32_t rc = kvip::validate_sparse_attention(args);
     if (rc != KVIP_OK) return rc;
     const int groups = (args->heads + kvip::kSaHeads - 1) / kvip::kSaHeads;
-    const dim3 grid(((args->rows + 7) / 8) * 8 * groups);
-    hipLaunchKernelGGL(kvip::sparse_attention_kernel, grid, dim3(kvip::kSaThreads), 0,
-                       static_cast<hipStream_t>(stream), *args);
+    const int splits = kvip::sa_splits(args->rows, groups);
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(kvip::sparse_attention_kernel, dim3(((args->rows + 7) / 8) * 8 * groups * splits),
+                       dim3(kvip::kSaThreads), 0, s, *args);
+    if (splits > 1) {
+        hipLaunchKernelGGL(kvip::sparse_attention_merge_kernel, dim3(args->rows * groups * 8), dim3(kvip::kSaThreads),
+                           0, s, *args);
+    }
     return static_cast<uint32_t>(hipGetLastError());
+}
+
+extern "C" uint64_t kvip_hip_sparse_attention_workspace_bytes(int32_t rows, int32_t heads) {
+    return kvip::sparse_attention_workspace_bytes(rows, heads);
 }

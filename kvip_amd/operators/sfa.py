@@ -36,6 +36,10 @@ class SparseAttention:
         self.output = torch.zeros((rows, heads, VALUE_DIM), dtype=torch.float32, device=self.device)
         self.status = torch.zeros(1, dtype=torch.int32, device=self.device)
         self.library = abi.load_library()
+        # Partials of the index splits (the launch splits each row's 2048 indices when there
+        # are too few rows to fill the GPU).
+        nbytes = int(self.library.kvip_hip_sparse_attention_workspace_bytes(rows, heads))
+        self.workspace = torch.empty(max(nbytes // 4, 1), dtype=torch.float32, device=self.device)
         self.args = None
 
     def bind(self, query, kv_cache, block_table, indices, scale=KEY_DIM ** -0.5):
@@ -64,7 +68,8 @@ class SparseAttention:
         p = abi.ptr
         self.args = abi.SparseAttnArgs(
             query=p(query), kv_cache=p(kv_cache), block_table=p(block_table), indices=p(indices),
-            output=p(self.output), status=p(self.status), kv_block_stride=kv_cache.stride(0),
+            output=p(self.output), status=p(self.status), workspace=p(self.workspace),
+            kv_block_stride=kv_cache.stride(0),
             row_stride=kv_cache.stride(1), rows=self.rows, rows_per_request=self.rows_per_request, heads=self.heads,
             max_blocks=int(block_table.shape[1]), num_blocks=int(kv_cache.shape[0]), scale=float(scale))
         self._bound = (query, kv_cache, block_table, indices)

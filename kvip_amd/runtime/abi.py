@@ -9,7 +9,7 @@ import ctypes
 from pathlib import Path
 
 LIBRARY = Path(__file__).resolve().parents[1] / "_lib" / "libkvip_hip.so"
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 KVIP_OK = 0
 KVIP_ERR_INVALID = 100000
@@ -171,7 +171,7 @@ class PrefixClassifyArgs(ctypes.Structure):
 class SparseAttnArgs(ctypes.Structure):
     _fields_ = [
         ("query", _p), ("kv_cache", _p), ("block_table", _p), ("indices", _p), ("output", _p), ("status", _p),
-        ("kv_block_stride", _i64), ("row_stride", _i32), ("rows", _i32), ("rows_per_request", _i32),
+        ("workspace", _p), ("kv_block_stride", _i64), ("row_stride", _i32), ("rows", _i32), ("rows_per_request", _i32),
         ("heads", _i32), ("max_blocks", _i32), ("num_blocks", _i32), ("scale", ctypes.c_float), ("reserved", _i32),
     ]
 
@@ -180,6 +180,7 @@ class SparseAttnArgs(ctypes.Structure):
 PROTOTYPES = {
     "kvip_hip_abi_version": ([], ctypes.c_uint32),
     "kvip_hip_sparse_attention": ([ctypes.POINTER(SparseAttnArgs), _p], ctypes.c_uint32),
+    "kvip_hip_sparse_attention_workspace_bytes": ([_i32, _i32], ctypes.c_uint64),
     "kvip_hip_indexer_decode": ([ctypes.POINTER(IndexerArgs), _p], ctypes.c_uint32),
     "kvip_hip_indexer_prefill": ([ctypes.POINTER(PrefillArgs), _p], ctypes.c_uint32),
     "kvip_hip_topk": ([ctypes.POINTER(TopkArgs), _p], ctypes.c_uint32),
