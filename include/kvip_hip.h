@@ -72,7 +72,7 @@
 extern "C" {
 #endif
 
-#define KVIP_HIP_ABI_VERSION 7u
+#define KVIP_HIP_ABI_VERSION 8u
 
 #define KVIP_TOPK 2048
 #define KVIP_BLOCK_TOKENS 128
@@ -460,6 +460,32 @@ typedef struct KvipResidentArgs {
     const int64_t* output_valid;    /* [batch * 4] */
 } KvipResidentArgs;
 
+/* Publication of appended KV pages (PageUpdates.submit, python/kvip/cache/page_updates.py:
+ * 27-62; kernel _page_updates_kernel.py:8-37): for each of `count` rows {flat page index,
+ * address, clear} of `rows`: addresses[index] = address; valid[index] = 1; clear >= 0:
+ * token_to_slot[clear .. clear + block_size) = -1; with fused tables, owner = index /
+ * (groups * pages), group = index / pages % groups, page = index % pages and fused[2g] the
+ * int64 [owners, history] table of group g, fused[2g + 1] its token bytes:
+ * table[owner][page * block_size + i] = address + i * token bytes, for positions < history.
+ * A row whose index or clear range is out of bounds is skipped and sets
+ * KVIP_STATUS_BAD_TOKEN. */
+typedef struct KvipPageArgs {
+    const int64_t* rows;          /* [count, 3] */
+    int64_t* addresses;           /* [entries] = [owners, groups, pages] */
+    uint8_t* valid;               /* [entries] */
+    int32_t* token_to_slot;       /* [map_entries] */
+    const int64_t* fused;         /* [groups, 2] {table pointer, token bytes}, or null */
+    uint32_t* status;             /* optional */
+    int64_t entries;
+    int64_t map_entries;
+    int32_t count;
+    int32_t groups;
+    int32_t pages;
+    int32_t block_size;           /* 1..256 */
+    int32_t history;              /* positions per owner in the fused tables */
+    int32_t reserved;
+} KvipPageArgs;
+
 /* Sparse attention over the selected KV rows (the consumer of the LIFetch outputs: the
  * service's sparse flash attention, tests/operators/lifetch/support/correctness.py:261-339;
  * row format workloads.py:493-515). A 656-byte row is 512 fp8 e4m3 nope features, 64 bf16
@@ -557,6 +583,8 @@ uint32_t kvip_hip_resident_forward(const KvipIndexerArgs* indexer, const KvipTop
  * reference's tests run on its outputs, correctness.py:261-339). */
 uint32_t kvip_hip_sparse_attention(const KvipSparseAttnArgs* args, void* stream);
 uint64_t kvip_hip_sparse_attention_workspace_bytes(int32_t rows, int32_t heads);
+/* Page publication of one step (PageUpdates.submit, python/kvip/cache/page_updates.py:27-62). */
+uint32_t kvip_hip_publish_pages(const KvipPageArgs* args, void* stream);
 
 #ifdef __cplusplus
 }

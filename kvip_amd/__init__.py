@@ -23,6 +23,7 @@ __all__ = [
     "PagedIndexer",
     "RequestPlan",
     "SlotLRU",
+    "PageUpdates",
     "update_abc",
     "lidu",
     "lidu_prepare",
@@ -47,6 +48,7 @@ _EXPORTS = {
     "PagedIndexer": ("adapters.vllm.selector", "PagedIndexer"),
     "RequestPlan": ("adapters.vllm.selector", "RequestPlan"),
     "SlotLRU": ("cache.lru", "SlotLRU"),
+    "PageUpdates": ("cache.page_updates", "PageUpdates"),
     "update_abc": ("cache.abc", "update_abc"),
     "lidu": ("operators.lidu", "lidu"),
     "lidu_prepare": ("operators.lidu", "lidu_prepare"),

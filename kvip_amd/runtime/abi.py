@@ -9,7 +9,7 @@ import ctypes
 from pathlib import Path
 
 LIBRARY = Path(__file__).resolve().parents[1] / "_lib" / "libkvip_hip.so"
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 KVIP_OK = 0
 KVIP_ERR_INVALID = 100000
@@ -168,6 +168,14 @@ class PrefixClassifyArgs(ctypes.Structure):
     ]
 
 
+class PageArgs(ctypes.Structure):
+    _fields_ = [
+        ("rows", _p), ("addresses", _p), ("valid", _p), ("token_to_slot", _p), ("fused", _p), ("status", _p),
+        ("entries", _i64), ("map_entries", _i64), ("count", _i32), ("groups", _i32), ("pages", _i32),
+        ("block_size", _i32), ("history", _i32), ("reserved", _i32),
+    ]
+
+
 class SparseAttnArgs(ctypes.Structure):
     _fields_ = [
         ("query", _p), ("kv_cache", _p), ("block_table", _p), ("indices", _p), ("output", _p), ("status", _p),
@@ -181,6 +189,7 @@ PROTOTYPES = {
     "kvip_hip_abi_version": ([], ctypes.c_uint32),
     "kvip_hip_sparse_attention": ([ctypes.POINTER(SparseAttnArgs), _p], ctypes.c_uint32),
     "kvip_hip_sparse_attention_workspace_bytes": ([_i32, _i32], ctypes.c_uint64),
+    "kvip_hip_publish_pages": ([ctypes.POINTER(PageArgs), _p], ctypes.c_uint32),
     "kvip_hip_indexer_decode": ([ctypes.POINTER(IndexerArgs), _p], ctypes.c_uint32),
     "kvip_hip_indexer_prefill": ([ctypes.POINTER(PrefillArgs), _p], ctypes.c_uint32),
     "kvip_hip_topk": ([ctypes.POINTER(TopkArgs), _p], ctypes.c_uint32),

@@ -7,6 +7,9 @@ SlotLRU     - python/kvip/cache/lru.py:14-118 with the numba kernels of
               same doubly linked list (numba is not importable here, so this restatement
               is pinned by the invariants of tests/cache/test_lru.py:5-15 and by brute force
               against an independent list model in tests/test_oracle_cache.py).
+publish_pages - PageUpdates.submit's CPU branch (python/kvip/cache/page_updates.py:43-62,
+              the reference's golden for _page_updates_kernel.py:8-37); pinned by a hand
+              known answer and the untouched-entries invariant in tests/test_oracle_cache.py.
 """
 from __future__ import annotations
 
@@ -141,3 +144,23 @@ class SlotLRU:
             out.append(slot)
             slot = int(self.next[slot])
         return out
+
+
+def publish_pages(addresses, valid, token_to_slot, rows, block_size, fused=(), widths=(), token_bytes=656):
+    """PageUpdates.submit (python/kvip/cache/page_updates.py:43-62), in place: addresses /
+    valid [owners, groups, pages], token_to_slot flat, fused per group [owners, history]."""
+    owners, groups, pages = addresses.shape
+    flat_a, flat_v, flat_m = addresses.reshape(-1), valid.reshape(-1), token_to_slot.reshape(-1)
+    for index, address, clear in rows:
+        owner, rem = divmod(int(index), groups * pages)
+        group, page = divmod(rem, pages)
+        flat_a[index] = address
+        flat_v[index] = 1
+        if clear >= 0:
+            flat_m[clear:clear + block_size] = -1
+        if fused:
+            table = fused[group]
+            for i in range(block_size):
+                pos = page * block_size + i
+                if pos < table.shape[1]:
+                    table[owner, pos] = address + i * widths[group] * token_bytes

@@ -111,3 +111,41 @@ def test_slot_lru_matches_oracle(torch_gpu):
     torch.cuda.synchronize()
     check_lru(torch, gpu, cpu)
     assert (gpu.slots[0, 100:] == -1).all()
+
+
+def test_publish_pages_matches_oracle(torch_gpu):
+    """PageUpdates.submit (kvip_hip_publish_pages) against oracle.cache.publish_pages over
+    three submissions alternating the staging ring: addresses, validity, cleared map ranges
+    and the fused per-group token-address tables bit-exact; a row with an out-of-range
+    index is skipped and reported."""
+    import kvip_amd
+    from oracle.cache import publish_pages
+
+    torch = torch_gpu
+    rng = np.random.default_rng(17)
+    owners, groups, pages, block, history = 5, 2, 24, 128, 3000  # history ends inside page 23
+    widths = (1, 2)
+    addresses = torch.zeros((owners, groups, pages), dtype=torch.int64, device="cuda")
+    valid = torch.zeros((owners, groups, pages), dtype=torch.uint8, device="cuda")
+    mapping = torch.arange(owners * 4096, dtype=torch.int32, device="cuda")
+    fused = tuple(torch.zeros((owners, history), dtype=torch.int64, device="cuda") for _ in range(groups))
+    pu = kvip_amd.PageUpdates(torch, addresses, valid, mapping, fused=fused, widths=widths)
+    h_addr, h_valid, h_map = (t.cpu().numpy() for t in (addresses, valid, mapping))
+    h_fused = tuple(t.cpu().numpy() for t in fused)
+    for step in range(3):
+        index = rng.choice(owners * groups * pages, 40, replace=False)
+        rows = [(int(i), int(rng.integers(0, 1 << 40)) * 16, int(rng.integers(0, owners * 4096 - block))
+                 if rng.random() < 0.5 else -1) for i in index]
+        pu.submit(rows, step % 2)
+        publish_pages(h_addr, h_valid, h_map, rows, block, h_fused, widths, 656)
+    torch.cuda.synchronize()
+    assert int(pu.status.item()) == 0
+    assert np.array_equal(addresses.cpu().numpy(), h_addr)
+    assert np.array_equal(valid.cpu().numpy(), h_valid)
+    assert np.array_equal(mapping.cpu().numpy(), h_map)
+    for got, want in zip(fused, h_fused):
+        assert np.array_equal(got.cpu().numpy(), want)
+    pu.submit([(owners * groups * pages, 5, -1)], 1)
+    torch.cuda.synchronize()
+    assert int(pu.status.item()) == 4  # KVIP_STATUS_BAD_TOKEN
+    assert np.array_equal(addresses.cpu().numpy(), h_addr)

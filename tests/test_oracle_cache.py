@@ -102,3 +102,21 @@ def test_slot_lru_brute_force_against_list_model():
             if s >= 0:
                 bits[s >> 5] |= np.uint32(1) << np.uint32(s & 31)
         assert np.array_equal(bits, lru.bitmap)
+
+
+def test_publish_pages_known_answer():
+    """Hand-derived: owners 2, groups 2, pages 3, block 4. Row (7, 1000, 8): index 7 is
+    owner 1, group 0, page 1; row (0, 50, -1): owner 0, group 0, page 0."""
+    from oracle.cache import publish_pages
+
+    addresses = np.zeros((2, 2, 3), np.int64)
+    valid = np.zeros((2, 2, 3), np.uint8)
+    mapping = np.arange(20, dtype=np.int32)
+    fused = (np.zeros((2, 6), np.int64), np.zeros((2, 6), np.int64))  # history 6: page 1 keeps 2 positions
+    publish_pages(addresses, valid, mapping, [(7, 1000, 8), (0, 50, -1)], 4, fused, (2, 1), 656)
+    assert addresses.reshape(-1).tolist() == [50, 0, 0, 0, 0, 0, 0, 1000, 0, 0, 0, 0]
+    assert valid.reshape(-1).tolist() == [1, 0, 0, 0, 0, 0, 0, 1, 0, 0, 0, 0]
+    assert mapping.tolist() == list(range(8)) + [-1] * 4 + list(range(12, 20))
+    assert fused[0][1].tolist() == [0, 0, 0, 0, 1000, 1000 + 1312]
+    assert fused[0][0].tolist() == [50, 50 + 1312, 50 + 2624, 50 + 3936, 0, 0]
+    assert not fused[1].any()
