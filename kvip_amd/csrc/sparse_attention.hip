@@ -317,12 +317,16 @@ __global__ __launch_bounds__(kSaThreads) void sparse_attention_merge_kernel(cons
         s_inv[tid] = l > 0.f ? 1.f / l : 0.f;
     }
     __syncthreads();
-    for (int o = tid; o < kSaHeads * 64; o += kSaThreads) {
-        const int h = o / 64, col = part * 64 + o % 64;
-        if (h0 + h >= p.heads) continue;
-        float v = 0.f;
-        for (int s = 0; s < splits; ++s) v += s_w[s][h] * ws[s * kPartial + 2 * kSaHeads + h * kValueDim + col];
-        p.output[(static_cast<size_t>(r) * p.heads + h0 + h) * kValueDim + col] = v * s_inv[h];
+    // One thread per 4 features of one head (16 heads x 64 features = 256 float4).
+    const int h = tid / 16, col = part * 64 + (tid % 16) * 4;
+    if (h0 + h < p.heads) {
+        f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int s = 0; s < splits; ++s) {
+            const f32x4 o = *reinterpret_cast<const f32x4*>(ws + s * kPartial + 2 * kSaHeads + h * kValueDim + col);
+            v += s_w[s][h] * o;
+        }
+        *reinterpret_cast<f32x4*>(p.output + (static_cast<size_t>(r) * p.heads + h0 + h) * kValueDim + col) =
+            v * s_inv[h];
     }
 }
 
