@@ -155,3 +155,32 @@ def test_sparse_attention_on_resident_hot_cache(torch_gpu):
     want = np.stack([sfa.sparse_attention(qh[r], sfa.kv_payload(r // q_rows, logical[r]), SCALE)
                      for r in range(batch * q_rows)])
     check(out, want, "resident hot cache")
+
+
+def test_sparse_attention_graph_replay(torch_gpu):
+    """The split launch and its merge captured in a hipGraph: every replay, with eager work
+    between replays, equals the eager call bit for bit."""
+    torch = torch_gpu
+    rng = np.random.default_rng(33)
+    rows, heads, blocks = 16, 16, 40
+    h_kv = np.concatenate([sfa.kv_payload(int(b % 3), np.arange(128) + b * 128) for b in range(blocks)])
+    kv = torch.from_numpy(h_kv.reshape(blocks, 128, ROW)).cuda()
+    table = torch.from_numpy(np.stack([rng.permutation(blocks)[:16] for _ in range(rows)]).astype(np.int32)).cuda()
+    idx = torch.from_numpy(rng.integers(0, 16 * 128, (rows, TOPK)).astype(np.int32)).cuda()
+    q, _ = bf16_query(torch, rng, rows, heads)
+    op = kvip_amd.SparseAttention(torch, rows=rows, heads=heads, device="cuda").bind(q, kv, table, idx, SCALE)
+    eager = op().clone()
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph):
+            op()
+    torch.cuda.current_stream().wait_stream(side)
+    for replay in range(3):
+        op.output.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(op.output, eager), replay
+        _ = (q.float() * 2).sum().item()  # eager work between replays
