@@ -82,6 +82,9 @@ KVIP_DEVICE RowSelection select_row(const uint32_t (&kk)[KPT / 2], int count, in
     r.ok = hb >= 0 && lb >= 0;
     r.kth = r.ok ? ((static_cast<uint32_t>(hb) << 8) | static_cast<uint32_t>(lb)) : 0x10000u;
     r.n_gt = r.ok ? gt_hi + gt_lo : 0u;
+    // Live keys equal to kth, counted exactly by the low-byte histogram (same key set as
+    // the eq masks below).
+    const uint32_t n_eq = r.ok ? s_lo[lb] : 0u;
     const uint32_t need = r.ok ? kTopK - r.n_gt : 0u;
     // 2. Masks of the keys above and equal to kth, per 32 keys.
     uint32_t gtm[M], eqm[M];
@@ -103,10 +106,14 @@ KVIP_DEVICE RowSelection select_row(const uint32_t (&kk)[KPT / 2], int count, in
         ngt += static_cast<uint32_t>(__popc(gtm[m]));
         neq += static_cast<uint32_t>(__popc(eqm[m]));
     }
-    // Packed gt << 16 | eq (per-thread counts <= KPT, row totals below 65536).
+    // Packed gt << 16 | eq. Per-thread counts are <= KPT and every exclusive prefix of the
+    // eq counts stays below 65536 (a row holds at most 65536 keys and the thread's own
+    // keys are not in its prefix), so both fields of `excl` are exact. Only the row total
+    // of eq can reach 65536 (every key of a full row equal) and carry into the gt field:
+    // the gt total is therefore taken as (total - n_eq) >> 16.
     uint32_t total;
     const uint32_t excl = block_exclusive_scan((ngt << 16) | neq, s_wave, &total);
-    if (r.ok && (total >> 16) != r.n_gt) r.ok = false;
+    if (r.ok && ((total - n_eq) >> 16) != r.n_gt) r.ok = false;
     // 3. Emission of this thread's selected keys.
     uint32_t pg = excl >> 16;
     const uint32_t pe = excl & 0xFFFFu;

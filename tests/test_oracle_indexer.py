@@ -138,6 +138,76 @@ def test_topk_set_matches_closed_form_any_trunk(valid, levels, trunk):
     assert np.array_equal(np.sort(got), np.sort(want))
 
 
+def _literal_trunk_topk(keys, valid, topk, trunk, align=256):
+    """The reference's trunked TopK restated on explicit buffers, independently of the
+    oracle's selection: QLIVector::ProcessTopK's trunk loop (indexer_vector.h:864-936: the
+    first trunk alone, then [prior winners' keys, zero fill to the 256-aligned TopK count,
+    the trunk's keys, zero fill to a multiple of 256]), LITopk<uint16_t>::operator()
+    (topk.h:155-187), LiTopKVF (topk_common.h:1137-1187: the kth value is the
+    (len - topk + 1)-th smallest of the buffer, then the positions above it and the
+    positions equal to it, both in buffer order, first topk) and FindRealIndexVFImpl
+    (:1094-1122: buffer index i > topk - 1 is position i + trunk start - aligned TopK
+    count, else prior winner i)."""
+    keys = [int(k) for k in keys]
+    if valid <= 0:
+        return [-1] * topk
+    if valid < topk:
+        return list(range(valid)) + [-1] * (topk - valid)
+    up = lambda n: -(-n // align) * align
+    topk_al = up(topk)
+
+    def litopkvf(buf):
+        kth = sorted(buf)[len(buf) - topk]
+        idx = [i for i, v in enumerate(buf) if v > kth] + [i for i, v in enumerate(buf) if v == kth]
+        idx = idx[:topk]
+        return idx, [buf[i] for i in idx]
+
+    loops = -(-valid // trunk)
+    if loops == 1:
+        buf = keys[:valid] + [0] * (up(valid) - valid)
+        return litopkvf(buf)[0]
+    his_idx, his_val = litopkvf(keys[:trunk])
+    for loop in range(1, loops):
+        vtl = valid % trunk if loop * trunk + trunk > valid else trunk
+        buf = his_val + [0] * (topk_al - topk) + keys[loop * trunk:loop * trunk + vtl]
+        buf += [0] * (up(len(buf)) - len(buf))
+        idx, his_val = litopkvf(buf)
+        base = loop * trunk - topk_al
+        his_idx = [i + base if i > topk - 1 else his_idx[i] for i in idx]
+    return his_idx
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_trunked_topk_order_equals_single_pass(seed):
+    """The emission order of the reference's trunk merge (prior winners first) equals the
+    single-pass GT-then-EQ order. Why: the kth key of a merge is the topk-th largest of
+    the whole prefix scored so far, so it never decreases from one trunk to the next; a
+    prior winner equal to an earlier kth can therefore never rise above a later kth, and
+    both the above-kth and the equal-to-kth parts of every merge stay in token order.
+    Pinned here by the literal buffer restatement on tie-heavy random rows (TopK counts
+    aligned and not aligned to 256, rows ending inside and on trunk boundaries), and at
+    the reference's sizes (TopK 2048, trunks 8192 and 16384)."""
+    rng = np.random.default_rng(seed)
+    for _ in range(40):
+        topk = int(rng.choice([256, 300, 512]))
+        trunk = int(rng.choice([512, 768, 1024, 2048]))
+        if trunk < topk:
+            continue
+        valid = int(rng.integers(topk, 6 * trunk + 1))
+        if rng.random() < 0.2:
+            valid = trunk * int(rng.integers(1, 6))
+        levels = int(rng.choice([2, 4, 40, 3000]))
+        keys = rng.integers(1, levels + 1, valid + 64).astype(np.uint16)
+        want = _literal_trunk_topk(keys, valid, topk, trunk)
+        assert np.array_equal(ref.topk_reference(keys, valid, topk, trunk=trunk), want)
+        assert np.array_equal(ref.topk_reference(keys, valid, topk), want)
+    for valid, trunk in ((32768, 8192), (20000, 16384), (131072, 16384), (57344, 8192)):
+        keys = rng.integers(0x8000, 0x8000 + int(rng.choice([60, 5000])), valid).astype(np.uint16)
+        want = _literal_trunk_topk(keys, valid, 2048, trunk)
+        assert np.array_equal(ref.topk_reference(keys, valid, trunk=trunk), want)
+        assert np.array_equal(ref.topk_reference(keys, valid), want)
+
+
 def test_topk_brute_force_tiny():
     rng = np.random.default_rng(3)
     for _ in range(200):
