@@ -408,7 +408,13 @@ typedef struct KvipIngestArgs {
  *            keys, scales, addresses and logical ids move with their rows; finally every
  *            miss slot becomes valid.
  * Device errors (bits of KVIP_RESIDENT_ERR_*) go to status[b]; a failed request's later
- * phases are skipped. The workspace (kvip_hip_resident_workspace_bytes) is prepared once
+ * phases are skipped and its owner's whole hot_valid row is cleared (the reference's
+ * CompleteEarlyUpdate, op_kernel/index_cache_update.h:5-21), so its next round reads every
+ * position cold. A request that fails before the Fetch (bad token, owner or candidate, an
+ * in-range hot slot named by two candidates, a source outside host_pool) publishes -1 in
+ * both outputs and moves nothing; one whose Index update is rejected keeps its published
+ * outputs (their slots hold the fetched rows) and the chunks applied before the rejected
+ * one (each a complete permutation). The workspace (kvip_hip_resident_workspace_bytes) is prepared once
  * by kvip_hip_resident_prepare and left prepared by every round; rounds sharing it must
  * be stream-ordered. */
 #define KVIP_RESIDENT_MAX_QUERIES 4
@@ -565,6 +571,15 @@ uint32_t kvip_hip_lru_reset(const KvipLruArgs* args, int32_t committed, void* st
 uint32_t kvip_hip_lru_extend(const KvipLruArgs* args, int32_t active, int32_t committed, void* stream);
 uint32_t kvip_hip_lru_commit(const KvipLruArgs* args, const int32_t* destinations, int32_t count, int32_t active,
                              void* stream);
+/* The same over `chains` LRUs laid out back to back (one per request of a batch; no
+ * reference counterpart: the reference keeps one SlotLRU object per request and commits
+ * each from the host, python/kvip/cache/lru.py:96-118). Chain c uses order/scratch +
+ * c * capacity, slots + c * 2048, bitmap + c * bitmap_words, and commits destinations
+ * [c * dest_stride, + count). One launch for the whole set, so a serving round can commit
+ * its slots inside a captured hipGraph. */
+uint32_t kvip_hip_lru_reset_chains(const KvipLruArgs* args, int32_t chains, int32_t committed, void* stream);
+uint32_t kvip_hip_lru_commit_chains(const KvipLruArgs* args, int32_t chains, const int32_t* destinations,
+                                    int64_t dest_stride, int32_t count, int32_t active, void* stream);
 uint64_t kvip_hip_lidu_workspace_bytes(int32_t batch);
 uint32_t kvip_hip_lidu(const KvipLiduArgs* args, void* stream);
 uint32_t kvip_hip_pack_queries(const KvipQueryPackArgs* args, void* stream);

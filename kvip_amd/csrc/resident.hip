@@ -83,12 +83,18 @@ __global__ void resident_prepare_kernel(const KvipResidentArgs p) {
     }
 }
 
-// Round initialisation of request b.
+// Round initialisation of request b. A hot slot named by two candidates fails the request
+// (KVIP_RESIDENT_ERR_CANDIDATE): both ordinals would otherwise see it free and receive it.
 __global__ __launch_bounds__(kRsThreads) void resident_init_kernel(const KvipResidentArgs p) {
+    __shared__ uint32_t s_seen[kMaxWords];
+    __shared__ uint32_t s_dup;
     const int b = blockIdx.x;
     const int tid = threadIdx.x;
+    const int words = (p.resident + 31) / 32;
     int32_t* reserved = p.reserved_hot + static_cast<size_t>(b) * p.resident;
     for (int s = tid; s < p.resident; s += kRsThreads) reserved[s] = -1;
+    for (int w = tid; w < words; w += kRsThreads) s_seen[w] = 0u;
+    if (tid == 0) s_dup = 0u;
     const int nchg = kLru + p.rows_per_request * kTopK;
     const int32_t* lru = p.lru_slots + static_cast<size_t>(b) * kLru;
     for (int i = tid; i < nchg; i += kRsThreads) {
@@ -96,12 +102,17 @@ __global__ __launch_bounds__(kRsThreads) void resident_init_kernel(const KvipRes
         p.change_slots[static_cast<size_t>(b) * nchg + i] = i < kLru ? lru[i] : -1;
     }
     if (tid < 5) p.miss_counts[b * 5 + tid] = 0;
-    if (tid == 0) p.status[b] = 0;
     __syncthreads();
     for (int i = tid; i < kLru; i += kRsThreads) {
         const int s = lru[i];
-        if (s >= 0 && s < p.resident) reserved[s] = i;
+        if (s >= 0 && s < p.resident) {
+            const uint32_t bit = 1u << (s & 31);
+            if ((atomicOr(&s_seen[s >> 5], bit) & bit) != 0u) s_dup = 1u;
+            reserved[s] = i;
+        }
     }
+    __syncthreads();
+    if (tid == 0) p.status[b] = s_dup != 0u ? static_cast<int32_t>(KVIP_RESIDENT_ERR_CANDIDATE) : 0;
 }
 
 __global__ __launch_bounds__(kRsThreads) void resident_resolve_kernel(const KvipResidentArgs p) {
@@ -128,7 +139,8 @@ __global__ __launch_bounds__(kRsThreads) void resident_resolve_kernel(const Kvip
     const int nchg = kLru + Q * kTopK;
 
     for (int i = tid; i < words; i += kRsThreads) s_bitmap[i] = 0u;
-    if (tid == 0) s_err = owner_ok(p, o) ? 0u : KVIP_RESIDENT_ERR_TOKEN;
+    // Errors found by the round initialisation (duplicate candidates) carry over.
+    if (tid == 0) s_err = static_cast<uint32_t>(p.status[b]) | (owner_ok(p, o) ? 0u : KVIP_RESIDENT_ERR_TOKEN);
     if (tid < kMaxQ) s_dest[tid] = -1;
     __syncthreads();
     const bool good_owner = owner_ok(p, o);
@@ -459,8 +471,16 @@ __global__ __launch_bounds__(kRsThreads) void resident_update_kernel(const KvipR
     const int Q = p.rows_per_request;
     const int R = p.resident;
     const int H = p.history;
-    if (p.status[b] != 0) return;  // uniform
     const int o = p.row_owners[b];
+    if (p.status[b] != 0) {  // uniform
+        // A failed request's owner loses all residency: nothing it holds is trusted, so
+        // its next round reads every position cold.
+        if (owner_ok(p, o)) {
+            int32_t* hv = p.hot_valid + static_cast<size_t>(o) * R;
+            for (int s = tid; s < R; s += kRsThreads) hv[s] = 0;
+        }
+        return;
+    }
     const Workspace ws = workspace_of(p);
     int32_t* row_at = ws.row_at + static_cast<size_t>(b) * H;
     int32_t* pos_of = ws.pos_of + static_cast<size_t>(b) * H;
@@ -552,10 +572,15 @@ __global__ __launch_bounds__(kRsThreads) void resident_update_kernel(const KvipR
         }
         r0 += count;
     }
-    // Residency of every fetched slot (after the freed positions were invalidated).
+    // Residency of every fetched slot (after the freed positions were invalidated). A
+    // permutation rejected in a later chunk leaves the earlier chunks applied (each one a
+    // complete permutation of the Index rows, addresses and logical ids moving together),
+    // so the owner then loses all residency instead.
     const int total = p.miss_counts[b * 5 + 4];
     if (s_err == 0u) {
         for (int i = tid; i < total; i += kRsThreads) hot_valid[p.fetch_slots[dbase + i]] = 1;
+    } else {
+        for (int s = tid; s < R; s += kRsThreads) hot_valid[s] = 0;
     }
     // Maps back to identity: read every logged position's row, then reset both maps.
     const int nlog = min(s_nlog, kMaxLog);

@@ -31,6 +31,15 @@ csrc/operators/lightning_indexer_with_fetch/op_kernel/ unless noted):
   outputs    streaming.cpp:66-90 (PublishQueryOutputs) with the harness check
              tests/operators/lifetch/support/execution.py:2109-2130 (logical output =
              pre-update logical ids of the TopK positions, slot output = locations)
+  failure    index_cache_update.h:5-21 (CompleteEarlyUpdate, called from
+             streaming.cpp:580-583): any error of a request clears its owner's whole
+             hot_valid row, so nothing partially written is trusted afterwards
+
+Contract points that are this build's own (the reference has no counterpart): an
+in-range hot slot named by two LRU candidates fails the request with ERR_CANDIDATE
+before anything is resolved, and a request that fails before the Fetch publishes -1 in
+both outputs (the reference publishes its outputs per query and signals errors through
+status alone).
 
 Scope of this restatement: no speculative prefetch (`used` candidates consumed by an
 earlier window are supported by the two allocation passes, but no prefetch mapping is
@@ -49,6 +58,7 @@ EMPTY = -1
 
 ERR_TOKEN = 1          # a TopK position >= history
 ERR_CANDIDATE = 4      # an LRU candidate >= resident, or too few free hot slots
+ERR_SOURCE = 8         # a miss whose KV address is outside the host pool or not 16-byte aligned
 ERR_UPDATE = 16        # an Index change that is not a valid partial permutation
 
 
@@ -78,14 +88,21 @@ def classify(selected, history, resident, hot_valid, reserved):
     return loc, protect, err
 
 
-def resolve(selected, history, resident, hot_valid, reserved, lru, used=0):
+def resolve(selected, history, resident, hot_valid, reserved, lru, used=0, sources=None):
     """Per-query miss resolution of one request (StagedQuery). Returns a dict with
     loc [Q, 2048] (hot slot of every selected position, -1 for empty entries), slots
     [misses] (slot of each miss rank), tokens [misses] (position of each miss rank),
     added [Q] (new misses per query), changes / change_slots [2048 + Q*2048] records and
-    the error bits. Stops (like the reference) at the first query that fails."""
+    the error bits. Stops (like the reference) at the first query that fails.
+    sources = (addresses [history], pool_bytes, row_bytes): every new miss's KV address is
+    checked against the host pool as its query is resolved (ERR_SOURCE), before any
+    Fetch; this check is this build's own (the reference's transport validates its
+    descriptors, cache_metadata.h:32-44)."""
     q_rows = selected.shape[0]
     loc, protect, err = classify(selected, history, resident, hot_valid, reserved)
+    in_range = [int(s) for s in lru[:LRU_SLOTS] if 0 <= s < resident]
+    if len(set(in_range)) != len(in_range):
+        err |= ERR_CANDIDATE  # a hot slot named by two candidates
     bitmap = protect.copy()
     rank_of = {}
     slots, tokens, added_per_q = [], [], []
@@ -164,6 +181,11 @@ def resolve(selected, history, resident, hot_valid, reserved, lru, used=0):
             record = int(reserved[s]) if reserved[s] >= 0 else LRU_SLOTS + r
             change_slots[record] = s
             changes[record] = tokens[r]
+            if sources is not None:
+                addresses, pool_bytes, row_bytes = sources
+                a = int(addresses[tokens[r]])
+                if a < 0 or a > pool_bytes - row_bytes or a % 16:
+                    err |= ERR_SOURCE
         added_per_q.append(need)
     return dict(loc=loc, slots=np.array(slots, np.int64), tokens=np.array(tokens, np.int64),
                 added=np.array(added_per_q, np.int64), changes=changes, change_slots=change_slots, error=err)
@@ -180,8 +202,19 @@ def apply_changes(batches, history, resident, keys, scales, addresses, logical, 
     positions lose their residency. Returns the error bits (0 = applied)."""
     row_at = np.arange(history)
     pos_of = np.arange(history)
-    keys0, scales0 = keys.copy(), scales.copy()
     addresses0, logical0 = addresses.copy(), logical.copy()
+    err = _permute(batches, history, resident, keys, scales, hot_valid, row_at, pos_of)
+    # Addresses and logical ids follow their rows, also for the chunks applied before a
+    # rejected one.
+    changed = np.nonzero(row_at != np.arange(history))[0]
+    addresses[changed] = addresses0[row_at[changed]]
+    logical[changed] = logical0[row_at[changed]]
+    return err
+
+
+def _permute(batches, history, resident, keys, scales, hot_valid, row_at, pos_of):
+    """The chunk loop of apply_changes; stops at the first rejected chunk, leaving the
+    earlier chunks applied. Returns the error bits."""
     for batch in batches:
         for c0 in range(0, len(batch), CHUNK):
             chunk = batch[c0:c0 + CHUNK]
@@ -208,10 +241,6 @@ def apply_changes(batches, history, resident, keys, scales, addresses, logical, 
             for d in freed:
                 if d < resident:
                     hot_valid[d] = 0
-    changed = np.nonzero(row_at != np.arange(history))[0]
-    addresses[changed] = addresses0[row_at[changed]]
-    logical[changed] = logical0[row_at[changed]]
-    del keys0, scales0
     return 0
 
 
@@ -220,17 +249,21 @@ def resident_round(selected, history, resident, keys, scales, addresses, logical
     """One request's full round after TopK, in place on its tables: resolve, outputs,
     Fetch (hot_cache[slot] = host_pool[addresses[token]]), Index update, residency
     publication. Returns (logical_output [Q, 2048], slot_output [Q, 2048], resolve dict,
-    error bits)."""
-    res = resolve(selected, history, resident, hot_valid, reserved, lru, used)
+    error bits). A failed request's owner loses all residency (hot_valid cleared); when
+    it fails before the Fetch both outputs are -1 and nothing else changes."""
+    res = resolve(selected, history, resident, hot_valid, reserved, lru, used,
+                  sources=(addresses, host_pool.size, hot_cache.shape[1]))
     q_rows = selected.shape[0]
+    if res["error"]:
+        hot_valid[:] = 0
+        empty = np.full(selected.shape, EMPTY, np.int64)
+        return empty, empty.copy(), res, res["error"]
     logical_out = np.full(selected.shape, EMPTY, np.int64)
     for q in range(q_rows):
         for i in range(TOPK):
             t = int(selected[q, i])
             if 0 <= t < history:
                 logical_out[q, i] = logical[t]
-    if res["error"]:
-        return logical_out, res["loc"], res, res["error"]
     row_bytes = hot_cache.shape[1]
     for t, s in zip(res["tokens"], res["slots"]):
         a = int(addresses[t])
@@ -241,6 +274,7 @@ def resident_round(selected, history, resident, keys, scales, addresses, logical
         r += n
     err = apply_changes(batches, history, resident, keys, scales, addresses, logical, hot_valid)
     if err:
+        hot_valid[:] = 0
         return logical_out, res["loc"], res, err
     for s in res["slots"]:
         hot_valid[s] = 1

@@ -6,7 +6,8 @@ Bars: every output and every table the round touches is bit-exact against the or
 permuted Index keys / scales / addresses / logical ids, the hot KV cache), over several
 consecutive rounds so that each round starts from the state the previous one left; the
 reference's stateful known answer (reads 2048, 0, 4096, 2048) through the full forward
-with LI and TopK on the device; errors reported in status without touching the tables."""
+with LI and TopK on the device; errors reported in status, the failed owner's residency
+cleared as the reference's CompleteEarlyUpdate does."""
 import ctypes
 
 import numpy as np
@@ -108,10 +109,10 @@ class Setup:
         for b, (lout, sout, res, err, rsv) in enumerate(outs):
             assert status[b] == err, (b, status[b], err)
             assert np.array_equal(reserved[b], rsv), b
-            if err:
-                continue
             assert np.array_equal(lo[b], lout), b
             assert np.array_equal(so[b], sout), b
+            if err:
+                continue
             added = list(res["added"]) + [0] * (4 - len(res["added"]))
             assert counts[b].tolist() == added + [int(res["added"].sum())], b
             assert np.array_equal(changes[b], res["changes"]), b
@@ -221,28 +222,55 @@ def test_resident_forward_stateful_known_answer(torch_gpu):
     assert reads == [[2048, 2048], [0, 0], [4096, 4096], [2048, 2048]]
 
 
-def test_resident_errors_are_reported_and_leave_tables(torch_gpu):
+def test_resident_errors_clear_the_owner_residency(torch_gpu):
+    """Failure contract of the reference (index_cache_update.h:5-21): a failed request's
+    owner loses all residency; a request failing before the Fetch publishes -1 and moves
+    nothing. Checked against the oracle on every table, then over a second round in which
+    that owner reads every position cold."""
     torch = torch_gpu
     st = Setup(torch, batch=2, owners=2, history=8192, resident=4096, q_rows=1, seed=9)
     rng = st.rng
     selected = np.concatenate([mtp_selection(rng, 1, 8192, 4096, 0.5) for _ in range(2)])
     lru = np.stack([np.arange(2048), np.arange(2048, 4096)])
     lru[1, 5] = 9999  # outside the hot range: request 1 fails, request 0 runs
-    before = [x.clone() for x in (st.keys, st.logical, st.valid, st.hot)]
+    say("case candidate outside the hot range")
     st.run_round(selected, lru)
+    outs = st.oracle_round(selected, lru)
+    st.compare(outs)
     status = st.upd.status.cpu().numpy()
     assert status[0] == 0 and status[1] & abi.RESIDENT_ERR_CANDIDATE
-    assert (st.upd.slot_output[1].cpu() == -1).all()
-    assert torch.equal(st.logical[1], before[1][1]) and torch.equal(st.hot[1], before[3][1])
+    assert (st.upd.slot_output[1].cpu() == -1).all() and (st.upd.logical_output[1].cpu() == -1).all()
+    assert not st.valid[1].any() and st.valid[0].any()
+    # Duplicate candidates (advisor case): both ordinals would get the same slot.
+    say("case duplicate candidates, then a cold round")
+    lru = np.stack([np.arange(2048, 4096), np.arange(2048, 4096)])
+    lru[0, 17] = lru[0, 1900]
+    selected = np.concatenate([mtp_selection(rng, 1, 8192, 4096, 0.6) for _ in range(2)])
+    st.run_round(selected, lru)
+    st.compare(st.oracle_round(selected, lru))
+    status = st.upd.status.cpu().numpy()
+    assert status[0] == abi.RESIDENT_ERR_CANDIDATE and status[1] == 0
+    assert not st.valid[0].any()
+    lru = np.stack([np.arange(2048), np.arange(2048)])
+    selected = np.concatenate([mtp_selection(rng, 1, 8192, 4096, 0.6, n=1800) for _ in range(2)])
+    st.run_round(selected, lru)
+    outs = st.oracle_round(selected, lru)
+    st.compare(outs)
+    counts = st.upd.miss_counts.cpu().numpy()
+    assert counts[0, 4] == 1800  # every selected position of the cleared owner is a miss
+    assert not st.upd.status.any()
     # A KV address outside the host pool fails the request before anything is fetched.
+    say("case source outside the host pool")
     st2 = Setup(torch, batch=1, owners=1, history=8192, resident=4096, q_rows=1, seed=10)
     st2.addresses[0, 5000] = st2.pool.numel()
+    st2.h_addresses[0, 5000] = st2.pool.numel()
     sel = np.full((1, TOPK), -1, np.int64)
     sel[0, :3] = [5000, 6000, 7000]
     hot_before = st2.hot.clone()
     st2.run_round(sel, np.arange(2048)[None, :])
+    st2.compare(st2.oracle_round(sel, np.arange(2048)[None, :]))
     assert st2.upd.status.cpu().numpy()[0] & abi.RESIDENT_ERR_SOURCE
-    assert torch.equal(st2.hot, hot_before)
+    assert torch.equal(st2.hot, hot_before) and not st2.valid.any()
 
 
 def test_resident_forward_graph_replay(torch_gpu):

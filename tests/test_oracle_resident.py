@@ -175,6 +175,110 @@ def test_candidate_outside_hot_range_fails_the_request():
     assert res["error"] & ref.ERR_CANDIDATE
 
 
+def test_duplicate_candidates_fail_the_request_and_clear_residency():
+    """A hot slot named by two candidates fails the request before anything moves: both
+    outputs -1, the owner's hot_valid cleared (index_cache_update.h:5-21), every other table
+    unchanged."""
+    st = make_state(8192, 4096)
+    lru = np.arange(2048, 4096)
+    lru[9] = lru[1500]
+    selected = np.full((2, TOPK), -1, np.int64)
+    selected[:, :3] = [[10, 5000, 6000], [11, 5000, 7000]]
+    before = {k: v.copy() for k, v in st.items() if isinstance(v, np.ndarray)}
+    lout, sout, res, err = ref.resident_round(
+        selected, st["history"], st["resident"], st["keys"], st["scales"], st["addresses"], st["logical"],
+        st["hot_valid"], ref.reserved_from_candidates(lru, 4096), lru, st["hot_cache"], st["pool"])
+    assert err == ref.ERR_CANDIDATE
+    assert (lout == -1).all() and (sout == -1).all()
+    assert not st["hot_valid"].any()
+    for k, v in before.items():
+        if k != "hot_valid":
+            assert np.array_equal(st[k], v), k
+    # Padding (-1) candidates may repeat.
+    lru2 = np.full(2048, -1)
+    lru2[:100] = np.arange(100)
+    res = ref.resolve(np.full((1, TOPK), -1, np.int64), 8192, 4096, np.ones(4096), 
+                      ref.reserved_from_candidates(lru2, 4096), lru2)
+    assert res["error"] == 0
+
+
+def test_source_outside_the_pool_fails_before_the_fetch():
+    """A miss whose KV address lies outside the host pool (or is not 16-byte aligned) fails
+    its request before anything is fetched: -1 outputs, residency cleared, hot cache and
+    Index untouched."""
+    for bad in (None, 5):
+        st = make_state(8192, 4096)
+        st["addresses"][5000] = st["pool"].size if bad is None else st["addresses"][5000] + bad
+        hot_before = st["hot_cache"].copy()
+        logical_before = st["logical"].copy()
+        lru = np.arange(2048)
+        selected = np.full((1, TOPK), -1, np.int64)
+        selected[0, :3] = [5000, 6000, 7000]
+        lout, sout, res, err = ref.resident_round(
+            selected, st["history"], st["resident"], st["keys"], st["scales"], st["addresses"], st["logical"],
+            st["hot_valid"], ref.reserved_from_candidates(lru, 4096), lru, st["hot_cache"], st["pool"])
+        assert err == ref.ERR_SOURCE
+        assert (lout == -1).all() and (sout == -1).all() and not st["hot_valid"].any()
+        assert np.array_equal(st["hot_cache"], hot_before) and np.array_equal(st["logical"], logical_before)
+
+
+def test_rejected_later_chunk_keeps_a_consistent_permutation():
+    """A chunk rejected after earlier chunks were applied: the earlier chunks stay applied
+    and every table is still one permutation of the original rows (keys, scales, addresses
+    and logical ids moving together). The mistake is planted in the oracle's input: the
+    second chunk repeats a destination."""
+    history, resident = 4096, 2048
+    rng = np.random.default_rng(4)
+    keys = rng.integers(0, 256, (history, 128), dtype=np.uint8)
+    scales = rng.random(history).astype(np.float32)
+    addresses = np.arange(history, dtype=np.int64) * 656
+    logical = np.arange(history, dtype=np.int64)
+    valid = np.ones(resident, np.int64)
+    k0, s0, a0 = keys.copy(), scales.copy(), addresses.copy()
+    origs = rng.choice(np.arange(resident, history), ref.CHUNK + 10, replace=False)
+    dsts = rng.choice(resident, ref.CHUNK + 10, replace=False)
+    dsts[ref.CHUNK + 3] = dsts[ref.CHUNK + 1]  # duplicate destination in chunk 2
+    batch = list(zip(origs.tolist(), dsts.tolist()))
+    err = ref.apply_changes([batch], history, resident, keys, scales, addresses, logical, valid)
+    assert err == ref.ERR_UPDATE
+    assert np.array_equal(np.sort(logical), np.arange(history))
+    assert np.array_equal(keys, k0[logical]) and np.array_equal(scales, s0[logical])
+    assert np.array_equal(addresses, a0[logical])
+    # Chunk 1 applied: each of its tokens sits at its destination.
+    for o, d in batch[:ref.CHUNK]:
+        assert logical[d] == o
+    # Chunk 2 not applied: its sources still hold their own rows.
+    for o, d in batch[ref.CHUNK:]:
+        assert logical[o] == o
+
+
+def test_failure_after_the_fetch_clears_residency(monkeypatch):
+    """resident_round when the Index update rejects its changes after the Fetch: the owner
+    loses all residency and the outputs stay as published. The failure is planted in the
+    oracle by a resolve result whose later miss repeats a slot."""
+    st = make_state(8192, 4096)
+    lru = np.arange(2048, 4096)
+    selected = np.full((1, TOPK), -1, np.int64)
+    selected[0, :600] = np.arange(5000, 5600)
+    real = ref.resolve
+
+    def broken(*args, **kw):
+        res = real(*args, **kw)
+        res["slots"] = res["slots"].copy()
+        res["slots"][599] = res["slots"][550]
+        return res
+
+    monkeypatch.setattr(ref, "resolve", broken)
+    lout, sout, res, err = ref.resident_round(
+        selected, st["history"], st["resident"], st["keys"], st["scales"], st["addresses"], st["logical"],
+        st["hot_valid"], ref.reserved_from_candidates(lru, 4096), lru, st["hot_cache"], st["pool"])
+    assert err == ref.ERR_UPDATE
+    assert not st["hot_valid"].any()
+    assert np.array_equal(lout[0, :600], np.arange(5000, 5600))
+    # The first 512-change chunk was applied.
+    assert np.array_equal(st["logical"][2048:2048 + 512], np.arange(5000, 5512))
+
+
 def test_apply_changes_chunk_closure_known_answer():
     """shadow_exchange_parallel.h:28-78 on a hand case: 2 changes, one destination is also
     a source; the displaced row fills the freed position, which loses residency."""
