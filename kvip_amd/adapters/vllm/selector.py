@@ -1,15 +1,19 @@
 """vLLM indexer selector over service-owned LIFetch inputs and Index updates.
 
-Mirrors the reference's VllmIndexSelector (python/kvip/adapters/vllm/selector.py:46-161):
-the same constructor checks, `prepare(plans)` (host request layout, once per step, no
-device readback), `__call__(query, weights, indexer, metadata, query_scale)` and
-`slots(token_count)`. A step of decode requests runs Index ingest (one
-`kvip_hip_ingest_index` launch), the packing of the token batch's index queries into the
-fixed [batch * 4] rows (`kvip_hip_pack_queries`) and the resident LIFetch forward, whose
-Index update publishes the logical and slot TopK in token order; nothing is gathered,
-cast or masked afterwards. Prefill-only steps go to the indexer's native selection, and
-mixed steps run the forward for the decode requests and the native selection for each
-prefill request, assembled in token order.
+Interface of the reference's VllmIndexSelector (python/kvip/adapters/vllm/selector.py:
+46-161): built over a QueryInputs, a LIFetch binding reading them, an Index update and
+the storage's logical ids; `prepare(plans)` once per scheduler step on the host (no
+device read), `__call__(query, weights, indexer, metadata, query_scale)` returning the
+step's TopK-2048 logical positions per token, int32 [tokens, 1, 2048], and
+`slots(token_count)` returning the hot-cache slots the sparse attention reads.
+
+Step kinds, as in the reference: decode-only steps run the Index ingest, the query
+packing and the resident LIFetch forward, whose update publishes logical and slot
+outputs in token order; prefill-only steps go to the indexer's native selection;
+mixed steps do both. Design of the mixed step on MI355X: all prefill requests of the
+step are packed as the sequences of one TND prefill launch (their token rows gathered,
+cumulative query lengths, key lengths and block-table rows stacked), instead of one
+native call per request, and the two halves land in token order with one scatter each.
 
 `RequestPlan` names the fields of a scheduled request that the selector and the Index
 storage read. `PagedIndexer` is the indexer side on MI355X: the paged index-K cache the
@@ -19,10 +23,11 @@ native indexer call the reference's vLLM build makes.
 """
 from __future__ import annotations
 
-from copy import copy
 from dataclasses import dataclass
 from types import SimpleNamespace
 from typing import Any
+
+import numpy as np
 
 from kvip_amd.operators.lifetch.forward import LIFetchForward
 from kvip_amd.operators.lifetch.resident import ResidentIndexUpdate
@@ -82,6 +87,10 @@ class PagedIndexer:
                                       device=device, heads=heads, weight_dtype=torch.bfloat16)
         self.cu_seqlens = torch.zeros(max_sequences + 1, dtype=torch.int32, device=self.prefill.device)
 
+    @property
+    def max_sequences(self):
+        return self.prefill.max_sequences
+
     def select_topk_native(self, query, weights, metadata, query_scale):
         rows, heads = int(weights.shape[0]), self.prefill.heads
         ends = metadata.cum_query_lens.reshape(-1)
@@ -102,44 +111,50 @@ class PagedIndexer:
 class VllmIndexSelector:
     def __init__(self, torch, *, inputs, rotating, update, logical_ids, row_owners, prefix_workspace=None,
                  storage=None, forward_factory=LIFetchForward, unique_active_owners=False):
-        """inputs: QueryInputs; rotating: a LIFetchBinding that reads them
+        """inputs: QueryInputs; rotating: a LIFetchBinding reading them
         (`bind_query_inputs`); update: a ResidentIndexUpdate publishing token-order
         outputs of those inputs; logical_ids: the storage's int64 [owners, history];
         row_owners: int32 [batch], the inputs' owner row or a copy refreshed by prepare;
         storage: the VllmIndexCacheStorage ingested into (None: the caller ingests)."""
-        self.torch = torch
-        self.inputs, self.rotating, self.update = inputs, rotating, update
-        if logical_ids.ndim != 2 or not logical_ids.is_contiguous() or logical_ids.dtype != torch.int64:
-            raise ValueError("LIFetch logical IDs require contiguous int64 owner/history rows")
+        problems = []
+        if logical_ids.ndim != 2 or logical_ids.dtype != torch.int64 or not logical_ids.is_contiguous():
+            problems.append("logical ids must be contiguous int64 [owners, history]")
         if tuple(row_owners.shape) != (inputs.batch,) or row_owners.dtype != torch.int32:
-            raise ValueError("LIFetch row owners must match the bound batch")
+            problems.append(f"row owners must be int32 [{inputs.batch}]")
         if rotating.batch != inputs.batch or rotating.rows_per_request != QUERIES_PER_REQUEST:
-            raise ValueError("LIFetch locations and TopK must share the bound shape")
-        for actual, expected in ((rotating.query, inputs.query), (rotating.weights, inputs.weights),
-                                 (rotating.query_scale, inputs.scale)):
-            if actual is None or actual.data_ptr() != expected.data_ptr():
-                raise ValueError("LIFetch kernel must bind the persistent packed query buffers")
+            problems.append(f"the binding must hold {inputs.batch} requests x {QUERIES_PER_REQUEST} query rows")
+        bound = {"query": (rotating.query, inputs.query), "weights": (rotating.weights, inputs.weights),
+                 "query scale": (rotating.query_scale, inputs.scale)}
+        for name, (have, want) in bound.items():
+            if have is None or have.data_ptr() != want.data_ptr():
+                problems.append(f"the binding's {name} is not the packed QueryInputs buffer")
         if not isinstance(update, ResidentIndexUpdate) or update.query_inputs is not inputs:
-            raise ValueError("LIFetch update must publish token-order outputs of the bound query inputs")
+            problems.append("the Index update must publish token-order outputs of these QueryInputs")
+        if problems:
+            raise ValueError("VllmIndexSelector: " + "; ".join(problems))
+        self.torch, self.inputs, self.rotating, self.update = torch, inputs, rotating, update
         self.forward = forward_factory(rotating, update)
         self.unique_active_owners = unique_active_owners
         self.logical_ids, self.row_owners = logical_ids, row_owners
         self.prefix_workspace = prefix_workspace
         self.storage, self.positions = storage, None
+        self.history = int(logical_ids.shape[1])
         self.topk = rotating.topk.view(inputs.batch, QUERIES_PER_REQUEST, TOPK)
-        self.history = logical_ids.shape[1]
         self.attention_indices = None
         self.plans = None
         self.decodes = ()
+        self.prefills = ()
 
     def prepare(self, plans, *, prepare_inputs=True):
-        """Host request layout, once per step; no device readback (selector.py:87-104)."""
+        """Host layout of one scheduler step, no device read: the Index owners of new
+        requests are reset and the decode requests' query rows laid out."""
         self.plans = tuple(plans)
         self.decodes = tuple(p for p in self.plans if p.decode)
+        self.prefills = tuple((row, p) for row, p in enumerate(self.plans) if not p.decode)
         if self.unique_active_owners:
-            owners = [p.owner for p in self.decodes if p.stop > p.begin]
-            if len(owners) != len(set(owners)):
-                raise ValueError("active decode rows must have distinct stable owners")
+            live = [p.owner for p in self.decodes if p.stop > p.begin]
+            if len(set(live)) != len(live):
+                raise ValueError(f"decode requests share an owner row: {sorted(live)}")
         if self.storage is not None:
             self.storage.prepare(self.plans)
         if prepare_inputs:
@@ -150,56 +165,66 @@ class VllmIndexSelector:
             self.row_owners.copy_(self.inputs.row_owners)
 
     def __call__(self, query, weights, indexer, metadata, query_scale):
-        """TopK-2048 logical positions of the step's tokens, int32 [tokens, 1, 2048]
-        (selector.py:106-154); the slot of every selected position is kept for `slots`."""
-        mixed = self.plans is not None and len(self.decodes) != len(self.plans)
+        """TopK-2048 logical positions of the step's tokens, int32 [tokens, 1, 2048]; the
+        slots of the decode tokens' selections are kept for `slots`."""
+        mixed = bool(self.decodes) and bool(self.prefills)
         if self.storage is not None:
-            if mixed:
-                self.storage.ingest_prefill(indexer.k_cache.kv_cache, metadata, self.plans, self.positions)
+            cache = indexer.k_cache.kv_cache
+            if self.prefills:
+                self.storage.ingest_prefill(cache, metadata, self.plans, self.positions)
             else:
-                self.storage.ingest_decode(indexer.k_cache.kv_cache, metadata, self.inputs, self.row_owners)
+                self.storage.ingest_decode(cache, metadata, self.inputs, self.row_owners)
         if self.plans and not self.decodes:
             return indexer.select_topk_native(query, weights, metadata, query_scale)
         self.inputs.pack(query, weights, query_scale)
         self.forward()
-
         tokens = int(weights.shape[0])
-        token_count = self.inputs.token_count if mixed or tokens > self.inputs.batch * QUERIES_PER_REQUEST else tokens
-        logical = self.update.logical_output[:token_count]
-        self.attention_indices = self.update.slot_output[:token_count]
+        live = self.inputs.token_count if mixed or tokens > self.inputs.capacity else tokens
+        logical = self.update.logical_output[:live]
+        self.attention_indices = self.update.slot_output[:live]
         if not mixed:
             return logical
+        return self._mixed(query, weights, query_scale, indexer, metadata, logical, tokens)
 
-        # Prefill requests keep the paged Index cache and the native selection; decode rows
-        # are not recomputed.
-        torch = self.torch
-        result = torch.full((tokens, 1, TOPK), -1, dtype=torch.int32, device=weights.device)
+    def _mixed(self, query, weights, query_scale, indexer, metadata, logical, tokens):
+        """Token-order result of a mixed step: the decode tokens' published rows and one
+        batched native selection per group of at most `indexer.max_sequences` prefill
+        requests."""
+        torch, dev = self.torch, weights.device
         heads = self.inputs.index_heads
-        query_rows = query.view(tokens, heads, INDEX_DIM)
-        scale_rows = query_scale.view(tokens, heads)
-        offset = 0
-        for row, plan in enumerate(self.plans):
-            count = plan.stop - plan.begin
-            if plan.decode:
-                result[plan.begin:plan.stop].copy_(logical[offset:offset + count])
-                offset += count
+        result = torch.full((tokens, 1, TOPK), -1, dtype=torch.int32, device=dev)
+        dec = np.concatenate([np.arange(p.begin, p.stop) for p in self.decodes]).astype(np.int64)
+        if dec.size:
+            result.index_copy_(0, torch.from_numpy(dec).to(dev), logical[:dec.size].reshape(dec.size, 1, TOPK))
+        q_rows = query.reshape(tokens, heads, INDEX_DIM)
+        s_rows = query_scale.reshape(tokens, heads)
+        group = getattr(indexer, "max_sequences", len(self.prefills))
+        for g0 in range(0, len(self.prefills), group):
+            part = self.prefills[g0:g0 + group]
+            counts = np.array([p.stop - p.begin for _, p in part], np.int64)
+            rows = np.concatenate([np.arange(p.begin, p.stop) for _, p in part]).astype(np.int64)
+            if rows.size == 0:
                 continue
-            prefill = copy(metadata)
-            prefill.topk_selector = None
-            prefill.num_actual_tokens = count
-            prefill.block_table = metadata.block_table[row:row + 1]
-            prefill.actual_seq_lengths_query = prefill.cum_query_lens = plan.query_end
-            prefill.actual_seq_lengths_key = prefill.seq_lens = plan.key_end
-            selected = indexer.select_topk_native(query_rows[plan.begin:plan.stop], weights[plan.begin:plan.stop],
-                                                  prefill, scale_rows[plan.begin:plan.stop])
-            result[plan.begin:plan.stop].copy_(selected.view(count, 1, TOPK))
+            rows_d = torch.from_numpy(rows).to(dev)
+            packed = SimpleNamespace(
+                block_size=getattr(metadata, "block_size", BLOCK_TOKENS),
+                block_table=metadata.block_table.index_select(
+                    0, torch.tensor([r for r, _ in part], dtype=torch.int64, device=dev)),
+                cum_query_lens=torch.from_numpy(np.cumsum(counts).astype(np.int32)).to(dev),
+                seq_lens=torch.cat([p.key_end.reshape(-1).to(torch.int32) for _, p in part]))
+            packed.actual_seq_lengths_query = packed.cum_query_lens
+            packed.actual_seq_lengths_key = packed.seq_lens
+            selected = indexer.select_topk_native(q_rows.index_select(0, rows_d), weights.index_select(0, rows_d),
+                                                  packed, s_rows.index_select(0, rows_d))
+            result.index_copy_(0, rows_d, selected.reshape(rows.size, 1, TOPK))
         return result
 
     def slots(self, token_count):
-        """Hot-cache slots of the last selection's first `token_count` tokens (the SFA
-        consumer's indices, selector.py:156-161)."""
+        """Hot-cache slots of the last selection's first `token_count` decode tokens (the
+        indices the sparse attention reads)."""
         if self.attention_indices is None:
-            raise RuntimeError("LIFetch selection must execute before SFA")
+            raise RuntimeError("slots() needs a selection: call the selector for this step first")
         if token_count > self.attention_indices.shape[0]:
-            raise ValueError("SFA query count exceeds the fused selection")
+            raise ValueError(f"{token_count} tokens requested, the last selection holds "
+                             f"{self.attention_indices.shape[0]}")
         return self.attention_indices[:token_count]

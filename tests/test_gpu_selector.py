@@ -275,16 +275,16 @@ def test_selector_rejects_unbound_inputs(torch_gpu):
     torch = torch_gpu
     w = World(torch, seed=5)
     s = w.storage
-    with pytest.raises(RuntimeError, match="execute before SFA"):
+    with pytest.raises(RuntimeError, match="needs a selection"):
         w.selector.slots(1)
     other = kvip_amd.QueryInputs(torch, B, "cuda", history=HISTORY)
-    with pytest.raises(ValueError, match="packed query buffers"):
+    with pytest.raises(ValueError, match="not the packed QueryInputs buffer"):
         kvip_amd.VllmIndexSelector(torch, inputs=other, rotating=w.rot, update=w.update, logical_ids=s.logical_ids,
                                    row_owners=other.row_owners)
     with pytest.raises(ValueError, match="row owners"):
         kvip_amd.VllmIndexSelector(torch, inputs=w.inputs, rotating=w.rot, update=w.update,
                                    logical_ids=s.logical_ids, row_owners=w.inputs.row_owners[:2])
-    with pytest.raises(ValueError, match="distinct stable owners"):
+    with pytest.raises(ValueError, match="share an owner row"):
         sel = kvip_amd.VllmIndexSelector(torch, inputs=w.inputs, rotating=w.rot, update=w.update,
                                          logical_ids=s.logical_ids, row_owners=w.inputs.row_owners,
                                          unique_active_owners=True)
