@@ -23,6 +23,7 @@ __all__ = [
     "PagedIndexer",
     "RequestPlan",
     "SlotLRU",
+    "SlotLRUChains",
     "PageUpdates",
     "update_abc",
     "lidu",
@@ -48,6 +49,7 @@ _EXPORTS = {
     "PagedIndexer": ("adapters.vllm.selector", "PagedIndexer"),
     "RequestPlan": ("adapters.vllm.selector", "RequestPlan"),
     "SlotLRU": ("cache.lru", "SlotLRU"),
+    "SlotLRUChains": ("cache.lru", "SlotLRUChains"),
     "PageUpdates": ("cache.page_updates", "PageUpdates"),
     "update_abc": ("cache.abc", "update_abc"),
     "lidu": ("operators.lidu", "lidu"),

@@ -93,3 +93,63 @@ class SlotLRU:
         abi.check(lib.kvip_hip_lru_commit(ctypes.byref(self._args), abi.ptr(destinations), destinations.numel(),
                                           self.active, self._stream()), "SlotLRU commit")
         self.version += 1
+
+
+class SlotLRUChains:
+    """The slot LRUs of a whole batch, one chain per request, as one set of device arrays
+    (no reference counterpart: the reference holds one SlotLRU per request and commits
+    each from the host). Every chain has the same fixed `capacity` and evicts among the
+    committed slots [0, active). `slots` [chains, 2048] holds every chain's victim
+    candidates, oldest first, -1 padded; it may be a caller's buffer (for instance a
+    ResidentIndexUpdate's `lru_slots`), so that a commit refreshes the next round's
+    candidates in place. `commit(destinations)` takes int32 [chains, count] (a row per
+    chain; slots outside [0, active), such as -1 padding, are ignored) and is one launch
+    for the whole batch, enqueued on the current stream: a serving round can commit inside
+    its captured hipGraph."""
+
+    def __init__(self, torch, chains, capacity, device, *, active=None, slots=None):
+        if not 1 <= chains <= 65535:
+            raise ValueError(f"chains must be in 1..65535 (got {chains})")
+        if not 1 <= capacity <= MAX_SLOTS:
+            raise ValueError(f"capacity must be in 1..{MAX_SLOTS} (got {capacity})")
+        self.torch, self.device = torch, abi.device_of(torch, device)
+        self.chains, self.capacity = int(chains), int(capacity)
+        words = (capacity + BITMAP_WORD_BITS - 1) // BITMAP_WORD_BITS
+        words = (words + BITMAP_ALIGNMENT_WORDS - 1) // BITMAP_ALIGNMENT_WORDS * BITMAP_ALIGNMENT_WORDS
+        dev = self.device
+        self.order = torch.full((chains, capacity), -1, dtype=torch.int32, device=dev)
+        self.scratch = torch.empty((chains, capacity), dtype=torch.int32, device=dev)
+        self.bitmap = torch.zeros((chains, words), dtype=torch.int32, device=dev)
+        if slots is None:
+            slots = torch.full((chains, TOPK), -1, dtype=torch.int32, device=dev)
+        if (tuple(slots.shape) != (chains, TOPK) or slots.dtype != torch.int32 or not slots.is_contiguous()
+                or slots.device != dev):
+            raise ValueError(f"slots must be a contiguous int32 [{chains}, {TOPK}] tensor on {dev}")
+        self.slots = slots
+        self._args = abi.LruArgs(order=abi.ptr(self.order), scratch=abi.ptr(self.scratch), slots=abi.ptr(slots),
+                                 bitmap=abi.ptr(self.bitmap), capacity=self.capacity, bitmap_words=words)
+        self.library = abi.load_library()
+        self.active = 0
+        self.reset(self.capacity if active is None else active)
+
+    def _stream(self):
+        return abi.stream_handle(self.torch, self.device)
+
+    def reset(self, active):
+        """Every chain becomes a cold LRU of the slots [0, active) in ascending order."""
+        if not 0 <= active <= self.capacity:
+            raise ValueError(f"active must be in 0..{self.capacity} (got {active})")
+        abi.check(self.library.kvip_hip_lru_reset_chains(ctypes.byref(self._args), self.chains, int(active),
+                                                         self._stream()), "SlotLRUChains reset")
+        self.active = int(active)
+
+    def commit(self, destinations):
+        """Move each chain's accessed slots (row c of `destinations`) to its most recent
+        end in ascending slot order, then refresh `slots` and the bitmaps."""
+        torch = self.torch
+        if (destinations.dim() != 2 or destinations.shape[0] != self.chains or destinations.dtype != torch.int32
+                or destinations.device != self.device or destinations.stride(1) != 1):
+            raise ValueError(f"destinations must be int32 [{self.chains}, count] rows on {self.device}")
+        abi.check(self.library.kvip_hip_lru_commit_chains(
+            ctypes.byref(self._args), self.chains, abi.ptr(destinations), destinations.stride(0),
+            int(destinations.shape[1]), self.active, self._stream()), "SlotLRUChains commit")

@@ -66,9 +66,21 @@ __global__ __launch_bounds__(kAbcThreads) void update_abc_kernel(const KvipAbcAr
     }
 }
 
+// Chain c of a set of `chains` LRUs laid out back to back: order/scratch rows of
+// `capacity`, slots rows of 2048, bitmap rows of `bitmap_words` (a single LRU is chain 0).
+KVIP_DEVICE KvipLruArgs chain_of(const KvipLruArgs& p, int c) {
+    KvipLruArgs q = p;
+    q.order += static_cast<size_t>(c) * p.capacity;
+    q.scratch += static_cast<size_t>(c) * p.capacity;
+    q.slots += static_cast<size_t>(c) * kTopK;
+    q.bitmap += static_cast<size_t>(c) * p.bitmap_words;
+    return q;
+}
+
 // order[0, committed) = 0, 1, ..., committed-1 (a cold LRU in ascending slot order) and
-// the victim list/bitmap of it.
-__global__ __launch_bounds__(kLruThreads) void lru_reset_kernel(const KvipLruArgs p, int committed) {
+// the victim list/bitmap of it; chain blockIdx.y.
+__global__ __launch_bounds__(kLruThreads) void lru_reset_kernel(const KvipLruArgs args, int committed) {
+    const KvipLruArgs p = chain_of(args, blockIdx.y);
     for (int i = blockIdx.x * kLruThreads + threadIdx.x; i < p.capacity; i += gridDim.x * kLruThreads) {
         p.order[i] = i < committed ? i : -1;
     }
@@ -81,12 +93,16 @@ __global__ __launch_bounds__(kLruThreads) void lru_extend_kernel(const KvipLruAr
     }
 }
 
-// One workgroup: stable partition of order[0, active) into (not committed, committed in
-// ascending slot order) through `scratch`, then the victims of the new order.
-__global__ __launch_bounds__(kLruThreads) void lru_commit_kernel(const KvipLruArgs p, const int32_t* dest, int count,
-                                                                 int active, int commit) {
+// One workgroup per chain (blockIdx.x): stable partition of order[0, active) into (not
+// committed, committed in ascending slot order) through `scratch`, then the victims of
+// the new order. Chain c commits dest[c * dest_stride, + count).
+__global__ __launch_bounds__(kLruThreads) void lru_commit_kernel(const KvipLruArgs args, const int32_t* dest,
+                                                                 int64_t dest_stride, int count, int active,
+                                                                 int commit) {
     __shared__ uint32_t s_member[kLruBitmapWords];
     __shared__ uint32_t s_wave[kLruThreads / 64];
+    const KvipLruArgs p = chain_of(args, blockIdx.x);
+    if (commit) dest += static_cast<size_t>(blockIdx.x) * dest_stride;
     const int tid = threadIdx.x;
     const int words = (active + 31) / 32;
     for (int i = tid; i < words; i += kLruThreads) s_member[i] = 0u;
@@ -172,13 +188,31 @@ static bool lru_ok(const KvipLruArgs* a) {
            a->bitmap_words >= (a->capacity + 31) / 32 && a->bitmap_words <= kvip::kLruBitmapWords;
 }
 
-extern "C" uint32_t kvip_hip_lru_reset(const KvipLruArgs* a, int32_t committed, void* stream) {
-    if (!lru_ok(a) || committed < 0 || committed > a->capacity) return KVIP_ERR_INVALID;
+static uint32_t lru_reset_chains(const KvipLruArgs* a, int32_t chains, int32_t committed, void* stream) {
+    if (!lru_ok(a) || chains < 1 || chains > 65535 || committed < 0 || committed > a->capacity) {
+        return KVIP_ERR_INVALID;
+    }
     const hipStream_t s = static_cast<hipStream_t>(stream);
     const int grid = (a->capacity + kvip::kLruThreads - 1) / kvip::kLruThreads;
-    hipLaunchKernelGGL(kvip::lru_reset_kernel, dim3(grid), dim3(kvip::kLruThreads), 0, s, *a, committed);
-    hipLaunchKernelGGL(kvip::lru_commit_kernel, dim3(1), dim3(kvip::kLruThreads), 0, s, *a, nullptr, 0, committed, 0);
+    hipLaunchKernelGGL(kvip::lru_reset_kernel, dim3(grid, chains), dim3(kvip::kLruThreads), 0, s, *a, committed);
+    hipLaunchKernelGGL(kvip::lru_commit_kernel, dim3(chains), dim3(kvip::kLruThreads), 0, s, *a, nullptr, int64_t{0},
+                       0, committed, 0);
     return static_cast<uint32_t>(hipGetLastError());
+}
+
+static uint32_t lru_commit_chains(const KvipLruArgs* a, int32_t chains, const int32_t* destinations,
+                                  int64_t dest_stride, int32_t count, int32_t active, void* stream) {
+    if (!lru_ok(a) || chains < 1 || chains > 65535 || count < 0 || (count > 0 && destinations == nullptr) ||
+        (chains > 1 && dest_stride < count) || active < 0 || active > a->capacity) {
+        return KVIP_ERR_INVALID;
+    }
+    hipLaunchKernelGGL(kvip::lru_commit_kernel, dim3(chains), dim3(kvip::kLruThreads), 0,
+                       static_cast<hipStream_t>(stream), *a, destinations, dest_stride, count, active, 1);
+    return static_cast<uint32_t>(hipGetLastError());
+}
+
+extern "C" uint32_t kvip_hip_lru_reset(const KvipLruArgs* a, int32_t committed, void* stream) {
+    return lru_reset_chains(a, 1, committed, stream);
 }
 
 extern "C" uint32_t kvip_hip_lru_extend(const KvipLruArgs* a, int32_t active, int32_t committed, void* stream) {
@@ -186,16 +220,21 @@ extern "C" uint32_t kvip_hip_lru_extend(const KvipLruArgs* a, int32_t active, in
     const hipStream_t s = static_cast<hipStream_t>(stream);
     const int grid = max(1, (committed - active + kvip::kLruThreads - 1) / kvip::kLruThreads);
     hipLaunchKernelGGL(kvip::lru_extend_kernel, dim3(grid), dim3(kvip::kLruThreads), 0, s, *a, active, committed);
-    hipLaunchKernelGGL(kvip::lru_commit_kernel, dim3(1), dim3(kvip::kLruThreads), 0, s, *a, nullptr, 0, committed, 0);
+    hipLaunchKernelGGL(kvip::lru_commit_kernel, dim3(1), dim3(kvip::kLruThreads), 0, s, *a, nullptr, int64_t{0}, 0,
+                       committed, 0);
     return static_cast<uint32_t>(hipGetLastError());
 }
 
 extern "C" uint32_t kvip_hip_lru_commit(const KvipLruArgs* a, const int32_t* destinations, int32_t count,
                                         int32_t active, void* stream) {
-    if (!lru_ok(a) || count < 0 || (count > 0 && destinations == nullptr) || active < 0 || active > a->capacity) {
-        return KVIP_ERR_INVALID;
-    }
-    hipLaunchKernelGGL(kvip::lru_commit_kernel, dim3(1), dim3(kvip::kLruThreads), 0, static_cast<hipStream_t>(stream),
-                       *a, destinations, count, active, 1);
-    return static_cast<uint32_t>(hipGetLastError());
+    return lru_commit_chains(a, 1, destinations, 0, count, active, stream);
+}
+
+extern "C" uint32_t kvip_hip_lru_reset_chains(const KvipLruArgs* a, int32_t chains, int32_t committed, void* stream) {
+    return lru_reset_chains(a, chains, committed, stream);
+}
+
+extern "C" uint32_t kvip_hip_lru_commit_chains(const KvipLruArgs* a, int32_t chains, const int32_t* destinations,
+                                               int64_t dest_stride, int32_t count, int32_t active, void* stream) {
+    return lru_commit_chains(a, chains, destinations, dest_stride, count, active, stream);
 }

@@ -21,11 +21,18 @@ class LIFetchForward:
     ResidentIndexUpdate (hot-cache round: resolve, Fetch of the misses from host memory,
     Index update)."""
 
-    def __init__(self, rotating, update, *, fused=False):
-        """fused: hand the round work memory to the contiguous-Fetch forward, which then
+    def __init__(self, rotating, update, *, q_workers=2, fused=False):
+        """q_workers: the reference's per-request Fetch worker count
+        (python/kvip/operators/lifetch/forward.py:8); accepted for call compatibility (a
+        positive int). On MI355X the Fetch work is spread by the hardware dispatcher over
+        every CU, so it selects nothing here.
+        fused: hand the round work memory to the contiguous-Fetch forward, which then
         runs the XCD-local round where it applies (fp8, one row per request: scoring with
         each request selected inside that launch, then the gather); False (the default)
         keeps three launches: scoring, TopK, gather."""
+        if type(q_workers) is not int or q_workers < 1:
+            raise ValueError(f"q_workers must be a positive int (got {q_workers!r})")
+        self.q_workers = q_workers
         if not isinstance(rotating, LIFetchBinding):
             raise ValueError("LIFetch rotating must be a kvip_amd LIFetchBinding")
         if not isinstance(update, (ContiguousFetch, ResidentIndexUpdate)):

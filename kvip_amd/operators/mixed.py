@@ -12,7 +12,11 @@ buffers bound once, so the whole round is one hipGraph:
   2. the decode forward (`kvip_amd.LIFetch` over a `ResidentIndexUpdate`, or a
      `ContiguousFetch`): LI over the owners' Index rows, TopK, resolver, Fetch, Index update
      and outputs;
-  3. the prefill indexer bound with `PrefillIndexer.bind`: LI over the paged cache for the
+  3. with `lru` (a SlotLRUChains whose `slots` are the resident update's candidates), one
+     launch committing every decode request's selected slots, so the next round's victim
+     candidates follow the cache's own recency, as the reference's selector commits each
+     request's SlotLRU after a step (python/kvip/cache/lru.py:96-118);
+  4. the prefill indexer bound with `PrefillIndexer.bind`: LI over the paged cache for the
      packed chunks (cumulative query lengths) and TopK-2048 per row.
 
 The caller fills the per-round inputs in place before a launch or replay: decode Q /
@@ -30,7 +34,7 @@ INDEX_DIM = 128
 
 class MixedRound:
     def __init__(self, torch, *, decode, prefill, storage_keys, storage_scales, cache_keys, cache_scales,
-                 new_tokens, status=None):
+                 new_tokens, status=None, lru=None):
         """decode: a LIFetch forward; prefill: a PrefillIndexer after `bind(...)`;
         storage_keys [owners, history, 128] (fp8 or uint8) and storage_scales
         [owners, history] float32: the persistent Index rows; cache_keys
@@ -67,6 +71,15 @@ class MixedRound:
             target_rows=storage_keys.shape[0] * storage_keys.shape[1], count=new_tokens, target_base=0,
             mode=abi.INGEST_LIST)
         self.library = abi.load_library()
+        self.lru, self.commit_rows = lru, None
+        if lru is not None:
+            upd = getattr(decode, "update", None)
+            if not getattr(decode, "resident", False) or lru.slots.data_ptr() != upd.lru_slots.data_ptr():
+                raise ValueError("the LRU chains must feed the resident decode update's candidates (slots aliasing "
+                                 "its lru_slots)")
+            if lru.chains != upd.rotating.batch:
+                raise ValueError(f"{lru.chains} LRU chains for {upd.rotating.batch} decode requests")
+            self.commit_rows = upd.slot_output.view(upd.rotating.batch, -1)
 
     def ingest(self):
         abi.check(self.library.kvip_hip_ingest_index(ctypes.byref(self.ingest_args),
@@ -75,5 +88,7 @@ class MixedRound:
     def __call__(self):
         self.ingest()
         self.decode()
+        if self.lru is not None:
+            self.lru.commit(self.commit_rows)
         self.prefill.score()
         return self.prefill.select()

@@ -201,6 +201,9 @@ PROTOTYPES = {
     "kvip_hip_lru_reset": ([ctypes.POINTER(LruArgs), _i32, _p], ctypes.c_uint32),
     "kvip_hip_lru_extend": ([ctypes.POINTER(LruArgs), _i32, _i32, _p], ctypes.c_uint32),
     "kvip_hip_lru_commit": ([ctypes.POINTER(LruArgs), _p, _i32, _i32, _p], ctypes.c_uint32),
+    "kvip_hip_lru_reset_chains": ([ctypes.POINTER(LruArgs), _i32, _i32, _p], ctypes.c_uint32),
+    "kvip_hip_lru_commit_chains": ([ctypes.POINTER(LruArgs), _i32, _p, ctypes.c_int64, _i32, _i32, _p],
+                                   ctypes.c_uint32),
     "kvip_hip_lidu_workspace_bytes": ([_i32], ctypes.c_uint64),
     "kvip_hip_lidu": ([ctypes.POINTER(LiduArgs), _p], ctypes.c_uint32),
     "kvip_hip_pack_queries": ([ctypes.POINTER(QueryPackArgs), _p], ctypes.c_uint32),

@@ -137,15 +137,33 @@ def prefill_workload(torch, device, *, seed=2026, q_len=4096, k_len=65536, heads
                 q_len=q_len, k_len=k_len, heads=heads)
 
 
+def _filled_pool(torch, gen, owners, history, resident, device):
+    """Pinned host KV pool of random 656-byte rows for every (owner, position) and the hot
+    cache holding positions [0, resident) of each owner, so every hit and every Fetch is
+    byte-checkable."""
+    pool = torch.empty(owners * history * 656, dtype=torch.uint8, pin_memory=True)
+    rows = history * 656
+    for o in range(owners):
+        pool[o * rows:(o + 1) * rows].copy_(torch.randint(0, 256, (rows,), generator=gen, device=device,
+                                                          dtype=torch.uint8))
+    hot = torch.empty((owners, resident, 656), dtype=torch.uint8, device=device)
+    hot.copy_(pool.view(owners, history, 656)[:, :resident])
+    return pool, hot
+
+
 def mixed_workload(torch, kvip, device, *, seed=2026, decode_ctx=None, history=65536, resident=16384,
-                   prefill=((2048, 8192), (1536, 1536)), heads=64):
+                   prefill=((2048, 8192), (1536, 1536)), heads=64, lru=False, fill_pool=False):
     """BASELINE config 5 round: decode requests (one row each, contexts `decode_ctx`, default
     32 requests ~U[4096, 65536]) on the resident cache (owner Index rows of `history`
     positions, `resident` hot slots, misses from a pinned host pool) plus prefill chunks
     (q_len, k_len) packed TND-style against a paged index-K cache; every new token (the
     last position of each decode request, the chunks' rows) is ingested into the Index
-    storage. Returns a SimpleNamespace with the bound `round` (a kvip.MixedRound) and its
-    parts; inputs are seeded and already resident on the device."""
+    storage. lru: the decode requests' victim candidates come from a SlotLRUChains that
+    the round commits every step (else fixed candidates 0..2047); fill_pool: random KV
+    bytes in the host pool with the hot cache holding each owner's first `resident` rows
+    (else the pool is left uninitialised, enough for timing). Returns a SimpleNamespace
+    with the bound `round` (a kvip.MixedRound) and its parts; inputs are seeded and already
+    resident on the device."""
     from types import SimpleNamespace
 
     rng = np.random.default_rng(seed)
@@ -167,8 +185,11 @@ def mixed_workload(torch, kvip, device, *, seed=2026, decode_ctx=None, history=6
     scales = torch.rand((owners, history), generator=gen, device=dev) * 1.5 + 0.5
     addresses = (torch.arange(owners * history, device=dev, dtype=torch.int64) * 656).view(owners, history)
     logical = torch.arange(history, device=dev, dtype=torch.int64).repeat(owners, 1)
-    pool = torch.empty(owners * history * 656, dtype=torch.uint8, pin_memory=True)
-    hot = torch.zeros((owners, resident, 656), dtype=torch.uint8, device=dev)
+    if fill_pool:
+        pool, hot = _filled_pool(torch, gen, owners, history, resident, dev)
+    else:
+        pool = torch.empty(owners * history * 656, dtype=torch.uint8, pin_memory=True)
+        hot = torch.zeros((owners, resident, 656), dtype=torch.uint8, device=dev)
     valid = torch.ones((owners, resident), dtype=torch.int32, device=dev)
     # Paged index-K cache: the prefill sequences' pages, then one page per 128 decode tokens.
     pf_blocks = [(k + BLOCK_TOKENS - 1) // BLOCK_TOKENS for _, k in prefill]
@@ -204,7 +225,11 @@ def mixed_workload(torch, kvip, device, *, seed=2026, decode_ctx=None, history=6
     upd = kvip.ResidentIndexUpdate(torch, keys=keys, scales=scales, addresses=addresses, logical_ids=logical,
                                    row_owners=torch.arange(nd, dtype=torch.int32, device=dev), rotating=rot,
                                    hot_valid=valid, hot_cache=hot, host_pool=pool, resident=resident)
-    upd.set_candidates(torch.arange(2048, dtype=torch.int32, device=dev).repeat(nd, 1))
+    chains = None
+    if lru:
+        chains = kvip.SlotLRUChains(torch, nd, resident, dev, slots=upd.lru_slots)
+    else:
+        upd.set_candidates(torch.arange(2048, dtype=torch.int32, device=dev).repeat(nd, 1))
     # Prefill chunks.
     rows = sum(q for q, _ in prefill)
     pf_query = saturating_fp8(torch, normal((rows, heads, INDEX_DIM)))
@@ -218,10 +243,11 @@ def mixed_workload(torch, kvip, device, *, seed=2026, decode_ctx=None, history=6
     pidx.bind(pf_query, pf_weights, pf_qscale, cache_keys, cache_scales, cu, kl, table)
     forward = kvip.LIFetch(rot, upd)
     rnd = kvip.MixedRound(torch, decode=forward, prefill=pidx, storage_keys=keys, storage_scales=scales,
-                          cache_keys=cache_keys, cache_scales=cache_scales, new_tokens=len(sources))
+                          cache_keys=cache_keys, cache_scales=cache_scales, new_tokens=len(sources), lru=chains)
     rnd.sources.copy_(torch.tensor(sources, dtype=torch.int64))
     rnd.targets.copy_(torch.tensor(targets, dtype=torch.int64))
-    return SimpleNamespace(round=rnd, rot=rot, update=upd, forward=forward, prefill=pidx, keys=keys, scales=scales,
+    return SimpleNamespace(round=rnd, rot=rot, update=upd, forward=forward, prefill=pidx, lru=chains, keys=keys,
+                           scales=scales,
                            addresses=addresses, logical=logical, hot=hot, valid=valid, pool=pool,
                            cache_keys=cache_keys, cache_scales=cache_scales, pf_query=pf_query, pf_weights=pf_weights,
                            pf_qscale=pf_qscale, cu=cu, kl=kl, table=table, decode_ctx=decode_ctx, chunks=prefill,
@@ -319,12 +345,13 @@ def lidu_workload(torch, device, *, seed=2026, batch=16, queries=4, budget=16384
 
 
 def resident_workload(torch, kvip, device, *, seed=2026, batch=16, history=131072, resident=16384, q_rows=1,
-                      heads=64):
+                      heads=64, fill_pool=False):
     """BASELINE config 4 shape for the resident-cache round: `batch` requests, each owning
     `history` Index rows (fp8 keys ~ random finite codes, scales U(0.5, 2)) and a hot
     cache of `resident` slots holding positions 0..resident-1; every row's KV lives in a
-    pinned host pool (contents irrelevant to timing). Returns (rotating, update,
-    forward)."""
+    pinned host pool (random bytes with fill_pool, the hot cache then holding each owner's
+    first `resident` rows; else uninitialised, enough for timing). Returns (rotating,
+    update, forward)."""
     g = torch.Generator(device=device).manual_seed(seed)
     owners = batch
     keys = (torch.randint(0, 256, (owners, history, 128), generator=g, device=device, dtype=torch.uint8) & 0x77)
@@ -332,8 +359,11 @@ def resident_workload(torch, kvip, device, *, seed=2026, batch=16, history=13107
     scales = torch.rand((owners, history), generator=g, device=device) * 1.5 + 0.5
     addresses = (torch.arange(owners * history, device=device, dtype=torch.int64) * 656).view(owners, history)
     logical = torch.arange(history, device=device, dtype=torch.int64).repeat(owners, 1)
-    pool = torch.empty(owners * history * 656, dtype=torch.uint8, pin_memory=True)
-    hot = torch.zeros((owners, resident, 656), dtype=torch.uint8, device=device)
+    if fill_pool:
+        pool, hot = _filled_pool(torch, g, owners, history, resident, device)
+    else:
+        pool = torch.empty(owners * history * 656, dtype=torch.uint8, pin_memory=True)
+        hot = torch.zeros((owners, resident, 656), dtype=torch.uint8, device=device)
     valid = torch.ones((owners, resident), dtype=torch.int32, device=device)
     rot = kvip.LIFetchBinding(torch, batch=batch, max_context=history, device=device, heads=heads,
                               rows_per_request=q_rows, qk_dtype="fp8", query_ends=True)

@@ -113,6 +113,66 @@ def test_slot_lru_matches_oracle(torch_gpu):
     assert (gpu.slots[0, 100:] == -1).all()
 
 
+def test_slot_lru_chains_match_per_chain_oracles(torch_gpu):
+    """SlotLRUChains (kvip_hip_lru_reset_chains / _commit_chains, one launch per batch)
+    against one oracle SlotLRU per chain: destinations are rows of a wider buffer (row
+    stride above the count) with -1 padding and out-of-range slots; the chains' slots
+    alias a caller's candidate buffer; committing inside a captured hipGraph equals the
+    eager commits."""
+    torch = torch_gpu
+    rng = np.random.default_rng(31)
+    chains, capacity = 5, 6000
+    cand = torch.full((chains, 2048), -7, dtype=torch.int32, device="cuda")
+    gpu = kvip_amd.SlotLRUChains(torch, chains, capacity, "cuda", slots=cand)
+    cpus = [ref.SlotLRU() for _ in range(chains)]
+    for c in cpus:
+        c.resize(capacity, capacity)
+
+    def check():
+        torch.cuda.synchronize()
+        order = gpu.order.cpu().numpy()
+        slots = cand.cpu().numpy()
+        bitmap = gpu.bitmap.cpu().numpy()
+        for k, c in enumerate(cpus):
+            assert slots[k].tolist() == c.slots.tolist(), k
+            assert order[k][:c.active].tolist() == c.order(), k
+            assert (order[k][c.active:] == -1).all(), k
+            assert np.array_equal(bitmap[k][:c.bitmap.shape[0]].view(np.uint32), c.bitmap), k
+
+    check()
+    buf = torch.full((chains, 3000), -1, dtype=torch.int32, device="cuda")
+    for step in range(6):
+        host = np.full((chains, 2500), -1, np.int32)
+        for k in range(chains):
+            n = int(rng.integers(0, 2500))
+            host[k, :n] = rng.integers(-2, capacity + 10, n)
+        buf[:, :2500].copy_(torch.from_numpy(host))
+        gpu.commit(buf[:, :2500])
+        for k, c in enumerate(cpus):
+            c.commit(host[k])
+        check()
+    # Captured: the commit of a fixed buffer, replayed after the buffer is refilled.
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            gpu.commit(buf[:, :2500])
+    torch.cuda.current_stream().wait_stream(side)
+    for step in range(3):
+        host = rng.integers(0, capacity, (chains, 2500)).astype(np.int32)
+        buf[:, :2500].copy_(torch.from_numpy(host))
+        graph.replay()
+        for k, c in enumerate(cpus):
+            c.commit(host[k])
+        check()
+    gpu.reset(100)
+    for c in cpus:
+        c.resize(capacity, 100)
+    check()
+    assert (cand[:, 100:] == -1).all()
+
+
 def test_publish_pages_matches_oracle(torch_gpu):
     """PageUpdates.submit (kvip_hip_publish_pages) against oracle.cache.publish_pages over
     three submissions alternating the staging ring: addresses, validity, cleared map ranges
