@@ -109,6 +109,7 @@ def keys_case(kind, n, rng):
     ("random", [32768, 20000, 2048, 2047, 0, 8193]),
     ("few_levels", [16384, 30000]),
     ("all_equal", [4096, 2048]),
+    ("all_equal", [65536, 4096]),  # a full register row of equal keys: the eq total reaches 65536
     ("one_bin", [131072]),
 ])
 def test_topk_bit_exact_on_oracle_keys(torch_gpu, kind, ctx):
