@@ -72,7 +72,7 @@
 extern "C" {
 #endif
 
-#define KVIP_HIP_ABI_VERSION 8u
+#define KVIP_HIP_ABI_VERSION 9u
 
 #define KVIP_TOPK 2048
 #define KVIP_BLOCK_TOKENS 128
@@ -562,6 +562,18 @@ uint32_t kvip_hip_lifetch_forward(const KvipLIFetchArgs* args, void* stream);
 #define KVIP_LIFETCH_PLAN_ROUND 2u
 #define KVIP_TOPK_REGS_MAX_KEYS 65536
 uint32_t kvip_hip_lifetch_plan(const KvipLIFetchArgs* args);
+/* kvip_hip_lifetch_forward without caller scratch, for callers that cannot allocate device
+ * memory (code under hipGraph capture, serving loops or harnesses that forbid hipMalloc).
+ * No counterpart in the reference. The score keys and histograms come from one
+ * library-owned array of KVIP_LIFETCH_STATIC_SCRATCH_BYTES per GPU (held until the process
+ * ends): indexer.score_keys, indexer.histogram, topk.score_keys, topk.histogram,
+ * topk.segments and round_work must be NULL, and rows * 1024 (rounded up to 256) + rows *
+ * key_stride * 2 bytes must fit the array (rows = batch * rows_per_request), else
+ * KVIP_ERR_INVALID and nothing is launched. Same outputs as kvip_hip_lifetch_forward's
+ * three-launch plan (plus one small fill launch that clears the histograms first); no
+ * hipMalloc, hipFree or memset. Calls that overlap on one GPU share the array and race. */
+#define KVIP_LIFETCH_STATIC_SCRATCH_BYTES (16u << 20)
+uint32_t kvip_hip_lifetch_forward_static(const KvipLIFetchArgs* args, void* stream);
 /* TopK-2048 of rows scored by kvip_hip_indexer_decode fused with the Fetch gather of the
  * selected rows: same outputs as kvip_hip_topk followed by kvip_hip_fetch_gather. Needs
  * topk->histogram and topk->segments; fetch->topk must be topk->topk. */

@@ -9,7 +9,7 @@ import ctypes
 from pathlib import Path
 
 LIBRARY = Path(__file__).resolve().parents[1] / "_lib" / "libkvip_hip.so"
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 KVIP_OK = 0
 KVIP_ERR_INVALID = 100000
@@ -121,6 +121,7 @@ class QueryPackArgs(ctypes.Structure):
 # kvip_hip_lifetch_plan results.
 LIFETCH_PLANS = {0: "three", 2: "round"}
 TOPK_REGS_MAX_KEYS = 65536  # KVIP_TOPK_REGS_MAX_KEYS
+LIFETCH_STATIC_SCRATCH_BYTES = 16 << 20  # KVIP_LIFETCH_STATIC_SCRATCH_BYTES
 
 INGEST_DECODE = 0
 INGEST_LIST = 1
@@ -196,6 +197,7 @@ PROTOTYPES = {
     "kvip_hip_fetch_gather": ([ctypes.POINTER(FetchArgs), _p], ctypes.c_uint32),
     "kvip_hip_lifetch_forward": ([ctypes.POINTER(LIFetchArgs), _p], ctypes.c_uint32),
     "kvip_hip_lifetch_plan": ([ctypes.POINTER(LIFetchArgs)], ctypes.c_uint32),
+    "kvip_hip_lifetch_forward_static": ([ctypes.POINTER(LIFetchArgs), _p], ctypes.c_uint32),
     "kvip_hip_select_fetch": ([ctypes.POINTER(TopkArgs), ctypes.POINTER(FetchArgs), _p], ctypes.c_uint32),
     "kvip_hip_update_abc": ([ctypes.POINTER(AbcArgs), _p], ctypes.c_uint32),
     "kvip_hip_lru_reset": ([ctypes.POINTER(LruArgs), _i32, _p], ctypes.c_uint32),
