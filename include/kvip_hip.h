@@ -142,10 +142,10 @@ typedef struct KvipIndexerArgs {
  * sequences. */
 #define KVIP_PREFILL_MAX_SEQUENCES 1024
 typedef struct KvipPrefillArgs {
-    const void* query;           /* [rows, heads, 128] fp8 e4m3 */
+    const void* query;           /* [rows, heads, 128] fp8 e4m3 or bf16 (qk_dtype) */
     const void* weights;         /* [rows, heads] fp32 or bf16 (weight_dtype) */
     const float* query_scale;    /* [rows, heads], or NULL for 1.0 */
-    const void* keys;            /* paged index-K, as KvipIndexerArgs */
+    const void* keys;            /* paged index-K of qk_dtype, as KvipIndexerArgs */
     const float* key_scale;      /* per-token scales, as KvipIndexerArgs, or NULL */
     const int32_t* block_table;  /* [sequences, max_blocks] */
     const int32_t* cu_seqlens_q; /* [sequences + 1] cumulative query rows, cu[0] = 0 */
@@ -154,7 +154,7 @@ typedef struct KvipPrefillArgs {
     uint32_t* histogram;         /* [rows, 256], zero before the launch */
     int32_t* row_valid;          /* [rows] out */
     uint32_t* status;            /* device status word, or NULL */
-    int64_t key_block_stride;    /* bytes between index-K blocks (multiple of 16, >= 16 KiB) */
+    int64_t key_block_stride;    /* bytes between index-K blocks (multiple of 16, >= 16 KiB fp8, 32 KiB bf16) */
     int64_t scale_block_stride;  /* floats between key-scale blocks */
     int32_t sequences;
     int32_t rows;                /* = cu_seqlens_q[sequences] */
@@ -162,7 +162,7 @@ typedef struct KvipPrefillArgs {
     int32_t max_blocks;
     int32_t num_blocks;
     int32_t key_stride;          /* multiple of 8, >= max_blocks * 128 */
-    int32_t qk_dtype;            /* KVIP_DTYPE_FP8_E4M3 */
+    int32_t qk_dtype;            /* KVIP_DTYPE_FP8_E4M3 or KVIP_DTYPE_BF16 */
     int32_t weight_dtype;        /* KVIP_DTYPE_FP32 or KVIP_DTYPE_BF16 */
 } KvipPrefillArgs;
 
@@ -255,7 +255,8 @@ typedef struct KvipAbcArgs {
 /* Slot LRU of one request/layer chain on the device. order[i] is the slot at LRU position
  * i (0 = least recently used) for i < active; slots [2048] = the min(2048, active) oldest
  * slots (-1 padded); bitmap [bitmap_words] = their membership bits; scratch [capacity] is
- * work memory. capacity <= 133632 slots. */
+ * reserved work memory (required non-NULL; the commit partitions the order in place and
+ * leaves it untouched). capacity <= 133632 slots. */
 typedef struct KvipLruArgs {
     int32_t* order;
     int32_t* scratch;

@@ -1,19 +1,22 @@
 // Prefill (and mixed-batch) lightning-indexer scoring on gfx950 MFMA: packed query rows of
-// several sequences against their paged index-K under a right-down causal mask.
+// several sequences against their paged index-K under a right-down causal mask, fp8 e4m3
+// or bf16 Q/K.
 //
 // Work unit = (query block, context segment): 8 consecutive query rows of one sequence
 // against 4096 key positions. The workgroup's 4 waves own 2 query rows each and keep their
 // Q fragments and per-lane head weights (w'_h = w_h * qscale_h for the 32 heads a lane
-// reduces) in registers. The segment streams through LDS in 256-token chunks, double
-// buffered: every wave issues direct-to-LDS 16-byte loads (global_load_lds_dwordx4) for a
-// quarter of the next chunk, with the XOR swizzle applied on the global side so that the
-// fragment reads (lane n of a 32-token tile reads row n) hit distinct bank groups. Each
-// chunk tile (32 tokens) is one B fragment set read once from LDS and reused by the wave's
-// 2 rows x 2 head tiles x 2 K slices = 8 MFMAs (v_mfma_scale_f32_32x32x64_f8f6f4). The
+// reduces) in registers. The segment streams through LDS in 32 KiB chunks (256 fp8 or 128
+// bf16 tokens), double buffered: every wave issues direct-to-LDS 16-byte loads
+// (global_load_lds_dwordx4) for a quarter of the next chunk, with the XOR swizzle applied
+// on the global side so that the fragment reads (lane n of a 32-token tile reads row n)
+// hit distinct bank groups. Each chunk tile (32 tokens) is one B fragment set read once
+// from LDS and reused by the wave's 2 rows x 2 head tiles: 2 K slices each of
+// v_mfma_scale_f32_32x32x64_f8f6f4 (fp8) or 8 of v_mfma_f32_32x32x16_bf16 (bf16). The
 // epilogue is the decode kernel's: ReLU, head weights, head reduction, key scale, bf16
 // half-away rounding, sortable key; keys go through a per-wave LDS strip to coalesced
 // stores, and a per-workgroup 256-bin histogram of the key high byte (two 16-bit counters
-// per word) is added to the row histograms at the end.
+// per word) is added to the row histograms at the end. bf16 holds twice the Q fragment
+// registers, so its kernel runs one workgroup (one wave per SIMD) per CU.
 //
 // Reference: the native prefill LI (torch_npu.npu_quant_lightning_indexer, TND layout,
 // sparse_mode 3) that the vLLM selector runs for prefill rows (python/kvip/adapters/vllm/
@@ -29,16 +32,16 @@ constexpr int kPfWaves = 4;
 constexpr int kPfThreads = kPfWaves * 64;
 constexpr int kPfRowsPerWave = 2;                           // one row per lane half at the finish
 constexpr int kPfBlockRows = kPfWaves * kPfRowsPerWave;     // 8 query rows per workgroup
-constexpr int kPfChunk = 256;                               // tokens per LDS chunk
-constexpr int kPfTiles = kPfChunk / 32;
+constexpr int kPfChunkBytes = 256 * kIndexDim;             // 32 KiB of K rows per LDS chunk
 constexpr int kPfSegment = 4096;                            // key positions per workgroup
-constexpr int kPfChunks = kPfSegment / kPfChunk;
 constexpr int kPfPages = kPfSegment / kBlockTokens;         // 32
 constexpr int kPfMaxSeq = KVIP_PREFILL_MAX_SEQUENCES;
-// LDS piece swizzle of a staged 128-byte K row: piece j of row r sits at slot j ^ (r & 7).
-// A fragment read (lane n reads piece j of row n) then touches 8 distinct 16-byte slots
-// in every group of 8 consecutive lanes, i.e. all 32 banks once per 128-byte phase.
-KVIP_DEVICE int pf_swizzle(int row) { return row & 7; }
+// LDS piece swizzle of a staged K row of 8 (fp8) or 16 (bf16) 16-byte pieces: piece j of
+// row r sits at slot j ^ (r & 15) (j ^ (r & 7) for 8 pieces). A fragment read (lane n
+// reads piece j of row n) then touches distinct 16-byte slots in every group of 8 (16)
+// consecutive lanes, i.e. every bank once per phase.
+template <int ELEM>
+KVIP_DEVICE int pf_swizzle(int row) { return row & (8 * ELEM - 1); }
 
 template <bool W_BF16>
 KVIP_DEVICE float pf_weight(const KvipPrefillArgs& p, size_t idx) {
@@ -51,12 +54,20 @@ KVIP_DEVICE float pf_weight(const KvipPrefillArgs& p, size_t idx) {
     return w * (p.query_scale != nullptr ? p.query_scale[idx] : 1.0f);
 }
 
-template <int HEADS, bool W_BF16>
-__global__ __launch_bounds__(kPfThreads, 2) void indexer_prefill_kernel(const KvipPrefillArgs p) {
+template <int ELEM, int HEADS, bool W_BF16>
+__global__ __launch_bounds__(kPfThreads, 3 - ELEM) void indexer_prefill_kernel(const KvipPrefillArgs p) {
     constexpr int MT = HEADS / 32;
-    constexpr int NV = Mma<1>::NV;                 // 4 x 16 bytes of a 128-byte fp8 row
+    constexpr int NV = Mma<ELEM>::NV;              // 16-byte pieces of a half row per lane
+    constexpr int STEPS = Mma<ELEM>::STEPS;        // MFMAs per 128-dim contraction
+    constexpr int kRowBytes = kIndexDim * ELEM;
+    constexpr int kPieces = kRowBytes / 16;        // 16-byte pieces per K row
+    constexpr int kPfChunk = kPfChunkBytes / kRowBytes;  // tokens per LDS chunk (256 or 128)
+    constexpr int kPfTiles = kPfChunk / 32;
+    constexpr int kChunkPages = kPfChunk / kBlockTokens;  // pages per chunk (2 or 1)
+    constexpr int kRowsPerLoad = 64 / kPieces;     // K rows one 64-lane 16-byte load fills
     static_assert(kPfRowsPerWave == 2, "the finish maps row q to lane half q");
-    __shared__ __align__(16) uint8_t s_k[2][kPfChunk * kIndexDim];
+    static_assert((kPfChunk / kPfWaves) / kRowsPerLoad == 8, "8 staging loads per wave and chunk");
+    __shared__ __align__(16) uint8_t s_k[2][kPfChunkBytes];
     __shared__ __align__(16) float s_ks[2][kPfChunk];
     __shared__ __align__(16) uint16_t s_keys[kPfWaves][kPfRowsPerWave][kPfChunk];
     __shared__ uint32_t s_hist[kPfBlockRows][128];  // two 16-bit counters per word
@@ -121,8 +132,8 @@ __global__ __launch_bounds__(kPfThreads, 2) void indexer_prefill_kernel(const Kv
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
             const v4i* src = reinterpret_cast<const v4i*>(static_cast<const uint8_t*>(p.query) +
-                                                          (static_cast<size_t>(rowi[q]) * HEADS + mt * 32 + n) * kIndexDim +
-                                                          g * (kIndexDim / 2));
+                                                          (static_cast<size_t>(rowi[q]) * HEADS + mt * 32 + n) * kRowBytes +
+                                                          g * (kRowBytes / 2));
 #pragma unroll
             for (int v = 0; v < NV; ++v) qa[q][mt][v] = src[v];
 #pragma unroll
@@ -152,22 +163,25 @@ __global__ __launch_bounds__(kPfThreads, 2) void indexer_prefill_kernel(const Kv
     }
     const uint8_t* kbase = static_cast<const uint8_t*>(p.keys);
 
-    // Wave w stages rows [64w, 64w + 64) of a chunk: 8 direct-to-LDS loads of 8 rows each.
+    // Wave w stages rows [w * chunk/4, (w + 1) * chunk/4) of a chunk (one page's rows):
+    // 8 direct-to-LDS loads of kRowsPerLoad rows each.
+    constexpr int kWaveRows = kPfChunk / kPfWaves;
     auto stage = [&](int c, int buf) {
+        const int pg = __builtin_amdgcn_readlane(my_page, c * kChunkPages + (wave * kWaveRows) / kBlockTokens);
 #pragma unroll
         for (int v = 0; v < 8; ++v) {
-            const int row = wave * 64 + v * 8 + (lane >> 3);
-            const int piece = (lane & 7) ^ pf_swizzle(row);
-            const int pg = __builtin_amdgcn_readlane(my_page, c * 2 + (wave >> 1));
+            const int row = wave * kWaveRows + v * kRowsPerLoad + lane / kPieces;
+            const int piece = (lane % kPieces) ^ pf_swizzle<ELEM>(row);
             const uint8_t* src = kbase + static_cast<size_t>(pg) * p.key_block_stride +
-                                 (row & (kBlockTokens - 1)) * kIndexDim + piece * 16;
-            __builtin_amdgcn_global_load_lds(src, LDS_PTR(&s_k[buf][(wave * 64 + v * 8) * kIndexDim]), 16, 0, 0);
+                                 (row & (kBlockTokens - 1)) * kRowBytes + piece * 16;
+            __builtin_amdgcn_global_load_lds(src, LDS_PTR(&s_k[buf][(wave * kWaveRows + v * kRowsPerLoad) * kRowBytes]),
+                                             16, 0, 0);
         }
-        if (wave == 0 && p.key_scale != nullptr) {
+        if (wave == 0 && p.key_scale != nullptr && lane < kPfChunk / 4) {
             const int row = lane * 4;  // 4 consecutive scales of one page
             // readlane takes a wave-uniform lane index: read both pages, pick per half-wave.
-            const int pg0 = __builtin_amdgcn_readlane(my_page, c * 2);
-            const int pg1 = __builtin_amdgcn_readlane(my_page, c * 2 + 1);
+            const int pg0 = __builtin_amdgcn_readlane(my_page, c * kChunkPages);
+            const int pg1 = __builtin_amdgcn_readlane(my_page, c * kChunkPages + kChunkPages - 1);
             const int pg = lane < 32 ? pg0 : pg1;
             const float* src = p.key_scale + static_cast<size_t>(pg) * p.scale_block_stride + (row & 127);
             __builtin_amdgcn_global_load_lds(src, LDS_PTR(&s_ks[buf][0]), 16, 0, 0);
@@ -184,11 +198,11 @@ __global__ __launch_bounds__(kPfThreads, 2) void indexer_prefill_kernel(const Kv
     // k*32 + n does not depend on k), its key scale, and the key strip slots.
     uint32_t ka[NV];
 #pragma unroll
-    for (int u = 0; u < NV; ++u) ka[u] = lds_addr(&s_k[0][n * kIndexDim + (((g * NV + u) ^ pf_swizzle(n)) * 16)]);
+    for (int u = 0; u < NV; ++u) ka[u] = lds_addr(&s_k[0][n * kRowBytes + (((g * NV + u) ^ pf_swizzle<ELEM>(n)) * 16)]);
     const uint32_t ksa = lds_addr(&s_ks[0][n]);
     const uint32_t keya = lds_addr(&s_keys[wave][g][n]);
     const uint32_t hista = lds_addr(&s_hist[hist_row][0]);
-    constexpr uint32_t kKBuf = kPfChunk * kIndexDim;   // bytes between the two K buffers
+    constexpr uint32_t kKBuf = kPfChunkBytes;          // bytes between the two K buffers
     constexpr uint32_t kSBuf = kPfChunk * 4;           // bytes between the two scale buffers
 
     stage(0, 0);
@@ -198,18 +212,23 @@ __global__ __launch_bounds__(kPfThreads, 2) void indexer_prefill_kernel(const Kv
         lds_barrier(stores);  // chunk c landed and is visible; buffer c+1 is free again
         if (c + 1 < nchunks) stage(c + 1, buf ^ 1);
         const int cstart = seg0 + c * kPfChunk;
-        const float page_ok0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_ok), c * 2));
-        const float page_ok1 =
-            __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_ok), c * 2 + 1));
+        const float page_ok0 =
+            __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_ok), c * kChunkPages));
+        const float page_ok1 = __builtin_bit_cast(
+            float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_ok), c * kChunkPages + kChunkPages - 1));
 #pragma unroll 1
         for (int k = 0; k < kPfTiles; ++k) {
             const int t0 = cstart + k * 32;
             if (t0 >= vis[0] && t0 >= vis[1]) break;  // uniform per wave: later tiles are masked too
             v4i kb[NV];
             float ks_raw;
-            const uint32_t toff = buf * kKBuf + k * 32 * kIndexDim;
-            lds_read_tile(ka[0] + toff, ka[1] + toff, ka[2] + toff, ka[3] + toff, ksa + buf * kSBuf + k * 128, kb,
-                          ks_raw);
+            const uint32_t toff = buf * kKBuf + k * 32 * kRowBytes;
+            if constexpr (ELEM == 1) {
+                lds_read_tile(ka[0] + toff, ka[1] + toff, ka[2] + toff, ka[3] + toff, ksa + buf * kSBuf + k * 128, kb,
+                              ks_raw);
+            } else {
+                lds_read_tile8(ka, toff, ksa + buf * kSBuf + k * 128, kb, ks_raw);
+            }
             const float ks = ks_raw * (k < kPfTiles / 2 ? page_ok0 : page_ok1);
             // Units u = (row q = u / MT, head tile mt = u % MT), two dependent K-slice MFMAs
             // each. Unit u+1's MFMAs are issued between the 32 VALU ops (ReLU, weight FMA) of
@@ -220,8 +239,8 @@ __global__ __launch_bounds__(kPfThreads, 2) void indexer_prefill_kernel(const Kv
             for (int q = 0; q < kPfRowsPerWave; ++q) pj[q][0] = pj[q][1] = pj[q][2] = pj[q][3] = 0.f;
             v16f acc[2];
             acc[0] = v16f{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-            Mma<1>::step(0, qa[0][0], kb, acc[0]);
-            Mma<1>::step(1, qa[0][0], kb, acc[0]);
+#pragma unroll
+            for (int st = 0; st < STEPS; ++st) Mma<ELEM>::step(st, qa[0][0], kb, acc[0]);
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int u = 0; u < U; ++u) {
@@ -230,8 +249,8 @@ __global__ __launch_bounds__(kPfThreads, 2) void indexer_prefill_kernel(const Kv
                 v16f& nxt = acc[(u + 1) & 1];
                 if (u + 1 < U) {
                     nxt = v16f{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-                    Mma<1>::step(0, qa[(u + 1) / MT][(u + 1) % MT], kb, nxt);
-                    Mma<1>::step(1, qa[(u + 1) / MT][(u + 1) % MT], kb, nxt);
+#pragma unroll
+                    for (int st = 0; st < STEPS; ++st) Mma<ELEM>::step(st, qa[(u + 1) / MT][(u + 1) % MT], kb, nxt);
                 }
 #pragma unroll
                 for (int r4 = 0; r4 < 4; ++r4) {
@@ -242,11 +261,14 @@ __global__ __launch_bounds__(kPfThreads, 2) void indexer_prefill_kernel(const Kv
                     }
                 }
                 if (u + 1 < U) {
-                    // 1 MFMA, 16 VALU, 1 MFMA, 16 VALU; nothing crosses into the next unit.
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);
+                    // The next unit's STEPS MFMAs spread over this unit's 32 VALU ops (fp8:
+                    // 1 MFMA, 16 VALU, 1 MFMA, 16 VALU; bf16: 1 MFMA, 4 VALU, ...); nothing
+                    // crosses into the next unit.
+#pragma unroll
+                    for (int st = 0; st < STEPS; ++st) {
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                        __builtin_amdgcn_sched_group_barrier(0x002, 32 / STEPS, 0);
+                    }
                     __builtin_amdgcn_sched_barrier(0);
                 }
             }
@@ -273,9 +295,9 @@ __global__ __launch_bounds__(kPfThreads, 2) void indexer_prefill_kernel(const Kv
 #pragma unroll
         for (int q = 0; q < kPfRowsPerWave; ++q) {
             if (cstart >= vis[q]) continue;  // uniform
-            const int o = lane * 4;
+            const int o = min(lane * 4, kPfChunk - 4);
             const v2i v = lds_read_b64(lds_addr(&s_keys[wave][q][o]));
-            if (cstart + o + 4 <= p.key_stride) {
+            if (lane * 4 < kPfChunk && cstart + o + 4 <= p.key_stride) {
                 *reinterpret_cast<v2i*>(p.score_keys + static_cast<size_t>(rowi[q]) * p.key_stride + cstart + o) = v;
             }
             ++stores;
@@ -293,14 +315,14 @@ __global__ __launch_bounds__(kPfThreads, 2) void indexer_prefill_kernel(const Kv
     report(p.status, err);
 }
 
-template <int HEADS>
+template <int ELEM, int HEADS>
 hipError_t launch_heads(const KvipPrefillArgs& a, hipStream_t stream) {
     const int blocks = a.rows / kPfBlockRows + a.sequences;  // bound on the per-sequence blocks
     const dim3 grid(blocks, (a.max_blocks * kBlockTokens + kPfSegment - 1) / kPfSegment);
     if (a.weight_dtype == KVIP_DTYPE_BF16) {
-        hipLaunchKernelGGL((indexer_prefill_kernel<HEADS, true>), grid, dim3(kPfThreads), 0, stream, a);
+        hipLaunchKernelGGL((indexer_prefill_kernel<ELEM, HEADS, true>), grid, dim3(kPfThreads), 0, stream, a);
     } else {
-        hipLaunchKernelGGL((indexer_prefill_kernel<HEADS, false>), grid, dim3(kPfThreads), 0, stream, a);
+        hipLaunchKernelGGL((indexer_prefill_kernel<ELEM, HEADS, false>), grid, dim3(kPfThreads), 0, stream, a);
     }
     return hipGetLastError();
 }
@@ -314,14 +336,16 @@ uint32_t validate_prefill(const KvipPrefillArgs* a) {
     const bool ok =
         a->query != nullptr && a->weights != nullptr && a->keys != nullptr && a->block_table != nullptr &&
         a->cu_seqlens_q != nullptr && a->seq_lens_k != nullptr && a->score_keys != nullptr &&
-        a->histogram != nullptr && a->row_valid != nullptr && a->qk_dtype == KVIP_DTYPE_FP8_E4M3 &&
+        a->histogram != nullptr && a->row_valid != nullptr &&
+        (a->qk_dtype == KVIP_DTYPE_FP8_E4M3 || a->qk_dtype == KVIP_DTYPE_BF16) &&
         (a->weight_dtype == KVIP_DTYPE_FP32 || a->weight_dtype == KVIP_DTYPE_BF16) &&
         (a->heads == 32 || a->heads == 64) && a->sequences >= 1 && a->sequences <= kPfMaxSeq && a->rows >= 1 &&
         a->rows <= (1 << 24) && a->max_blocks >= 1 && a->num_blocks >= 1 &&
         a->max_blocks <= (1 << 24) / kBlockTokens &&
         static_cast<int64_t>(a->key_stride) >= static_cast<int64_t>(a->max_blocks) * kBlockTokens &&
         a->key_stride % 8 == 0 && a->key_block_stride % 16 == 0 &&
-        a->key_block_stride >= static_cast<int64_t>(kBlockTokens) * kIndexDim &&
+        a->key_block_stride >=
+            static_cast<int64_t>(kBlockTokens) * kIndexDim * (a->qk_dtype == KVIP_DTYPE_BF16 ? 2 : 1) &&
         (a->key_scale == nullptr || (a->scale_block_stride >= kBlockTokens && a->scale_block_stride % 4 == 0 &&
                                      (reinterpret_cast<uintptr_t>(a->key_scale) & 15u) == 0)) &&
         aligned16(a->query) && aligned16(a->keys) && aligned16(a->score_keys) &&
@@ -330,7 +354,10 @@ uint32_t validate_prefill(const KvipPrefillArgs* a) {
 }
 
 hipError_t launch_prefill(const KvipPrefillArgs& a, hipStream_t stream) {
-    return a.heads == 64 ? launch_heads<64>(a, stream) : launch_heads<32>(a, stream);
+    if (a.qk_dtype == KVIP_DTYPE_BF16) {
+        return a.heads == 64 ? launch_heads<2, 64>(a, stream) : launch_heads<2, 32>(a, stream);
+    }
+    return a.heads == 64 ? launch_heads<1, 64>(a, stream) : launch_heads<1, 32>(a, stream);
 }
 
 }  // namespace kvip

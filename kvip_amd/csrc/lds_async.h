@@ -41,6 +41,26 @@ KVIP_DEVICE void lds_read_tile(uint32_t a0, uint32_t a1, uint32_t a2, uint32_t a
         : "v"(a0), "v"(a1), "v"(a2), "v"(a3), "v"(as));
 }
 
+// The eight 16-byte K fragment pieces of a bf16 tile row (addresses a[u] + off) and its key
+// scale, then wait for them.
+KVIP_DEVICE void lds_read_tile8(const uint32_t (&a)[8], uint32_t off, uint32_t as, v4i (&kb)[8], float& ks) {
+    asm volatile(
+        "ds_read_b128 %0, %9\n"
+        "ds_read_b128 %1, %10\n"
+        "ds_read_b128 %2, %11\n"
+        "ds_read_b128 %3, %12\n"
+        "ds_read_b128 %4, %13\n"
+        "ds_read_b128 %5, %14\n"
+        "ds_read_b128 %6, %15\n"
+        "ds_read_b128 %7, %16\n"
+        "ds_read_b32 %8, %17\n"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(kb[0]), "=&v"(kb[1]), "=&v"(kb[2]), "=&v"(kb[3]), "=&v"(kb[4]), "=&v"(kb[5]), "=&v"(kb[6]),
+          "=&v"(kb[7]), "=&v"(ks)
+        : "v"(a[0] + off), "v"(a[1] + off), "v"(a[2] + off), "v"(a[3] + off), "v"(a[4] + off), "v"(a[5] + off),
+          "v"(a[6] + off), "v"(a[7] + off), "v"(as));
+}
+
 KVIP_DEVICE v2i lds_read_b64(uint32_t a) {
     v2i v;
     asm volatile("ds_read_b64 %0, %1\ns_waitcnt lgkmcnt(0)" : "=&v"(v) : "v"(a));

@@ -6,7 +6,8 @@ through the native quantised lightning indexer (python/kvip/adapters/vllm/select
 126-154, torch_npu.npu_quant_lightning_indexer with layout TND and sparse_mode 3, as
 called in tests/operators/lifetch/support/execution.py:126-145). This module is that
 surface on MI355X: packed query rows of several sequences (cumulative query lengths)
-against their paged index-K, right-down causal, fp8 Q/K, per-row TopK-2048 of positions
+against their paged index-K, right-down causal, fp8 e4m3 or bf16 Q/K (the bf16 form is the
+unquantised lightning indexer of the same selector path), per-row TopK-2048 of positions
 within each sequence (-1 padded), tie-broken to the lower position as in decode.
 
 `PrefillIndexer` allocates its buffers once (rows and context bounds fixed at
@@ -49,8 +50,9 @@ class PrefillIndexer:
         self.library = abi.load_library()
 
     def __call__(self, query, weights, query_scale, key, key_scale, cu_seqlens_q, seq_lens_k, block_table):
-        """query [rows, heads, 128] fp8; weights [rows, heads]; query_scale [rows, heads]
-        float32 or None; key [blocks, 128, 128] fp8 (contiguous blocks); key_scale
+        """query [rows, heads, 128] fp8 e4m3 or bf16; weights [rows, heads]; query_scale
+        [rows, heads] float32 or None; key [blocks, 128, 128] of the query's dtype
+        (contiguous blocks); key_scale
         [blocks, 128] float32 or None; cu_seqlens_q [sequences + 1] int32 (device);
         seq_lens_k [sequences] int32; block_table [sequences, max_blocks] int32. Returns the
         TopK view [rows, 2048] int32 (positions within each row's sequence)."""
@@ -65,14 +67,16 @@ class PrefillIndexer:
         rows, sequences = int(query.shape[0]), int(seq_lens_k.shape[0])
         if not 1 <= rows <= self.max_rows or not 1 <= sequences <= self.max_sequences:
             raise ValueError("rows / sequences exceed the bound sizes")
-        if query.dtype != t.float8_e4m3fn or tuple(query.shape[1:]) != (self.heads, INDEX_DIM):
-            raise ValueError(f"query must be float8_e4m3fn [rows, {self.heads}, 128]")
+        if query.dtype not in (t.float8_e4m3fn, t.bfloat16) or tuple(query.shape[1:]) != (self.heads, INDEX_DIM):
+            raise ValueError(f"query must be float8_e4m3fn or bfloat16 [rows, {self.heads}, 128]")
+        if not query.is_contiguous():
+            raise ValueError("query must be contiguous")
         if weights.dtype != self.weight_dtype or tuple(weights.shape) != (rows, self.heads):
             raise ValueError("weights must match the bound dtype and [rows, heads]")
         if query_scale is not None and (query_scale.dtype != t.float32 or tuple(query_scale.shape) != (rows, self.heads)):
             raise ValueError("query_scale must be float32 [rows, heads]")
-        if key.dtype != t.float8_e4m3fn or key.dim() != 3 or tuple(key.shape[1:]) != (BLOCK_TOKENS, INDEX_DIM):
-            raise ValueError("key must be float8_e4m3fn [blocks, 128, 128]")
+        if key.dtype != query.dtype or key.dim() != 3 or tuple(key.shape[1:]) != (BLOCK_TOKENS, INDEX_DIM):
+            raise ValueError(f"key must be {query.dtype} [blocks, 128, 128] (the query's dtype)")
         if key.stride(2) != 1 or key.stride(1) != INDEX_DIM:
             raise ValueError("index-K blocks must be contiguous")
         if key_scale is not None and (key_scale.dtype != t.float32 or key_scale.dim() != 2 or
@@ -92,10 +96,11 @@ class PrefillIndexer:
             query=p(query), weights=p(weights), query_scale=p(query_scale), keys=p(key), key_scale=p(key_scale),
             block_table=p(block_table), cu_seqlens_q=p(cu_seqlens_q), seq_lens_k=p(seq_lens_k),
             score_keys=p(self.score_keys), histogram=p(self.histogram), row_valid=p(self.row_valid),
-            status=p(self.status), key_block_stride=key.stride(0), scale_block_stride=0 if key_scale is None
+            status=p(self.status), key_block_stride=key.stride(0) * key.element_size(), scale_block_stride=0 if key_scale is None
             else key_scale.stride(0), sequences=sequences, rows=rows, heads=self.heads,
             max_blocks=int(block_table.shape[1]), num_blocks=int(key.shape[0]), key_stride=self.key_stride,
-            qk_dtype=abi.DTYPE_FP8_E4M3, weight_dtype=self.weight_code)
+            qk_dtype=abi.DTYPE_FP8_E4M3 if query.dtype == t.float8_e4m3fn else abi.DTYPE_BF16,
+            weight_dtype=self.weight_code)
         topk = abi.TopkArgs(score_keys=p(self.score_keys), histogram=p(self.histogram), segments=0,
                             seq_lens=p(self.row_valid), query_ends=0, topk=p(self.topk), status=p(self.status),
                             batch=rows, rows_per_request=1, key_stride=self.key_stride)

@@ -109,9 +109,10 @@ def config_workload(torch, name, device, seed=2026):
     raise ValueError(f"unknown decode configuration {name!r}")
 
 
-def prefill_workload(torch, device, *, seed=2026, q_len=4096, k_len=65536, heads=64):
+def prefill_workload(torch, device, *, seed=2026, q_len=4096, k_len=65536, heads=64, qk="fp8"):
     """Config-3 prefill chunk on the device: dict of the PrefillIndexer inputs plus the
-    slot_mapping [q_len] int64 and target positions [q_len] int64 of the new rows."""
+    slot_mapping [q_len] int64 and target positions [q_len] int64 of the new rows. qk:
+    "fp8" (e4m3 Q/K with per-row query and per-token key scales) or "bf16" (no scales)."""
     rng = np.random.default_rng(seed)
     gen = torch.Generator(device=device)
     gen.manual_seed(seed)
@@ -122,11 +123,16 @@ def prefill_workload(torch, device, *, seed=2026, q_len=4096, k_len=65536, heads
     def normal(shape):
         return torch.randn(shape, generator=gen, device=dev, dtype=torch.float32)
 
-    keys = saturating_fp8(torch, normal((blocks, BLOCK_TOKENS, INDEX_DIM)))
-    query = saturating_fp8(torch, normal((q_len, heads, INDEX_DIM)))
+    if qk not in ("fp8", "bf16"):
+        raise ValueError(f"qk must be fp8 or bf16 (got {qk})")
+    cast = (lambda x: saturating_fp8(torch, x)) if qk == "fp8" else (lambda x: x.to(torch.bfloat16))
+    keys = cast(normal((blocks, BLOCK_TOKENS, INDEX_DIM)))
+    query = cast(normal((q_len, heads, INDEX_DIM)))
     weights = normal((q_len, heads)) / 8
     query_scale = torch.rand((q_len, heads), generator=gen, device=dev, dtype=torch.float32) + 0.5
     key_scale = torch.rand((blocks, BLOCK_TOKENS), generator=gen, device=dev, dtype=torch.float32) * 1.5 + 0.5
+    if qk == "bf16":
+        query_scale = key_scale = None
     positions = np.arange(k_len - q_len, k_len, dtype=np.int64)
     slots = table[0, positions // BLOCK_TOKENS].astype(np.int64) * BLOCK_TOKENS + positions % BLOCK_TOKENS
     return dict(query=query, weights=weights, query_scale=query_scale, keys=keys, key_scale=key_scale,

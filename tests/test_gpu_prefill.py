@@ -1,8 +1,8 @@
 """GPU parity of the prefill lightning indexer (kvip_hip_indexer_prefill + TopK) against
 the CPU oracle, through the C ABI.
 
-Bars: scores within 3e-2 relative (fp8, with an absolute floor of 3e-2 of the row's
-largest |score|) and at least 99 % of the keys with |score| >= 3e-2 of the row's largest
+Bars: scores within 3e-2 relative for fp8 and 1e-2 for bf16 Q/K (each with an absolute
+floor of that fraction of the row's largest |score|) and at least 99 % of the keys with |score| >= 3e-2 of the row's largest
 bit-identical (fp8 MFMA dot products are not correctly rounded, so scores that cancel to
 near zero differ in their last bits more often; measured 0.3 % there); visible lengths and the
 high-byte histogram exact; TopK bit-exact against the oracle's TopK of the GPU's own
@@ -21,14 +21,19 @@ def say(*args):
     print(*args, flush=True)
 
 
-def make_case(torch, *, q_lens, k_lens, heads, wdt, qscale, kscale, seed):
+def make_case(torch, *, q_lens, k_lens, heads, wdt, qscale, kscale, seed, qk="fp8"):
     g = torch.Generator(device="cuda").manual_seed(seed)
     rows = int(sum(q_lens))
     max_blocks = max((k + 127) // 128 for k in k_lens)
     blocks = sum((k + 127) // 128 for k in k_lens) + 3
-    keys = synthetic.saturating_fp8(torch, torch.randn((blocks, 128, 128), generator=g, device="cuda"))
+
+    def operand(shape):
+        x = torch.randn(shape, generator=g, device="cuda")
+        return synthetic.saturating_fp8(torch, x) if qk == "fp8" else x.to(torch.bfloat16)
+
+    keys = operand((blocks, 128, 128))
     key_scale = (torch.rand((blocks, 128), generator=g, device="cuda") * 1.5 + 0.5) if kscale else None
-    query = synthetic.saturating_fp8(torch, torch.randn((rows, heads, 128), generator=g, device="cuda"))
+    query = operand((rows, heads, 128))
     weights = (torch.randn((rows, heads), generator=g, device="cuda") / 8).to(wdt)
     query_scale = (torch.rand((rows, heads), generator=g, device="cuda") + 0.5) if qscale else None
     perm = torch.randperm(blocks, generator=torch.Generator().manual_seed(seed)).int()
@@ -53,20 +58,26 @@ def host(torch, t):
 
 
 CASES = [
-    # name, q_lens, k_lens, heads, weight dtype, qscale, kscale
-    ("h64_two_seqs", [37, 100], [3000, 5000], 64, "f32", True, True),
-    ("h32_bf16w_short_ctx", [20, 5, 64], [300, 2, 4096], 32, "bf16", False, True),
-    ("h64_more_rows_than_keys", [300], [260], 64, "f32", False, False),
-    ("h64_long_rows", [64], [9000], 64, "f32", True, True),
+    # name, q_lens, k_lens, heads, weight dtype, qscale, kscale, Q/K dtype
+    ("h64_two_seqs", [37, 100], [3000, 5000], 64, "f32", True, True, "fp8"),
+    ("h32_bf16w_short_ctx", [20, 5, 64], [300, 2, 4096], 32, "bf16", False, True, "fp8"),
+    ("h64_more_rows_than_keys", [300], [260], 64, "f32", False, False, "fp8"),
+    ("h64_long_rows", [64], [9000], 64, "f32", True, True, "fp8"),
+    ("bf16qk_h64_two_seqs", [37, 100], [3000, 5000], 64, "f32", False, False, "bf16"),
+    ("bf16qk_h32_scaled_short_ctx", [20, 5, 64], [300, 2, 4096], 32, "bf16", True, True, "bf16"),
+    ("bf16qk_h64_long_rows", [64], [9000], 64, "f32", False, True, "bf16"),
+    ("bf16qk_h64_more_rows_than_keys", [300], [260], 64, "bf16", True, False, "bf16"),
 ]
 
 
-@pytest.mark.parametrize("name,q_lens,k_lens,heads,wdt,qscale,kscale", CASES, ids=[c[0] for c in CASES])
-def test_prefill_matches_oracle(torch_gpu, name, q_lens, k_lens, heads, wdt, qscale, kscale):
+@pytest.mark.parametrize("name,q_lens,k_lens,heads,wdt,qscale,kscale,qk", CASES, ids=[c[0] for c in CASES])
+def test_prefill_matches_oracle(torch_gpu, name, q_lens, k_lens, heads, wdt, qscale, kscale, qk):
     torch = torch_gpu
     say(f"case prefill {name}")
     c = make_case(torch, q_lens=q_lens, k_lens=k_lens, heads=heads,
-                  wdt=torch.float32 if wdt == "f32" else torch.bfloat16, qscale=qscale, kscale=kscale, seed=17)
+                  wdt=torch.float32 if wdt == "f32" else torch.bfloat16, qscale=qscale, kscale=kscale, seed=17,
+                  qk=qk)
+    tol = 3e-2 if qk == "fp8" else 1e-2
     idx = kvip_amd.PrefillIndexer(torch, max_rows=c["rows"] + 5, max_context=c["max_ctx"],
                                   max_sequences=len(q_lens), device="cuda", heads=heads,
                                   weight_dtype=c["weights"].dtype)
@@ -84,7 +95,7 @@ def test_prefill_matches_oracle(torch_gpu, name, q_lens, k_lens, heads, wdt, qsc
             continue
         gv = ref.score_values(got[r, :v]).astype(np.float64)
         wv = ref.score_values(want[r, :v]).astype(np.float64)
-        bad = np.abs(gv - wv) > 3e-2 * np.abs(wv) + 3e-2 * np.abs(wv).max()
+        bad = np.abs(gv - wv) > tol * np.abs(wv) + tol * np.abs(wv).max()
         assert not bad.any(), (r, int(bad.sum()))
     same = ref.identical_share(got, want, vis)
     say(f"  identical keys (|score| >= 3e-2 of row max): {same:.5f}")
