@@ -12,9 +12,9 @@
 // Slot LRU (reference: python/kvip/cache/lru.py:14-118, _lru_kernel.py:33-199). The
 // doubly linked list of the reference is held as its order array: order[i] is the slot at
 // LRU position i (0 = oldest). commit moves the unique committed slots (< active) to the
-// end in ascending slot-id order: a stable partition of the order, done by one workgroup
-// with LDS membership bits and block scans. The victims are order[0 .. min(2048, active)),
-// with their bitmap.
+// end in ascending slot-id order: a stable partition of the order, done in place by one
+// workgroup with LDS membership bits and block scans. The victims are
+// order[0 .. min(2048, active)), with their bitmap.
 #include "kvip_device.h"
 
 namespace kvip {
@@ -94,18 +94,43 @@ __global__ __launch_bounds__(kLruThreads) void lru_extend_kernel(const KvipLruAr
 }
 
 // One workgroup per chain (blockIdx.x): stable partition of order[0, active) into (not
-// committed, committed in ascending slot order) through `scratch`, then the victims of
-// the new order. Chain c commits dest[c * dest_stride, + count).
+// committed, committed in ascending slot order), in place, then the victims of the new
+// order. Chain c commits dest[c * dest_stride, + count). The order moves through LDS in
+// tiles of 16384 entries: a coalesced copy in, a block scan over each thread's 16
+// consecutive entries, the kept entries compacted in LDS, a coalesced copy out (LDS index
+// i sits at i + i/16, so a thread's 16 consecutive entries and 64 consecutive indices
+// both spread over the banks). A kept
+// entry only moves to a lower position and a tile is written after it was read, so the
+// partition overwrites nothing still unread; the committed slots follow the last tile the
+// same way, 16384 at a time. Victims (the first min(2048, active) positions) and their
+// bitmap are taken from the values as they are written.
+constexpr int kLruPer = 16;                       // entries per thread and tile
+constexpr int kLruTile = kLruThreads * kLruPer;   // 16384
+KVIP_DEVICE uint32_t lru_lds(uint32_t i) { return i + (i >> 4); }
 __global__ __launch_bounds__(kLruThreads) void lru_commit_kernel(const KvipLruArgs args, const int32_t* dest,
                                                                  int64_t dest_stride, int count, int active,
                                                                  int commit) {
     __shared__ uint32_t s_member[kLruBitmapWords];
+    __shared__ uint32_t s_victim[kLruBitmapWords];
+    __shared__ int32_t s_tile[kLruTile + kLruTile / 16];
     __shared__ uint32_t s_wave[kLruThreads / 64];
     const KvipLruArgs p = chain_of(args, blockIdx.x);
     if (commit) dest += static_cast<size_t>(blockIdx.x) * dest_stride;
     const int tid = threadIdx.x;
     const int words = (active + 31) / 32;
-    for (int i = tid; i < words; i += kLruThreads) s_member[i] = 0u;
+    const int victims = min(kTopK, active);
+
+    // The first tile's entries (coalesced), in flight together with the committed slots.
+    int first[kLruPer];
+#pragma unroll
+    for (int m = 0; m < kLruPer; ++m) {
+        const int k = m * kLruThreads + tid;
+        first[m] = k < active ? p.order[k] : -1;
+    }
+    for (int i = tid; i < p.bitmap_words; i += kLruThreads) {
+        s_member[i] = 0u;
+        s_victim[i] = 0u;
+    }
     __syncthreads();
     if (commit) {
         for (int i = tid; i < count; i += kLruThreads) {
@@ -113,57 +138,71 @@ __global__ __launch_bounds__(kLruThreads) void lru_commit_kernel(const KvipLruAr
             if (s >= 0 && s < active) atomicOr(&s_member[s >> 5], 1u << (s & 31));
         }
     }
-    __syncthreads();
 
-    // Kept slots, in order, then committed slots in ascending id order.
+    // Writes s_tile[0, n) to order[base, base + n) and records the victims among them.
+    auto flush = [&](uint32_t base, int n) {
+        for (int k = tid; k < n; k += kLruThreads) {
+            const int slot = s_tile[lru_lds(k)];
+            const uint32_t pos = base + k;
+            p.order[pos] = slot;
+            if (pos < static_cast<uint32_t>(victims)) {
+                p.slots[pos] = slot;
+                atomicOr(&s_victim[slot >> 5], 1u << (slot & 31));
+            }
+        }
+    };
+
+    // Kept slots, in order.
     uint32_t kept_base = 0;
-    for (int tile = 0; tile < active; tile += kLruThreads * 8) {
-        int v[8];
+    for (int tile = 0; tile < active; tile += kLruTile) {
+        const int n = min(active - tile, kLruTile);
+        __syncthreads();  // membership bits complete; the previous tile's flush read s_tile
+        if (tile == 0) {
+#pragma unroll
+            for (int m = 0; m < kLruPer; ++m) s_tile[lru_lds(m * kLruThreads + tid)] = first[m];
+        } else {
+            for (int k = tid; k < n; k += kLruThreads) s_tile[lru_lds(k)] = p.order[tile + k];
+        }
+        __syncthreads();
+        int v[kLruPer];
         uint32_t keep = 0;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int i = tile + tid * 8 + j;
-            v[j] = i < active ? p.order[i] : -1;
+        for (int j = 0; j < kLruPer; ++j) {
+            const int i = tid * kLruPer + j;
+            v[j] = i < n ? s_tile[lru_lds(i)] : -1;
             const bool k = v[j] >= 0 && !((s_member[v[j] >> 5] >> (v[j] & 31)) & 1u);
             keep |= (k ? 1u : 0u) << j;
         }
         uint32_t tile_total;
-        uint32_t pos = kept_base + block_exclusive_scan(__popc(keep), s_wave, &tile_total);
+        uint32_t pos = block_exclusive_scan(__popc(keep), s_wave, &tile_total);  // barriers: s_tile read
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            if ((keep >> j) & 1u) p.scratch[pos++] = v[j];
+        for (int j = 0; j < kLruPer; ++j) {
+            if ((keep >> j) & 1u) s_tile[lru_lds(pos++)] = v[j];
         }
+        __syncthreads();
+        flush(kept_base, static_cast<int>(tile_total));
         kept_base += tile_total;
     }
+    // Committed slots in ascending id order, 512 membership words (<= 16384 slots) at a time.
     uint32_t moved_base = kept_base;
-    for (int w0 = 0; w0 < words; w0 += kLruThreads) {
+    for (int w0 = 0; w0 < words; w0 += kLruTile / 32) {
         const int w = w0 + tid;
-        const uint32_t bits = w < words ? s_member[w] : 0u;
-        uint32_t tile_total;
-        uint32_t pos = moved_base + block_exclusive_scan(__popc(bits), s_wave, &tile_total);
+        const uint32_t bits = (tid < kLruTile / 32 && w < words) ? s_member[w] : 0u;
+        uint32_t total;
+        uint32_t pos = block_exclusive_scan(__popc(bits), s_wave, &total);  // barriers: last flush done
         uint32_t rest = bits;
         while (rest) {
             const int b = __ffs(rest) - 1;
-            p.scratch[pos++] = w * 32 + b;
+            s_tile[lru_lds(pos++)] = w * 32 + b;
             rest &= rest - 1;
         }
-        moved_base += tile_total;
+        __syncthreads();
+        flush(moved_base, static_cast<int>(total));
+        moved_base += total;
     }
-    __syncthreads();  // scratch complete (workgroup fence + barrier)
-    for (int i = tid; i < active; i += kLruThreads) p.order[i] = p.scratch[i];
-
-    // Victims: the oldest min(2048, active) slots and their bitmap.
-    const int victims = min(kTopK, active);
-    for (int i = tid; i < kTopK; i += kLruThreads) p.slots[i] = i < victims ? p.scratch[i] : -1;
+    for (int i = victims + tid; i < kTopK; i += kLruThreads) p.slots[i] = -1;
     __syncthreads();
-    for (int i = tid; i < p.bitmap_words; i += kLruThreads) s_member[i] = 0u;
-    __syncthreads();
-    for (int i = tid; i < victims; i += kLruThreads) {
-        const int s = p.scratch[i];
-        atomicOr(&s_member[s >> 5], 1u << (s & 31));
-    }
-    __syncthreads();
-    for (int i = tid; i < p.bitmap_words; i += kLruThreads) p.bitmap[i] = static_cast<int32_t>(s_member[i]);
+    for (int i = tid; i < p.bitmap_words; i += kLruThreads) p.bitmap[i] = static_cast<int32_t>(s_victim[i]);
 }
 
 }  // namespace
