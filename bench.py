@@ -26,6 +26,7 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
 FP8_MFMA_PEAK_TFLOPS = 5000.0
+BF16_MFMA_PEAK_TFLOPS = 2500.0
 TOPK = 2048
 
 
@@ -80,47 +81,53 @@ def measured_traffic(kernel):
 
 
 def cpu_baseline(torch, wl, rot, budget_s):
-    """The oracle (oracle/indexer.py) on the first rows of the same workload until the
-    time budget is spent: LI keys, TopK-2048, Fetch gather, per query row."""
-    from oracle import indexer as ref
+    """The torch-CPU restatement (oracle/cpu_torch.py) of one decode query row, timed on the
+    host over the rows of the same workload until the time budget is spent: decode the fp8
+    Q/K bytes to float32, LI keys (two threaded BLAS products), TopK-2048, Fetch gather.
+    Threads: os.cpu_count() as planned, capped by this process's CPU affinity and by
+    OMP_NUM_THREADS when set (the CPU share a job gets on a shared host)."""
+    from oracle import cpu_torch
 
+    logical = os.cpu_count() or 1
+    threads = min(logical, len(os.sched_getaffinity(0)))
+    if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+        threads = min(threads, max(int(os.environ["OMP_NUM_THREADS"]), 1))
     try:
-        from threadpoolctl import threadpool_info
+        import psutil
 
-        blas_threads = max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
+        physical = psutil.cpu_count(logical=False)
     except Exception:  # noqa: BLE001 - informational only
-        blas_threads = 1
-    q = ref.fp8_e4m3_decode(wl.query.view(torch.uint8).cpu().numpy()) if wl.query.element_size() == 1 \
-        else wl.query.float().cpu().numpy()
-    w = wl.weights.float().cpu().numpy()
-    table = wl.block_table.cpu().numpy()
-    ks_all = None if wl.key_scale is None else wl.key_scale.cpu().numpy()
-    kv = wl.kv_cache.cpu().numpy()
-    keys_dev = wl.keys
-    done, elapsed = 0, 0.0
-    for step in range(10 ** 6):
-        r = step % rot.rows
-        b = r // wl.rows_per_request
-        v = int(wl.ctx[b])
-        pages = table[b, :(v + 127) // 128]
-        kraw = keys_dev[torch.from_numpy(pages.astype(np.int64)).to(keys_dev.device)]
-        kvals = ref.fp8_e4m3_decode(kraw.view(torch.uint8).cpu().numpy()) if kraw.element_size() == 1 \
-            else kraw.float().cpu().numpy()
-        kvals = kvals.reshape(-1, 128)[:v]
-        ks = None if ks_all is None else ks_all[pages].reshape(-1)[:v]
-        t0 = time.perf_counter()
-        keys = ref.li_keys(q[r], kvals, w[r], None, ks)
-        sel = ref.topk_reference(keys, v)
-        ref.fetch_gather(kv, table[b:b + 1], sel[None, :])
-        elapsed += time.perf_counter() - t0
-        done += 1
-        if elapsed >= budget_s:
-            break
-    return {"value": round(done / elapsed, 3), "unit": "queries/s", "cores": int(blas_threads),
-            "kind": "port",
-            "sample": f"{done} query rows (cycling over the {rot.rows} rows) of the same workload (numpy oracle: float64 dot "
-                      f"products on {blas_threads} BLAS threads, single-threaded head reduction, TopK, gather); "
-                      f"{elapsed:.1f} s; host has {os.cpu_count()} logical CPUs"}
+        physical = None
+    saved = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        table = wl.block_table.cpu()
+        kv_rows = wl.kv_cache.cpu().reshape(-1, int(wl.kv_cache.shape[2]))
+        staged = []  # per request: fp8 Q/K bytes and scales on the host (staging, untimed)
+        for b in range(wl.batch):
+            v = int(wl.ctx[b])
+            pages = table[b, :(v + 127) // 128]
+            k_raw = wl.keys[pages.to(wl.keys.device).long()].view(torch.uint8).reshape(-1, 128)[:v].cpu()
+            ks = None if wl.key_scale is None else wl.key_scale[pages.to(wl.keys.device).long()].reshape(-1)[:v].cpu()
+            qs = None if wl.query_scale is None else wl.query_scale[b].float().cpu()
+            staged.append((wl.query[b].view(torch.uint8).cpu(), k_raw, wl.weights[b].float().cpu(), qs, ks, pages, v))
+        cpu_torch.decode_row(torch, *staged[0][:5], kv_rows, staged[0][5], staged[0][6])  # warm-up
+        done, elapsed, nbytes = 0, 0.0, 0
+        while elapsed < budget_s:
+            q, k, w, qs, ks, pages, v = staged[done % len(staged)]
+            t0 = time.perf_counter()
+            cpu_torch.decode_row(torch, q, k, w, qs, ks, kv_rows, pages, v)
+            elapsed += time.perf_counter() - t0
+            nbytes += v * (128 + (4 if ks is not None else 0)) + 4 * ((v + 127) // 128) + 2 * TOPK * kv_rows.shape[1]
+            done += 1
+    finally:
+        torch.set_num_threads(saved)
+    return {"value": round(done / elapsed, 3), "unit": "queries/s", "cores": threads, "kind": "port",
+            "physical_cores": physical, "logical_cpus": logical, "gbs": round(nbytes / elapsed / 1e9, 2),
+            "sample": f"{done} query rows cycling over the {len(staged)} requests of the same workload, "
+                      f"{elapsed:.1f} s: torch-CPU restatement (fp8 decode, float32 BLAS dot products and head "
+                      f"reduction, bf16 keys, TopK-2048, 656-byte row gather) on {threads} torch threads; host "
+                      f"has {physical} physical cores, {logical} logical CPUs"}
 
 
 def lidu_leg(torch, kvip_amd, device, seed, iters=50):
@@ -166,12 +173,138 @@ def lidu_leg(torch, kvip_amd, device, seed, iters=50):
             "unique_misses_per_request": round(float(counts[:-1].mean()), 1), "calls": iters}
 
 
-def resident_leg(torch, kvip_amd, device, seed, steps=8):
-    """Device time of the resident-cache round (init, resolve, Fetch of the misses from
-    pinned host memory, Index update) at the BASELINE config-4 shape: 16 requests, history
-    131072, 16384 hot slots, TopK rows drawn with ~80 % hot positions under Zipf(1.1)
-    popularity, the device SlotLRU supplying each step's candidates. Also times one full
-    resident forward (LI over the 16 x 131072 Index rows, TopK, round)."""
+def _query_sets(torch, base, sets, seed, step=0.3):
+    """`sets` fp8 query tensors shaped like `base` along a random walk (set 0 is the base,
+    set k = sqrt(1 - step^2) * set k-1 + step * N(0, 1)): consecutive rounds select
+    overlapping but drifting positions, as consecutive decode steps do."""
+    from kvip_amd import synthetic
+
+    gen = torch.Generator(device=base.device)
+    gen.manual_seed(seed)
+    vals = base.float()
+    out = [base.clone()]
+    for _ in range(sets - 1):
+        vals = (1.0 - step * step) ** 0.5 * vals + step * torch.randn(vals.shape, generator=gen, device=base.device)
+        out.append(synthetic.saturating_fp8(torch, vals))
+    return out
+
+
+def _graph_rounds(torch, bodies, rounds, warm=4, probe=None):
+    """Captures each body as a hipGraph (after one eager call on a side stream), replays
+    them in rotation `warm` times, then times `rounds` back-to-back replays with HIP events
+    on the launch stream. With `probe`, a second pass of `rounds` replays calls it after
+    each replay (host-synchronised, untimed) and returns its values."""
+    stream = torch.cuda.current_stream()
+    side = torch.cuda.Stream()
+    side.wait_stream(stream)
+    with torch.cuda.stream(side):
+        for body in bodies:
+            body()
+    stream.wait_stream(side)
+    torch.cuda.synchronize()
+    graphs = []
+    for body in bodies:
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            body()
+        graphs.append(g)
+    for i in range(warm):
+        graphs[i % len(graphs)].replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(rounds):
+        graphs[i % len(graphs)].replay()
+    e1.record(stream)
+    e1.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / rounds
+    probes = []
+    if probe is not None:
+        for i in range(rounds):
+            graphs[i % len(graphs)].replay()
+            torch.cuda.synchronize()
+            probes.append(probe())
+    return us, probes
+
+
+def host_read_gbs(torch, device, nbytes=256 << 20):
+    """Host-to-device bandwidth from pinned memory (one large copy): the ceiling of a Fetch
+    whose rows live in a pinned host pool."""
+    src = torch.empty(nbytes, dtype=torch.uint8, pin_memory=True)
+    dst = torch.empty(nbytes, dtype=torch.uint8, device=device)
+    for _ in range(2):
+        dst.copy_(src, non_blocking=True)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(4):
+        dst.copy_(src, non_blocking=True)
+    e1.record()
+    e1.synchronize()
+    return 4 * nbytes / (e0.elapsed_time(e1) * 1e-3) / 1e9
+
+
+def cache_ops_leg(torch, kvip_amd, device, seed, iters=20):
+    """The per-step cache bookkeeping kernels alone, each captured 10 times in a hipGraph
+    and replayed `iters` times (HIP events around the replays):
+      update_abc:  one decode step of the ABC ring maps (python/kvip/cache/abc.py): 16
+                   requests x 4 new tokens into a 2048-slot tail after 16384 history slots,
+                   one layer;
+      lru_commit:  SlotLRUChains.commit for 32 chains of 16384 slots with 2048 accessed slots
+                   each (the C5 decode batch).
+    Bytes are the arrays each kernel must read and write once."""
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    out = {}
+    history, tail, req, new = 16384, 2048, 16, 4
+    t2s = torch.full((1, req, history + tail), -1, dtype=torch.int32, device=device)
+    s2t = torch.full((1, req, history + tail), -1, dtype=torch.int32, device=device)
+    begin = torch.randint(history, history + tail - new, (req,), generator=gen, device=device, dtype=torch.int32)
+    desc = torch.stack([torch.zeros_like(begin), torch.arange(req, dtype=torch.int32, device=device), begin,
+                        begin + new], dim=1)[None].contiguous()
+    chains, cap = 32, 16384
+    lru = kvip_amd.SlotLRUChains(torch, chains, cap, device)
+    dest = torch.argsort(torch.rand((chains, cap), generator=gen, device=device), dim=1)[:, :TOPK]
+    dest = dest.to(torch.int32).contiguous()
+    calls = {"update_abc": (lambda: kvip_amd.update_abc(t2s, s2t, desc, req, history, tail),
+                            req * (new * 4 * 2 + tail * 4 + 16)),
+             "lru_commit": (lambda: lru.commit(dest), chains * (cap * 4 * 3 + TOPK * 4 + TOPK * 4))}
+    stream = torch.cuda.current_stream()
+    for name, (call, nbytes) in calls.items():
+        call()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for _ in range(10):
+                call()
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(iters):
+            g.replay()
+        e1.record(stream)
+        e1.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / (iters * 10)
+        out[name] = {"us": round(us, 2), "bytes": nbytes, "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
+                     "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    out["workload"] = ("update_abc: 16 requests x 4 new tokens, tail 2048 after 16384 history slots; lru_commit: "
+                       "32 chains x 16384 slots, 2048 accessed per chain")
+    return out
+
+
+def resident_leg(torch, kvip_amd, device, seed, rounds=24, sets=24):
+    """BASELINE config 4 on the resident cache: 16 requests, history 131072, 16384 hot
+    slots, misses fetched from a pinned host pool, the device LRU chains (one per request)
+    committed by every round inside its hipGraph. Two loops of graph replays, each timed
+    back to back with HIP events:
+      round:   the resident round alone (init, resolve, Fetch of the misses, Index update,
+               LRU commit) on TopK rows drawn ~80 % hot under Zipf(1.1) popularity, a fresh
+               draw per round (`sets` graphs replayed in rotation);
+      forward: the whole resident forward (LI over 16 x 131072 Index rows, TopK-2048, the
+               round, LRU commit) on `sets` query sets along a random walk (consecutive
+               rounds select overlapping, drifting positions).
+    Misses per round come from a second, host-synchronised pass of the same replays."""
     import ctypes
     from kvip_amd import synthetic
     from kvip_amd.runtime import abi
@@ -180,47 +313,51 @@ def resident_leg(torch, kvip_amd, device, seed, steps=8):
     rot, upd, fwd = synthetic.resident_workload(torch, kvip_amd, device, seed=seed, batch=batch,
                                                 history=history, resident=resident)
     rng = np.random.default_rng(seed)
-    picks = synthetic.resident_selections(torch, rng, steps=steps + 2, batch=batch, q_rows=1, history=history,
-                                          resident=resident)
-    lrus = [kvip_amd.SlotLRU(device) for _ in range(batch)]
-    for p in lrus:
-        p.resize(resident, resident)
+    picks = torch.from_numpy(synthetic.resident_selections(torch, rng, steps=sets, batch=batch, q_rows=1,
+                                                           history=history, resident=resident)).to(device)
+    lru = kvip_amd.SlotLRUChains(torch, batch, resident, device, slots=upd.lru_slots)
     lib = abi.load_library()
-    stream = abi.stream_handle(torch, rot.device)
-    times, misses = [], []
-    for s in range(steps + 2):
-        rot.topk.copy_(torch.from_numpy(picks[s]))
-        upd.set_candidates(torch.cat([p.slots for p in lrus]))
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        abi.check(lib.kvip_hip_resident_round(ctypes.byref(upd.args), stream), "resident round")
-        e1.record()
-        e1.synchronize()
-        if upd.status.any():
-            raise RuntimeError(f"resident round failed: {upd.status.cpu().tolist()}")
-        slots = upd.slot_output.view(batch, -1)
-        for b, p in enumerate(lrus):
-            p.commit(slots[b][slots[b] >= 0].contiguous())
-        if s >= 2:
-            times.append(e0.elapsed_time(e1) * 1e3)
-            misses.append(int(upd.miss_counts[:, 4].sum().item()))
-    us = float(np.mean(times))
-    miss = float(np.mean(misses))
-    upd.set_candidates(torch.cat([p.slots for p in lrus]))
-    fwd()  # first launch of the forward's kernels (code-object loading) stays untimed
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    fwd()
-    e1.record()
-    e1.synchronize()
-    return {"workload": "c4 shape: 16 requests x 1 row, history 131072, resident 16384, TopK drawn ~80% hot "
-                        "(Zipf 1.1 popularity), misses fetched from pinned host memory",
-            "us_per_round": round(us, 2), "misses_per_round": round(miss, 1),
-            "hit_fraction": round(1.0 - miss / (batch * 2048), 4),
-            "host_fetch_gbs_lower_bound": round(miss * 656 / (us * 1e-6) / 1e9, 2),
-            "full_forward_us": round(e0.elapsed_time(e1) * 1e3, 2), "rounds": steps}
+    commit_rows = upd.slot_output.view(batch, -1)
+
+    def round_body(k):
+        def body():
+            rot.topk.copy_(picks[k])
+            abi.check(lib.kvip_hip_resident_round(ctypes.byref(upd.args), abi.stream_handle(torch, rot.device)),
+                      "resident round")
+            lru.commit(commit_rows)
+        return body
+
+    def misses():
+        return int(upd.miss_counts[:, 4].sum().item())
+
+    round_us, round_miss = _graph_rounds(torch, [round_body(k) for k in range(sets)], rounds, probe=misses)
+    if upd.status.any():
+        raise RuntimeError(f"resident round failed: {upd.status.cpu().tolist()}")
+    queries = _query_sets(torch, rot.query, sets, seed)
+
+    def forward_body(k):
+        def body():
+            rot.query.copy_(queries[k])
+            fwd()
+            lru.commit(commit_rows)
+        return body
+
+    fwd_us, fwd_miss = _graph_rounds(torch, [forward_body(k) for k in range(sets)], rounds, probe=misses)
+    if upd.status.any() or rot.status.any():
+        raise RuntimeError(f"resident forward failed: {upd.status.cpu().tolist()} {int(rot.status.item())}")
+    host_gbs = host_read_gbs(torch, device)
+    miss = float(np.mean(round_miss))
+    fmiss = float(np.mean(fwd_miss))
+    return {"workload": "c4 shape: 16 requests x 1 row, history 131072, resident 16384, misses fetched from pinned "
+                        "host memory, LRU chains committed in the graph; round: TopK rows drawn ~80% hot (Zipf 1.1), "
+                        f"{sets} draws; forward: LI + TopK + round on {sets} query sets along a random walk",
+            "us_per_round": round(round_us, 2), "misses_per_round": round(miss, 1),
+            "hit_fraction": round(1.0 - miss / (batch * TOPK), 4),
+            "fetch_gbs_lower_bound": round(miss * 656 / (round_us * 1e-6) / 1e9, 2),
+            "host_read_ceiling_gbs": round(host_gbs, 1),
+            "forward_us": round(fwd_us, 2), "forward_misses_per_round": round(fmiss, 1),
+            "forward_hit_fraction": round(1.0 - fmiss / (batch * TOPK), 4),
+            "forward_index_gbs": round(batch * history * 132 / (fwd_us * 1e-6) / 1e9, 1), "rounds": rounds}
 
 
 def prefill_leg(torch, kvip_amd, device, seed, iters=5):
@@ -276,6 +413,34 @@ def prefill_leg(torch, kvip_amd, device, seed, iters=5):
     topk_bytes = pairs * 2 + q_len * (256 * 4 * 2 + TOPK * 4)
     update_bytes = q_len * (2 * (128 + 4) + 2 * 8)
     total = sum(t.values())
+
+    # The same chunk with bf16 Q/K (no scales): scoring and TopK, priced against the dense
+    # bf16 MFMA peak.
+    wb = synthetic.prefill_workload(torch, device, seed=seed, qk="bf16")
+    bidx = kvip_amd.PrefillIndexer(torch, max_rows=q_len, max_context=k_len, max_sequences=1, device=device,
+                                   heads=heads)
+    bidx.bind(wb["query"], wb["weights"], None, wb["keys"], None, wb["cu_seqlens_q"], wb["seq_lens_k"],
+              wb["block_table"])
+    for _ in range(3):
+        bidx.score()
+        bidx.select()
+    torch.cuda.synchronize()
+    bev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(iters)]
+    for e in bev:
+        e[0].record(stream)
+        bidx.score()
+        e[1].record(stream)
+        bidx.select()
+        e[2].record(stream)
+    torch.cuda.synchronize()
+    if int(bidx.status.item()) != 0:
+        raise RuntimeError("prefill leg (bf16): device status set")
+    bt = {name: float(np.mean([e[i].elapsed_time(e[i + 1]) for e in bev])) * 1e3
+          for i, name in enumerate(["score", "topk"])}
+    btflops = flops / (bt["score"] * 1e-6) / 1e12
+    bf16 = {"us": {k: round(v, 1) for k, v in bt.items()},
+            "score_roofline": {"bound": "mfma", "achieved": round(btflops, 1), "peak": BF16_MFMA_PEAK_TFLOPS,
+                               "unit": "TFLOP/s", "frac": round(btflops / BF16_MFMA_PEAK_TFLOPS, 4), "flops": flops}}
     return {"workload": f"c3: 1 sequence, {q_len} query rows x {k_len} context tokens, right-down causal, "
                         f"fp8 Q/K, {heads} heads x 128, per-token scales; TopK-2048 per row; Index update of "
                         f"{q_len} rows",
@@ -285,7 +450,8 @@ def prefill_leg(torch, kvip_amd, device, seed, iters=5):
                                "unit": "TFLOP/s", "frac": round(tflops / FP8_MFMA_PEAK_TFLOPS, 4),
                                "flops": flops},
             "topk_gbs": round(topk_bytes / (t["topk"] * 1e-6) / 1e9, 1),
-            "index_update_gbs": round(update_bytes / (t["index_update"] * 1e-6) / 1e9, 1), "iters": iters}
+            "index_update_gbs": round(update_bytes / (t["index_update"] * 1e-6) / 1e9, 1), "iters": iters,
+            "bf16": bf16}
 
 
 def sfa_leg(torch, kvip_amd, device, seed, iters=20):
@@ -339,48 +505,43 @@ def sfa_leg(torch, kvip_amd, device, seed, iters=20):
     return out
 
 
-def mixed_leg(torch, kvip_amd, device, seed, iters=20):
-    """one continuous-batching round captured as a single hipGraph and
-    replayed back to back: Index ingest of all new tokens (32 decode + 2048 + 1536 prefill
-    rows), resident decode LIFetch for 32 requests (ctx ~U[4096, 65536], 16384 hot slots,
-    misses from pinned host memory) and prefill LI + TopK for the two chunks (k_len 8192
-    and 1536). Rounds replay on the evolving cache state, as consecutive serving rounds."""
+def mixed_leg(torch, kvip_amd, device, seed, rounds=20, sets=20):
+    """one continuous-batching round captured as a single hipGraph:
+    Index ingest of all new tokens (32 decode + 2048 + 1536 prefill rows), resident decode
+    LIFetch for 32 requests (ctx ~U[4096, 65536], 16384 hot slots, misses from pinned host
+    memory, the LRU chains committed inside the graph) and prefill LI + TopK for the two
+    chunks (k_len 8192 and 1536). `sets` graphs differ in the decode queries (a random walk,
+    so consecutive rounds select overlapping, drifting positions) and replay in rotation on
+    the evolving cache state, as consecutive serving rounds. Misses per round come from a
+    second, host-synchronised pass."""
     from kvip_amd import synthetic
 
-    wl = synthetic.mixed_workload(torch, kvip_amd, device, seed=seed)
+    wl = synthetic.mixed_workload(torch, kvip_amd, device, seed=seed, lru=True)
     rnd = wl.round
-    stream = torch.cuda.current_stream()
-    side = torch.cuda.Stream()
-    side.wait_stream(stream)
-    with torch.cuda.stream(side):
-        rnd()  # first launches (code-object loading) outside the capture
-    stream.wait_stream(side)
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        rnd()
-    for _ in range(3):
-        graph.replay()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for _ in range(iters):
-        graph.replay()
-    e1.record(stream)
-    e1.synchronize()
-    us = e0.elapsed_time(e1) * 1e3 / iters
+    queries = _query_sets(torch, wl.rot.query, sets, seed)
+
+    def body(k):
+        def run():
+            wl.rot.query.copy_(queries[k])
+            rnd()
+        return run
+
+    us, miss = _graph_rounds(torch, [body(k) for k in range(sets)], rounds,
+                             probe=lambda: int(wl.update.miss_counts[:, 4].sum().item()))
     for st in (wl.update.status, wl.rot.status, wl.prefill.status, rnd.status):
         if st.any():
             raise RuntimeError(f"mixed round: device status {st.cpu().tolist()}")
-    misses = int(wl.update.miss_counts[:, 4].sum().item())
     pf_rows = sum(q for q, _ in wl.chunks)
-    return {"workload": f"c5: {len(wl.decode_ctx)} decode requests (ctx U[4096,{wl.history}], mean "
+    nd = len(wl.decode_ctx)
+    return {"workload": f"c5: {nd} decode requests (ctx U[4096,{wl.history}], mean "
                         f"{wl.decode_ctx.mean():.0f}; resident {wl.resident} hot slots, misses from pinned host "
-                        f"memory) + prefill chunks {[list(c) for c in wl.chunks]} (q_len, k_len); Index ingest of "
+                        f"memory, LRU chains committed in the graph, {sets} query sets along a random walk) + prefill "
+                        f"chunks {[list(c) for c in wl.chunks]} (q_len, k_len); Index ingest of "
                         f"{len(wl.sources)} new tokens; one hipGraph per round",
-            "us_per_round": round(us, 1), "decode_rows": len(wl.decode_ctx), "prefill_rows": pf_rows,
-            "rows_per_s": round((len(wl.decode_ctx) + pf_rows) / (us * 1e-6), 1),
-            "decode_misses_last_round": misses, "rounds": iters}
+            "us_per_round": round(us, 1), "decode_rows": nd, "prefill_rows": pf_rows,
+            "rows_per_s": round((nd + pf_rows) / (us * 1e-6), 1),
+            "decode_misses_per_round": round(float(np.mean(miss)), 1),
+            "decode_hit_fraction": round(1.0 - float(np.mean(miss)) / (nd * TOPK), 4), "rounds": rounds}
 
 
 def main():
@@ -531,18 +692,18 @@ def main():
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(dominant) if args.config == "c2" else None},
     }
-    if not args.no_lidu:
-        result["lidu"] = lidu_leg(torch, kvip_amd, device, args.seed)
-    if not args.no_resident:
-        result["resident"] = resident_leg(torch, kvip_amd, device, args.seed)
-    if not args.no_prefill:
-        result["prefill"] = prefill_leg(torch, kvip_amd, device, args.seed)
-    if not args.no_mixed:
-        result["mixed"] = mixed_leg(torch, kvip_amd, device, args.seed)
-    if not args.no_sfa:
-        result["sfa"] = sfa_leg(torch, kvip_amd, device, args.seed)
-    if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(torch, wl, rot, args.cpu_seconds)
+    legs = [("lidu", args.no_lidu, lambda: lidu_leg(torch, kvip_amd, device, args.seed)),
+            ("resident", args.no_resident, lambda: resident_leg(torch, kvip_amd, device, args.seed)),
+            ("cache_ops", args.no_resident, lambda: cache_ops_leg(torch, kvip_amd, device, args.seed)),
+            ("prefill", args.no_prefill, lambda: prefill_leg(torch, kvip_amd, device, args.seed)),
+            ("mixed", args.no_mixed, lambda: mixed_leg(torch, kvip_amd, device, args.seed)),
+            ("sfa", args.no_sfa, lambda: sfa_leg(torch, kvip_amd, device, args.seed)),
+            ("cpu_baseline", args.no_cpu_baseline, lambda: cpu_baseline(torch, wl, rot, args.cpu_seconds))]
+    print(f"bench: decode steps done ({result['ms_per_step']} ms/step)", file=sys.stderr, flush=True)
+    for name, skip, leg in legs:
+        if not skip:
+            result[name] = leg()
+            print(f"bench: {name} leg done", file=sys.stderr, flush=True)
     print(json.dumps(result), flush=True)
 
 
