@@ -173,58 +173,61 @@ def lidu_leg(torch, kvip_amd, device, seed, iters=50):
             "unique_misses_per_request": round(float(counts[:-1].mean()), 1), "calls": iters}
 
 
-def _query_sets(torch, base, sets, seed, step=0.3):
-    """`sets` fp8 query tensors shaped like `base` along a random walk (set 0 is the base,
-    set k = sqrt(1 - step^2) * set k-1 + step * N(0, 1)): consecutive rounds select
+def _query_walk(torch, base, sets, seed, step=0.3):
+    """uint8 view [sets, *base.shape] of fp8 query sets along a random walk (set 0 is the
+    base, set k = sqrt(1 - step^2) * set k-1 + step * N(0, 1)): consecutive rounds select
     overlapping but drifting positions, as consecutive decode steps do."""
     from kvip_amd import synthetic
 
     gen = torch.Generator(device=base.device)
     gen.manual_seed(seed)
     vals = base.float()
-    out = [base.clone()]
-    for _ in range(sets - 1):
+    out = torch.empty((sets, *base.shape), dtype=torch.uint8, device=base.device)
+    out[0].copy_(base.view(torch.uint8))
+    for k in range(1, sets):
         vals = (1.0 - step * step) ** 0.5 * vals + step * torch.randn(vals.shape, generator=gen, device=base.device)
-        out.append(synthetic.saturating_fp8(torch, vals))
+        out[k].copy_(synthetic.saturating_fp8(torch, vals).view(torch.uint8))
     return out
 
 
-def _graph_rounds(torch, bodies, rounds, warm=4, probe=None):
-    """Captures each body as a hipGraph (after one eager call on a side stream), replays
-    them in rotation `warm` times, then times `rounds` back-to-back replays with HIP events
-    on the launch stream. With `probe`, a second pass of `rounds` replays calls it after
-    each replay (host-synchronised, untimed) and returns its values."""
+def _cursor_rounds(torch, body, warm, rounds, sets):
+    """Consecutive rounds from one captured hipGraph: body(cursor) enqueues round `cursor`
+    (a device int64 [1] that the graph then advances), reading that round's inputs and
+    recording its outcome by device indexing. One eager call on a side stream (code-object
+    loading), cursor reset, capture; `warm` untimed replays, then `rounds` back-to-back
+    replays timed with HIP events on the launch stream; the cursor stays below `sets`, the
+    number of input sets the body indexes. Returns us per round."""
+    if warm + rounds > sets:
+        raise ValueError(f"{warm} + {rounds} rounds need as many input sets (have {sets})")
     stream = torch.cuda.current_stream()
+    cursor = torch.zeros(1, dtype=torch.int64, device=stream.device)
+
+    def step():
+        body(cursor)
+        cursor.add_(1)
+
     side = torch.cuda.Stream()
     side.wait_stream(stream)
     with torch.cuda.stream(side):
-        for body in bodies:
-            body()
+        step()
     stream.wait_stream(side)
     torch.cuda.synchronize()
-    graphs = []
-    for body in bodies:
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            body()
-        graphs.append(g)
-    for i in range(warm):
-        graphs[i % len(graphs)].replay()
+    cursor.zero_()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    cursor.zero_()
+    torch.cuda.synchronize()
+    for _ in range(warm):
+        graph.replay()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(stream)
-    for i in range(rounds):
-        graphs[i % len(graphs)].replay()
+    for _ in range(rounds):
+        graph.replay()
     e1.record(stream)
     e1.synchronize()
-    us = e0.elapsed_time(e1) * 1e3 / rounds
-    probes = []
-    if probe is not None:
-        for i in range(rounds):
-            graphs[i % len(graphs)].replay()
-            torch.cuda.synchronize()
-            probes.append(probe())
-    return us, probes
+    return e0.elapsed_time(e1) * 1e3 / rounds
 
 
 def host_read_gbs(torch, device, nbytes=256 << 20):
@@ -293,70 +296,71 @@ def cache_ops_leg(torch, kvip_amd, device, seed, iters=20):
     return out
 
 
-def resident_leg(torch, kvip_amd, device, seed, rounds=24, sets=24):
+def resident_leg(torch, kvip_amd, device, seed, rounds=24, warm=4):
     """BASELINE config 4 on the resident cache: 16 requests, history 131072, 16384 hot
     slots, misses fetched from a pinned host pool, the device LRU chains (one per request)
-    committed by every round inside its hipGraph. Two loops of graph replays, each timed
-    back to back with HIP events:
+    committed by every round inside the graph. Two loops of consecutive rounds, each one
+    captured hipGraph replayed back to back (HIP events around the timed replays), every
+    round on inputs of its own (picked by a device cursor) and recording its misses:
       round:   the resident round alone (init, resolve, Fetch of the misses, Index update,
                LRU commit) on TopK rows drawn ~80 % hot under Zipf(1.1) popularity, a fresh
-               draw per round (`sets` graphs replayed in rotation);
+               draw per round;
       forward: the whole resident forward (LI over 16 x 131072 Index rows, TopK-2048, the
-               round, LRU commit) on `sets` query sets along a random walk (consecutive
-               rounds select overlapping, drifting positions).
-    Misses per round come from a second, host-synchronised pass of the same replays."""
+               round, LRU commit) on query sets along a random walk (consecutive rounds
+               select overlapping, drifting positions)."""
     import ctypes
     from kvip_amd import synthetic
     from kvip_amd.runtime import abi
 
     batch, history, resident = 16, 131072, 16384
+    n = warm + rounds + 1  # + the eager round before capture
     rot, upd, fwd = synthetic.resident_workload(torch, kvip_amd, device, seed=seed, batch=batch,
                                                 history=history, resident=resident)
     rng = np.random.default_rng(seed)
-    picks = torch.from_numpy(synthetic.resident_selections(torch, rng, steps=sets, batch=batch, q_rows=1,
+    picks = torch.from_numpy(synthetic.resident_selections(torch, rng, steps=n, batch=batch, q_rows=1,
                                                            history=history, resident=resident)).to(device)
     lru = kvip_amd.SlotLRUChains(torch, batch, resident, device, slots=upd.lru_slots)
     lib = abi.load_library()
     commit_rows = upd.slot_output.view(batch, -1)
+    trace = torch.zeros((n, batch), dtype=torch.int32, device=device)
 
-    def round_body(k):
-        def body():
-            rot.topk.copy_(picks[k])
-            abi.check(lib.kvip_hip_resident_round(ctypes.byref(upd.args), abi.stream_handle(torch, rot.device)),
-                      "resident round")
-            lru.commit(commit_rows)
-        return body
+    def record(cursor):
+        lru.commit(commit_rows)
+        trace.index_copy_(0, cursor, upd.miss_counts[:, 4].view(1, batch))
 
-    def misses():
-        return int(upd.miss_counts[:, 4].sum().item())
+    def round_body(cursor):
+        rot.topk.copy_(torch.index_select(picks, 0, cursor)[0])
+        abi.check(lib.kvip_hip_resident_round(ctypes.byref(upd.args), abi.stream_handle(torch, rot.device)),
+                  "resident round")
+        record(cursor)
 
-    round_us, round_miss = _graph_rounds(torch, [round_body(k) for k in range(sets)], rounds, probe=misses)
+    round_us = _cursor_rounds(torch, round_body, warm, rounds, n)
     if upd.status.any():
         raise RuntimeError(f"resident round failed: {upd.status.cpu().tolist()}")
-    queries = _query_sets(torch, rot.query, sets, seed)
+    round_miss = trace[warm:warm + rounds].sum(1).float().mean().item()
+    queries = _query_walk(torch, rot.query, n, seed)
+    q_bytes = rot.query.view(torch.uint8)
+    trace.zero_()
 
-    def forward_body(k):
-        def body():
-            rot.query.copy_(queries[k])
-            fwd()
-            lru.commit(commit_rows)
-        return body
+    def forward_body(cursor):
+        q_bytes.copy_(torch.index_select(queries, 0, cursor)[0])
+        fwd()
+        record(cursor)
 
-    fwd_us, fwd_miss = _graph_rounds(torch, [forward_body(k) for k in range(sets)], rounds, probe=misses)
+    fwd_us = _cursor_rounds(torch, forward_body, warm, rounds, n)
     if upd.status.any() or rot.status.any():
         raise RuntimeError(f"resident forward failed: {upd.status.cpu().tolist()} {int(rot.status.item())}")
+    fwd_miss = trace[warm:warm + rounds].sum(1).float().mean().item()
     host_gbs = host_read_gbs(torch, device)
-    miss = float(np.mean(round_miss))
-    fmiss = float(np.mean(fwd_miss))
     return {"workload": "c4 shape: 16 requests x 1 row, history 131072, resident 16384, misses fetched from pinned "
                         "host memory, LRU chains committed in the graph; round: TopK rows drawn ~80% hot (Zipf 1.1), "
-                        f"{sets} draws; forward: LI + TopK + round on {sets} query sets along a random walk",
-            "us_per_round": round(round_us, 2), "misses_per_round": round(miss, 1),
-            "hit_fraction": round(1.0 - miss / (batch * TOPK), 4),
-            "fetch_gbs_lower_bound": round(miss * 656 / (round_us * 1e-6) / 1e9, 2),
+                        "a fresh draw per round; forward: LI + TopK + round on query sets along a random walk",
+            "us_per_round": round(round_us, 2), "misses_per_round": round(round_miss, 1),
+            "hit_fraction": round(1.0 - round_miss / (batch * TOPK), 4),
+            "fetch_gbs_lower_bound": round(round_miss * 656 / (round_us * 1e-6) / 1e9, 2),
             "host_read_ceiling_gbs": round(host_gbs, 1),
-            "forward_us": round(fwd_us, 2), "forward_misses_per_round": round(fmiss, 1),
-            "forward_hit_fraction": round(1.0 - fmiss / (batch * TOPK), 4),
+            "forward_us": round(fwd_us, 2), "forward_misses_per_round": round(fwd_miss, 1),
+            "forward_hit_fraction": round(1.0 - fwd_miss / (batch * TOPK), 4),
             "forward_index_gbs": round(batch * history * 132 / (fwd_us * 1e-6) / 1e9, 1), "rounds": rounds}
 
 
@@ -505,43 +509,44 @@ def sfa_leg(torch, kvip_amd, device, seed, iters=20):
     return out
 
 
-def mixed_leg(torch, kvip_amd, device, seed, rounds=20, sets=20):
+def mixed_leg(torch, kvip_amd, device, seed, rounds=20, warm=4):
     """one continuous-batching round captured as a single hipGraph:
     Index ingest of all new tokens (32 decode + 2048 + 1536 prefill rows), resident decode
     LIFetch for 32 requests (ctx ~U[4096, 65536], 16384 hot slots, misses from pinned host
     memory, the LRU chains committed inside the graph) and prefill LI + TopK for the two
-    chunks (k_len 8192 and 1536). `sets` graphs differ in the decode queries (a random walk,
-    so consecutive rounds select overlapping, drifting positions) and replay in rotation on
-    the evolving cache state, as consecutive serving rounds. Misses per round come from a
-    second, host-synchronised pass."""
+    chunks (k_len 8192 and 1536). Consecutive replays are consecutive serving rounds on the
+    evolving cache state: each picks its decode queries by a device cursor from a random
+    walk (overlapping, drifting selections) and records its misses."""
     from kvip_amd import synthetic
 
     wl = synthetic.mixed_workload(torch, kvip_amd, device, seed=seed, lru=True)
     rnd = wl.round
-    queries = _query_sets(torch, wl.rot.query, sets, seed)
+    nd = len(wl.decode_ctx)
+    n = warm + rounds + 1
+    queries = _query_walk(torch, wl.rot.query, n, seed)
+    q_bytes = wl.rot.query.view(torch.uint8)
+    trace = torch.zeros((n, nd), dtype=torch.int32, device=device)
 
-    def body(k):
-        def run():
-            wl.rot.query.copy_(queries[k])
-            rnd()
-        return run
+    def body(cursor):
+        q_bytes.copy_(torch.index_select(queries, 0, cursor)[0])
+        rnd()
+        trace.index_copy_(0, cursor, wl.update.miss_counts[:, 4].view(1, nd))
 
-    us, miss = _graph_rounds(torch, [body(k) for k in range(sets)], rounds,
-                             probe=lambda: int(wl.update.miss_counts[:, 4].sum().item()))
+    us = _cursor_rounds(torch, body, warm, rounds, n)
     for st in (wl.update.status, wl.rot.status, wl.prefill.status, rnd.status):
         if st.any():
             raise RuntimeError(f"mixed round: device status {st.cpu().tolist()}")
+    miss = trace[warm:warm + rounds].sum(1).float().mean().item()
     pf_rows = sum(q for q, _ in wl.chunks)
-    nd = len(wl.decode_ctx)
     return {"workload": f"c5: {nd} decode requests (ctx U[4096,{wl.history}], mean "
                         f"{wl.decode_ctx.mean():.0f}; resident {wl.resident} hot slots, misses from pinned host "
-                        f"memory, LRU chains committed in the graph, {sets} query sets along a random walk) + prefill "
+                        f"memory, LRU chains committed in the graph, queries along a random walk) + prefill "
                         f"chunks {[list(c) for c in wl.chunks]} (q_len, k_len); Index ingest of "
                         f"{len(wl.sources)} new tokens; one hipGraph per round",
             "us_per_round": round(us, 1), "decode_rows": nd, "prefill_rows": pf_rows,
             "rows_per_s": round((nd + pf_rows) / (us * 1e-6), 1),
-            "decode_misses_per_round": round(float(np.mean(miss)), 1),
-            "decode_hit_fraction": round(1.0 - float(np.mean(miss)) / (nd * TOPK), 4), "rounds": rounds}
+            "decode_misses_per_round": round(miss, 1),
+            "decode_hit_fraction": round(1.0 - miss / (nd * TOPK), 4), "rounds": rounds}
 
 
 def main():
