@@ -94,8 +94,10 @@ extern "C" {
 #define KVIP_STATUS_BAD_BLOCK 1u     /* a block-table entry outside [0, num_blocks) */
 #define KVIP_STATUS_HISTOGRAM 2u     /* TopK histogram inconsistent with the row length */
 #define KVIP_STATUS_BAD_TOKEN 4u     /* a TopK token id outside the block table */
-#define KVIP_STATUS_STALLED 8u       /* a multi-workgroup select waited past its spin bound; the
-                                        segment work memory must be re-zeroed before reuse */
+#define KVIP_STATUS_STALLED 8u       /* XCD-local round only: a request went unselected or the
+                                        dispatcher did not place each group of workgroups on
+                                        one XCD; that round's outputs are unusable (rerun it
+                                        with the three-launch plan) */
 
 /* Lightning-indexer scoring over a paged index-K cache.
  *
