@@ -72,7 +72,7 @@
 extern "C" {
 #endif
 
-#define KVIP_HIP_ABI_VERSION 9u
+#define KVIP_HIP_ABI_VERSION 10u
 
 #define KVIP_TOPK 2048
 #define KVIP_BLOCK_TOKENS 128
@@ -392,11 +392,19 @@ typedef struct KvipIngestArgs {
 /* Resident-cache round of one LIFetch step (hot/cold split of the TopK positions):
  * every request b owns the Index rows [row_owners[b], 0..history) (keys, scales, KV
  * addresses in host_pool, logical ids); position p < resident is hot, its KV row living
- * in hot_cache[owner, p] when hot_valid[owner, p] != 0. After TopK over positions:
+ * in hot_cache[owner, p] when hot_valid[owner, p] != 0. With tail_bounds, positions
+ * [begin_b, end_b) of request b are its ABC tail (the recent tokens whose KV the serving
+ * step keeps in the ABC ring, the hot_stride - resident = T slots after the hot ones):
+ * they are never hot hits; the first T of them, p < begin_b + T, sit in ring slot
+ * resident + p % T and resolve to it without a Fetch; the rest are ordinary misses
+ * (the reference's tail mapping, op_kernel/prefetch.h:25-43, resolved by
+ * ResolvePhysicalSlot, common/lifetch/cache_metadata.h:102-106, in the final
+ * classification, staged_topk_classify.h:9-36). After TopK over positions:
  *   init     reserved_hot[b] = LRU ordinal of each candidate slot of lru_slots[b] (-1
  *            otherwise); changes = -1; change_slots = candidates then -1; counts zero;
  *   resolve  per request, query rows in order: hot hits (p < resident, hot_valid, not a
- *            candidate) keep slot p; rows q >= 2 reuse row q-2's slot for the same position
+ *            candidate, not in the tail) keep slot p, mapped tail positions take their
+ *            ring slot; rows q >= 2 reuse row q-2's slot for the same position
  *            at the same index; the other positions' first occurrences become misses
  *            ranked in index order over the rows, each given the next free candidate in
  *            ordinal order (pass 0 ordinals >= used, pass 1 < used; slots holding this
@@ -424,7 +432,8 @@ typedef struct KvipIngestArgs {
 #define KVIP_RESIDENT_MAX_RESIDENT 131072
 #define KVIP_RESIDENT_LRU_SLOTS 2048
 #define KVIP_RESIDENT_CHANGES (KVIP_RESIDENT_LRU_SLOTS + KVIP_RESIDENT_MAX_QUERIES * KVIP_TOPK)
-#define KVIP_RESIDENT_ERR_TOKEN 1u       /* a TopK position >= history, or a bad owner row */
+#define KVIP_RESIDENT_ERR_TOKEN 1u       /* a TopK position >= history, a bad owner row, or tail
+                                            bounds outside 0 <= begin <= end <= history */
 #define KVIP_RESIDENT_ERR_CANDIDATE 4u   /* a candidate outside [0, resident), or no free hot slot */
 #define KVIP_RESIDENT_ERR_SOURCE 8u      /* a Fetch source outside host_pool */
 #define KVIP_RESIDENT_ERR_UPDATE 16u     /* the changes are not a partial permutation */
@@ -467,6 +476,10 @@ typedef struct KvipResidentArgs {
      * op_kernel/streaming.cpp:31-44, :66-89.) */
     const int64_t* unpack_indices;  /* [batch * 4] */
     const int64_t* output_valid;    /* [batch * 4] */
+    /* ABC tail of each request, {begin, end} Index positions, or NULL (then no position is a
+     * tail position). Set: hot_stride - resident (the ring slots) is a multiple of 128 and at
+     * least 384 (python/kvip/operators/lifetch/binding.py:159-164). */
+    const int32_t* tail_bounds;     /* [batch, 2] */
 } KvipResidentArgs;
 
 /* Publication of appended KV pages (PageUpdates.submit, python/kvip/cache/page_updates.py:

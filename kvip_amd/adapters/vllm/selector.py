@@ -141,6 +141,10 @@ class VllmIndexSelector:
         self.history = int(logical_ids.shape[1])
         self.topk = rotating.topk.view(inputs.batch, QUERIES_PER_REQUEST, TOPK)
         self.attention_indices = None
+        # ABC tail bounds of the step ([batch, 2] int32 {begin, end}, e.g. columns 2:4 of the
+        # serving policy's ABC descriptors), copied into the update's tail_bounds before each
+        # decode forward (selector.py:42, :115-116 of the reference).
+        self.tail_source = None
         self.plans = None
         self.decodes = ()
         self.prefills = ()
@@ -177,6 +181,10 @@ class VllmIndexSelector:
         if self.plans and not self.decodes:
             return indexer.select_topk_native(query, weights, metadata, query_scale)
         self.inputs.pack(query, weights, query_scale)
+        if self.tail_source is not None:
+            if self.update.tail_bounds is None:
+                raise ValueError("tail_source needs a ResidentIndexUpdate bound with tail_bounds")
+            self.update.tail_bounds.copy_(self.tail_source)
         self.forward()
         tokens = int(weights.shape[0])
         live = self.inputs.token_count if mixed or tokens > self.inputs.capacity else tokens

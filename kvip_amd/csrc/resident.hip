@@ -138,24 +138,44 @@ __global__ __launch_bounds__(kRsThreads) void resident_resolve_kernel(const Kvip
     const int32_t* lru = p.lru_slots + static_cast<size_t>(b) * kLru;
     const int nchg = kLru + Q * kTopK;
 
+    // ABC tail [tail_begin, tail_end); its first T positions sit in ring slot R + p % T.
+    const int T = p.hot_stride - R;
+    int tail_begin = 0, tail_end = 0;
+    bool tail_ok = true;
+    if (p.tail_bounds != nullptr) {
+        tail_begin = p.tail_bounds[2 * b];
+        tail_end = p.tail_bounds[2 * b + 1];
+        tail_ok = 0 <= tail_begin && tail_begin <= tail_end && tail_end <= H;
+        if (!tail_ok) tail_begin = tail_end = 0;
+    }
+    const int tail_mapped = min(tail_end, tail_begin + T);
+
     for (int i = tid; i < words; i += kRsThreads) s_bitmap[i] = 0u;
     // Errors found by the round initialisation (duplicate candidates) carry over.
-    if (tid == 0) s_err = static_cast<uint32_t>(p.status[b]) | (owner_ok(p, o) ? 0u : KVIP_RESIDENT_ERR_TOKEN);
+    if (tid == 0) {
+        s_err = static_cast<uint32_t>(p.status[b]) |
+                (owner_ok(p, o) && tail_ok ? 0u : static_cast<uint32_t>(KVIP_RESIDENT_ERR_TOKEN));
+    }
     if (tid < kMaxQ) s_dest[tid] = -1;
     __syncthreads();
     const bool good_owner = owner_ok(p, o);
     const int32_t* hot_valid = p.hot_valid + static_cast<size_t>(good_owner ? o : 0) * R;
 
-    // Classification of every query row: hot hits keep their position as slot.
+    // Classification of every query row: hot hits keep their position as slot, mapped
+    // tail positions take their ring slot (>= R: neither protected nor fetched).
     for (int e = tid; e < Q * kTopK; e += kRsThreads) {
         const int t = p.topk[static_cast<size_t>(b) * Q * kTopK + e];
         s_sel[e] = t;
         int loc = -1;
         if (t >= H) {
             atomicOr(&s_err, KVIP_RESIDENT_ERR_TOKEN);
-        } else if (good_owner && t >= 0 && t < R && hot_valid[t] != 0 && reserved[t] < 0) {
-            loc = t;
-            atomicOr(&s_bitmap[t >> 5], 1u << (t & 31));
+        } else if (good_owner && t >= 0) {
+            if (t >= tail_begin && t < tail_end) {
+                if (t < tail_mapped) loc = R + t % T;
+            } else if (t < R && hot_valid[t] != 0 && reserved[t] < 0) {
+                loc = t;
+                atomicOr(&s_bitmap[t >> 5], 1u << (t & 31));
+            }
         }
         s_loc[e] = loc;
     }
@@ -631,7 +651,9 @@ uint32_t validate_resident(const KvipResidentArgs* a) {
                     a->row_bytes % 16 == 0 && a->used >= 0 && a->used <= kLru && a->host_pool_bytes >= a->row_bytes &&
                     aligned(a->index_keys, 16) && aligned(a->host_pool, 16) && aligned(a->hot_cache, 16) &&
                     aligned(a->workspace, 16) && (a->unpack_indices == nullptr) == (a->output_valid == nullptr) &&
-                    (a->unpack_indices == nullptr || a->rows_per_request == kMaxQ);
+                    (a->unpack_indices == nullptr || a->rows_per_request == kMaxQ) &&
+                    (a->tail_bounds == nullptr ||
+                     ((a->hot_stride - a->resident) % 128 == 0 && a->hot_stride - a->resident >= 384));
     return ok ? KVIP_OK : KVIP_ERR_INVALID;
 }
 

@@ -10,7 +10,12 @@ what the reference keeps behind KVAF: the hot KV cache [owners, hot_stride, row_
 device-accessible (pinned) host tensor in which `addresses` are byte offsets. With
 `query_inputs` (a vLLM-adapter QueryInputs, four query rows per request) the outputs are
 published in token order like the reference's (index_update.py:18-21, 85-99): output row
-t holds the query row unpack_indices[t] when output_valid[t], else -1 throughout.
+t holds the query row unpack_indices[t] when output_valid[t], else -1 throughout. With
+`tail_bounds` ([batch, 2] int32 {begin, end}, the reference binding's tail_bounds,
+binding.py:150) positions [begin, end) of each request are its ABC tail: never hot hits,
+the first T = hot_stride - resident of them resolved to ring slot resident + p % T of the
+hot cache without a Fetch (the hot cache then holds resident + T rows per owner, T a
+multiple of 128 and at least 384).
 
 The forward enqueues, on the current stream and without host synchronisation: the
 owner block table, LI scoring of the owners' Index rows, TopK-2048 per query row, and the
@@ -31,7 +36,7 @@ LRU_SLOTS = abi.RESIDENT_LRU_SLOTS
 
 class ResidentIndexUpdate:
     def __init__(self, torch, *, keys, scales, addresses, logical_ids, row_owners, rotating, hot_valid, hot_cache,
-                 host_pool, resident, status=None, outputs=None, used=0, query_inputs=None):
+                 host_pool, resident, status=None, outputs=None, used=0, query_inputs=None, tail_bounds=None):
         self.torch, self.rotating, self.device = torch, rotating, rotating.device
         if keys.dim() != 3 or keys.shape[2] != INDEX_DIM or keys.dtype != torch.float8_e4m3fn or not keys.is_contiguous():
             raise ValueError("Index keys must be contiguous float8_e4m3fn [owners, history, 128]")
@@ -63,6 +68,15 @@ class ResidentIndexUpdate:
                                          query_inputs.device != rotating.device):
             raise ValueError("token-order outputs need the binding's batch, four query rows and device")
         dev = self.device
+        if tail_bounds is not None:
+            ring = int(hot_cache.shape[1]) - resident
+            if (tail_bounds.dtype != torch.int32 or tuple(tail_bounds.shape) != (rotating.batch, 2) or
+                    not tail_bounds.is_contiguous() or tail_bounds.device != dev):
+                raise ValueError(f"tail_bounds must be contiguous int32 [{rotating.batch}, 2] on {dev}")
+            if ring < 384 or ring % 128:
+                raise ValueError("ABC tail bounds need hot-cache ring slots after the hot ones: hot_cache.shape[1] "
+                                 "- resident must be a multiple of 128 and at least 384")
+        self.tail_bounds = tail_bounds
         if any(t.device != dev for t in (keys, scales, addresses, logical_ids, row_owners, hot_valid, hot_cache)):
             raise ValueError("Index storage, hot cache and the LIFetch binding must share one device")
         self.keys, self.scales, self.addresses, self.logical_ids = keys, scales, addresses, logical_ids
@@ -120,6 +134,7 @@ class ResidentIndexUpdate:
             row_bytes=int(self.hot_cache.shape[2]), used=self.used,
             unpack_indices=p(self.query_inputs.unpack_indices) if self.query_inputs is not None else 0,
             output_valid=p(self.query_inputs.output_valid) if self.query_inputs is not None else 0,
+            tail_bounds=p(self.tail_bounds),
         )
 
 

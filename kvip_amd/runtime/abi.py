@@ -9,7 +9,7 @@ import ctypes
 from pathlib import Path
 
 LIBRARY = Path(__file__).resolve().parents[1] / "_lib" / "libkvip_hip.so"
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 KVIP_OK = 0
 KVIP_ERR_INVALID = 100000
@@ -157,6 +157,7 @@ class ResidentArgs(ctypes.Structure):
         ("workspace", _p), ("host_pool_bytes", _i64),
         ("batch", _i32), ("rows_per_request", _i32), ("owners", _i32), ("history", _i32), ("resident", _i32),
         ("hot_stride", _i32), ("row_bytes", _i32), ("used", _i32), ("unpack_indices", _p), ("output_valid", _p),
+        ("tail_bounds", _p),
     ]
 
 

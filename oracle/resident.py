@@ -11,7 +11,11 @@ Follows (paths relative to the KVIP reference tree,
 csrc/operators/lightning_indexer_with_fetch/op_kernel/ unless noted):
   classify   staged_topk_classify.h:9-36 (ClassifyTopkHalf), resolver_staged_dma2.h:9-22
              (StagedKnownSlot), :34-77 (StagedInitialize: Q3/Q4 same-position shortcut,
-             protection bitmap of every query's hot hits)
+             protection bitmap of every query's hot hits); ABC tail: positions in
+             [begin, end) are never hot (cache_metadata.h:22-26 IsTailToken), the first
+             T = stride - resident of them are mapped to resident + kSlots + p % T at round
+             start (prefetch.h:25-43 InitializeTailMappings) and ResolvePhysicalSlot
+             (cache_metadata.h:102-106) turns that into ring slot resident + p % T
   resolve    resolver_staged_dma2.h:98-237 (StagedQuery): first-occurrence dedup per
              query, ranks continuing over queries, LRU candidates in ordinal order (pass 0
              ordinals >= used, pass 1 < used) skipping protected slots, fallback scan of the
@@ -43,7 +47,7 @@ status alone).
 
 Scope of this restatement: no speculative prefetch (`used` candidates consumed by an
 earlier window are supported by the two allocation passes, but no prefetch mapping is
-consulted) and no ABC tail bounds (tail tokens are ordinary positions).
+consulted); the only mapping entries are those of the ABC tail.
 """
 from __future__ import annotations
 
@@ -62,15 +66,33 @@ ERR_SOURCE = 8         # a miss whose KV address is outside the host pool or not
 ERR_UPDATE = 16        # an Index change that is not a valid partial permutation
 
 
-def classify(selected, history, resident, hot_valid, reserved):
-    """Hot hits of every query row of one request (StagedKnownSlot without prefetch
-    mapping). selected [Q, 2048] positions (-1 empty). Returns (loc [Q, 2048] with the hit
-    slot or -1, protection bitmap as a bool array [resident], error bits). Rows q >= 2
-    copy loc from row q - 2 where they select the same position at the same index."""
+def tail_slot(t, tail):
+    """Ring slot of position t under tail = (begin, end, ring_slots) or None: the ABC tail
+    mapping (prefetch.h:25-43) resolved by ResolvePhysicalSlot (cache_metadata.h:102-106).
+    Returns (in_tail, slot or None); the slot is relative to resident."""
+    if tail is None:
+        return False, None
+    begin, end, ring = tail
+    if not begin <= t < end:
+        return False, None
+    return True, (t % ring if t < begin + ring else None)
+
+
+def classify(selected, history, resident, hot_valid, reserved, tail=None):
+    """Hot hits of every query row of one request (StagedKnownSlot, the only mapping
+    entries being the ABC tail's). selected [Q, 2048] positions (-1 empty); tail =
+    (begin, end, ring_slots) or None. Returns (loc [Q, 2048] with the hit slot, the ring
+    slot resident + p % ring of a mapped tail position, or -1; protection bitmap as a bool
+    array [resident]; error bits). Rows q >= 2 copy loc from row q - 2 where they select
+    the same position at the same index. Tail bounds outside 0 <= begin <= end <= history
+    set ERR_TOKEN (this build's check)."""
     q_rows = selected.shape[0]
     loc = np.full(selected.shape, EMPTY, np.int64)
     protect = np.zeros(resident, bool)
     err = 0
+    if tail is not None and not 0 <= tail[0] <= tail[1] <= history:
+        err |= ERR_TOKEN
+        tail = None
     for q in range(q_rows):
         for i in range(TOPK):
             t = int(selected[q, i])
@@ -82,13 +104,17 @@ def classify(selected, history, resident, hot_valid, reserved):
             if t >= history:
                 err |= ERR_TOKEN
                 continue
-            if t < resident and hot_valid[t] != 0 and reserved[t] < 0:
+            in_tail, ring_slot = tail_slot(t, tail)
+            if in_tail:
+                if ring_slot is not None:
+                    loc[q, i] = resident + ring_slot
+            elif t < resident and hot_valid[t] != 0 and reserved[t] < 0:
                 loc[q, i] = t
                 protect[t] = True
     return loc, protect, err
 
 
-def resolve(selected, history, resident, hot_valid, reserved, lru, used=0, sources=None):
+def resolve(selected, history, resident, hot_valid, reserved, lru, used=0, sources=None, tail=None):
     """Per-query miss resolution of one request (StagedQuery). Returns a dict with
     loc [Q, 2048] (hot slot of every selected position, -1 for empty entries), slots
     [misses] (slot of each miss rank), tokens [misses] (position of each miss rank),
@@ -97,9 +123,9 @@ def resolve(selected, history, resident, hot_valid, reserved, lru, used=0, sourc
     sources = (addresses [history], pool_bytes, row_bytes): every new miss's KV address is
     checked against the host pool as its query is resolved (ERR_SOURCE), before any
     Fetch; this check is this build's own (the reference's transport validates its
-    descriptors, cache_metadata.h:32-44)."""
+    descriptors, cache_metadata.h:32-44). tail: the ABC tail, as for classify."""
     q_rows = selected.shape[0]
-    loc, protect, err = classify(selected, history, resident, hot_valid, reserved)
+    loc, protect, err = classify(selected, history, resident, hot_valid, reserved, tail)
     in_range = [int(s) for s in lru[:LRU_SLOTS] if 0 <= s < resident]
     if len(set(in_range)) != len(in_range):
         err |= ERR_CANDIDATE  # a hot slot named by two candidates
@@ -245,14 +271,15 @@ def _permute(batches, history, resident, keys, scales, hot_valid, row_at, pos_of
 
 
 def resident_round(selected, history, resident, keys, scales, addresses, logical, hot_valid, reserved, lru,
-                   hot_cache, host_pool, used=0):
+                   hot_cache, host_pool, used=0, tail=None):
     """One request's full round after TopK, in place on its tables: resolve, outputs,
     Fetch (hot_cache[slot] = host_pool[addresses[token]]), Index update, residency
     publication. Returns (logical_output [Q, 2048], slot_output [Q, 2048], resolve dict,
     error bits). A failed request's owner loses all residency (hot_valid cleared); when
-    it fails before the Fetch both outputs are -1 and nothing else changes."""
+    it fails before the Fetch both outputs are -1 and nothing else changes. tail: the ABC
+    tail (begin, end, ring_slots), as for classify."""
     res = resolve(selected, history, resident, hot_valid, reserved, lru, used,
-                  sources=(addresses, host_pool.size, hot_cache.shape[1]))
+                  sources=(addresses, host_pool.size, hot_cache.shape[1]), tail=tail)
     q_rows = selected.shape[0]
     if res["error"]:
         hot_valid[:] = 0

@@ -33,7 +33,7 @@ class Setup:
     holding positions 0..resident-1, and a resident-mode LIFetch binding."""
 
     def __init__(self, torch, *, batch, owners, history, resident, q_rows, seed, heads=64, invalid=0.0,
-                 row_owners=None):
+                 row_owners=None, ring=0):
         rng = np.random.default_rng(seed)
         self.torch, self.rng = torch, rng
         self.batch, self.owners, self.history, self.resident, self.q = batch, owners, history, resident, q_rows
@@ -47,9 +47,10 @@ class Setup:
         self.h_logical = np.broadcast_to(np.arange(history), (owners, history)).astype(np.int64).copy()
         pool = li_ref.identity_rows(tokens.reshape(-1), ROW)
         self.h_pool = pool.reshape(-1)
-        self.h_hot = np.zeros((owners, resident, ROW), np.uint8)
+        self.ring = ring  # ABC ring slots after the hot ones (tail bounds bound when > 0)
+        self.h_hot = np.zeros((owners, resident + ring, ROW), np.uint8)
         for o in range(owners):
-            self.h_hot[o] = pool[o * history:o * history + resident]
+            self.h_hot[o, :resident] = pool[o * history:o * history + resident]
         self.h_valid = (rng.random((owners, resident)) >= invalid).astype(np.int32)
         owners_of = np.arange(batch) if row_owners is None else np.asarray(row_owners)
         self.h_owners = owners_of.astype(np.int32)
@@ -63,6 +64,8 @@ class Setup:
         self.hot = t.from_numpy(self.h_hot).to(dev)
         self.valid = t.from_numpy(self.h_valid).to(dev)
         self.row_owners = t.from_numpy(self.h_owners).to(dev)
+        self.h_tail = np.zeros((batch, 2), np.int32)
+        self.tail = t.zeros((batch, 2), dtype=t.int32, device=dev) if ring else None
         self.rot = kvip_amd.LIFetchBinding(t, batch=batch, max_context=history, device=dev, heads=heads,
                                            rows_per_request=q_rows, qk_dtype="fp8", query_ends=True)
         self.rot.seq_lens.fill_(history)
@@ -70,13 +73,15 @@ class Setup:
         self.upd = kvip_amd.ResidentIndexUpdate(
             t, keys=self.keys, scales=self.scales, addresses=self.addresses, logical_ids=self.logical,
             row_owners=self.row_owners, rotating=self.rot, hot_valid=self.valid, hot_cache=self.hot,
-            host_pool=self.pool, resident=resident)
+            host_pool=self.pool, resident=resident, tail_bounds=self.tail)
         self.lib = abi.load_library()
 
     def run_round(self, selected, lru):
         """Device round on the given TopK rows [batch*q, 2048] and candidates [batch, 2048]."""
         t = self.torch
         self.rot.topk.copy_(t.from_numpy(selected.astype(np.int32)))
+        if self.tail is not None:
+            self.tail.copy_(t.from_numpy(self.h_tail))
         self.upd.set_candidates(t.from_numpy(lru.astype(np.int32)).to("cuda"))
         rc = self.lib.kvip_hip_resident_round(ctypes.byref(self.upd.args), abi.stream_handle(t, self.rot.device))
         abi.check(rc, "resident round")
@@ -90,9 +95,10 @@ class Setup:
             sel = selected[b * self.q:(b + 1) * self.q]
             reserved = ref.reserved_from_candidates(lru[b], self.resident)
             keys = self.h_keys[o].copy()
+            tail = (int(self.h_tail[b, 0]), int(self.h_tail[b, 1]), self.ring) if self.ring else None
             lout, sout, res, err = ref.resident_round(
                 sel, self.history, self.resident, keys, self.h_scales[o], self.h_addresses[o], self.h_logical[o],
-                self.h_valid[o], reserved, lru[b], self.h_hot[o], self.h_pool)
+                self.h_valid[o], reserved, lru[b], self.h_hot[o], self.h_pool, tail=tail)
             self.h_keys[o] = keys
             outs.append((lout, sout, res, err, reserved))
         return outs
@@ -168,6 +174,58 @@ def test_resident_round_matches_oracle_over_rounds(torch_gpu, batch, owners, q_r
         for b, p in enumerate(policies):
             s = outs[b][1]
             p.commit(s[s >= 0])
+
+
+def test_resident_round_abc_tail_matches_oracle(torch_gpu):
+    """ABC tail bounds over three rounds (the tail grows by a decode step each round): a
+    tail longer than the ring (its last positions are ordinary misses), a tail inside the
+    hot range (hot, valid positions that must not count as hits) and an empty tail; every
+    row also selects ~15 % tail positions. Everything bit-exact against the oracle."""
+    torch = torch_gpu
+    batch, q_rows, history, resident, ring = 3, 4, 16384, 4096, 512
+    say(f"case resident abc tail b={batch} q={q_rows} h={history} r={resident} ring={ring}")
+    st = Setup(torch, batch=batch, owners=batch, history=history, resident=resident, q_rows=q_rows, seed=11,
+               invalid=0.05, ring=ring)
+    rng = st.rng
+    policies = []
+    for _ in range(batch):
+        p = lru_ref.SlotLRU()
+        p.resize(resident, resident)
+        policies.append(p)
+    tails = np.array([[15000, 15600], [1000, 1300], [0, 0]], np.int32)
+    for rnd in range(3):
+        say(f"  round {rnd}")
+        st.h_tail = tails + np.array([[0, 2], [0, 2], [0, 0]], np.int32) * rnd
+        rows = []
+        for b in range(batch):
+            sel = mtp_selection(rng, q_rows, history, resident, 0.6, n=2048)
+            lo, hi = map(int, st.h_tail[b])
+            if hi > lo:
+                picks = rng.choice(np.arange(lo, hi), min(300, hi - lo), replace=False)
+                for q in range(q_rows):
+                    row = sel[q]
+                    keep = ~np.isin(row, picks)
+                    row = np.concatenate([row[keep], picks])[:TOPK]
+                    row = row[np.unique(row, return_index=True)[1]]
+                    pad = np.setdiff1d(np.arange(resident, history), row)[:TOPK - len(row)]
+                    sel[q] = rng.permutation(np.concatenate([row, pad]))
+            rows.append(sel)
+        selected = np.concatenate(rows)
+        lru = np.stack([p.slots.astype(np.int64) for p in policies])
+        outs = st.oracle_round(selected, lru)
+        for b, (lout, sout, res, err, rsv) in enumerate(outs):
+            assert err == 0, (b, err)
+            lo, hi = map(int, st.h_tail[b])
+            sel = selected[b * q_rows:(b + 1) * q_rows]
+            mapped = (sel >= lo) & (sel < min(hi, lo + ring))
+            assert np.array_equal(sout[mapped], resident + sel[mapped] % ring), b
+            beyond = sel[(sel >= lo + ring) & (sel < hi)]
+            assert np.isin(beyond, res["tokens"]).all(), b  # unmapped tail positions are misses
+        st.run_round(selected, lru)
+        st.compare(outs)
+        for b, p in enumerate(policies):
+            s = outs[b][1]
+            p.commit(s[(s >= 0) & (s < resident)])
 
 
 def test_resident_forward_stateful_known_answer(torch_gpu):

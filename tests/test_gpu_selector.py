@@ -40,8 +40,10 @@ class World:
     """Paged vLLM index cache (each request owns 64 private pages), the Index storage of six
     owners, a pinned host KV pool of identity rows, the hot cache and the selector."""
 
-    def __init__(self, torch, seed):
+    def __init__(self, torch, seed, ring=0):
         self.torch, self.rng = torch, np.random.default_rng(seed)
+        self.ring = ring  # ABC ring slots after the hot ones (the update then binds tail bounds)
+        self.h_tail = np.zeros((B, 2), np.int32)
         rng, t, dev = self.rng, torch, "cuda"
         blocks = 5 * MAXB + 8
         self.h_cache_keys = rng.integers(0, 256, (blocks, 128, 128), dtype=np.uint8) & 0x77
@@ -55,7 +57,8 @@ class World:
         self.pool = t.empty(self.h_pool.size, dtype=t.uint8, pin_memory=True)
         self.pool.copy_(t.from_numpy(self.h_pool))
         self.storage = kvip_amd.IndexCacheStorage(t, OWNERS, HISTORY, RESIDENT, dev)
-        self.hot = t.zeros((OWNERS, RESIDENT, ROW), dtype=t.uint8, device=dev)
+        self.hot = t.zeros((OWNERS, RESIDENT + ring, ROW), dtype=t.uint8, device=dev)
+        self.tail = t.zeros((B, 2), dtype=t.int32, device=dev) if ring else None
         self.inputs = kvip_amd.QueryInputs(t, B, dev, history=HISTORY)
         self.rot = kvip_amd.LIFetchBinding(t, batch=B, max_context=HISTORY, device=dev, heads=HEADS, rows_per_request=4,
                                            qk_dtype="fp8", weight_dtype=t.bfloat16,
@@ -64,7 +67,7 @@ class World:
         self.update = kvip_amd.ResidentIndexUpdate(
             t, keys=s.keys.view(t.float8_e4m3fn), scales=s.scales, addresses=s.addresses, logical_ids=s.logical_ids,
             row_owners=self.inputs.row_owners, rotating=self.rot, hot_valid=s.hot_valid, hot_cache=self.hot,
-            host_pool=self.pool, resident=RESIDENT, query_inputs=self.inputs)
+            host_pool=self.pool, resident=RESIDENT, query_inputs=self.inputs, tail_bounds=self.tail)
         self.indexer = kvip_amd.PagedIndexer(t, keys=self.cache_keys, scales=self.cache_scales, max_rows=128,
                                              max_context=HISTORY, device=dev, heads=HEADS, max_sequences=4)
         self.selector = kvip_amd.VllmIndexSelector(t, inputs=self.inputs, rotating=self.rot, update=self.update,
@@ -209,9 +212,11 @@ class World:
             o = int(owners[b])
             reserved = rs.reserved_from_candidates(host.lru[b], RESIDENT)
             keys = state["keys"][o].copy()
+            tail = (int(self.h_tail[b, 0]), int(self.h_tail[b, 1]), self.ring) if self.ring else None
             lo, so, res, err = rs.resident_round(
                 got_top[b * 4:(b + 1) * 4], HISTORY, RESIDENT, keys, state["scales"][o], state["addresses"][o],
-                state["logical"][o], state["valid"][o], reserved, host.lru[b], state["hot"][o], self.h_pool)
+                state["logical"][o], state["valid"][o], reserved, host.lru[b], state["hot"][o], self.h_pool,
+                tail=tail)
             state["keys"][o] = keys
             assert err == 0, (b, err)
             lout[b * 4:(b + 1) * 4], sout[b * 4:(b + 1) * 4] = lo, so
@@ -269,6 +274,35 @@ def test_selector_steps_against_oracle(torch_gpu):
     w.check_state(state)
     w.check_prefill_rows(rows, host, [(i, rows[p.begin:p.stop]) for i, p in enumerate(host.plans) if not p.decode])
     assert w.storage.imported == {1, 2, 3, 4, 5}
+
+
+def test_selector_tail_source_against_oracle(torch_gpu):
+    """The selector copies `tail_source` (columns 2:4 of [batch, 4] ABC descriptors, as the
+    reference's binding slices them) into the update's tail bounds before each decode
+    forward: a tail of recent positions shorter than the ring, one longer than the ring
+    inside the hot range, an empty one. Decode outputs against the oracle's round with the
+    same tails."""
+    torch = torch_gpu
+    ring = 384
+    w = World(torch, seed=41, ring=ring)
+    say("case selector tail: prefill")
+    w.step([(1, "a", 4100, 30, False), (2, "b", 4990, 10, False), (3, "c", 5990, 20, False)])
+    descriptors = torch.zeros((B, 4), dtype=torch.int32, device="cuda")
+    w.selector.tail_source = descriptors[:, 2:4]
+    for step, reqs in enumerate([[(2, "b", 5000, 4, True), (1, "a", 4130, 1, True), (3, "c", 6010, 3, True)],
+                                 [(2, "b", 5004, 2, True), (1, "a", 4131, 1, True), (3, "c", 6013, 1, True)]]):
+        say(f"case selector tail: decode step {step}")
+        ends = [start + count for _, _, start, count, _ in reqs]
+        tails = np.array([[ends[0] - 300, ends[0]], [1000, 1500], [0, 0], [0, 0]], np.int32)
+        descriptors[:, 2:4].copy_(torch.from_numpy(tails))
+        w.h_tail = tails
+        out, state, host = w.step(reqs)
+        assert np.array_equal(w.tail.cpu().numpy(), tails)
+        meta, q_ends = w.oracle_ingest(state, host, False)
+        w.check_decode(state, host, meta, q_ends, out[:, 0].cpu().numpy())
+        w.check_state(state)
+        so = w.update.slot_output[:, 0].cpu().numpy()
+        assert (so >= RESIDENT).any()  # some selections resolved to ring slots
 
 
 def test_selector_rejects_unbound_inputs(torch_gpu):

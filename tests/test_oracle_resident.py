@@ -397,3 +397,72 @@ def test_prefix_classify_closed_forms():
     # A short prefix selects everything below it and has threshold 0.
     sel, thr, _, _ = ref.prefix_classify(keys, 1000, resident, lru, 200)
     assert thr == 0 and np.array_equal(sel[:1000], np.arange(1000)) and (sel[1000:] == -1).all()
+
+
+# ----------------------------------------------------------------------------
+# ABC tail bounds
+# ----------------------------------------------------------------------------
+def _tail_mapping_literal(history, resident, ring, begin, end):
+    """The reference's round-start tail mapping written out as its loop
+    (prefetch.h:25-43: mapping[begin + i] = resident + kSlots + (begin + i) % ring for
+    i < ring while begin + i < end and < history) followed by ResolvePhysicalSlot
+    (cache_metadata.h:102-106, no LRU ordinal range hit: slot - kSlots)."""
+    k_slots = 8192
+    mapping = np.full(history, 0xFFFFFFFF, np.int64)
+    for i in range(ring):
+        t = begin + i
+        if t < end and t < history:
+            mapping[t] = resident + k_slots + t % ring
+    resolved = np.where((mapping >= resident + k_slots) & (mapping < 0x80000000), mapping - k_slots, -1)
+    return resolved
+
+
+def test_tail_slot_equals_the_literal_mapping_loop():
+    history, resident, ring = 9000, 2048, 384
+    for begin, end in [(0, 0), (5000, 5100), (5000, 5384), (5000, 6000), (100, 900), (8800, 9000), (0, 9000)]:
+        want = _tail_mapping_literal(history, resident, ring, begin, end)
+        for t in range(history):
+            in_tail, slot = ref.tail_slot(t, (begin, end, ring))
+            assert in_tail == (begin <= t < end)
+            got = -1 if slot is None else resident + slot
+            assert got == want[t], (begin, end, t)
+
+
+def test_tail_positions_known_answer():
+    """Hand case: hot, valid positions inside the tail are not hits; the first `ring`
+    tail positions resolve to ring slots without a Fetch; later ones are misses."""
+    history, resident, ring = 8192, 4096, 384
+    hot_valid = np.ones(resident, np.int32)
+    lru = np.arange(2048, 4096, dtype=np.int64)  # candidates: the upper half of the hot slots
+    reserved = ref.reserved_from_candidates(lru, resident)
+    sel = np.full((1, TOPK), -1, np.int64)
+    # 100 and 483: tail and mapped (100 + 384 = 484); 484: tail, unmapped -> miss; 50: hot
+    # hit; 5000: cold -> miss.
+    sel[0, :5] = [100, 483, 484, 50, 5000]
+    res = ref.resolve(sel, history, resident, hot_valid, reserved, lru, tail=(100, 600, ring))
+    assert res["error"] == 0
+    assert res["loc"][0, 0] == resident + 100 % ring  # 4196
+    assert res["loc"][0, 1] == resident + 483 % ring  # 4195
+    assert res["loc"][0, 3] == 50
+    assert res["tokens"].tolist() == [484, 5000]
+    assert res["slots"].tolist() == [2048, 2049]  # the first free candidates, in ordinal order
+    # Without the tail, 100 and 483 are hot hits.
+    plain = ref.resolve(sel, history, resident, hot_valid, reserved, lru)
+    assert plain["loc"][0, 0] == 100 and plain["loc"][0, 1] == 483 and plain["loc"][0, 2] == 484
+    assert plain["tokens"].tolist() == [5000]
+    # Tail bounds outside 0 <= begin <= end <= history fail the request.
+    bad = ref.resolve(sel, history, resident, hot_valid, reserved, lru, tail=(600, 100, ring))
+    assert bad["error"] & ref.ERR_TOKEN
+
+
+def test_empty_tail_equals_no_tail():
+    rng = np.random.default_rng(17)
+    history, resident = 12288, 4096
+    hot_valid = (rng.random(resident) > 0.1).astype(np.int32)
+    lru = rng.permutation(resident)[:2048].astype(np.int64)
+    reserved = ref.reserved_from_candidates(lru, resident)
+    sel = np.stack([rng.permutation(history)[:TOPK] for _ in range(2)]).astype(np.int64)
+    a = ref.resolve(sel, history, resident, hot_valid, reserved, lru)
+    b = ref.resolve(sel, history, resident, hot_valid, reserved, lru, tail=(7000, 7000, 512))
+    assert np.array_equal(a["loc"], b["loc"]) and np.array_equal(a["tokens"], b["tokens"])
+    assert np.array_equal(a["changes"], b["changes"])
