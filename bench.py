@@ -351,6 +351,27 @@ def resident_leg(torch, kvip_amd, device, seed, rounds=24, warm=4):
     if upd.status.any() or rot.status.any():
         raise RuntimeError(f"resident forward failed: {upd.status.cpu().tolist()} {int(rot.status.item())}")
     fwd_miss = trace[warm:warm + rounds].sum(1).float().mean().item()
+
+    # The same forward loop with the speculative windowed prefetch (default budgets), on a
+    # fresh copy of the workload so that both loops start from the same state.
+    rot2, upd2, _ = synthetic.resident_workload(torch, kvip_amd, device, seed=seed, batch=batch, history=history,
+                                                resident=resident, prefetch=kvip_amd.ResidentPrefetch())
+    fwd2 = kvip_amd.LIFetch(rot2, upd2)
+    lru2 = kvip_amd.SlotLRUChains(torch, batch, resident, device, slots=upd2.lru_slots)
+    rows2 = upd2.slot_output.view(batch, -1)
+    q2 = rot2.query.view(torch.uint8)
+    trace2 = torch.zeros((n, 2, batch), dtype=torch.int32, device=device)
+
+    def prefetch_body(cursor):
+        q2.copy_(torch.index_select(queries, 0, cursor)[0])
+        fwd2()
+        lru2.commit(rows2)
+        trace2.index_copy_(0, cursor, torch.stack([upd2.miss_counts[:, 4], upd2.prefetch_counts]).view(1, 2, batch))
+
+    pf_us = _cursor_rounds(torch, prefetch_body, warm, rounds, n)
+    if upd2.status.any() or rot2.status.any():
+        raise RuntimeError(f"resident prefetch forward failed: {upd2.status.cpu().tolist()}")
+    pf_trace = trace2[warm:warm + rounds].sum(2).float().mean(0).tolist()
     host_gbs = host_read_gbs(torch, device)
     return {"workload": "c4 shape: 16 requests x 1 row, history 131072, resident 16384, misses fetched from pinned "
                         "host memory, LRU chains committed in the graph; round: TopK rows drawn ~80% hot (Zipf 1.1), "
@@ -361,7 +382,9 @@ def resident_leg(torch, kvip_amd, device, seed, rounds=24, warm=4):
             "host_read_ceiling_gbs": round(host_gbs, 1),
             "forward_us": round(fwd_us, 2), "forward_misses_per_round": round(fwd_miss, 1),
             "forward_hit_fraction": round(1.0 - fwd_miss / (batch * TOPK), 4),
-            "forward_index_gbs": round(batch * history * 132 / (fwd_us * 1e-6) / 1e9, 1), "rounds": rounds}
+            "forward_index_gbs": round(batch * history * 132 / (fwd_us * 1e-6) / 1e9, 1),
+            "prefetch_forward_us": round(pf_us, 2), "prefetch_final_misses_per_round": round(pf_trace[0], 1),
+            "prefetched_per_round": round(pf_trace[1], 1), "rounds": rounds}
 
 
 def prefill_leg(torch, kvip_amd, device, seed, iters=5):

@@ -58,6 +58,14 @@
  *                                (indexer_vector.h:584-593, :626-638)
  *   kvip_hip_resident_forward <- kvip_lifetch_streaming_forward in resident mode
  *                                (include/api.h:7, op_host/launch.cpp:76-83)
+ *   kvip_hip_resident_begin / _prefetch / _finish
+ *                             <- the same round split around the speculative windowed
+ *                                prefetch: InitializeRound + InitializeTailMappings
+ *                                (prefetch.h:25-43), FastService (prefetch.h:578-832) with
+ *                                the window scan of common/lifetch/sequence_candidates.h and
+ *                                PrefetchAllowance (common/lifetch/prefetch_budget.h:7-17),
+ *                                then the final round with PublishPrefetch (streaming.cpp:
+ *                                23-27, :119-121) and PublishPrefetchResidency (:330-339)
  *   kvip_hip_resident_workspace_bytes / kvip_hip_resident_prepare
  *                             <- the rotation scratch allocated and reset at bind time
  *                                (python/kvip/operators/lifetch/workspace.py:9-31,
@@ -72,7 +80,7 @@
 extern "C" {
 #endif
 
-#define KVIP_HIP_ABI_VERSION 10u
+#define KVIP_HIP_ABI_VERSION 11u
 
 #define KVIP_TOPK 2048
 #define KVIP_BLOCK_TOKENS 128
@@ -480,7 +488,36 @@ typedef struct KvipResidentArgs {
      * tail position). Set: hot_stride - resident (the ring slots) is a multiple of 128 and at
      * least 384 (python/kvip/operators/lifetch/binding.py:159-164). */
     const int32_t* tail_bounds;     /* [batch, 2] */
+    /* Speculative prefetch of the round, both NULL or both set: kvip_hip_resident_prefetch
+     * writes the token of every prefetch ordinal and the count per request (which then
+     * replaces `used`); kvip_hip_resident_finish resolves selected prefetched tokens to
+     * their candidate slot, applies the prefetch as the first Index-update batch and makes
+     * every prefetch slot resident. */
+    int32_t* prefetch_tokens;       /* [batch, 2048] */
+    int32_t* prefetch_counts;       /* [batch] */
 } KvipResidentArgs;
+
+/* Speculative windowed prefetch after the prefix classification (kvip_hip_resident_prefix
+ * of the same scores and candidates), for each request b: window 0 takes the victim
+ * coordinates i (candidate lru_slots[b][i] above its row's prefix threshold, any query
+ * row) in ordinal order, window e >= 1 the cold positions of [end_{e-1}, end_e), end_e =
+ * resident + 128 * floor(cold_tiles * e / max(1, windows - 1)), cold_tiles = (history -
+ * resident) / 128 (trigger_tokens, python/kvip/operators/lifetch/geometry.py:55-61), hit
+ * in any query row, in ascending order; mapped ABC tail positions are skipped; each window
+ * takes the first min(window_limit, 2048 - used, prefetch_limit - used) of its candidates
+ * as ordinals used, used + 1, ...: token -> candidate slot lru_slots[b][ordinal], its
+ * change record at the ordinal, its KV row fetched from host_pool into the hot cache.
+ * This is the reference's service when every window is serviced after scoring has passed
+ * the window's end (it caps each progress snapshot at the window boundary,
+ * op_kernel/prefetch.h:609-627); the final round repairs whatever was not prefetched. */
+typedef struct KvipPrefetchArgs {
+    const uint32_t* victim_hits;  /* [batch * rows_per_request, 64], kvip_hip_resident_prefix */
+    const uint32_t* cold_hits;    /* [batch * rows_per_request, cold_words] */
+    int32_t cold_words;           /* >= (history - resident) / 32 */
+    int32_t windows;              /* 1..32, fewer than cold_tiles */
+    int32_t window_limit;         /* 1..480 */
+    int32_t prefetch_limit;       /* 0..2048 */
+} KvipPrefetchArgs;
 
 /* Publication of appended KV pages (PageUpdates.submit, python/kvip/cache/page_updates.py:
  * 27-62; kernel _page_updates_kernel.py:8-37): for each of `count` rows {flat page index,
@@ -618,6 +655,19 @@ uint32_t kvip_hip_resident_prefix(const KvipTopkArgs* topk, const KvipPrefixClas
 uint64_t kvip_hip_resident_workspace_bytes(int32_t batch, int32_t history);
 uint32_t kvip_hip_resident_prepare(const KvipResidentArgs* args, void* stream);
 uint32_t kvip_hip_resident_round(const KvipResidentArgs* args, void* stream);
+/* kvip_hip_resident_round in two halves (round = begin then finish) with the prefetch in
+ * between: begin = initialisation (and the prefetch counts zeroed), finish = resolve,
+ * Fetch, Index update. The prefetch may run on another stream after begin and after the
+ * prefix classification; finish must follow both. */
+uint32_t kvip_hip_resident_begin(const KvipResidentArgs* args, void* stream);
+uint32_t kvip_hip_resident_prefetch(const KvipResidentArgs* args, const KvipPrefetchArgs* prefetch, void* stream);
+uint32_t kvip_hip_resident_finish(const KvipResidentArgs* args, void* stream);
+/* The first half of kvip_hip_resident_forward with the round's initialisation: owner block
+ * table, scoring of the owners' Index rows, then kvip_hip_resident_begin. A prefetching
+ * forward follows it with kvip_hip_resident_prefix + kvip_hip_resident_prefetch (possibly
+ * on a second stream), the final kvip_hip_topk, then kvip_hip_resident_finish. */
+uint32_t kvip_hip_resident_score(const KvipIndexerArgs* indexer, const KvipTopkArgs* topk,
+                                 const KvipResidentArgs* resident, void* stream);
 /* One resident-cache LIFetch step: block_table[b][j] = row_owners[b] * (history / 128) + j,
  * scoring of the owners' Index rows, TopK-2048, then kvip_hip_resident_round. */
 uint32_t kvip_hip_resident_forward(const KvipIndexerArgs* indexer, const KvipTopkArgs* topk,

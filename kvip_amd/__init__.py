@@ -14,6 +14,7 @@ __all__ = [
     "ContiguousFetch",
     "ResidentIndexUpdate",
     "ResidentPrefix",
+    "ResidentPrefetch",
     "PrefillIndexer",
     "quant_lightning_indexer",
     "MixedRound",
@@ -40,6 +41,7 @@ _EXPORTS = {
     "ContiguousFetch": ("operators.lifetch.binding", "ContiguousFetch"),
     "ResidentIndexUpdate": ("operators.lifetch.resident", "ResidentIndexUpdate"),
     "ResidentPrefix": ("operators.lifetch.resident", "ResidentPrefix"),
+    "ResidentPrefetch": ("operators.lifetch.resident", "ResidentPrefetch"),
     "PrefillIndexer": ("operators.prefill", "PrefillIndexer"),
     "quant_lightning_indexer": ("operators.prefill", "quant_lightning_indexer"),
     "MixedRound": ("operators.mixed", "MixedRound"),

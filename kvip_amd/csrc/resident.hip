@@ -49,13 +49,32 @@ struct Workspace {
     int32_t* rank;     // [batch, history] miss rank of each position, -1 = none
     int32_t* row_at;   // [batch, history] row now at each position (identity between rounds)
     int32_t* pos_of;   // [batch, history] position of each row (identity between rounds)
+    int32_t* map;      // [batch, history] prefetch ordinal of each position, -1 = none
 };
 
 KVIP_DEVICE Workspace workspace_of(const KvipResidentArgs& p) {
     const size_t n = static_cast<size_t>(p.batch) * p.history;
     uint32_t* base = static_cast<uint32_t*>(p.workspace);
     return {base, reinterpret_cast<int32_t*>(base + n), reinterpret_cast<int32_t*>(base + 2 * n),
-            reinterpret_cast<int32_t*>(base + 3 * n)};
+            reinterpret_cast<int32_t*>(base + 3 * n), reinterpret_cast<int32_t*>(base + 4 * n)};
+}
+
+// ABC tail of request b: positions [begin, end), the first T = hot_stride - resident of them
+// (p < mapped) in ring slot resident + p % T. ok = false for bounds outside the history.
+struct Tail {
+    int begin, end, mapped, ring;
+    bool ok;
+};
+KVIP_DEVICE Tail tail_of(const KvipResidentArgs& p, int b) {
+    Tail t{0, 0, 0, p.hot_stride - p.resident, true};
+    if (p.tail_bounds != nullptr) {
+        t.begin = p.tail_bounds[2 * b];
+        t.end = p.tail_bounds[2 * b + 1];
+        t.ok = 0 <= t.begin && t.begin <= t.end && t.end <= p.history;
+        if (!t.ok) t.begin = t.end = 0;
+        t.mapped = min(t.end, t.begin + t.ring);
+    }
+    return t;
 }
 
 template <typename T>
@@ -69,7 +88,7 @@ KVIP_DEVICE void store_agent(T* p, T v) {
 
 KVIP_DEVICE bool owner_ok(const KvipResidentArgs& p, int o) { return o >= 0 && o < p.owners; }
 
-// Workspace preparation: first = none, rank = none, maps = identity.
+// Workspace preparation: first = none, rank = none, maps = identity, no prefetch ordinal.
 __global__ void resident_prepare_kernel(const KvipResidentArgs p) {
     const Workspace ws = workspace_of(p);
     const size_t n = static_cast<size_t>(p.batch) * p.history;
@@ -80,6 +99,7 @@ __global__ void resident_prepare_kernel(const KvipResidentArgs p) {
         ws.rank[i] = -1;
         ws.row_at[i] = pos;
         ws.pos_of[i] = pos;
+        ws.map[i] = -1;
     }
 }
 
@@ -102,6 +122,7 @@ __global__ __launch_bounds__(kRsThreads) void resident_init_kernel(const KvipRes
         p.change_slots[static_cast<size_t>(b) * nchg + i] = i < kLru ? lru[i] : -1;
     }
     if (tid < 5) p.miss_counts[b * 5 + tid] = 0;
+    if (tid == 0 && p.prefetch_counts != nullptr) p.prefetch_counts[b] = 0;
     __syncthreads();
     for (int i = tid; i < kLru; i += kRsThreads) {
         const int s = lru[i];
@@ -138,23 +159,17 @@ __global__ __launch_bounds__(kRsThreads) void resident_resolve_kernel(const Kvip
     const int32_t* lru = p.lru_slots + static_cast<size_t>(b) * kLru;
     const int nchg = kLru + Q * kTopK;
 
-    // ABC tail [tail_begin, tail_end); its first T positions sit in ring slot R + p % T.
-    const int T = p.hot_stride - R;
-    int tail_begin = 0, tail_end = 0;
-    bool tail_ok = true;
-    if (p.tail_bounds != nullptr) {
-        tail_begin = p.tail_bounds[2 * b];
-        tail_end = p.tail_bounds[2 * b + 1];
-        tail_ok = 0 <= tail_begin && tail_begin <= tail_end && tail_end <= H;
-        if (!tail_ok) tail_begin = tail_end = 0;
-    }
-    const int tail_mapped = min(tail_end, tail_begin + T);
+    // ABC tail [tail.begin, tail.end); its first T positions sit in ring slot R + p % T.
+    const Tail tail = tail_of(p, b);
+    const bool prefetched = p.prefetch_counts != nullptr;
+    const int used = prefetched ? p.prefetch_counts[b] : p.used;
+    const int32_t* pmap = ws.map + static_cast<size_t>(b) * H;
 
     for (int i = tid; i < words; i += kRsThreads) s_bitmap[i] = 0u;
     // Errors found by the round initialisation (duplicate candidates) carry over.
     if (tid == 0) {
         s_err = static_cast<uint32_t>(p.status[b]) |
-                (owner_ok(p, o) && tail_ok ? 0u : static_cast<uint32_t>(KVIP_RESIDENT_ERR_TOKEN));
+                (owner_ok(p, o) && tail.ok ? 0u : static_cast<uint32_t>(KVIP_RESIDENT_ERR_TOKEN));
     }
     if (tid < kMaxQ) s_dest[tid] = -1;
     __syncthreads();
@@ -162,7 +177,8 @@ __global__ __launch_bounds__(kRsThreads) void resident_resolve_kernel(const Kvip
     const int32_t* hot_valid = p.hot_valid + static_cast<size_t>(good_owner ? o : 0) * R;
 
     // Classification of every query row: hot hits keep their position as slot, mapped
-    // tail positions take their ring slot (>= R: neither protected nor fetched).
+    // tail positions take their ring slot (>= R: neither protected nor fetched), prefetched
+    // positions their candidate slot (protected).
     for (int e = tid; e < Q * kTopK; e += kRsThreads) {
         const int t = p.topk[static_cast<size_t>(b) * Q * kTopK + e];
         s_sel[e] = t;
@@ -170,11 +186,19 @@ __global__ __launch_bounds__(kRsThreads) void resident_resolve_kernel(const Kvip
         if (t >= H) {
             atomicOr(&s_err, KVIP_RESIDENT_ERR_TOKEN);
         } else if (good_owner && t >= 0) {
-            if (t >= tail_begin && t < tail_end) {
-                if (t < tail_mapped) loc = R + t % T;
-            } else if (t < R && hot_valid[t] != 0 && reserved[t] < 0) {
+            const bool in_tail = t >= tail.begin && t < tail.end;
+            if (in_tail && t < tail.mapped) {
+                loc = R + t % tail.ring;
+            } else if (!in_tail && t < R && hot_valid[t] != 0 && reserved[t] < 0) {
                 loc = t;
                 atomicOr(&s_bitmap[t >> 5], 1u << (t & 31));
+            } else if (prefetched) {
+                const int k = pmap[t];
+                const int s = k >= 0 && k < used ? lru[k] : -1;
+                if (s >= 0 && s < R) {
+                    loc = s;
+                    atomicOr(&s_bitmap[s >> 5], 1u << (s & 31));
+                }
             }
         }
         s_loc[e] = loc;
@@ -226,7 +250,7 @@ __global__ __launch_bounds__(kRsThreads) void resident_resolve_kernel(const Kvip
                     const int s = lru[ord];
                     cand[k] = s;
                     ok[k] = false;
-                    if ((ord >= p.used) == (pass == 0)) {
+                    if ((ord >= used) == (pass == 0)) {
                         if (s < 0 || s >= R) {
                             atomicOr(&s_err, KVIP_RESIDENT_ERR_CANDIDATE);
                         } else {
@@ -385,15 +409,120 @@ __global__ __launch_bounds__(kRsThreads) void resident_resolve_kernel(const Kvip
     }
 }
 
-// Fetch of the missed rows: wave w of workgroup (x, b) moves ranks [32*(4x+w), +32).
+// Speculative windowed prefetch of request b (one 1024-thread workgroup): the window
+// candidates in order, the first `available` of each window taken as the next ordinals.
+// Records go to prefetch_tokens / the ordinal change records / the workspace map; the
+// rows are copied by resident_fetch_kernel<., true>.
+__global__ __launch_bounds__(kRsThreads) void resident_prefetch_kernel(const KvipResidentArgs p,
+                                                                       const KvipPrefetchArgs f) {
+    __shared__ uint32_t s_wave[kRsThreads / 64];
+    __shared__ uint32_t s_err;
+    const int b = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int Q = p.rows_per_request;
+    const int R = p.resident;
+    const int H = p.history;
+    if (p.status[b] != 0) return;  // uniform: the round already failed (count stays 0)
+    if (!owner_ok(p, p.row_owners[b])) {  // uniform; the prefetch Fetch then skips the request
+        if (tid == 0) atomicOr(&p.status[b], static_cast<int32_t>(KVIP_RESIDENT_ERR_TOKEN));
+        return;
+    }
+    const Tail tail = tail_of(p, b);
+    const int32_t* lru = p.lru_slots + static_cast<size_t>(b) * kLru;
+    int32_t* map = workspace_of(p).map + static_cast<size_t>(b) * H;
+    int32_t* tokens = p.prefetch_tokens + static_cast<size_t>(b) * kLru;
+    const int nchg = kLru + Q * kTopK;
+    int32_t* changes = p.changes + static_cast<size_t>(b) * nchg;
+    if (tid == 0) s_err = 0u;
+    __syncthreads();
+    auto mapped_tail = [&](int t) { return t >= tail.begin && t < tail.mapped; };
+    // Takes ordinal k for token t.
+    auto take = [&](int k, int t) {
+        const int s = lru[k];
+        if (s < 0 || s >= R) atomicOr(&s_err, KVIP_RESIDENT_ERR_CANDIDATE);
+        tokens[k] = t;
+        map[t] = k;
+        changes[k] = t;
+    };
+    int used = 0;  // uniform
+    const int cold_tiles = (H - R) / kBlockTokens;
+    int lo = R;
+    for (int e = 0; e < f.windows; ++e) {
+        const int available = min(f.window_limit, min(kLru - used, f.prefetch_limit - used));
+        const int hi = R + kBlockTokens * static_cast<int>(static_cast<int64_t>(cold_tiles) * e / max(1, f.windows - 1));
+        if (available <= 0) break;
+        int taken = 0;
+        if (e == 0) {
+            // Victim coordinates i = 2 tid + k, in ordinal order; candidate token lru[i].
+            uint32_t mine = 0;
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                const int i = 2 * tid + k;
+                uint32_t hit = 0;
+                for (int q = 0; q < Q; ++q) {
+                    hit |= (f.victim_hits[static_cast<size_t>(b * Q + q) * (kLru / 32) + i / 32] >> (i % 32)) & 1u;
+                }
+                const int t = lru[i];
+                if (hit != 0u && t >= 0 && t < H && !mapped_tail(t)) mine |= 1u << k;
+            }
+            uint32_t total;
+            uint32_t r = block_exclusive_scan(__popc(mine), s_wave, &total);
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                if ((mine >> k) & 1u) {
+                    if (r < static_cast<uint32_t>(available)) take(used + static_cast<int>(r), lru[2 * tid + k]);
+                    ++r;
+                }
+            }
+            taken = min(static_cast<int>(total), available);
+        } else {
+            // Cold positions [lo, hi) (128-aligned offsets from R), 32 per hit word.
+            const int w_lo = (lo - R) / 32, w_hi = min((hi - R) / 32, f.cold_words);
+            for (int w0 = w_lo; w0 < w_hi && taken < available; w0 += kRsThreads) {
+                const int w = w0 + tid;
+                uint32_t bits = 0u;
+                if (w < w_hi) {
+                    for (int q = 0; q < Q; ++q) bits |= f.cold_hits[static_cast<size_t>(b * Q + q) * f.cold_words + w];
+                    const int base = R + 32 * w;
+                    if (tail.mapped > tail.begin && base < tail.mapped && base + 32 > tail.begin) {
+                        for (int j = 0; j < 32; ++j) {
+                            if (mapped_tail(base + j)) bits &= ~(1u << j);
+                        }
+                    }
+                    if (base + 32 > H) bits &= H - base >= 32 ? 0xFFFFFFFFu : ((1u << max(H - base, 0)) - 1u);
+                }
+                uint32_t total;
+                uint32_t r = static_cast<uint32_t>(taken) + block_exclusive_scan(__popc(bits), s_wave, &total);
+                while (bits != 0u && r < static_cast<uint32_t>(available)) {
+                    const int j = __ffs(bits) - 1;
+                    take(used + static_cast<int>(r), R + 32 * w + j);
+                    ++r;
+                    bits &= bits - 1u;
+                }
+                taken = min(taken + static_cast<int>(total), available);
+            }
+            lo = hi;
+        }
+        used += taken;
+        __syncthreads();
+    }
+    if (tid == 0) {
+        p.prefetch_counts[b] = used;
+        if (s_err != 0u) atomicOr(&p.status[b], static_cast<int32_t>(s_err));
+    }
+}
+
+// Fetch of the missed rows (PREFETCH: of the prefetched rows, source = the token's KV
+// address, slot = its candidate slot): wave w of workgroup (x, b) moves ranks
+// [32*(4x+w), +32).
 constexpr int kFetchRows = 32;
-template <int PIECES>
+template <int PIECES, bool PREFETCH>
 __global__ __launch_bounds__(256) void resident_fetch_kernel(const KvipResidentArgs p) {
     const int b = blockIdx.y;
     const int lane = threadIdx.x & 63;
     const int r0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * kFetchRows;
     if (p.status[b] != 0) return;
-    const int total = p.miss_counts[b * 5 + 4];
+    const int total = PREFETCH ? p.prefetch_counts[b] : p.miss_counts[b * 5 + 4];
     if (r0 >= total) return;
     const int o = p.row_owners[b];
     const int pieces = PIECES > 0 ? PIECES : p.row_bytes / 16;
@@ -401,9 +530,19 @@ __global__ __launch_bounds__(256) void resident_fetch_kernel(const KvipResidentA
     int64_t src = -1, dst = -1;
     uint32_t err = 0;
     if (lane < rows) {
-        const size_t d = static_cast<size_t>(b) * p.rows_per_request * kTopK + r0 + lane;
-        const int64_t off = p.fetch_sources[d];
-        const int slot = p.fetch_slots[d];
+        int64_t off;
+        int slot;
+        if constexpr (PREFETCH) {
+            const int k = r0 + lane;
+            const int t = p.prefetch_tokens[static_cast<size_t>(b) * kLru + k];
+            slot = p.lru_slots[static_cast<size_t>(b) * kLru + k];
+            off = t >= 0 && t < p.history ? p.addresses[static_cast<size_t>(o) * p.history + t] : -1;
+            if (slot < 0 || slot >= p.resident) off = -1;
+        } else {
+            const size_t d = static_cast<size_t>(b) * p.rows_per_request * kTopK + r0 + lane;
+            off = p.fetch_sources[d];
+            slot = p.fetch_slots[d];
+        }
         if (off >= 0 && off <= p.host_pool_bytes - p.row_bytes && (off & 15) == 0) {
             src = off;
             dst = (static_cast<int64_t>(o) * p.hot_stride + slot) * p.row_bytes;
@@ -474,8 +613,9 @@ KVIP_DEVICE bool set_contains(const uint32_t* set, uint32_t k) {
     return false;
 }
 
-// Index update of request b, then residency of its miss slots.
-constexpr int kMaxLog = 2 * kMaxQ * kTopK;  // destinations written this round
+// Index update of request b (the prefetch batch first, then each query's misses), then
+// residency of its prefetch and miss slots.
+constexpr int kMaxLog = 2 * (kLru + kMaxQ * kTopK);  // destinations written this round
 __global__ __launch_bounds__(kRsThreads) void resident_update_kernel(const KvipResidentArgs p) {
     __shared__ uint32_t s_src_set[kSetSize];
     __shared__ uint32_t s_dst_set[kSetSize];
@@ -492,6 +632,18 @@ __global__ __launch_bounds__(kRsThreads) void resident_update_kernel(const KvipR
     const int R = p.resident;
     const int H = p.history;
     const int o = p.row_owners[b];
+    const bool prefetched = p.prefetch_counts != nullptr;
+    const int used = prefetched ? p.prefetch_counts[b] : 0;
+    const int32_t* pf_tokens = prefetched ? p.prefetch_tokens + static_cast<size_t>(b) * kLru : nullptr;
+    const int32_t* lru = p.lru_slots + static_cast<size_t>(b) * kLru;
+    if (prefetched) {
+        // The prefetch map back to its prepared state (the resolve has read it).
+        int32_t* map = workspace_of(p).map + static_cast<size_t>(b) * H;
+        for (int k = tid; k < used; k += kRsThreads) {
+            const int t = pf_tokens[k];
+            if (t >= 0 && t < H) map[t] = -1;
+        }
+    }
     if (p.status[b] != 0) {  // uniform
         // A failed request's owner loses all residency: nothing it holds is trusted, so
         // its next round reads every position cold.
@@ -517,8 +669,8 @@ __global__ __launch_bounds__(kRsThreads) void resident_update_kernel(const KvipR
     __syncthreads();
 
     int r0 = 0;
-    for (int q = 0; q < Q; ++q) {
-        const int count = p.miss_counts[b * 5 + q];
+    for (int q = prefetched ? -1 : 0; q < Q; ++q) {  // q = -1: the prefetch batch, in ordinal order
+        const int count = q < 0 ? used : p.miss_counts[b * 5 + q];
         for (int c0 = 0; c0 < count; c0 += kChunk) {
             if (s_err != 0u) break;  // uniform
             const int n = min(kChunk, count - c0);
@@ -529,8 +681,8 @@ __global__ __launch_bounds__(kRsThreads) void resident_update_kernel(const KvipR
             __syncthreads();
             int src = -1, dst = -1;
             if (tid < n) {
-                const int orig = p.fetch_positions[dbase + r0 + c0 + tid];
-                dst = p.fetch_slots[dbase + r0 + c0 + tid];
+                const int orig = q < 0 ? pf_tokens[c0 + tid] : p.fetch_positions[dbase + r0 + c0 + tid];
+                dst = q < 0 ? lru[c0 + tid] : p.fetch_slots[dbase + r0 + c0 + tid];
                 const bool in_range = orig >= 0 && orig < H && dst >= 0 && dst < R;
                 src = in_range ? pos_of[orig] : -1;
                 if (!in_range || !set_insert(s_src_set, static_cast<uint32_t>(src)) ||
@@ -590,7 +742,7 @@ __global__ __launch_bounds__(kRsThreads) void resident_update_kernel(const KvipR
             __builtin_amdgcn_s_waitcnt(0);
             __syncthreads();
         }
-        r0 += count;
+        if (q >= 0) r0 += count;
     }
     // Residency of every fetched slot (after the freed positions were invalidated). A
     // permutation rejected in a later chunk leaves the earlier chunks applied (each one a
@@ -599,6 +751,7 @@ __global__ __launch_bounds__(kRsThreads) void resident_update_kernel(const KvipR
     const int total = p.miss_counts[b * 5 + 4];
     if (s_err == 0u) {
         for (int i = tid; i < total; i += kRsThreads) hot_valid[p.fetch_slots[dbase + i]] = 1;
+        for (int k = tid; k < used; k += kRsThreads) hot_valid[lru[k]] = 1;
     } else {
         for (int s = tid; s < R; s += kRsThreads) hot_valid[s] = 0;
     }
@@ -653,28 +806,44 @@ uint32_t validate_resident(const KvipResidentArgs* a) {
                     aligned(a->workspace, 16) && (a->unpack_indices == nullptr) == (a->output_valid == nullptr) &&
                     (a->unpack_indices == nullptr || a->rows_per_request == kMaxQ) &&
                     (a->tail_bounds == nullptr ||
-                     ((a->hot_stride - a->resident) % 128 == 0 && a->hot_stride - a->resident >= 384));
+                     ((a->hot_stride - a->resident) % 128 == 0 && a->hot_stride - a->resident >= 384)) &&
+                    (a->prefetch_tokens == nullptr) == (a->prefetch_counts == nullptr);
     return ok ? KVIP_OK : KVIP_ERR_INVALID;
 }
 
-hipError_t launch_resident_round(const KvipResidentArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL(resident_init_kernel, dim3(a.batch), dim3(kRsThreads), 0, s, a);
-    hipLaunchKernelGGL(resident_resolve_kernel, dim3(a.batch), dim3(kRsThreads), 0, s, a);
-    const dim3 fgrid((a.rows_per_request * kTopK + 4 * kFetchRows - 1) / (4 * kFetchRows), a.batch);
+template <bool PREFETCH>
+void launch_resident_fetch(const KvipResidentArgs& a, hipStream_t s) {
+    const int rows = PREFETCH ? kLru : a.rows_per_request * kTopK;
+    const dim3 fgrid((rows + 4 * kFetchRows - 1) / (4 * kFetchRows), a.batch);
     if (a.row_bytes == KVIP_KV_ROW_BYTES) {
-        hipLaunchKernelGGL(resident_fetch_kernel<KVIP_KV_ROW_BYTES / 16>, fgrid, dim3(256), 0, s, a);
+        hipLaunchKernelGGL((resident_fetch_kernel<KVIP_KV_ROW_BYTES / 16, PREFETCH>), fgrid, dim3(256), 0, s, a);
     } else {
-        hipLaunchKernelGGL(resident_fetch_kernel<0>, fgrid, dim3(256), 0, s, a);
+        hipLaunchKernelGGL((resident_fetch_kernel<0, PREFETCH>), fgrid, dim3(256), 0, s, a);
     }
+}
+
+hipError_t launch_resident_begin(const KvipResidentArgs& a, hipStream_t s) {
+    hipLaunchKernelGGL(resident_init_kernel, dim3(a.batch), dim3(kRsThreads), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_resident_finish(const KvipResidentArgs& a, hipStream_t s) {
+    hipLaunchKernelGGL(resident_resolve_kernel, dim3(a.batch), dim3(kRsThreads), 0, s, a);
+    launch_resident_fetch<false>(a, s);
     hipLaunchKernelGGL(resident_update_kernel, dim3(a.batch), dim3(kRsThreads), 0, s, a);
     return hipGetLastError();
+}
+
+hipError_t launch_resident_round(const KvipResidentArgs& a, hipStream_t s) {
+    const hipError_t e = launch_resident_begin(a, s);
+    return e != hipSuccess ? e : launch_resident_finish(a, s);
 }
 
 }  // namespace kvip
 
 extern "C" uint64_t kvip_hip_resident_workspace_bytes(int32_t batch, int32_t history) {
     if (batch < 1 || history < 1) return 0;
-    return 16ull * static_cast<uint64_t>(batch) * static_cast<uint64_t>(history);
+    return 20ull * static_cast<uint64_t>(batch) * static_cast<uint64_t>(history);
 }
 
 extern "C" uint32_t kvip_hip_resident_prepare(const KvipResidentArgs* args, void* stream) {
@@ -691,8 +860,62 @@ extern "C" uint32_t kvip_hip_resident_round(const KvipResidentArgs* args, void* 
     return static_cast<uint32_t>(kvip::launch_resident_round(*args, static_cast<hipStream_t>(stream)));
 }
 
+extern "C" uint32_t kvip_hip_resident_begin(const KvipResidentArgs* args, void* stream) {
+    const uint32_t rc = kvip::validate_resident(args);
+    if (rc != KVIP_OK) return rc;
+    return static_cast<uint32_t>(kvip::launch_resident_begin(*args, static_cast<hipStream_t>(stream)));
+}
+
+extern "C" uint32_t kvip_hip_resident_finish(const KvipResidentArgs* args, void* stream) {
+    const uint32_t rc = kvip::validate_resident(args);
+    if (rc != KVIP_OK) return rc;
+    return static_cast<uint32_t>(kvip::launch_resident_finish(*args, static_cast<hipStream_t>(stream)));
+}
+
+extern "C" uint32_t kvip_hip_resident_prefetch(const KvipResidentArgs* args, const KvipPrefetchArgs* f,
+                                               void* stream) {
+    const uint32_t rc = kvip::validate_resident(args);
+    if (rc != KVIP_OK) return rc;
+    if (f == nullptr || args->prefetch_tokens == nullptr) return KVIP_ERR_INVALID;
+    const int cold_tiles = (args->history - args->resident) / kvip::kBlockTokens;
+    const bool ok = f->victim_hits != nullptr && f->cold_hits != nullptr && args->resident % kvip::kBlockTokens == 0 &&
+                    f->windows >= 1 && f->windows <= 32 && cold_tiles > f->windows && f->window_limit >= 1 &&
+                    f->window_limit <= 480 && f->prefetch_limit >= 0 && f->prefetch_limit <= kvip::kLru &&
+                    static_cast<int64_t>(f->cold_words) * 32 >= static_cast<int64_t>(args->history) - args->resident;
+    if (!ok) return KVIP_ERR_INVALID;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(kvip::resident_prefetch_kernel, dim3(args->batch), dim3(kvip::kRsThreads), 0, s, *args, *f);
+    kvip::launch_resident_fetch<true>(*args, s);
+    return static_cast<uint32_t>(hipGetLastError());
+}
+
+namespace kvip {
+// Owner block table, then the scoring of the owners' Index rows (the first half of
+// kvip_hip_resident_forward); KVIP_ERR_INVALID when the three argument blocks do not chain.
+static uint32_t resident_score(const KvipIndexerArgs* indexer, const KvipTopkArgs* topk,
+                               const KvipResidentArgs* resident, hipStream_t s);
+}  // namespace kvip
+
+extern "C" uint32_t kvip_hip_resident_score(const KvipIndexerArgs* indexer, const KvipTopkArgs* topk,
+                                            const KvipResidentArgs* resident, void* stream) {
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    const uint32_t rc = kvip::resident_score(indexer, topk, resident, s);
+    if (rc != KVIP_OK) return rc;
+    return static_cast<uint32_t>(kvip::launch_resident_begin(*resident, s));
+}
+
 extern "C" uint32_t kvip_hip_resident_forward(const KvipIndexerArgs* indexer, const KvipTopkArgs* topk,
                                               const KvipResidentArgs* resident, void* stream) {
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    const uint32_t rc = kvip::resident_score(indexer, topk, resident, s);
+    if (rc != KVIP_OK) return rc;
+    const hipError_t e = kvip::launch_topk(*topk, s);
+    if (e != hipSuccess) return static_cast<uint32_t>(e);
+    return static_cast<uint32_t>(kvip::launch_resident_round(*resident, s));
+}
+
+uint32_t kvip::resident_score(const KvipIndexerArgs* indexer, const KvipTopkArgs* topk,
+                              const KvipResidentArgs* resident, hipStream_t s) {
     if (indexer == nullptr || topk == nullptr || resident == nullptr) return KVIP_ERR_INVALID;
     if (kvip::validate_indexer(indexer) != KVIP_OK || kvip::validate_topk(topk) != KVIP_OK ||
         kvip::validate_resident(resident) != KVIP_OK) {
@@ -710,16 +933,11 @@ extern "C" uint32_t kvip_hip_resident_forward(const KvipIndexerArgs* indexer, co
                          li.scale_block_stride == kvip::kBlockTokens && li.max_blocks >= blocks_per_owner &&
                          li.num_blocks == ra.owners * blocks_per_owner && li.qk_dtype == KVIP_DTYPE_FP8_E4M3;
     if (!chained) return KVIP_ERR_INVALID;
-    const hipStream_t s = static_cast<hipStream_t>(stream);
     hipLaunchKernelGGL(kvip::owner_table_kernel, dim3((li.max_blocks + 255) / 256, li.batch), dim3(256), 0, s,
                        const_cast<int32_t*>(li.block_table), ra.row_owners, li.batch, li.max_blocks, blocks_per_owner);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return static_cast<uint32_t>(e);
-    e = kvip::launch_indexer(li, s);
-    if (e != hipSuccess) return static_cast<uint32_t>(e);
-    e = kvip::launch_topk(*topk, s);
-    if (e != hipSuccess) return static_cast<uint32_t>(e);
-    return static_cast<uint32_t>(kvip::launch_resident_round(ra, s));
+    return static_cast<uint32_t>(kvip::launch_indexer(li, s));
 }
 
 namespace kvip {
@@ -727,6 +945,7 @@ namespace {
 
 constexpr int kPcThreads = 256;
 
+// Threshold and victim bits of query row blockIdx.x.
 __global__ __launch_bounds__(kPcThreads) void prefix_classify_kernel(const KvipPrefixClassifyArgs p) {
     __shared__ uint32_t s_min[kPcThreads / 64];
     const int row = blockIdx.x;
@@ -767,16 +986,43 @@ __global__ __launch_bounds__(kPcThreads) void prefix_classify_kernel(const KvipP
         }
         p.victim_hits[static_cast<size_t>(row) * (kTopK / 32) + tid] = word;
     }
-    // Cold bits: position resident + 32 w + k.
-    for (int w = tid; w < p.cold_words; w += kPcThreads) {
-        uint32_t word = 0u;
+}
+
+// Cold bits of query row blockIdx.y, words [256 x, 256 x + 256): position resident + 32 w + k
+// above the row's threshold. One word per thread, its 32 keys read as four 16-byte pieces
+// when the word is aligned and complete.
+__global__ __launch_bounds__(kPcThreads) void cold_hits_kernel(const KvipPrefixClassifyArgs p) {
+    const int row = blockIdx.y;
+    const int b = row / p.rows_per_request;
+    const int w = blockIdx.x * kPcThreads + threadIdx.x;
+    if (w >= p.cold_words) return;
+    int valid = max(p.seq_lens[b], 0);
+    if (p.query_ends != nullptr) valid = min(valid, p.query_ends[row]);
+    valid = min(max(valid, 0), p.key_stride);
+    const uint32_t thr = p.thresholds[row];
+    const uint16_t* keys = p.score_keys + static_cast<size_t>(row) * p.key_stride;
+    const int pos0 = p.resident + 32 * w;
+    uint32_t word = 0u;
+    if (pos0 + 32 <= valid && (pos0 & 7) == 0 && (p.key_stride & 7) == 0 &&
+        (reinterpret_cast<uintptr_t>(p.score_keys) & 15) == 0) {
+        const v4i* src = reinterpret_cast<const v4i*>(keys + pos0);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const v4i x = src[v];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const uint32_t key = (static_cast<uint32_t>(x[k >> 1]) >> (16 * (k & 1))) & 0xFFFFu;
+                word |= (key > thr ? 1u : 0u) << (8 * v + k);
+            }
+        }
+    } else {
         for (int k = 0; k < 32; ++k) {
-            const int pos = p.resident + 32 * w + k;
+            const int pos = pos0 + k;
             const bool hit = pos < valid && static_cast<uint32_t>(keys[pos]) > thr;
             word |= (hit ? 1u : 0u) << k;
         }
-        p.cold_hits[static_cast<size_t>(row) * p.cold_words + w] = word;
     }
+    p.cold_hits[static_cast<size_t>(row) * p.cold_words + w] = word;
 }
 
 }  // namespace
@@ -798,5 +1044,10 @@ extern "C" uint32_t kvip_hip_resident_prefix(const KvipTopkArgs* topk, const Kvi
     if (e != hipSuccess) return static_cast<uint32_t>(e);
     hipLaunchKernelGGL(kvip::prefix_classify_kernel, dim3(c.batch * c.rows_per_request), dim3(kvip::kPcThreads), 0, s,
                        c);
+    if (c.cold_words > 0) {
+        hipLaunchKernelGGL(kvip::cold_hits_kernel,
+                           dim3((c.cold_words + kvip::kPcThreads - 1) / kvip::kPcThreads, c.batch * c.rows_per_request),
+                           dim3(kvip::kPcThreads), 0, s, c);
+    }
     return static_cast<uint32_t>(hipGetLastError());
 }

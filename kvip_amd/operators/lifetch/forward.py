@@ -13,7 +13,7 @@ import ctypes
 
 from kvip_amd.runtime import abi
 from kvip_amd.operators.lifetch.binding import ContiguousFetch, LIFetchBinding
-from kvip_amd.operators.lifetch.resident import ResidentIndexUpdate
+from kvip_amd.operators.lifetch.resident import ResidentIndexUpdate, ResidentPrefix
 
 
 class LIFetchForward:
@@ -49,6 +49,20 @@ class LIFetchForward:
             self.resident_args = update.args
             self._refs = (ctypes.byref(self.indexer_args), ctypes.byref(self.topk_args),
                           ctypes.byref(self.resident_args))
+            self.prefix = None
+            if update.prefetch is not None:
+                torch = self.torch
+                self.prefix = ResidentPrefix(torch, rotating, update.lru_slots, update.resident)
+                pf = update.prefetch
+                self.prefetch_args = abi.PrefetchArgs(
+                    victim_hits=abi.ptr(self.prefix.victim_hits), cold_hits=abi.ptr(self.prefix.cold_hits),
+                    cold_words=self.prefix.cold_words, windows=pf.windows, window_limit=pf.window_limit,
+                    prefetch_limit=pf.prefetch_limit)
+                self._prefetch_ref = ctypes.byref(self.prefetch_args)
+                # The prefetch branch: its own stream (default priority), forked after the
+                # scoring and joined before the final round.
+                self.side = torch.cuda.Stream(device=rotating.device)
+                self.scored, self.prefetched = torch.cuda.Event(), torch.cuda.Event()
             return
         self.args = abi.LIFetchArgs(rotating.indexer_args(), rotating.topk_args(), update.fetch_args(),
                                     abi.ptr(rotating.round_work) if fused else 0)
@@ -81,7 +95,23 @@ class LIFetchForward:
 
     def __call__(self):
         if self.resident:
-            abi.check(self.library.kvip_hip_resident_forward(*self._refs, self._stream()), "resident LIFetch forward")
+            if self.prefix is None:
+                abi.check(self.library.kvip_hip_resident_forward(*self._refs, self._stream()),
+                          "resident LIFetch forward")
+                return
+            torch, lib = self.torch, self.library
+            main = torch.cuda.current_stream(self.rotating.device)
+            abi.check(lib.kvip_hip_resident_score(*self._refs, main.cuda_stream), "resident scoring")
+            self.scored.record(main)
+            self.side.wait_event(self.scored)
+            abi.check(lib.kvip_hip_resident_prefix(ctypes.byref(self.prefix.topk_args), ctypes.byref(self.prefix.args),
+                                                   self.side.cuda_stream), "resident prefix")
+            abi.check(lib.kvip_hip_resident_prefetch(self._refs[2], self._prefetch_ref, self.side.cuda_stream),
+                      "resident prefetch")
+            self.prefetched.record(self.side)
+            abi.check(lib.kvip_hip_topk(self._refs[1], main.cuda_stream), "TopK")
+            main.wait_event(self.prefetched)
+            abi.check(lib.kvip_hip_resident_finish(self._refs[2], main.cuda_stream), "resident round")
             return
         abi.check(self.library.kvip_hip_lifetch_forward(self._args_ref, self._stream()), "LIFetch forward")
 

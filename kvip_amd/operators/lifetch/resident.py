@@ -20,7 +20,13 @@ multiple of 128 and at least 384).
 The forward enqueues, on the current stream and without host synchronisation: the
 owner block table, LI scoring of the owners' Index rows, TopK-2048 per query row, and the
 round of kvip_hip_resident_round (init, resolve, Fetch from the host pool, Index update,
-residency). Per-step inputs are `rotating.lru_slots` ([batch, 2048] victim candidates,
+residency). With `prefetch` (a ResidentPrefetch) the forward also runs the speculative
+windowed prefetch (the reference's FastService, op_kernel/prefetch.h:578-832) on a second
+stream while the final TopK runs: the prefix TopK of the hot positions gives each query
+row a threshold, and the candidates and cold positions above it are fetched ahead into
+LRU candidate slots; the final round then resolves selected prefetched tokens to those
+slots and fetches only the rest. Outputs (logical ids, and the KV bytes behind every slot)
+are those of the round without prefetch. Per-step inputs are `rotating.lru_slots` ([batch, 2048] victim candidates,
 oldest first, e.g. ``SlotLRU.slots``) plus the query buffers of the binding. Device
 errors land in `status` ([batch] int32, KVIP_RESIDENT_ERR_* bits).
 """
@@ -34,9 +40,27 @@ from kvip_amd.operators.lifetch.binding import BLOCK_TOKENS, INDEX_DIM, TOPK
 LRU_SLOTS = abi.RESIDENT_LRU_SLOTS
 
 
+class ResidentPrefetch:
+    """Budgets of the speculative windowed prefetch (python/kvip/operators/lifetch/
+    geometry.py:4-13 prefetch_budget, :55-61 trigger_tokens): `windows` windows (the first
+    takes the victim candidates, the others the cold range split at the 128-aligned trigger
+    boundaries), at most `window_limit` fetches per window (default prefetch_limit //
+    windows) and `prefetch_limit` per request and round."""
+
+    def __init__(self, windows=8, prefetch_limit=512, window_limit=None):
+        if type(windows) is not int or not 1 <= windows <= 32:
+            raise ValueError("Prefetch requires 1..32 windows")
+        if window_limit is None:
+            window_limit = max(1, prefetch_limit // windows)
+        if not 0 <= prefetch_limit <= LRU_SLOTS or not 1 <= window_limit <= 480:
+            raise ValueError("Invalid prefetch budgets: total must be 0..2048 and window 1..480")
+        self.windows, self.prefetch_limit, self.window_limit = windows, int(prefetch_limit), int(window_limit)
+
+
 class ResidentIndexUpdate:
     def __init__(self, torch, *, keys, scales, addresses, logical_ids, row_owners, rotating, hot_valid, hot_cache,
-                 host_pool, resident, status=None, outputs=None, used=0, query_inputs=None, tail_bounds=None):
+                 host_pool, resident, status=None, outputs=None, used=0, query_inputs=None, tail_bounds=None,
+                 prefetch=None):
         self.torch, self.rotating, self.device = torch, rotating, rotating.device
         if keys.dim() != 3 or keys.shape[2] != INDEX_DIM or keys.dtype != torch.float8_e4m3fn or not keys.is_contiguous():
             raise ValueError("Index keys must be contiguous float8_e4m3fn [owners, history, 128]")
@@ -77,6 +101,13 @@ class ResidentIndexUpdate:
                 raise ValueError("ABC tail bounds need hot-cache ring slots after the hot ones: hot_cache.shape[1] "
                                  "- resident must be a multiple of 128 and at least 384")
         self.tail_bounds = tail_bounds
+        if prefetch is not None:
+            if not isinstance(prefetch, ResidentPrefetch):
+                raise ValueError("prefetch must be a ResidentPrefetch")
+            if resident % BLOCK_TOKENS or (history - resident) // BLOCK_TOKENS <= prefetch.windows:
+                raise ValueError("prefetch needs a 128-aligned resident range and more cold 128-token tiles "
+                                 "than windows")
+        self.prefetch = prefetch
         if any(t.device != dev for t in (keys, scales, addresses, logical_ids, row_owners, hot_valid, hot_cache)):
             raise ValueError("Index storage, hot cache and the LIFetch binding must share one device")
         self.keys, self.scales, self.addresses, self.logical_ids = keys, scales, addresses, logical_ids
@@ -102,6 +133,11 @@ class ResidentIndexUpdate:
         self.fetch_sources = torch.zeros((b, q * TOPK), dtype=torch.int64, device=dev)
         self.fetch_slots = torch.zeros((b, q * TOPK), dtype=torch.int32, device=dev)
         self.fetch_positions = torch.zeros((b, q * TOPK), dtype=torch.int32, device=dev)
+        # Prefetch records: the token of every prefetch ordinal and the count per request.
+        self.prefetch_tokens = self.prefetch_counts = None
+        if prefetch is not None:
+            self.prefetch_tokens = torch.full((b, LRU_SLOTS), -1, dtype=torch.int32, device=dev)
+            self.prefetch_counts = torch.zeros(b, dtype=torch.int32, device=dev)
         lib = abi.load_library()
         nbytes = int(lib.kvip_hip_resident_workspace_bytes(b, history))
         self.workspace = torch.empty(nbytes, dtype=torch.uint8, device=dev)
@@ -134,7 +170,8 @@ class ResidentIndexUpdate:
             row_bytes=int(self.hot_cache.shape[2]), used=self.used,
             unpack_indices=p(self.query_inputs.unpack_indices) if self.query_inputs is not None else 0,
             output_valid=p(self.query_inputs.output_valid) if self.query_inputs is not None else 0,
-            tail_bounds=p(self.tail_bounds),
+            tail_bounds=p(self.tail_bounds), prefetch_tokens=p(self.prefetch_tokens),
+            prefetch_counts=p(self.prefetch_counts),
         )
 
 

@@ -9,7 +9,7 @@ import ctypes
 from pathlib import Path
 
 LIBRARY = Path(__file__).resolve().parents[1] / "_lib" / "libkvip_hip.so"
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 KVIP_OK = 0
 KVIP_ERR_INVALID = 100000
@@ -157,7 +157,7 @@ class ResidentArgs(ctypes.Structure):
         ("workspace", _p), ("host_pool_bytes", _i64),
         ("batch", _i32), ("rows_per_request", _i32), ("owners", _i32), ("history", _i32), ("resident", _i32),
         ("hot_stride", _i32), ("row_bytes", _i32), ("used", _i32), ("unpack_indices", _p), ("output_valid", _p),
-        ("tail_bounds", _p),
+        ("tail_bounds", _p), ("prefetch_tokens", _p), ("prefetch_counts", _p),
     ]
 
 
@@ -167,6 +167,13 @@ class PrefixClassifyArgs(ctypes.Structure):
         ("thresholds", _p), ("victim_hits", _p), ("cold_hits", _p),
         ("batch", _i32), ("rows_per_request", _i32), ("key_stride", _i32), ("resident", _i32), ("cold_words", _i32),
         ("reserved", _i32),
+    ]
+
+
+class PrefetchArgs(ctypes.Structure):
+    _fields_ = [
+        ("victim_hits", _p), ("cold_hits", _p), ("cold_words", _i32), ("windows", _i32), ("window_limit", _i32),
+        ("prefetch_limit", _i32),
     ]
 
 
@@ -216,6 +223,11 @@ PROTOTYPES = {
     "kvip_hip_resident_workspace_bytes": ([_i32, _i32], ctypes.c_uint64),
     "kvip_hip_resident_prepare": ([ctypes.POINTER(ResidentArgs), _p], ctypes.c_uint32),
     "kvip_hip_resident_round": ([ctypes.POINTER(ResidentArgs), _p], ctypes.c_uint32),
+    "kvip_hip_resident_begin": ([ctypes.POINTER(ResidentArgs), _p], ctypes.c_uint32),
+    "kvip_hip_resident_finish": ([ctypes.POINTER(ResidentArgs), _p], ctypes.c_uint32),
+    "kvip_hip_resident_prefetch": ([ctypes.POINTER(ResidentArgs), ctypes.POINTER(PrefetchArgs), _p], ctypes.c_uint32),
+    "kvip_hip_resident_score": ([ctypes.POINTER(IndexerArgs), ctypes.POINTER(TopkArgs), ctypes.POINTER(ResidentArgs),
+                                 _p], ctypes.c_uint32),
     "kvip_hip_resident_forward": ([ctypes.POINTER(IndexerArgs), ctypes.POINTER(TopkArgs), ctypes.POINTER(ResidentArgs),
                                    _p], ctypes.c_uint32),
 }

@@ -351,13 +351,14 @@ def lidu_workload(torch, device, *, seed=2026, batch=16, queries=4, budget=16384
 
 
 def resident_workload(torch, kvip, device, *, seed=2026, batch=16, history=131072, resident=16384, q_rows=1,
-                      heads=64, fill_pool=False):
+                      heads=64, fill_pool=False, prefetch=None):
     """BASELINE config 4 shape for the resident-cache round: `batch` requests, each owning
     `history` Index rows (fp8 keys ~ random finite codes, scales U(0.5, 2)) and a hot
     cache of `resident` slots holding positions 0..resident-1; every row's KV lives in a
     pinned host pool (random bytes with fill_pool, the hot cache then holding each owner's
-    first `resident` rows; else uninitialised, enough for timing). Returns (rotating,
-    update, forward)."""
+    first `resident` rows; else uninitialised, enough for timing); prefetch: a
+    ResidentPrefetch for the speculative windowed prefetch. Returns (rotating, update,
+    forward)."""
     g = torch.Generator(device=device).manual_seed(seed)
     owners = batch
     keys = (torch.randint(0, 256, (owners, history, 128), generator=g, device=device, dtype=torch.uint8) & 0x77)
@@ -379,7 +380,8 @@ def resident_workload(torch, kvip, device, *, seed=2026, batch=16, history=13107
     rot.query_ends.fill_(history)
     upd = kvip.ResidentIndexUpdate(torch, keys=keys, scales=scales, addresses=addresses, logical_ids=logical,
                                    row_owners=torch.arange(batch, dtype=torch.int32, device=device), rotating=rot,
-                                   hot_valid=valid, hot_cache=hot, host_pool=pool, resident=resident)
+                                   hot_valid=valid, hot_cache=hot, host_pool=pool, resident=resident,
+                                   prefetch=prefetch)
     return rot, upd, kvip.LIFetch(rot, upd)
 
 

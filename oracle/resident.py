@@ -45,9 +45,23 @@ before anything is resolved, and a request that fails before the Fetch publishes
 both outputs (the reference publishes its outputs per query and signals errors through
 status alone).
 
-Scope of this restatement: no speculative prefetch (`used` candidates consumed by an
-earlier window are supported by the two allocation passes, but no prefetch mapping is
-consulted); the only mapping entries are those of the ABC tail.
+  prefetch   prefetch.h:578-832 (FastService), common/lifetch/sequence_candidates.h (the
+             window's hit scan: victim coordinates [0, 2048) -> lru[i], then cold positions
+             in ascending order, union over the query rows), prefetch.h:660-700
+             (GatherCandidateMap + CompactMisses: already-mapped tokens skipped, the first
+             `available` taken), common/lifetch/prefetch_budget.h:7-17 (PrefetchAllowance),
+             python/kvip/operators/lifetch/geometry.py:4-13 (prefetch_budget), :55-61
+             (trigger_tokens: window ends), prefetch.h:563-574 (PrepareCandidateWqes: slot
+             resident + ordinal, mapping, RecordChange), streaming.cpp:23-27, :119-121
+             (PublishPrefetch: the prefetch records are the first Index-update batch),
+             streaming.cpp:330-339 (PublishPrefetchResidency)
+
+Prefetch is restated for the case the reference reduces to when every window is serviced
+after scoring has passed the window's end (its service caps each snapshot at the scheduled
+boundary, prefetch.h:609-627): window 0 holds the victim candidates, window e >= 1 the cold
+positions [end_{e-1}, end_e). When the service runs ahead of scoring the reference
+prefetches a timing-dependent subset; the final round repairs whatever was not prefetched,
+so the selected KV rows and logical outputs do not depend on it.
 """
 from __future__ import annotations
 
@@ -114,7 +128,58 @@ def classify(selected, history, resident, hot_valid, reserved, tail=None):
     return loc, protect, err
 
 
-def resolve(selected, history, resident, hot_valid, reserved, lru, used=0, sources=None, tail=None):
+def prefetch_windows(resident, history, windows):
+    """Window ends: trigger_tokens (geometry.py:55-61) with `windows` rounds: resident (the
+    hot-ready first window), then evenly spaced 128-aligned cold boundaries up to history."""
+    cold_tiles = (history - resident) // 128
+    return [resident + 128 * (cold_tiles * e // max(1, windows - 1)) for e in range(windows)]
+
+
+def prefetch_budget(prefetch_limit=512, window_limit=None, windows=8):
+    """(prefetch_limit, window_limit) as geometry.py:4-13 derives them."""
+    if window_limit is None:
+        window_limit = max(1, prefetch_limit // windows)
+    if not 0 <= prefetch_limit <= LRU_SLOTS or not 1 <= window_limit <= 480:
+        raise ValueError("Invalid prefetch budgets: total must be 0..2048 and window 1..480")
+    return prefetch_limit, window_limit
+
+
+def prefetch(victim_hits, cold_hits, lru, history, resident, tail=None, windows=8, prefetch_limit=512,
+             window_limit=None):
+    """Speculative windowed prefetch of one request. victim_hits bool [Q, 2048]: candidate
+    ordinal i scores above its row's prefix threshold; cold_hits bool [Q, >= history -
+    resident]: position resident + j does (oracle.resident.prefix_classify, per query row).
+    Window 0 takes victim coordinates i in order (token lru[i]); window e >= 1 the cold
+    positions of [end_{e-1}, end_e) in order; a token hit by any row counts once; tokens
+    already mapped (earlier windows, the ABC tail's first positions) are skipped; each
+    window takes the first min(missing, PrefetchAllowance) of them. Returns [(token,
+    ordinal)] in ordinal order (ordinal k is candidate slot lru[k])."""
+    prefetch_limit, window_limit = prefetch_budget(prefetch_limit, window_limit, windows)
+    ends = prefetch_windows(resident, history, windows)
+    mapped = set()
+    out = []
+    victim_any = np.asarray(victim_hits, bool).any(axis=0)
+    cold_any = np.asarray(cold_hits, bool).any(axis=0)
+    begin = resident
+    for e, end in enumerate(ends):
+        if e == 0:
+            cands = [int(lru[i]) for i in range(LRU_SLOTS) if victim_any[i]]
+        else:
+            cands = [resident + j for j in range(begin - resident, end - resident) if cold_any[j]]
+            begin = end
+        missing = [t for t in cands if t not in mapped and tail_slot(t, tail)[1] is None]
+        used = len(out)
+        # PrefetchAllowance (prefetch_budget.h:7-17): window limit, LRU slots left, prefetch
+        # limit left (one request per token; no transport-queue limit here).
+        available = max(0, min(window_limit, LRU_SLOTS - used, prefetch_limit - used))
+        for t in missing[:available]:
+            mapped.add(t)
+            out.append((t, len(out)))
+    return out
+
+
+def resolve(selected, history, resident, hot_valid, reserved, lru, used=0, sources=None, tail=None,
+            prefetched=None):
     """Per-query miss resolution of one request (StagedQuery). Returns a dict with
     loc [Q, 2048] (hot slot of every selected position, -1 for empty entries), slots
     [misses] (slot of each miss rank), tokens [misses] (position of each miss rank),
@@ -123,9 +188,29 @@ def resolve(selected, history, resident, hot_valid, reserved, lru, used=0, sourc
     sources = (addresses [history], pool_bytes, row_bytes): every new miss's KV address is
     checked against the host pool as its query is resolved (ERR_SOURCE), before any
     Fetch; this check is this build's own (the reference's transport validates its
-    descriptors, cache_metadata.h:32-44). tail: the ABC tail, as for classify."""
+    descriptors, cache_metadata.h:32-44). tail: the ABC tail, as for classify.
+    prefetched: [(token, ordinal)] of this round's prefetch (then `used` is their count):
+    a selected token that is neither a hot hit nor a mapped tail position but was
+    prefetched resolves to its candidate slot lru[ordinal] and protects it
+    (staged_topk_classify.h:28-31 via ResolvePhysicalSlot); its change record is the
+    prefetch's (RecordChange at the ordinal) until a final miss takes that ordinal again."""
     q_rows = selected.shape[0]
     loc, protect, err = classify(selected, history, resident, hot_valid, reserved, tail)
+    pmap = {} if prefetched is None else {int(t): int(k) for t, k in prefetched}
+    if prefetched is not None:
+        used = len(prefetched)
+        for q in range(q_rows):
+            for i in range(TOPK):
+                t = int(selected[q, i])
+                if loc[q, i] >= 0 or t not in pmap or (q >= 2 and t == int(selected[q - 2, i])):
+                    continue
+                s = int(lru[pmap[t]])
+                if 0 <= s < resident:
+                    loc[q, i] = s
+                    protect[s] = True
+        for q in range(2, q_rows):  # the same-position shortcut copies the resolved slot
+            same = selected[q] == selected[q - 2]
+            loc[q, same] = loc[q - 2, same]
     in_range = [int(s) for s in lru[:LRU_SLOTS] if 0 <= s < resident]
     if len(set(in_range)) != len(in_range):
         err |= ERR_CANDIDATE  # a hot slot named by two candidates
@@ -137,6 +222,10 @@ def resolve(selected, history, resident, hot_valid, reserved, lru, used=0, sourc
     changes = np.full(LRU_SLOTS + q_rows * TOPK, EMPTY, np.int64)
     change_slots = np.full(LRU_SLOTS + q_rows * TOPK, EMPTY, np.int64)
     change_slots[:LRU_SLOTS] = lru[:LRU_SLOTS]
+    for t, k in pmap.items():
+        if not 0 <= int(lru[k]) < resident:
+            err |= ERR_CANDIDATE  # a prefetch slot outside the hot range
+        changes[k] = t
     for q in range(q_rows):
         if err:
             break
@@ -271,15 +360,25 @@ def _permute(batches, history, resident, keys, scales, hot_valid, row_at, pos_of
 
 
 def resident_round(selected, history, resident, keys, scales, addresses, logical, hot_valid, reserved, lru,
-                   hot_cache, host_pool, used=0, tail=None):
+                   hot_cache, host_pool, used=0, tail=None, prefetched=None):
     """One request's full round after TopK, in place on its tables: resolve, outputs,
     Fetch (hot_cache[slot] = host_pool[addresses[token]]), Index update, residency
     publication. Returns (logical_output [Q, 2048], slot_output [Q, 2048], resolve dict,
     error bits). A failed request's owner loses all residency (hot_valid cleared); when
     it fails before the Fetch both outputs are -1 and nothing else changes. tail: the ABC
-    tail (begin, end, ring_slots), as for classify."""
+    tail (begin, end, ring_slots), as for classify. prefetched: [(token, ordinal)] of this
+    round's prefetch (oracle.resident.prefetch): their rows were fetched into lru[ordinal]
+    before the final resolution, they form the first Index-update batch (ordinal order,
+    streaming.cpp:119-121) and every prefetch slot becomes resident (streaming.cpp:330-339)."""
+    row_bytes = hot_cache.shape[1]
+    pre = [] if prefetched is None else [(int(t), int(k)) for t, k in prefetched]
+    for t, k in pre:  # the prefetch Fetch happens before the final resolution
+        s = int(lru[k])
+        a = int(addresses[t])
+        if 0 <= s < resident and 0 <= a <= host_pool.size - row_bytes and a % 16 == 0:
+            hot_cache[s] = host_pool[a:a + row_bytes]
     res = resolve(selected, history, resident, hot_valid, reserved, lru, used,
-                  sources=(addresses, host_pool.size, hot_cache.shape[1]), tail=tail)
+                  sources=(addresses, host_pool.size, hot_cache.shape[1]), tail=tail, prefetched=prefetched)
     q_rows = selected.shape[0]
     if res["error"]:
         hot_valid[:] = 0
@@ -291,11 +390,12 @@ def resident_round(selected, history, resident, keys, scales, addresses, logical
             t = int(selected[q, i])
             if 0 <= t < history:
                 logical_out[q, i] = logical[t]
-    row_bytes = hot_cache.shape[1]
     for t, s in zip(res["tokens"], res["slots"]):
         a = int(addresses[t])
         hot_cache[s] = host_pool[a:a + row_bytes]
     batches, r = [], 0
+    if pre:
+        batches.append([(t, int(lru[k])) for t, k in pre])
     for n in res["added"]:
         batches.append([(int(res["tokens"][r + k]), int(res["slots"][r + k])) for k in range(n)])
         r += n
@@ -305,6 +405,8 @@ def resident_round(selected, history, resident, keys, scales, addresses, logical
         return logical_out, res["loc"], res, err
     for s in res["slots"]:
         hot_valid[s] = 1
+    for t, k in pre:
+        hot_valid[int(lru[k])] = 1
     return logical_out, res["loc"], res, 0
 
 

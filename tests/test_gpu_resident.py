@@ -33,7 +33,7 @@ class Setup:
     holding positions 0..resident-1, and a resident-mode LIFetch binding."""
 
     def __init__(self, torch, *, batch, owners, history, resident, q_rows, seed, heads=64, invalid=0.0,
-                 row_owners=None, ring=0):
+                 row_owners=None, ring=0, prefetch=None):
         rng = np.random.default_rng(seed)
         self.torch, self.rng = torch, rng
         self.batch, self.owners, self.history, self.resident, self.q = batch, owners, history, resident, q_rows
@@ -73,7 +73,7 @@ class Setup:
         self.upd = kvip_amd.ResidentIndexUpdate(
             t, keys=self.keys, scales=self.scales, addresses=self.addresses, logical_ids=self.logical,
             row_owners=self.row_owners, rotating=self.rot, hot_valid=self.valid, hot_cache=self.hot,
-            host_pool=self.pool, resident=resident, tail_bounds=self.tail)
+            host_pool=self.pool, resident=resident, tail_bounds=self.tail, prefetch=prefetch)
         self.lib = abi.load_library()
 
     def run_round(self, selected, lru):
@@ -87,8 +87,9 @@ class Setup:
         abi.check(rc, "resident round")
         t.cuda.synchronize()
 
-    def oracle_round(self, selected, lru):
-        """Oracle on the host copies, request by request (each owner once per round)."""
+    def oracle_round(self, selected, lru, prefetched=None):
+        """Oracle on the host copies, request by request (each owner once per round);
+        prefetched: per request, the oracle's prefetch list of the round."""
         outs = []
         for b in range(self.batch):
             o = int(self.h_owners[b])
@@ -98,7 +99,8 @@ class Setup:
             tail = (int(self.h_tail[b, 0]), int(self.h_tail[b, 1]), self.ring) if self.ring else None
             lout, sout, res, err = ref.resident_round(
                 sel, self.history, self.resident, keys, self.h_scales[o], self.h_addresses[o], self.h_logical[o],
-                self.h_valid[o], reserved, lru[b], self.h_hot[o], self.h_pool, tail=tail)
+                self.h_valid[o], reserved, lru[b], self.h_hot[o], self.h_pool, tail=tail,
+                prefetched=None if prefetched is None else prefetched[b])
             self.h_keys[o] = keys
             outs.append((lout, sout, res, err, reserved))
         return outs
@@ -331,11 +333,90 @@ def test_resident_errors_clear_the_owner_residency(torch_gpu):
     assert torch.equal(st2.hot, hot_before) and not st2.valid.any()
 
 
-def test_resident_forward_graph_replay(torch_gpu):
-    """The resident forward captured once and replayed: each replay equals the same step
-    run eagerly on a copy of the state (tables and outputs)."""
+def oracle_prefetch(st, keys, lru, pf):
+    """The oracle's prefix classification and prefetch of every request on the device keys."""
+    out = []
+    cold_len = st.history - st.resident
+    cold_words = (st.rot.key_stride - st.resident + 31) // 32
+    for b in range(st.batch):
+        victim = np.zeros((st.q, TOPK), bool)
+        cold = np.zeros((st.q, cold_len), bool)
+        for q in range(st.q):
+            r = b * st.q + q
+            _, _, vbits, cbits = ref.prefix_classify(keys[r], st.history, st.resident, lru[b], cold_words)
+            victim[q] = np.unpackbits(vbits.view(np.uint8), bitorder="little").astype(bool)
+            cold[q] = np.unpackbits(cbits.view(np.uint8), bitorder="little")[:cold_len].astype(bool)
+        tail = (int(st.h_tail[b, 0]), int(st.h_tail[b, 1]), st.ring) if st.ring else None
+        out.append(ref.prefetch(victim, cold, lru[b], st.history, st.resident, tail=tail, windows=pf.windows,
+                                prefetch_limit=pf.prefetch_limit, window_limit=pf.window_limit))
+    return out
+
+
+@pytest.mark.parametrize("q_rows,ring", [(1, 0), (2, 512)])
+def test_resident_prefetch_forward_matches_oracle(torch_gpu, q_rows, ring):
+    """The forward with the speculative windowed prefetch (prefix TopK and hit bits, the
+    window scan and budgets, the prefetch Fetch on a second stream, the final round with
+    prefetched tokens resolved to their slots and the prefetch applied first in the Index
+    update) over three rounds against the oracle, bit-exact: prefetch records, outputs,
+    change records, Index tables, residency and the hot cache; the queries drift from round
+    to round so that each round prefetches, hits and misses."""
     torch = torch_gpu
-    st = Setup(torch, batch=2, owners=2, history=8192, resident=4096, q_rows=2, seed=12)
+    batch, history, resident = 3, 16384, 4096
+    pf = kvip_amd.ResidentPrefetch(windows=4, prefetch_limit=600, window_limit=200)
+    say(f"case resident prefetch q={q_rows} ring={ring}")
+    st = Setup(torch, batch=batch, owners=batch, history=history, resident=resident, q_rows=q_rows, seed=13 + ring,
+               invalid=0.03, ring=ring, prefetch=pf)
+    rot, upd = st.rot, st.upd
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(7)
+    base = torch.randn(rot.query.shape, generator=gen, device="cuda")
+    rot.weights.copy_(torch.randn(rot.weights.shape, generator=gen, device="cuda").abs() / 8)
+    if ring:
+        st.h_tail = np.array([[history - 300, history], [2000, 2600], [0, 0]], np.int32)
+    policies = []
+    for _ in range(batch):
+        p = lru_ref.SlotLRU()
+        p.resize(resident, resident)
+        policies.append(p)
+    fwd = kvip_amd.LIFetch(rot, upd)
+    for rnd in range(3):
+        say(f"  round {rnd}")
+        q = base + 0.4 * rnd * torch.randn(base.shape, generator=gen, device="cuda")
+        rot.query.copy_(q.clamp(-8, 8).to(torch.float8_e4m3fn))
+        lru = np.stack([p.slots.astype(np.int64) for p in policies])
+        upd.set_candidates(torch.from_numpy(lru.astype(np.int32)).cuda())
+        if st.tail is not None:
+            st.tail.copy_(torch.from_numpy(st.h_tail))
+        fwd()
+        torch.cuda.synchronize()
+        assert int(rot.status.item()) == 0
+        keys = rot.score_keys.cpu().numpy().view(np.uint16)
+        top = rot.topk.cpu().numpy().astype(np.int64)
+        for r in range(batch * q_rows):
+            assert np.array_equal(top[r], li_ref.topk_reference(keys[r], history)), r
+        pre = oracle_prefetch(st, keys, lru, pf)
+        counts = upd.prefetch_counts.cpu().numpy()
+        tokens = upd.prefetch_tokens.cpu().numpy()
+        for b in range(batch):
+            assert counts[b] == len(pre[b]), (b, counts[b], len(pre[b]))
+            assert tokens[b, :counts[b]].tolist() == [t for t, _ in pre[b]], b
+        say(f"    prefetched {counts.tolist()}, final misses {upd.miss_counts[:, 4].cpu().tolist()}")
+        assert counts.sum() > 0
+        outs = st.oracle_round(top, lru, prefetched=pre)
+        st.compare(outs)
+        for b, p in enumerate(policies):
+            s_out = outs[b][1]
+            p.commit(s_out[(s_out >= 0) & (s_out < resident)])
+
+
+@pytest.mark.parametrize("prefetch", [False, True])
+def test_resident_forward_graph_replay(torch_gpu, prefetch):
+    """The resident forward captured once and replayed: each replay equals the same step
+    run eagerly on a copy of the state (tables and outputs); with the prefetch, the capture
+    forks the prefetch onto its second stream and joins it before the final round."""
+    torch = torch_gpu
+    st = Setup(torch, batch=2, owners=2, history=8192, resident=4096, q_rows=2, seed=12,
+               prefetch=kvip_amd.ResidentPrefetch(windows=3, prefetch_limit=300) if prefetch else None)
     rot, upd = st.rot, st.upd
     gen = torch.Generator(device="cuda")
     gen.manual_seed(5)
@@ -358,12 +439,16 @@ def test_resident_forward_graph_replay(torch_gpu):
         graph.replay()
         torch.cuda.synchronize()
         got = [x.clone() for x in state] + [upd.outputs.clone(), upd.miss_counts.clone()]
+        if prefetch:
+            got.append(upd.prefetch_counts.clone())
         for x, s in zip(state, start):
             x.copy_(s)
         upd.outputs.fill_(-9)
         fwd()
         torch.cuda.synchronize()
         want = [x for x in state] + [upd.outputs, upd.miss_counts]
+        if prefetch:
+            want.append(upd.prefetch_counts)
         for g, w in zip(got, want):
             assert torch.equal(g, w), step
         assert not upd.status.any()

@@ -466,3 +466,93 @@ def test_empty_tail_equals_no_tail():
     b = ref.resolve(sel, history, resident, hot_valid, reserved, lru, tail=(7000, 7000, 512))
     assert np.array_equal(a["loc"], b["loc"]) and np.array_equal(a["tokens"], b["tokens"])
     assert np.array_equal(a["changes"], b["changes"])
+
+
+# ----------------------------------------------------------------------------
+# Speculative windowed prefetch
+# ----------------------------------------------------------------------------
+def test_prefetch_windows_are_the_trigger_boundaries():
+    for resident, history, windows in [(4096, 5120, 3), (16384, 131072, 8), (2048, 10240, 1), (2048, 10240, 2)]:
+        ends = ref.prefetch_windows(resident, history, windows)
+        assert len(ends) == windows and ends[0] == resident
+        assert all(e % 128 == 0 for e in ends) and ends == sorted(ends)
+        if windows >= 2:
+            assert ends[-1] == history
+
+
+def test_prefetch_known_answer():
+    """Victim coordinates first (ordinal order, token lru[i]), then cold positions window by
+    window; window and total budgets; mapped tail positions skipped; rows united."""
+    resident, history = 4096, 5120            # windows 3: ends 4096, 4608, 5120
+    lru = np.arange(4096 - 2048, 4096)[::-1].astype(np.int64)
+    victim = np.zeros((2, 2048), bool)
+    victim[0, 5] = victim[1, 7] = True
+    cold = np.zeros((2, history - resident), bool)
+    for t in (4100, 5000):
+        cold[0, t - resident] = True
+    cold[1, 4700 - resident] = True
+    got = ref.prefetch(victim, cold, lru, history, resident, windows=3)
+    assert got == [(int(lru[5]), 0), (int(lru[7]), 1), (4100, 2), (4700, 3), (5000, 4)]
+    assert ref.prefetch(victim, cold, lru, history, resident, windows=3, window_limit=1) == \
+        [(int(lru[5]), 0), (4100, 1), (4700, 2)]
+    assert ref.prefetch(victim, cold, lru, history, resident, windows=3, prefetch_limit=2, window_limit=2) == \
+        [(int(lru[5]), 0), (int(lru[7]), 1)]
+    # 4700 is a mapped ABC tail position (first T of [4650, 4800) with T = 384)
+    assert ref.prefetch(victim, cold, lru, history, resident, tail=(4650, 4800, 384), windows=3) == \
+        [(int(lru[5]), 0), (int(lru[7]), 1), (4100, 2), (5000, 3)]
+    assert ref.prefetch(victim, cold, lru, history, resident, windows=1, window_limit=480) == \
+        [(int(lru[5]), 0), (int(lru[7]), 1)]
+    with pytest.raises(ValueError):  # geometry.py:10-11: a window posts at most 480 fetches
+        ref.prefetch(victim, cold, lru, history, resident, windows=1)
+
+
+def _round_state(rng, history, resident, row=64):
+    keys = rng.integers(0, 256, (history, 128), dtype=np.uint8)
+    scales = rng.random(history).astype(np.float32)
+    addresses = (np.arange(history) * row).astype(np.int64)
+    logical = np.arange(history).astype(np.int64) + 1000
+    pool = rng.integers(0, 256, history * row, dtype=np.uint8)
+    hot = pool.reshape(history, row)[:resident].copy()
+    valid = np.ones(resident, np.int32)
+    return keys, scales, addresses, logical, pool, hot, valid
+
+
+def test_prefetch_changes_no_output_and_keeps_residency_consistent():
+    """The same TopK rows through the round with and without a prefetch: identical logical
+    outputs and identical KV bytes behind every selected entry; afterwards every resident
+    slot holds the KV row of the Index row at that position, and the Index rows are a
+    permutation of the original ones."""
+    rng = np.random.default_rng(23)
+    history, resident = 8192, 4096
+    for trial in range(4):
+        q_rows = 1 + trial % 2
+        base = _round_state(rng, history, resident)
+        lru = rng.permutation(resident)[:2048].astype(np.int64)
+        reserved = ref.reserved_from_candidates(lru, resident)
+        sel = np.stack([rng.permutation(history)[:TOPK] for _ in range(q_rows)]).astype(np.int64)
+        # Hits: most final cold selections plus unselected cold positions and victims.
+        victim = rng.random((q_rows, 2048)) < 0.02
+        cold = np.zeros((q_rows, history - resident), bool)
+        for q in range(q_rows):
+            chosen = sel[q][sel[q] >= resident] - resident
+            cold[q, chosen[rng.random(len(chosen)) < 0.7]] = True
+        cold |= rng.random(cold.shape) < 0.02
+        pre = ref.prefetch(victim, cold, lru, history, resident, windows=4, prefetch_limit=700, window_limit=300)
+        assert 0 < len(pre) <= 700
+        runs = []
+        for prefetched in (None, pre):
+            keys, scales, addresses, logical, pool, hot, valid = (a.copy() for a in base)
+            lout, sout, res, err = ref.resident_round(sel, history, resident, keys, scales, addresses, logical, valid,
+                                                      reserved, lru, hot, pool, prefetched=prefetched)
+            assert err == 0
+            kv = np.stack([hot[sout[q]] for q in range(q_rows)])
+            runs.append((lout, kv, res))
+            # Residency: a valid hot slot holds the row of the Index entry now at that position.
+            for p in np.nonzero(valid)[0]:
+                a = int(addresses[p])
+                assert np.array_equal(hot[p], pool[a:a + hot.shape[1]]), (trial, p)
+            assert sorted(logical.tolist()) == sorted(base[3].tolist())
+        assert np.array_equal(runs[0][0], runs[1][0])
+        assert np.array_equal(runs[0][1], runs[1][1])
+        # The prefetch took some of the misses off the final Fetch.
+        assert len(runs[1][2]["tokens"]) < len(runs[0][2]["tokens"])
