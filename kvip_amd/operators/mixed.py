@@ -19,6 +19,12 @@ buffers bound once, so the whole round is one hipGraph:
   4. the prefill indexer bound with `PrefillIndexer.bind`: LI over the paged cache for the
      packed chunks (cumulative query lengths) and TopK-2048 per row.
 
+The prefill stage reads only the paged cache and its own buffers, so it runs on a second
+stream forked at the round's start and joined at its end (`overlap=True`, the default):
+its MFMA-bound scoring then overlaps the decode's HBM-bound scoring and PCIe-bound Fetch
+instead of following them. The fork and join are events, so the round stays one capturable
+sequence on the caller's stream.
+
 The caller fills the per-round inputs in place before a launch or replay: decode Q /
 weights / lengths, the prefill buffers it bound, and `sources` / `targets` of the new
 tokens. Device errors land in the status words of the three stages.
@@ -34,7 +40,7 @@ INDEX_DIM = 128
 
 class MixedRound:
     def __init__(self, torch, *, decode, prefill, storage_keys, storage_scales, cache_keys, cache_scales,
-                 new_tokens, status=None, lru=None):
+                 new_tokens, status=None, lru=None, overlap=True):
         """decode: a LIFetch forward; prefill: a PrefillIndexer after `bind(...)`;
         storage_keys [owners, history, 128] (fp8 or uint8) and storage_scales
         [owners, history] float32: the persistent Index rows; cache_keys
@@ -80,15 +86,32 @@ class MixedRound:
             if lru.chains != upd.rotating.batch:
                 raise ValueError(f"{lru.chains} LRU chains for {upd.rotating.batch} decode requests")
             self.commit_rows = upd.slot_output.view(upd.rotating.batch, -1)
+        self.overlap = overlap
+        if overlap:
+            # The prefill branch: its own stream (default priority) and the fork/join events.
+            self.side = torch.cuda.Stream(device=dev)
+            self.forked, self.joined = torch.cuda.Event(), torch.cuda.Event()
 
     def ingest(self):
         abi.check(self.library.kvip_hip_ingest_index(ctypes.byref(self.ingest_args),
                                                      abi.stream_handle(self.torch, self.device)), "mixed ingest")
 
     def __call__(self):
+        torch = self.torch
+        if self.overlap:
+            main = torch.cuda.current_stream(self.device)
+            self.forked.record(main)
+            self.side.wait_event(self.forked)
+            with torch.cuda.stream(self.side):
+                self.prefill.score()
+                self.prefill.select()
+            self.joined.record(self.side)
         self.ingest()
         self.decode()
         if self.lru is not None:
             self.lru.commit(self.commit_rows)
+        if self.overlap:
+            torch.cuda.current_stream(self.device).wait_event(self.joined)
+            return self.prefill.topk[:self.prefill._rows]
         self.prefill.score()
         return self.prefill.select()
