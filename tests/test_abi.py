@@ -42,7 +42,15 @@ STRUCTS = {
     "KvipIngestArgs": abi.IngestArgs,
     "KvipResidentArgs": abi.ResidentArgs,
     "KvipPrefixClassifyArgs": abi.PrefixClassifyArgs,
+    "KvipPrefetchArgs": abi.PrefetchArgs,
+    "KvipPageArgs": abi.PageArgs,
+    "KvipSparseAttnArgs": abi.SparseAttnArgs,
 }
+
+
+def test_every_declared_struct_has_a_checked_layout():
+    declared = set(re.findall(r"typedef struct (\w+)", (ROOT / "include" / "kvip_hip.h").read_text()))
+    assert declared == set(STRUCTS)
 
 
 def test_ctypes_layout_matches_c(tmp_path):
@@ -85,6 +93,32 @@ def test_invalid_arguments_rejected_before_launch():
     fetch = abi.FetchArgs(topk=16, kv_cache=16, block_table=16, output=16, kv_block_stride=128 * 656,
                           row_stride=656, row_bytes=650, batch=1, rows_per_request=1, max_blocks=1, num_blocks=1)
     assert lib.kvip_hip_fetch_gather(ctypes.byref(fetch), None) == abi.KVIP_ERR_INVALID
+
+
+def test_resident_entry_points_reject_before_launch():
+    lib = abi.load_library()
+    for name in ("kvip_hip_resident_round", "kvip_hip_resident_begin", "kvip_hip_resident_finish",
+                 "kvip_hip_resident_prepare"):
+        assert getattr(lib, name)(None, None) == abi.KVIP_ERR_INVALID, name
+    assert lib.kvip_hip_resident_prefetch(None, None, None) == abi.KVIP_ERR_INVALID
+    assert lib.kvip_hip_resident_score(None, None, None, None) == abi.KVIP_ERR_INVALID
+    # Well-formed resident arguments, then a prefetch whose windows do not fit the cold range
+    # and one half of the prefetch records missing.
+    names = [f for f, _ in abi.ResidentArgs._fields_]
+    ptrs = {n: 256 for n in names[:21]}
+    args = abi.ResidentArgs(**ptrs, host_pool_bytes=1 << 20, batch=1, rows_per_request=1, owners=1, history=8192,
+                            resident=4096, hot_stride=4096, row_bytes=656, used=0, prefetch_tokens=256,
+                            prefetch_counts=256)
+    pf = abi.PrefetchArgs(victim_hits=256, cold_hits=256, cold_words=128, windows=32, window_limit=64,
+                          prefetch_limit=512)
+    assert lib.kvip_hip_resident_prefetch(ctypes.byref(args), ctypes.byref(pf), None) == abi.KVIP_ERR_INVALID
+    pf.windows, pf.window_limit = 4, 481
+    assert lib.kvip_hip_resident_prefetch(ctypes.byref(args), ctypes.byref(pf), None) == abi.KVIP_ERR_INVALID
+    args.prefetch_counts = 0
+    assert lib.kvip_hip_resident_begin(ctypes.byref(args), None) == abi.KVIP_ERR_INVALID
+    # ABC tail bounds need at least 384 ring slots after the hot ones.
+    args.prefetch_counts, args.tail_bounds, args.hot_stride = 256, 256, 4096 + 256
+    assert lib.kvip_hip_resident_begin(ctypes.byref(args), None) == abi.KVIP_ERR_INVALID
 
 
 def test_lidu_arguments_rejected_before_launch():
