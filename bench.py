@@ -302,15 +302,14 @@ def resident_leg(torch, kvip_amd, device, seed, rounds=24, warm=4):
     committed by every round inside the graph. Two loops of consecutive rounds, each one
     captured hipGraph replayed back to back (HIP events around the timed replays), every
     round on inputs of its own (picked by a device cursor) and recording its misses:
-      round:   the resident round alone (init, resolve, Fetch of the misses, Index update,
-               LRU commit) on TopK rows drawn ~80 % hot under Zipf(1.1) popularity, a fresh
-               draw per round;
+      round:   the resident round alone (init, resolve, then the Fetch of the misses beside
+               the Index update and LRU commit on a second stream) on TopK rows drawn ~80 %
+               hot under Zipf(1.1) popularity, a fresh draw per round; timed again with the
+               three stages in sequence on one stream (`sequential_us_per_round`);
       forward: the whole resident forward (LI over 16 x 131072 Index rows, TopK-2048, the
                round, LRU commit) on query sets along a random walk (consecutive rounds
                select overlapping, drifting positions)."""
-    import ctypes
     from kvip_amd import synthetic
-    from kvip_amd.runtime import abi
 
     batch, history, resident = 16, 131072, 16384
     n = warm + rounds + 1  # + the eager round before capture
@@ -320,24 +319,34 @@ def resident_leg(torch, kvip_amd, device, seed, rounds=24, warm=4):
     picks = torch.from_numpy(synthetic.resident_selections(torch, rng, steps=n, batch=batch, q_rows=1,
                                                            history=history, resident=resident)).to(device)
     lru = kvip_amd.SlotLRUChains(torch, batch, resident, device, slots=upd.lru_slots)
-    lib = abi.load_library()
-    commit_rows = upd.slot_output.view(batch, -1)
+    upd.attach_lru(lru)  # committed by every round right after its Index update
     trace = torch.zeros((n, batch), dtype=torch.int32, device=device)
+    picks_now = [picks]
 
     def record(cursor):
-        lru.commit(commit_rows)
         trace.index_copy_(0, cursor, upd.miss_counts[:, 4].view(1, batch))
 
     def round_body(cursor):
-        rot.topk.copy_(torch.index_select(picks, 0, cursor)[0])
-        abi.check(lib.kvip_hip_resident_round(ctypes.byref(upd.args), abi.stream_handle(torch, rot.device)),
-                  "resident round")
+        rot.topk.copy_(torch.index_select(picks_now[0], 0, cursor)[0])
+        upd.round()
         record(cursor)
 
     round_us = _cursor_rounds(torch, round_body, warm, rounds, n)
     if upd.status.any():
         raise RuntimeError(f"resident round failed: {upd.status.cpu().tolist()}")
     round_miss = trace[warm:warm + rounds].sum(1).float().mean().item()
+    # The same loop with resolve, Fetch and Index update (+ LRU commit) in sequence on one
+    # stream, on fresh draws of the same popularity (the cache continues from the loop above).
+    picks_now[0] = torch.from_numpy(synthetic.resident_selections(
+        torch, np.random.default_rng(seed + 1), steps=n, batch=batch, q_rows=1, history=history,
+        resident=resident)).to(device)
+    trace.zero_()
+    upd.overlap = False
+    seq_us = _cursor_rounds(torch, round_body, warm, rounds, n)
+    upd.overlap = True
+    if upd.status.any():
+        raise RuntimeError(f"resident round failed: {upd.status.cpu().tolist()}")
+    seq_miss = trace[warm:warm + rounds].sum(1).float().mean().item()
     queries = _query_walk(torch, rot.query, n, seed)
     q_bytes = rot.query.view(torch.uint8)
     trace.zero_()
@@ -357,15 +366,13 @@ def resident_leg(torch, kvip_amd, device, seed, rounds=24, warm=4):
     rot2, upd2, _ = synthetic.resident_workload(torch, kvip_amd, device, seed=seed, batch=batch, history=history,
                                                 resident=resident, prefetch=kvip_amd.ResidentPrefetch())
     fwd2 = kvip_amd.LIFetch(rot2, upd2)
-    lru2 = kvip_amd.SlotLRUChains(torch, batch, resident, device, slots=upd2.lru_slots)
-    rows2 = upd2.slot_output.view(batch, -1)
+    upd2.attach_lru(kvip_amd.SlotLRUChains(torch, batch, resident, device, slots=upd2.lru_slots))
     q2 = rot2.query.view(torch.uint8)
     trace2 = torch.zeros((n, 2, batch), dtype=torch.int32, device=device)
 
     def prefetch_body(cursor):
         q2.copy_(torch.index_select(queries, 0, cursor)[0])
         fwd2()
-        lru2.commit(rows2)
         trace2.index_copy_(0, cursor, torch.stack([upd2.miss_counts[:, 4], upd2.prefetch_counts]).view(1, 2, batch))
 
     pf_us = _cursor_rounds(torch, prefetch_body, warm, rounds, n)
@@ -377,6 +384,7 @@ def resident_leg(torch, kvip_amd, device, seed, rounds=24, warm=4):
                         "host memory, LRU chains committed in the graph; round: TopK rows drawn ~80% hot (Zipf 1.1), "
                         "a fresh draw per round; forward: LI + TopK + round on query sets along a random walk",
             "us_per_round": round(round_us, 2), "misses_per_round": round(round_miss, 1),
+            "sequential_us_per_round": round(seq_us, 2), "sequential_misses_per_round": round(seq_miss, 1),
             "hit_fraction": round(1.0 - round_miss / (batch * TOPK), 4),
             "fetch_gbs_lower_bound": round(round_miss * 656 / (round_us * 1e-6) / 1e9, 2),
             "host_read_ceiling_gbs": round(host_gbs, 1),

@@ -66,6 +66,12 @@
  *                                PrefetchAllowance (common/lifetch/prefetch_budget.h:7-17),
  *                                then the final round with PublishPrefetch (streaming.cpp:
  *                                23-27, :119-121) and PublishPrefetchResidency (:330-339)
+ *   kvip_hip_resident_resolve / _fetch / _update
+ *                             <- kvip_hip_resident_finish in its three stages, so that the
+ *                                Fetch (FetchQueryGroup, streaming.cpp:365-500) and the Index
+ *                                update (Consumer + ApplyBatch, streaming.cpp:205-274) of one
+ *                                round can run on two streams, as the reference's producer and
+ *                                consumer run beside each other
  *   kvip_hip_resident_workspace_bytes / kvip_hip_resident_prepare
  *                             <- the rotation scratch allocated and reset at bind time
  *                                (python/kvip/operators/lifetch/workspace.py:9-31,
@@ -80,7 +86,7 @@
 extern "C" {
 #endif
 
-#define KVIP_HIP_ABI_VERSION 11u
+#define KVIP_HIP_ABI_VERSION 12u
 
 #define KVIP_TOPK 2048
 #define KVIP_BLOCK_TOKENS 128
@@ -662,6 +668,15 @@ uint32_t kvip_hip_resident_round(const KvipResidentArgs* args, void* stream);
 uint32_t kvip_hip_resident_begin(const KvipResidentArgs* args, void* stream);
 uint32_t kvip_hip_resident_prefetch(const KvipResidentArgs* args, const KvipPrefetchArgs* prefetch, void* stream);
 uint32_t kvip_hip_resident_finish(const KvipResidentArgs* args, void* stream);
+/* kvip_hip_resident_finish = resolve, then Fetch, then update. The Fetch copies the resolve's
+ * misses (it reads fetch_sources/fetch_slots/miss_counts and writes hot_cache only) and the
+ * update permutes the Index rows and publishes residency (it reads the resolve's outputs,
+ * never hot_cache), so after the resolve the two may run on two streams, in either order or
+ * concurrently, with the same results as the sequential finish; a caller joins both before
+ * anything reads hot_cache, hot_valid or the Index rows. */
+uint32_t kvip_hip_resident_resolve(const KvipResidentArgs* args, void* stream);
+uint32_t kvip_hip_resident_fetch(const KvipResidentArgs* args, void* stream);
+uint32_t kvip_hip_resident_update(const KvipResidentArgs* args, void* stream);
 /* The first half of kvip_hip_resident_forward with the round's initialisation: owner block
  * table, scoring of the owners' Index rows, then kvip_hip_resident_begin. A prefetching
  * forward follows it with kvip_hip_resident_prefix + kvip_hip_resident_prefetch (possibly

@@ -513,75 +513,88 @@ __global__ __launch_bounds__(kRsThreads) void resident_prefetch_kernel(const Kvi
 }
 
 // Fetch of the missed rows (PREFETCH: of the prefetched rows, source = the token's KV
-// address, slot = its candidate slot): wave w of workgroup (x, b) moves ranks
-// [32*(4x+w), +32).
+// address, slot = its candidate slot). Rows go in groups of 32, one group per wave at a
+// time: the wave issues the group's loads from the host pool (21 16-byte loads per lane),
+// then stores them to the hot cache, and moves on by the grid's wave count. The grid is
+// bounded (kFetchWaves waves in all): a few MB of host reads in flight at once fill the
+// L2 / fabric miss queues that the Index update's HBM accesses share, which then wait
+// for the whole Fetch; ~1 MB in flight already covers the host link's latency-bandwidth
+// product (57 GB/s x ~2 us).
 constexpr int kFetchRows = 32;
+constexpr int kFetchWaves = 64;
 template <int PIECES, bool PREFETCH>
 __global__ __launch_bounds__(256) void resident_fetch_kernel(const KvipResidentArgs p) {
     const int b = blockIdx.y;
     const int lane = threadIdx.x & 63;
-    const int r0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * kFetchRows;
-    if (p.status[b] != 0) return;
+    // The prefetch copy runs before the resolve and skips a failed round. The miss copy
+    // reads only the resolve's outputs (a failed request's miss total is 0, every source
+    // was checked by the resolve), never the status words that a concurrent Index update
+    // may set: the copy and the update can run side by side.
+    if (PREFETCH && p.status[b] != 0) return;
     const int total = PREFETCH ? p.prefetch_counts[b] : p.miss_counts[b * 5 + 4];
-    if (r0 >= total) return;
     const int o = p.row_owners[b];
     const int pieces = PIECES > 0 ? PIECES : p.row_bytes / 16;
-    const int rows = min(kFetchRows, total - r0);
-    int64_t src = -1, dst = -1;
     uint32_t err = 0;
-    if (lane < rows) {
-        int64_t off;
-        int slot;
-        if constexpr (PREFETCH) {
-            const int k = r0 + lane;
-            const int t = p.prefetch_tokens[static_cast<size_t>(b) * kLru + k];
-            slot = p.lru_slots[static_cast<size_t>(b) * kLru + k];
-            off = t >= 0 && t < p.history ? p.addresses[static_cast<size_t>(o) * p.history + t] : -1;
-            if (slot < 0 || slot >= p.resident) off = -1;
-        } else {
-            const size_t d = static_cast<size_t>(b) * p.rows_per_request * kTopK + r0 + lane;
-            off = p.fetch_sources[d];
-            slot = p.fetch_slots[d];
+    for (int r0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * kFetchRows; r0 < total;
+         r0 += gridDim.x * 4 * kFetchRows) {
+        const int rows = min(kFetchRows, total - r0);
+        int64_t src = -1, dst = -1;
+        if (lane < rows) {
+            int64_t off;
+            int slot;
+            if constexpr (PREFETCH) {
+                const int k = r0 + lane;
+                const int t = p.prefetch_tokens[static_cast<size_t>(b) * kLru + k];
+                slot = p.lru_slots[static_cast<size_t>(b) * kLru + k];
+                off = t >= 0 && t < p.history ? p.addresses[static_cast<size_t>(o) * p.history + t] : -1;
+                if (slot < 0 || slot >= p.resident) off = -1;
+            } else {
+                const size_t d = static_cast<size_t>(b) * p.rows_per_request * kTopK + r0 + lane;
+                off = p.fetch_sources[d];
+                slot = p.fetch_slots[d];
+            }
+            if (off >= 0 && off <= p.host_pool_bytes - p.row_bytes && (off & 15) == 0) {
+                src = off;
+                dst = (static_cast<int64_t>(o) * p.hot_stride + slot) * p.row_bytes;
+            } else {
+                err = KVIP_RESIDENT_ERR_SOURCE;
+            }
         }
-        if (off >= 0 && off <= p.host_pool_bytes - p.row_bytes && (off & 15) == 0) {
-            src = off;
-            dst = (static_cast<int64_t>(o) * p.hot_stride + slot) * p.row_bytes;
-        } else {
-            err = KVIP_RESIDENT_ERR_SOURCE;
-        }
-    }
-    const int n = rows * pieces;
-    if constexpr (PIECES > 0) {
-        constexpr int kIters = (kFetchRows * PIECES + 63) / 64;
-        v4i val[kIters];
+        const int n = rows * pieces;
+        if constexpr (PIECES > 0) {
+            constexpr int kIters = (kFetchRows * PIECES + 63) / 64;
+            v4i val[kIters];
 #pragma unroll
-        for (int it = 0; it < kIters; ++it) {
-            const int idx = it * 64 + lane;
-            const int r = idx / PIECES;
-            const int piece = idx - r * PIECES;
-            const int64_t s = __shfl(src, min(r, kFetchRows - 1));
-            val[it] = v4i{0, 0, 0, 0};
-            if (idx < n && s >= 0) val[it] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(p.host_pool + s + piece * 16));
-        }
+            for (int it = 0; it < kIters; ++it) {
+                const int idx = it * 64 + lane;
+                const int r = idx / PIECES;
+                const int piece = idx - r * PIECES;
+                const int64_t s = __shfl(src, min(r, kFetchRows - 1));
+                val[it] = v4i{0, 0, 0, 0};
+                if (idx < n && s >= 0) {
+                    val[it] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(p.host_pool + s + piece * 16));
+                }
+            }
 #pragma unroll
-        for (int it = 0; it < kIters; ++it) {
-            const int idx = it * 64 + lane;
-            const int r = idx / PIECES;
-            const int piece = idx - r * PIECES;
-            const int64_t d = __shfl(dst, min(r, kFetchRows - 1));
-            if (idx < n && d >= 0) *reinterpret_cast<v4i*>(p.hot_cache + d + piece * 16) = val[it];
-        }
-    } else {
-        const int iters = (kFetchRows * pieces + 63) / 64;
-        for (int it = 0; it < iters; ++it) {
-            const int idx = it * 64 + lane;
-            const int r = idx / pieces;
-            const int piece = idx - r * pieces;
-            const int64_t s = __shfl(src, min(r, kFetchRows - 1));
-            const int64_t d = __shfl(dst, min(r, kFetchRows - 1));
-            if (idx < n && s >= 0 && d >= 0) {
-                *reinterpret_cast<v4i*>(p.hot_cache + d + piece * 16) =
-                    *reinterpret_cast<const v4i*>(p.host_pool + s + piece * 16);
+            for (int it = 0; it < kIters; ++it) {
+                const int idx = it * 64 + lane;
+                const int r = idx / PIECES;
+                const int piece = idx - r * PIECES;
+                const int64_t d = __shfl(dst, min(r, kFetchRows - 1));
+                if (idx < n && d >= 0) *reinterpret_cast<v4i*>(p.hot_cache + d + piece * 16) = val[it];
+            }
+        } else {
+            const int iters = (kFetchRows * pieces + 63) / 64;
+            for (int it = 0; it < iters; ++it) {
+                const int idx = it * 64 + lane;
+                const int r = idx / pieces;
+                const int piece = idx - r * pieces;
+                const int64_t s = __shfl(src, min(r, kFetchRows - 1));
+                const int64_t d = __shfl(dst, min(r, kFetchRows - 1));
+                if (idx < n && s >= 0 && d >= 0) {
+                    *reinterpret_cast<v4i*>(p.hot_cache + d + piece * 16) =
+                        *reinterpret_cast<const v4i*>(p.host_pool + s + piece * 16);
+                }
             }
         }
     }
@@ -813,8 +826,10 @@ uint32_t validate_resident(const KvipResidentArgs* a) {
 
 template <bool PREFETCH>
 void launch_resident_fetch(const KvipResidentArgs& a, hipStream_t s) {
+    // Up to kFetchWaves waves in all (at least one workgroup per request).
     const int rows = PREFETCH ? kLru : a.rows_per_request * kTopK;
-    const dim3 fgrid((rows + 4 * kFetchRows - 1) / (4 * kFetchRows), a.batch);
+    const int per_request = max(1, kFetchWaves / (4 * a.batch));
+    const dim3 fgrid(min((rows + 4 * kFetchRows - 1) / (4 * kFetchRows), per_request), a.batch);
     if (a.row_bytes == KVIP_KV_ROW_BYTES) {
         hipLaunchKernelGGL((resident_fetch_kernel<KVIP_KV_ROW_BYTES / 16, PREFETCH>), fgrid, dim3(256), 0, s, a);
     } else {
@@ -827,11 +842,21 @@ hipError_t launch_resident_begin(const KvipResidentArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
-hipError_t launch_resident_finish(const KvipResidentArgs& a, hipStream_t s) {
+hipError_t launch_resident_resolve(const KvipResidentArgs& a, hipStream_t s) {
     hipLaunchKernelGGL(resident_resolve_kernel, dim3(a.batch), dim3(kRsThreads), 0, s, a);
-    launch_resident_fetch<false>(a, s);
+    return hipGetLastError();
+}
+
+hipError_t launch_resident_update(const KvipResidentArgs& a, hipStream_t s) {
     hipLaunchKernelGGL(resident_update_kernel, dim3(a.batch), dim3(kRsThreads), 0, s, a);
     return hipGetLastError();
+}
+
+hipError_t launch_resident_finish(const KvipResidentArgs& a, hipStream_t s) {
+    const hipError_t e = launch_resident_resolve(a, s);
+    if (e != hipSuccess) return e;
+    launch_resident_fetch<false>(a, s);
+    return launch_resident_update(a, s);
 }
 
 hipError_t launch_resident_round(const KvipResidentArgs& a, hipStream_t s) {
@@ -870,6 +895,25 @@ extern "C" uint32_t kvip_hip_resident_finish(const KvipResidentArgs* args, void*
     const uint32_t rc = kvip::validate_resident(args);
     if (rc != KVIP_OK) return rc;
     return static_cast<uint32_t>(kvip::launch_resident_finish(*args, static_cast<hipStream_t>(stream)));
+}
+
+extern "C" uint32_t kvip_hip_resident_resolve(const KvipResidentArgs* args, void* stream) {
+    const uint32_t rc = kvip::validate_resident(args);
+    if (rc != KVIP_OK) return rc;
+    return static_cast<uint32_t>(kvip::launch_resident_resolve(*args, static_cast<hipStream_t>(stream)));
+}
+
+extern "C" uint32_t kvip_hip_resident_fetch(const KvipResidentArgs* args, void* stream) {
+    const uint32_t rc = kvip::validate_resident(args);
+    if (rc != KVIP_OK) return rc;
+    kvip::launch_resident_fetch<false>(*args, static_cast<hipStream_t>(stream));
+    return static_cast<uint32_t>(hipGetLastError());
+}
+
+extern "C" uint32_t kvip_hip_resident_update(const KvipResidentArgs* args, void* stream) {
+    const uint32_t rc = kvip::validate_resident(args);
+    if (rc != KVIP_OK) return rc;
+    return static_cast<uint32_t>(kvip::launch_resident_update(*args, static_cast<hipStream_t>(stream)));
 }
 
 extern "C" uint32_t kvip_hip_resident_prefetch(const KvipResidentArgs* args, const KvipPrefetchArgs* f,

@@ -2,10 +2,12 @@
 
 Keeps the reference's call shape (python/kvip/operators/lifetch/forward.py:7-17,
 streaming.py:115-131): construction validates and packs every device address once;
-``forward()`` takes no arguments, enqueues the round on the current stream through
-one C call and returns None. It never allocates, synchronises or reads back, so it
-can be captured into a hipGraph; argument problems raise ValueError at construction,
-a failed launch raises RuntimeError.
+``forward()`` takes no arguments, enqueues the round on the current stream and returns
+None. The contiguous-Fetch forward is one C call; the resident forward is scoring + TopK
+and then the round's resolve, with its Fetch beside the Index update on a second stream
+joined before return (ResidentIndexUpdate(overlap=True)). It never allocates,
+synchronises or reads back, so it can be captured into a hipGraph; argument problems
+raise ValueError at construction, a failed launch raises RuntimeError.
 """
 from __future__ import annotations
 
@@ -95,9 +97,17 @@ class LIFetchForward:
 
     def __call__(self):
         if self.resident:
+            upd = self.update
             if self.prefix is None:
-                abi.check(self.library.kvip_hip_resident_forward(*self._refs, self._stream()),
-                          "resident LIFetch forward")
+                if not upd.overlap and upd.lru is None:
+                    abi.check(self.library.kvip_hip_resident_forward(*self._refs, self._stream()),
+                              "resident LIFetch forward")
+                    return
+                # Scoring + round initialisation, TopK, then the round's resolve / Fetch /
+                # Index update (the update beside the Fetch with overlap).
+                abi.check(self.library.kvip_hip_resident_score(*self._refs, self._stream()), "resident scoring")
+                abi.check(self.library.kvip_hip_topk(self._refs[1], self._stream()), "TopK")
+                upd.finish()
                 return
             torch, lib = self.torch, self.library
             main = torch.cuda.current_stream(self.rotating.device)
@@ -111,7 +121,7 @@ class LIFetchForward:
             self.prefetched.record(self.side)
             abi.check(lib.kvip_hip_topk(self._refs[1], main.cuda_stream), "TopK")
             main.wait_event(self.prefetched)
-            abi.check(lib.kvip_hip_resident_finish(self._refs[2], main.cuda_stream), "resident round")
+            upd.finish()
             return
         abi.check(self.library.kvip_hip_lifetch_forward(self._args_ref, self._stream()), "LIFetch forward")
 

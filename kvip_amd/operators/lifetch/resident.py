@@ -60,7 +60,11 @@ class ResidentPrefetch:
 class ResidentIndexUpdate:
     def __init__(self, torch, *, keys, scales, addresses, logical_ids, row_owners, rotating, hot_valid, hot_cache,
                  host_pool, resident, status=None, outputs=None, used=0, query_inputs=None, tail_bounds=None,
-                 prefetch=None):
+                 prefetch=None, overlap=True):
+        """overlap: run each round's Fetch of the misses beside its Index update (and the
+        attached LRU commit) on a second stream after the resolve, joined before the round
+        ends (`finish()`); False keeps the three stages on the caller's stream. Results are
+        the same either way."""
         self.torch, self.rotating, self.device = torch, rotating, rotating.device
         if keys.dim() != 3 or keys.shape[2] != INDEX_DIM or keys.dtype != torch.float8_e4m3fn or not keys.is_contiguous():
             raise ValueError("Index keys must be contiguous float8_e4m3fn [owners, history, 128]")
@@ -147,8 +151,60 @@ class ResidentIndexUpdate:
         if rotating.query_ends is None:
             rotating.seq_lens.fill_(history)
         self.args = self.resident_args()
-        abi.check(lib.kvip_hip_resident_prepare(ctypes.byref(self.args), abi.stream_handle(torch, dev)),
-                  "resident workspace")
+        self._ref = ctypes.byref(self.args)
+        self.library = lib
+        abi.check(lib.kvip_hip_resident_prepare(self._ref, abi.stream_handle(torch, dev)), "resident workspace")
+        self.lru = self.commit_rows = None
+        self.overlap = bool(overlap)
+        if self.overlap:
+            # The Index-update branch: its own stream (default priority), forked after the
+            # resolve and joined after the Fetch.
+            self.side = torch.cuda.Stream(device=dev)
+            self.resolved, self.updated = torch.cuda.Event(), torch.cuda.Event()
+
+    def attach_lru(self, chains):
+        """Commit `chains` (a SlotLRUChains with one chain per request whose `slots` alias
+        this update's lru_slots) with each round's selected slots right after the round's
+        Index update, so the next round's victim candidates follow the cache's recency (the
+        reference's selector commits each request's SlotLRU after a step,
+        python/kvip/cache/lru.py:96-118). With overlap the commit runs on the update branch,
+        beside the Fetch."""
+        if chains.slots.data_ptr() != self.lru_slots.data_ptr():
+            raise ValueError("the LRU chains must feed this update's candidates (slots aliasing its lru_slots)")
+        if chains.chains != self.rotating.batch:
+            raise ValueError(f"{chains.chains} LRU chains for {self.rotating.batch} requests")
+        self.lru = chains
+        self.commit_rows = self.slot_output.view(self.rotating.batch, -1)
+
+    def finish(self):
+        """The round after its TopK (and prefetch): resolve, then the Fetch of the misses and
+        the Index update (+ the attached LRU commit), enqueued on the current stream; with
+        overlap the update branch runs on the second stream and is joined before return.
+        Capturable: no allocation, synchronisation or read-back."""
+        torch, lib = self.torch, self.library
+        main = torch.cuda.current_stream(self.device)
+        if not self.overlap:
+            abi.check(lib.kvip_hip_resident_finish(self._ref, main.cuda_stream), "resident round")
+            if self.lru is not None:
+                self.lru.commit(self.commit_rows)
+            return
+        abi.check(lib.kvip_hip_resident_resolve(self._ref, main.cuda_stream), "resident resolve")
+        self.resolved.record(main)
+        self.side.wait_event(self.resolved)
+        abi.check(lib.kvip_hip_resident_update(self._ref, self.side.cuda_stream), "resident Index update")
+        if self.lru is not None:
+            with torch.cuda.stream(self.side):
+                self.lru.commit(self.commit_rows)
+        self.updated.record(self.side)
+        abi.check(lib.kvip_hip_resident_fetch(self._ref, main.cuda_stream), "resident Fetch")
+        main.wait_event(self.updated)
+
+    def round(self):
+        """kvip_hip_resident_round on the current stream (initialisation, then `finish()`),
+        for callers that produce the TopK rows themselves."""
+        abi.check(self.library.kvip_hip_resident_begin(self._ref, abi.stream_handle(self.torch, self.device)),
+                  "resident round")
+        self.finish()
 
     def set_candidates(self, lru_slots):
         """Victim candidates for the next step ([batch, 2048] int32, oldest first)."""

@@ -13,9 +13,10 @@ buffers bound once, so the whole round is one hipGraph:
      `ContiguousFetch`): LI over the owners' Index rows, TopK, resolver, Fetch, Index update
      and outputs;
   3. with `lru` (a SlotLRUChains whose `slots` are the resident update's candidates), one
-     launch committing every decode request's selected slots, so the next round's victim
-     candidates follow the cache's own recency, as the reference's selector commits each
-     request's SlotLRU after a step (python/kvip/cache/lru.py:96-118);
+     launch committing every decode request's selected slots, attached to the resident
+     update so that it runs right after the Index update (beside the Fetch), so the next
+     round's victim candidates follow the cache's own recency, as the reference's selector
+     commits each request's SlotLRU after a step (python/kvip/cache/lru.py:96-118);
   4. the prefill indexer bound with `PrefillIndexer.bind`: LI over the paged cache for the
      packed chunks (cumulative query lengths) and TopK-2048 per row.
 
@@ -77,15 +78,12 @@ class MixedRound:
             target_rows=storage_keys.shape[0] * storage_keys.shape[1], count=new_tokens, target_base=0,
             mode=abi.INGEST_LIST)
         self.library = abi.load_library()
-        self.lru, self.commit_rows = lru, None
+        self.lru = lru
         if lru is not None:
-            upd = getattr(decode, "update", None)
-            if not getattr(decode, "resident", False) or lru.slots.data_ptr() != upd.lru_slots.data_ptr():
-                raise ValueError("the LRU chains must feed the resident decode update's candidates (slots aliasing "
-                                 "its lru_slots)")
-            if lru.chains != upd.rotating.batch:
-                raise ValueError(f"{lru.chains} LRU chains for {upd.rotating.batch} decode requests")
-            self.commit_rows = upd.slot_output.view(upd.rotating.batch, -1)
+            if not getattr(decode, "resident", False):
+                raise ValueError("the LRU chains must feed a resident decode update's candidates")
+            # Committed by the decode round itself, right after its Index update.
+            decode.update.attach_lru(lru)
         self.overlap = overlap
         if overlap:
             # The prefill branch: its own stream (default priority) and the fork/join events.
@@ -108,8 +106,6 @@ class MixedRound:
             self.joined.record(self.side)
         self.ingest()
         self.decode()
-        if self.lru is not None:
-            self.lru.commit(self.commit_rows)
         if self.overlap:
             torch.cuda.current_stream(self.device).wait_event(self.joined)
             return self.prefill.topk[:self.prefill._rows]

@@ -9,7 +9,7 @@ import ctypes
 from pathlib import Path
 
 LIBRARY = Path(__file__).resolve().parents[1] / "_lib" / "libkvip_hip.so"
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 KVIP_OK = 0
 KVIP_ERR_INVALID = 100000
@@ -225,6 +225,9 @@ PROTOTYPES = {
     "kvip_hip_resident_round": ([ctypes.POINTER(ResidentArgs), _p], ctypes.c_uint32),
     "kvip_hip_resident_begin": ([ctypes.POINTER(ResidentArgs), _p], ctypes.c_uint32),
     "kvip_hip_resident_finish": ([ctypes.POINTER(ResidentArgs), _p], ctypes.c_uint32),
+    "kvip_hip_resident_resolve": ([ctypes.POINTER(ResidentArgs), _p], ctypes.c_uint32),
+    "kvip_hip_resident_fetch": ([ctypes.POINTER(ResidentArgs), _p], ctypes.c_uint32),
+    "kvip_hip_resident_update": ([ctypes.POINTER(ResidentArgs), _p], ctypes.c_uint32),
     "kvip_hip_resident_prefetch": ([ctypes.POINTER(ResidentArgs), ctypes.POINTER(PrefetchArgs), _p], ctypes.c_uint32),
     "kvip_hip_resident_score": ([ctypes.POINTER(IndexerArgs), ctypes.POINTER(TopkArgs), ctypes.POINTER(ResidentArgs),
                                  _p], ctypes.c_uint32),

@@ -76,15 +76,20 @@ class Setup:
             host_pool=self.pool, resident=resident, tail_bounds=self.tail, prefetch=prefetch)
         self.lib = abi.load_library()
 
-    def run_round(self, selected, lru):
-        """Device round on the given TopK rows [batch*q, 2048] and candidates [batch, 2048]."""
+    def run_round(self, selected, lru, overlap=False):
+        """Device round on the given TopK rows [batch*q, 2048] and candidates [batch, 2048]:
+        kvip_hip_resident_round on one stream, or with overlap ResidentIndexUpdate.round()
+        (the Fetch beside the Index update on a second stream)."""
         t = self.torch
         self.rot.topk.copy_(t.from_numpy(selected.astype(np.int32)))
         if self.tail is not None:
             self.tail.copy_(t.from_numpy(self.h_tail))
         self.upd.set_candidates(t.from_numpy(lru.astype(np.int32)).to("cuda"))
-        rc = self.lib.kvip_hip_resident_round(ctypes.byref(self.upd.args), abi.stream_handle(t, self.rot.device))
-        abi.check(rc, "resident round")
+        if overlap:
+            self.upd.round()
+        else:
+            rc = self.lib.kvip_hip_resident_round(ctypes.byref(self.upd.args), abi.stream_handle(t, self.rot.device))
+            abi.check(rc, "resident round")
         t.cuda.synchronize()
 
     def oracle_round(self, selected, lru, prefetched=None):
@@ -282,13 +287,16 @@ def test_resident_forward_stateful_known_answer(torch_gpu):
     assert reads == [[2048, 2048], [0, 0], [4096, 4096], [2048, 2048]]
 
 
-def test_resident_errors_clear_the_owner_residency(torch_gpu):
+@pytest.mark.parametrize("overlap", [False, True], ids=["one_stream", "fetch_beside_update"])
+def test_resident_errors_clear_the_owner_residency(torch_gpu, overlap):
     """Failure contract of the reference (index_cache_update.h:5-21): a failed request's
     owner loses all residency; a request failing before the Fetch publishes -1 and moves
     nothing. Checked against the oracle on every table, then over a second round in which
-    that owner reads every position cold."""
+    that owner reads every position cold; the same with the Fetch beside the Index update."""
     torch = torch_gpu
     st = Setup(torch, batch=2, owners=2, history=8192, resident=4096, q_rows=1, seed=9)
+    run = st.run_round
+    st.run_round = lambda sel, lru: run(sel, lru, overlap=overlap)
     rng = st.rng
     selected = np.concatenate([mtp_selection(rng, 1, 8192, 4096, 0.5) for _ in range(2)])
     lru = np.stack([np.arange(2048), np.arange(2048, 4096)])
@@ -322,6 +330,8 @@ def test_resident_errors_clear_the_owner_residency(torch_gpu):
     # A KV address outside the host pool fails the request before anything is fetched.
     say("case source outside the host pool")
     st2 = Setup(torch, batch=1, owners=1, history=8192, resident=4096, q_rows=1, seed=10)
+    run2 = st2.run_round
+    st2.run_round = lambda sel, lru: run2(sel, lru, overlap=overlap)
     st2.addresses[0, 5000] = st2.pool.numel()
     st2.h_addresses[0, 5000] = st2.pool.numel()
     sel = np.full((1, TOPK), -1, np.int64)
@@ -331,6 +341,60 @@ def test_resident_errors_clear_the_owner_residency(torch_gpu):
     st2.compare(st2.oracle_round(sel, np.arange(2048)[None, :]))
     assert st2.upd.status.cpu().numpy()[0] & abi.RESIDENT_ERR_SOURCE
     assert torch.equal(st2.hot, hot_before) and not st2.valid.any()
+
+
+def test_resident_round_overlap_equals_sequential(torch_gpu):
+    """ResidentIndexUpdate.round() with the Fetch beside the Index update and the attached
+    LRU commit (two streams) leaves exactly the state of kvip_hip_resident_round followed by
+    the commit on one stream: every table, output, hot-cache row and LRU chain, over
+    consecutive rounds whose victim candidates come from the chains, first eagerly, then
+    replayed from one captured graph (with eager work between replays); one request fails
+    in round 3 (a candidate outside the hot range)."""
+    torch = torch_gpu
+    batch, history, resident = 3, 8192, 4096
+    a = Setup(torch, batch=batch, owners=batch, history=history, resident=resident, q_rows=2, seed=21)
+    b = Setup(torch, batch=batch, owners=batch, history=history, resident=resident, q_rows=2, seed=21)
+    chains_a = kvip_amd.SlotLRUChains(torch, batch, resident, "cuda", slots=a.upd.lru_slots)
+    chains_b = kvip_amd.SlotLRUChains(torch, batch, resident, "cuda", slots=b.upd.lru_slots)
+    a.upd.attach_lru(chains_a)
+    rows_b = b.upd.slot_output.view(batch, -1)
+    stream = abi.stream_handle(torch, "cuda")
+
+    def tables(st, chains):
+        u = st.upd
+        return [st.keys.view(torch.uint8), st.scales, st.addresses, st.logical, st.valid, st.hot, u.outputs,
+                u.miss_counts, u.status, u.changes, u.change_slots, u.reserved_hot, u.lru_slots, chains.order,
+                chains.bitmap]
+
+    rng = np.random.default_rng(4)
+    graph = None
+    for step in range(6):
+        sel = np.concatenate([mtp_selection(rng, 2, history, resident, 0.7) for _ in range(batch)])
+        say(f"round {step} ({'eager' if step < 2 else 'graph replay'})")
+        for st in (a, b):
+            st.rot.topk.copy_(torch.from_numpy(sel.astype(np.int32)))
+            if step == 3:
+                st.upd.lru_slots[1, 7] = resident + 5
+        if step < 2:
+            a.upd.round()
+        else:
+            if graph is None:
+                torch.cuda.synchronize()
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph):
+                    a.upd.round()
+            graph.replay()
+        abi.check(b.lib.kvip_hip_resident_round(ctypes.byref(b.upd.args), stream), "resident round")
+        chains_b.commit(rows_b)
+        torch.cuda.synchronize()
+        for x, y in zip(tables(a, chains_a), tables(b, chains_b)):
+            assert torch.equal(x, y), step
+        status = a.upd.status.cpu().numpy()
+        if step == 3:
+            assert status[1] & abi.RESIDENT_ERR_CANDIDATE and not a.valid[1].any()
+        else:
+            assert not status.any(), (step, status)
+        assert int(a.upd.miss_counts[:, 4].sum()) > 0
 
 
 def oracle_prefetch(st, keys, lru, pf):
