@@ -44,6 +44,8 @@ def parse():
     p.add_argument("--no-prefill", action="store_true", help="skip the config-3 prefill timing leg")
     p.add_argument("--no-mixed", action="store_true", help="skip the config-5 mixed-round timing leg")
     p.add_argument("--no-sfa", action="store_true", help="skip the sparse-attention consumer timing leg")
+    p.add_argument("--coissue", action="store_true",
+                   help="also run the MFMA/VALU co-issue probe (the prefill scoring's ceiling at its VALU density)")
     p.add_argument("--copy-calibration", action="store_true",
                    help="also run a plain 1 GiB device copy (for rocprof FETCH/WRITE_SIZE scaling)")
     return p.parse_args()
@@ -401,7 +403,8 @@ def prefill_leg(torch, kvip_amd, device, seed, iters=5):
     TopK-2048 launch and the Index update of the 4096 new rows (VllmIndexCacheStorage.
     ingest_prefill, one list launch after the first call imported the restored prefix).
     Scoring is priced against the dense fp8 MFMA peak with 2*64*128 flops per visible
-    (query, key) pair."""
+    (query, key) pair. `index_update` is the device launch alone; `index_update_eager` the
+    whole eager adapter step (host-built plan and its copies included)."""
     from types import SimpleNamespace as NS
     from kvip_amd import synthetic
     from kvip_amd.adapters.vllm.index_import import VllmIndexCacheStorage
@@ -440,14 +443,37 @@ def prefill_leg(torch, kvip_amd, device, seed, iters=5):
     if int(idx.status.item()) != 0 or int(storage.status.item()) != 0:
         raise RuntimeError("prefill leg: device status set")
     t = {name: float(np.mean([e[i].elapsed_time(e[i + 1]) for e in ev])) * 1e3
-         for i, name in enumerate(["score", "topk", "index_update"])}
+         for i, name in enumerate(["score", "topk", "index_update_eager"])}
+    # The device part of the Index update: the step's one list launch (the 4096 rows'
+    # sources and targets as ingest_prefill builds them), timed on its own; the eager step
+    # above adds the host-built plan and its copies to the device.
+    import ctypes
+    from kvip_amd.runtime import abi
+    tokens = torch.arange(plan.begin, plan.stop, device=device)
+    sources = wl["slot_mapping"].to(torch.int64).index_select(0, tokens).contiguous()
+    targets = (wl["positions"].to(torch.int64).index_select(0, tokens) + plan.owner * k_len).contiguous()
+    pk, ps = cache[0].view(torch.uint8).reshape(-1, 128), cache[1].reshape(-1)
+    iargs = abi.IngestArgs(source_keys=abi.ptr(pk), source_scales=abi.ptr(ps), target_keys=abi.ptr(storage.keys),
+                           target_scales=abi.ptr(storage.scales), status=abi.ptr(storage.status),
+                           source_rows=pk.shape[0], target_rows=storage.owners * storage.history,
+                           mode=abi.INGEST_LIST, count=int(tokens.numel()), sources=abi.ptr(sources),
+                           targets=abi.ptr(targets), target_base=0)
+    lib = abi.load_library()
+    torch.cuda.synchronize()
+    uev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(iters)]
+    for e0, e1 in uev:
+        e0.record(stream)
+        abi.check(lib.kvip_hip_ingest_index(ctypes.byref(iargs), stream.cuda_stream), "Index update")
+        e1.record(stream)
+    torch.cuda.synchronize()
+    t["index_update"] = float(np.mean([e0.elapsed_time(e1) for e0, e1 in uev])) * 1e3
     vis = np.clip(k_len - q_len + np.arange(q_len) + 1, 0, k_len).astype(np.int64)
     pairs = int(vis.sum())
     flops = 2 * heads * 128 * pairs
     tflops = flops / (t["score"] * 1e-6) / 1e12
     topk_bytes = pairs * 2 + q_len * (256 * 4 * 2 + TOPK * 4)
     update_bytes = q_len * (2 * (128 + 4) + 2 * 8)
-    total = sum(t.values())
+    total = t["score"] + t["topk"] + t["index_update"]
 
     # The same chunk with bf16 Q/K (no scales): scoring and TopK, priced against the dense
     # bf16 MFMA peak.
@@ -578,6 +604,36 @@ def mixed_leg(torch, kvip_amd, device, seed, rounds=20, warm=4):
             "rows_per_s": round((nd + pf_rows) / (us * 1e-6), 1),
             "decode_misses_per_round": round(miss, 1),
             "decode_hit_fraction": round(1.0 - miss / (nd * TOPK), 4), "rounds": rounds}
+
+
+def coissue_leg(torch, device, iters=2000):
+    """MFMA / VALU co-issue probe (kvip_hip_probe_coissue): every wave retires 4 fp8
+    32x32x64 MFMAs per iteration with V independent fp32 FMAs interleaved; one or two waves
+    per SIMD on every CU. Reports each V's time and the fraction of the dense fp8 peak
+    (5 PFLOP/s) its MFMAs reach. The prefill indexer issues 22 VALU instructions per MFMA
+    (V = 88 per 4 MFMAs), so the V = 88 fraction is the ceiling of its epilogue density."""
+    from kvip_amd.runtime import abi
+    lib = abi.load_library()
+    cus = torch.cuda.get_device_properties(device).multi_processor_count
+    out = torch.empty(cus * 2 * 256, dtype=torch.float32, device=device)
+    stream = torch.cuda.current_stream()
+    result = {"workload": f"{cus} CUs x 4 SIMDs, {iters} iterations of 4 MFMAs + V FMAs per wave", "iters": iters}
+    for waves in (1, 2):
+        blocks = cus * waves
+        row = {}
+        for v in (0, 32, 64, 88, 96):
+            abi.check(lib.kvip_hip_probe_coissue(v, blocks, 10, abi.ptr(out), stream.cuda_stream), "co-issue probe")
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            abi.check(lib.kvip_hip_probe_coissue(v, blocks, iters, abi.ptr(out), stream.cuda_stream), "co-issue probe")
+            e1.record(stream)
+            e1.synchronize()
+            ms = e0.elapsed_time(e1)
+            flops = blocks * 4 * iters * 4 * (32 * 32 * 64 * 2)
+            tflops = flops / (ms * 1e-3) / 1e12
+            row[str(v)] = {"us": round(ms * 1e3, 1), "tflops": round(tflops, 1), "frac": round(tflops / 5000.0, 4)}
+        result[f"waves_per_simd_{waves}"] = row
+    return result
 
 
 def main():
@@ -734,6 +790,7 @@ def main():
             ("prefill", args.no_prefill, lambda: prefill_leg(torch, kvip_amd, device, args.seed)),
             ("mixed", args.no_mixed, lambda: mixed_leg(torch, kvip_amd, device, args.seed)),
             ("sfa", args.no_sfa, lambda: sfa_leg(torch, kvip_amd, device, args.seed)),
+            ("coissue", not args.coissue, lambda: coissue_leg(torch, device)),
             ("cpu_baseline", args.no_cpu_baseline, lambda: cpu_baseline(torch, wl, rot, args.cpu_seconds))]
     print(f"bench: decode steps done ({result['ms_per_step']} ms/step)", file=sys.stderr, flush=True)
     for name, skip, leg in legs:

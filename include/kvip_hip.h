@@ -693,6 +693,11 @@ uint32_t kvip_hip_sparse_attention(const KvipSparseAttnArgs* args, void* stream)
 uint64_t kvip_hip_sparse_attention_workspace_bytes(int32_t rows, int32_t heads);
 /* Page publication of one step (PageUpdates.submit, python/kvip/cache/page_updates.py:27-62). */
 uint32_t kvip_hip_publish_pages(const KvipPageArgs* args, void* stream);
+/* Measurement probe, no reference counterpart (bench.py --coissue): `blocks` workgroups of
+ * 256 threads each retire `iters` x 4 fp8 32x32x64 MFMAs interleaved with
+ * valu_per_4_mfma (0, 32, 64, 88 or 96) independent fp32 FMAs, then write one float per
+ * thread to out [blocks * 256]; timing it prices a VALU epilogue against the MFMA rate. */
+uint32_t kvip_hip_probe_coissue(int32_t valu_per_4_mfma, int32_t blocks, int32_t iters, float* out, void* stream);
 
 #ifdef __cplusplus
 }

@@ -225,6 +225,7 @@ PROTOTYPES = {
     "kvip_hip_resident_round": ([ctypes.POINTER(ResidentArgs), _p], ctypes.c_uint32),
     "kvip_hip_resident_begin": ([ctypes.POINTER(ResidentArgs), _p], ctypes.c_uint32),
     "kvip_hip_resident_finish": ([ctypes.POINTER(ResidentArgs), _p], ctypes.c_uint32),
+    "kvip_hip_probe_coissue": ([ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, _p, _p], ctypes.c_uint32),
     "kvip_hip_resident_resolve": ([ctypes.POINTER(ResidentArgs), _p], ctypes.c_uint32),
     "kvip_hip_resident_fetch": ([ctypes.POINTER(ResidentArgs), _p], ctypes.c_uint32),
     "kvip_hip_resident_update": ([ctypes.POINTER(ResidentArgs), _p], ctypes.c_uint32),
