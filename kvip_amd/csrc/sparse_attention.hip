@@ -11,10 +11,12 @@
 // i.e. softmax attention with bf16 probabilities in the value product (the reference rounds
 // the normalised probabilities to bf16; here the unnormalised ones, divided once at the end).
 //
-// One workgroup per (query row, group of 16 heads, split of the 2048 indices) streams its
-// indices in tiles of 64 tokens: the rows are gathered (all loads of a tile in flight at once)
-// and dequantised to bf16 in LDS with the hardware conversions (v_cvt_pk_f32_fp8, OCP e4m3 on
-// gfx950, and v_cvt_pk_bf16_f32), the logits of the tile come from bf16 MFMA
+// One workgroup per (query row, set of one or two groups of 16 heads, split of the 2048
+// indices) resolves its indices to cache rows once (block table), then streams them in tiles
+// of 64 tokens: a tile's rows are gathered into registers while the previous tile is computed,
+// dequantised to bf16 in LDS with the hardware conversions (v_cvt_pk_f32_fp8, OCP e4m3 on
+// gfx950, and v_cvt_pk_bf16_f32) once for every head group of the set, the logits of the
+// tile come from bf16 MFMA
 // (v_mfma_f32_16x16x32_bf16: 16 heads x 16 tokens x 32 features), an online softmax keeps the
 // running maximum and sum per head, and the value product is a second MFMA (16 heads x 16
 // features x 32 tokens) accumulated in registers. Splits (up to 8, enough workgroups to fill
@@ -38,15 +40,21 @@ constexpr int kValueDim = 512;
 constexpr int kPieces = KVIP_KV_ROW_BYTES / 16;  // 41 pieces of a row, the last holds the scales
 constexpr int kPitch = kKeyDim + 8;         // bf16 per LDS key row (16 bytes of padding)
 constexpr int kPPitch = kSaTile + 8;        // bf16 per LDS probability row
-constexpr int kStageIters = (kSaTile * (kPieces - 1) + kSaThreads - 1) / kSaThreads;
+constexpr int kVtPitch = kSaTile + 8;       // bf16 per LDS value row (feature-major, one row per feature)
+// 16-byte token-group slot of value row f holding tokens 8 tg .. 8 tg + 7: XOR-swizzled by the
+// row's 16-feature block, so that the staging writes (8 lanes: one token group, features 16
+// apart) and the fragment reads (16 lanes: consecutive features, one token group) each hit
+// distinct banks.
+KVIP_DEVICE int vt_slot(int f, int tg) { return (tg ^ ((f >> 4) & 7)) * 8; }
+constexpr int kTokGroup = 8;  // tokens staged per thread
 constexpr int kPartial = 2 * kSaHeads + kSaHeads * kValueDim;  // floats per split: max, sum, output
 constexpr int kMaxSplits = 8;
 
-// Index splits per (row, head group): doubled up to 8 while the launch has fewer than 512
-// workgroups.
-__host__ __device__ inline int sa_splits(int rows, int groups) {
+// Index splits per (row, head-group set): doubled up to 8 while the launch has fewer than 256
+// workgroups (one per CU: the kernel holds one workgroup per CU).
+__host__ __device__ inline int sa_splits(int rows, int sets) {
     int s = 1;
-    while (s < kMaxSplits && static_cast<int64_t>(rows) * groups * s < 512) s *= 2;
+    while (s < kMaxSplits && static_cast<int64_t>(rows) * sets * s < 256) s *= 2;
     return s;
 }
 
@@ -63,42 +71,101 @@ KVIP_DEVICE uint16_t bf16_bits(float f) {  // round to nearest even (finite inpu
     return static_cast<uint16_t>(u >> 16);
 }
 
+// Value of the lane chosen by a DPP control within each row of 16 lanes.
+template <int CTRL>
+KVIP_DEVICE float dpp(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+// Max / sum over the 16 lanes of a row, in every lane of it: row mirror, half-row mirror,
+// then the two quad swaps; every lane's value enters each result exactly once.
+KVIP_DEVICE float row_max16(float x) {
+    x = fmaxf(x, dpp<0x140>(x));  // row_mirror
+    x = fmaxf(x, dpp<0x141>(x));  // row_half_mirror
+    x = fmaxf(x, dpp<0xB1>(x));   // quad_perm [1, 0, 3, 2]
+    return fmaxf(x, dpp<0x4E>(x));  // quad_perm [2, 3, 0, 1]
+}
+KVIP_DEVICE float row_sum16(float x) {
+    x += dpp<0x140>(x);
+    x += dpp<0x141>(x);
+    x += dpp<0xB1>(x);
+    return x + dpp<0x4E>(x);
+}
+
 KVIP_DEVICE bf16x8 as_bf16x8(v4i v) {
     bf16x8 r;
     __builtin_memcpy(&r, &v, 16);
     return r;
 }
 
-__global__ __launch_bounds__(kSaThreads) void sparse_attention_kernel(const KvipSparseAttnArgs p) {
-    __shared__ __align__(16) uint16_t s_k[kSaTile * kPitch];
-    __shared__ __align__(16) uint16_t s_p[kSaHeads * kPPitch];
-    __shared__ float s_red[4][kSaHeads];
-    __shared__ int64_t s_src[kSaTile];
+// Head groups of 16 handled by one workgroup: G share every staged tile (its gather and
+// dequantisation); group g runs on waves 4 g .. 4 g + 3, which keep its Q fragments,
+// online-softmax state and value accumulators in registers (G waves per SIMD).
+__host__ __device__ inline int sa_group_set(int heads) { return heads > kSaHeads ? 2 : 1; }
+__host__ __device__ inline int sa_sets(int heads) {
+    const int groups = (heads + kSaHeads - 1) / kSaHeads;
+    return (groups + sa_group_set(heads) - 1) / sa_group_set(heads);
+}
 
-    // XCD-aware order: the workgroups of a query row (head groups x splits) share
+template <int G>
+__global__ __launch_bounds__(kSaThreads * G, 1) void sparse_attention_kernel(const KvipSparseAttnArgs p) {
+    constexpr int kThreads = kSaThreads * G;
+    constexpr int kFeat = 16 / G;  // nope features per thread and token (16-byte or 8-byte pieces)
+    __shared__ __align__(16) uint16_t s_k[kSaTile * kPitch];         // keys, token-major
+    __shared__ __align__(16) uint16_t s_vt[kValueDim * kVtPitch];    // values, feature-major
+    __shared__ __align__(16) uint16_t s_p[G][kSaHeads * kPPitch];
+    __shared__ float s_red[G][4][kSaHeads];
+    __shared__ int32_t s_row[kTopK];  // cache row (block * 128 + offset) of each index, -1 = none
+
+    // XCD-aware order: the workgroups of a query row (head-group sets x splits) share
     // blockIdx % 8, so they run on one XCD, whose L2 then serves the row's KV rows and query to
-    // every head group after the first read.
+    // every set after the first read.
     const int groups = (p.heads + kSaHeads - 1) / kSaHeads;
-    const int splits = sa_splits(p.rows, groups);
-    const int units = groups * splits;
+    const int sets = (groups + G - 1) / G;
+    const int splits = sa_splits(p.rows, sets);
+    const int units = sets * splits;
     const int chunk = blockIdx.x / (8 * units), within = blockIdx.x % (8 * units);
     const int r = chunk * 8 + within % 8;
-    const int unit = within / 8, hg = unit % groups, sp = unit / groups;
-    const int h0 = hg * kSaHeads;
+    const int unit = within / 8, hs = unit % sets, sp = unit / sets;
     if (r >= p.rows) return;
     const int b = r / p.rows_per_request;
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int gw = tid >> 8;           // head group of this wave within the set
+    const int w = (tid >> 6) & 3;      // quarter: logits of tokens 16 w .., values of features 128 w ..
     const int lr = lane & 15, lg = lane >> 4;  // MFMA lane row / group
+    const int grp = hs * G + gw;
+    const bool live = grp < groups;    // uniform per wave: a set's last group may hold no heads
     uint32_t err = 0;
 
-    // Query fragments (A operand of the logits): head h0 + lr, features 32 s + 8 lg .. + 8.
+    // Cache rows of the split's indices, resolved once through the block table.
+    const int span = kTopK / splits;
+    const int* idx_row = p.indices + static_cast<size_t>(r) * kTopK + sp * span;
+    const int capacity = p.max_blocks * kBlockTokens;
+    for (int i = tid; i < span; i += kThreads) {
+        const int t = idx_row[i];
+        int row = -1;
+        if (t >= capacity) {
+            err |= KVIP_STATUS_BAD_TOKEN;
+        } else if (t >= 0) {
+            const int blk = p.block_table[static_cast<size_t>(b) * p.max_blocks + (t >> 7)];
+            if (static_cast<unsigned>(blk) < static_cast<unsigned>(p.num_blocks)) {
+                row = blk * kBlockTokens + (t & 127);
+            } else {
+                err |= KVIP_STATUS_BAD_BLOCK;
+            }
+        }
+        s_row[i] = row;
+    }
+
+    // Query fragments (A operand of the logits) of the wave's group: head 16 grp + lr,
+    // features 32 s + 8 lg .. + 8; heads past p.heads read as zero.
     bf16x8 qf[kKeyDim / 32];
     {
-        const bool live = h0 + lr < p.heads;
-        const uint16_t* q = p.query + (static_cast<size_t>(r) * p.heads + (live ? h0 + lr : 0)) * kKeyDim;
+        const int h = grp * kSaHeads + lr;
+        const bool hl = h < p.heads;
+        const uint16_t* q = p.query + (static_cast<size_t>(r) * p.heads + (hl ? h : 0)) * kKeyDim;
 #pragma unroll
         for (int s = 0; s < kKeyDim / 32; ++s) {
-            const v4i v = live ? *reinterpret_cast<const v4i*>(q + s * 32 + lg * 8) : v4i{0, 0, 0, 0};
+            const v4i v = hl ? *reinterpret_cast<const v4i*>(q + s * 32 + lg * 8) : v4i{0, 0, 0, 0};
             qf[s] = as_bf16x8(v);
         }
     }
@@ -111,186 +178,195 @@ __global__ __launch_bounds__(kSaThreads) void sparse_attention_kernel(const Kvip
         m_run[i] = -INFINITY;
         l_part[i] = 0.f;
     }
-    const int* idx_row = p.indices + static_cast<size_t>(r) * kTopK;
-    const int capacity = p.max_blocks * kBlockTokens;
+    __syncthreads();
 
-    const int span = kTopK / splits;
-    for (int t0 = sp * span; t0 < (sp + 1) * span; t0 += kSaTile) {
-        // Source rows of the tile.
-        if (tid < kSaTile) {
-            const int t = idx_row[t0 + tid];
-            int64_t src = -1;
-            if (t >= capacity) {
-                err |= KVIP_STATUS_BAD_TOKEN;
-            } else if (t >= 0) {
-                const int blk = p.block_table[static_cast<size_t>(b) * p.max_blocks + (t >> 7)];
-                if (static_cast<unsigned>(blk) < static_cast<unsigned>(p.num_blocks)) {
-                    src = static_cast<int64_t>(blk) * p.kv_block_stride + static_cast<int64_t>(t & 127) * p.row_stride;
-                } else {
-                    err |= KVIP_STATUS_BAD_BLOCK;
-                }
-            }
-            s_src[tid] = src;
-        }
-        __syncthreads();
-        // Gather + dequantise: pieces 0..31 are 16 nope bytes, 32..39 8 rope values; the loads
-        // of half a tile are issued before their conversions (a whole tile's would cost the
-        // registers of a second wave per SIMD).
+    // Staging map: thread (token group tg, nope slice pc) holds kFeat nope features
+    // [16 pc' + kFeat h, + kFeat) of the 8 tokens 8 tg .. 8 tg + 7 (pc' = pc % 32, h = the
+    // thread's half of the piece when two workgroup halves share it), and the tile's 512
+    // rope pieces are dealt over every thread. The next tile's pieces are requested right
+    // after the current tile is staged, so that their latency passes under its MFMA work.
+    const int tg = (tid >> 5) & 7, pc = tid & 31, half = tid >> 8;
+    const int f0 = pc * 16 + half * kFeat;  // first nope feature of the thread
+    constexpr int kRope = kSaTile * 8 / kThreads;
+    typedef int vfi __attribute__((ext_vector_type(kFeat / 4)));
+    vfi nope[kTokGroup];
+    v4i rope[kRope];
+    float sc[kTokGroup];
+    auto row_base = [&](int row) {
+        return p.kv_cache + static_cast<int64_t>(row >> 7) * p.kv_block_stride +
+               static_cast<int64_t>(row & 127) * p.row_stride;
+    };
+    auto load_tile = [&](int k) {
 #pragma unroll
-        for (int half = 0; half < 2; ++half) {
-            constexpr int kHalf = (kStageIters + 1) / 2;
-            v4i raw[kHalf];
-            float sc[kHalf];
-#pragma unroll
-            for (int j = 0; j < kHalf; ++j) {
-                const int q = (half * kHalf + j) * kSaThreads + tid;
-                raw[j] = v4i{0, 0, 0, 0};
-                sc[j] = 0.f;
-                if (half * kHalf + j < kStageIters && q < kSaTile * (kPieces - 1)) {
-                    const int i = q / (kPieces - 1), pc = q - i * (kPieces - 1);
-                    const int64_t src = s_src[i];
-                    if (src >= 0) {
-                        const uint8_t* row = p.kv_cache + src;
-                        raw[j] = *reinterpret_cast<const v4i*>(row + (pc < 32 ? pc * 16 : 512 + (pc - 32) * 16));
-                        if (pc < 32) sc[j] = *reinterpret_cast<const float*>(row + 640 + (pc >> 3) * 4);
-                    }
-                }
-            }
-#pragma unroll
-            for (int j = 0; j < kHalf; ++j) {
-                const int q = (half * kHalf + j) * kSaThreads + tid;
-                if (half * kHalf + j < kStageIters && q < kSaTile * (kPieces - 1)) {
-                    const int i = q / (kPieces - 1), pc = q - i * (kPieces - 1);
-                    uint16_t* dst = s_k + i * kPitch;
-                    if (pc < 32) {
-                        uint32_t out[8];
-#pragma unroll
-                        for (int k = 0; k < 4; ++k) {
-                            const f32x2 a = __builtin_amdgcn_cvt_pk_f32_fp8(raw[j][k], false);
-                            const f32x2 c = __builtin_amdgcn_cvt_pk_f32_fp8(raw[j][k], true);
-                            out[2 * k] = pack_bf16(a[0] * sc[j], a[1] * sc[j]);
-                            out[2 * k + 1] = pack_bf16(c[0] * sc[j], c[1] * sc[j]);
-                        }
-                        v4i* d = reinterpret_cast<v4i*>(dst + pc * 16);
-                        d[0] = v4i{static_cast<int>(out[0]), static_cast<int>(out[1]), static_cast<int>(out[2]),
-                                   static_cast<int>(out[3])};
-                        d[1] = v4i{static_cast<int>(out[4]), static_cast<int>(out[5]), static_cast<int>(out[6]),
-                                   static_cast<int>(out[7])};
-                    } else {
-                        *reinterpret_cast<v4i*>(dst + 512 + (pc - 32) * 8) = raw[j];
-                    }
-                }
+        for (int u = 0; u < kTokGroup; ++u) {
+            const int row = s_row[k * kSaTile + tg * kTokGroup + u];
+            nope[u] = vfi{};
+            sc[u] = 0.f;
+            if (row >= 0) {
+                const uint8_t* base = row_base(row);
+                nope[u] = *reinterpret_cast<const vfi*>(base + f0);
+                sc[u] = *reinterpret_cast<const float*>(base + 640 + (pc >> 3) * 4);
             }
         }
-        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < kRope; ++j) {
+            const int q = j * kThreads + tid;
+            const int row = s_row[k * kSaTile + (q >> 3)];
+            rope[j] = row >= 0 ? *reinterpret_cast<const v4i*>(row_base(row) + 512 + (q & 7) * 16) : v4i{0, 0, 0, 0};
+        }
+    };
+    // Dequantisation to bf16: keys [nope * scale, rope] token-major in s_k, values
+    // nope * scale feature-major in s_vt (the 8-token block transposed in registers).
+    auto stage_tile = [&]() {
+        uint32_t out[kTokGroup][kFeat / 2];  // out[u][k]: features f0 + 2k, 2k + 1 of token u
+#pragma unroll
+        for (int u = 0; u < kTokGroup; ++u) {
+#pragma unroll
+            for (int k = 0; k < kFeat / 4; ++k) {
+                const f32x2 a = __builtin_amdgcn_cvt_pk_f32_fp8(nope[u][k], false);
+                const f32x2 c = __builtin_amdgcn_cvt_pk_f32_fp8(nope[u][k], true);
+                out[u][2 * k] = pack_bf16(a[0] * sc[u], a[1] * sc[u]);
+                out[u][2 * k + 1] = pack_bf16(c[0] * sc[u], c[1] * sc[u]);
+            }
+            uint16_t* d = s_k + (tg * kTokGroup + u) * kPitch + f0;
+            if constexpr (kFeat == 16) {
+                reinterpret_cast<v4i*>(d)[0] = v4i{static_cast<int>(out[u][0]), static_cast<int>(out[u][1]),
+                                                   static_cast<int>(out[u][2]), static_cast<int>(out[u][3])};
+                reinterpret_cast<v4i*>(d)[1] = v4i{static_cast<int>(out[u][4]), static_cast<int>(out[u][5]),
+                                                   static_cast<int>(out[u][6]), static_cast<int>(out[u][7])};
+            } else {
+                *reinterpret_cast<v4i*>(d) = v4i{static_cast<int>(out[u][0]), static_cast<int>(out[u][1]),
+                                                 static_cast<int>(out[u][2]), static_cast<int>(out[u][3])};
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < kFeat / 2; ++k) {
+            uint32_t lo[4], hi[4];  // tokens (2 m, 2 m + 1) of feature f0 + 2k (lo) and + 1 (hi)
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                const uint32_t x = out[2 * m][k], y = out[2 * m + 1][k];
+                lo[m] = (x & 0xFFFFu) | (y << 16);
+                hi[m] = (x >> 16) | (y & 0xFFFF0000u);
+            }
+            const int f = f0 + 2 * k;
+            *reinterpret_cast<v4i*>(s_vt + f * kVtPitch + vt_slot(f, tg)) =
+                v4i{static_cast<int>(lo[0]), static_cast<int>(lo[1]), static_cast<int>(lo[2]), static_cast<int>(lo[3])};
+            *reinterpret_cast<v4i*>(s_vt + (f + 1) * kVtPitch + vt_slot(f + 1, tg)) =
+                v4i{static_cast<int>(hi[0]), static_cast<int>(hi[1]), static_cast<int>(hi[2]), static_cast<int>(hi[3])};
+        }
+#pragma unroll
+        for (int j = 0; j < kRope; ++j) {
+            const int q = j * kThreads + tid;
+            *reinterpret_cast<v4i*>(s_k + (q >> 3) * kPitch + 512 + (q & 7) * 8) = rope[j];
+        }
+    };
 
+    const int tiles = span / kSaTile;
+    load_tile(0);
+    for (int k = 0; k < tiles; ++k) {
+        stage_tile();
+        __syncthreads();  // s_k / s_vt hold tile k
+        if (k + 1 < tiles) load_tile(k + 1);
+        const bool tok_live = s_row[k * kSaTile + w * 16 + lr] >= 0;
         // Logits of tokens 16 w .. 16 w + 15: lane holds heads 4 lg + i of token 16 w + lr.
-        f32x4 sv = f32x4{0.f, 0.f, 0.f, 0.f};
-        {
+        float lg_v[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+        if (live) {
+            f32x4 sv = f32x4{0.f, 0.f, 0.f, 0.f};
             const uint16_t* kr = s_k + (w * 16 + lr) * kPitch + lg * 8;
 #pragma unroll
             for (int s = 0; s < kKeyDim / 32; ++s) {
                 const bf16x8 kv = as_bf16x8(*reinterpret_cast<const v4i*>(kr + s * 32));
                 sv = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qf[s], kv, sv, 0, 0, 0);
             }
-        }
-        const bool tok_live = s_src[w * 16 + lr] >= 0;
-        float lg_v[4], mx[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            lg_v[i] = tok_live ? sv[i] * p.scale : -INFINITY;
-            float m = lg_v[i];
-#pragma unroll
-            for (int o = 1; o < 16; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
-            mx[i] = m;
-        }
-        if (lr == 0) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) s_red[w][lg * 4 + i] = mx[i];
+            for (int i = 0; i < 4; ++i) {
+                lg_v[i] = tok_live ? sv[i] * p.scale : -INFINITY;
+                const float mx = row_max16(lg_v[i]);
+                if (lr == 0) s_red[gw][w][lg * 4 + i] = mx;
+            }
         }
         __syncthreads();
-        float alpha[4];
+        float alpha[4] = {1.f, 1.f, 1.f, 1.f};
+        if (live) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int h = lg * 4 + i;
+                const float tile_max =
+                    fmaxf(fmaxf(s_red[gw][0][h], s_red[gw][1][h]), fmaxf(s_red[gw][2][h], s_red[gw][3][h]));
+                const float m_new = fmaxf(m_run[i], tile_max);
+                alpha[i] = m_new == -INFINITY ? 1.f : __expf(m_run[i] - m_new);
+                m_run[i] = m_new;
+                const float pr = m_new == -INFINITY ? 0.f : __expf(lg_v[i] - m_new);
+                l_part[i] = l_part[i] * alpha[i] + pr;
+                s_p[gw][h * kPPitch + w * 16 + lr] = bf16_bits(pr);
+            }
+        }
+        __syncthreads();  // s_p complete; s_red free for the next tile
+        if (live) {
+            // Value product for features 128 w .. 128 w + 127 (8 MFMA columns of 16).
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[t][i] *= alpha[i];
+            }
+#pragma unroll
+            for (int ks = 0; ks < kSaTile / 32; ++ks) {
+                const bf16x8 pa = as_bf16x8(*reinterpret_cast<const v4i*>(&s_p[gw][lr * kPPitch + ks * 32 + lg * 8]));
+                // B fragment: tokens ks * 32 + 8 lg .. + 8 of feature 128 w + 16 t + lr.
+#pragma unroll
+                for (int t = 0; t < 8; ++t) {
+                    const int f = w * 128 + t * 16 + lr;
+                    const v4i vb = *reinterpret_cast<const v4i*>(s_vt + f * kVtPitch + vt_slot(f, ks * 4 + lg));
+                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, as_bf16x8(vb), acc[t], 0, 0, 0);
+                }
+            }
+        }
+        __syncthreads();  // s_k, s_vt and s_p are rewritten by the next tile
+    }
+
+    // Row sums: over the 16 lanes of a group, then over the group's waves; then this split's
+    // partial (max, sum, unnormalised output per head) or the normalised output.
+    float l_tot[4];
+    if (live) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float l = row_sum16(l_part[i]);
+            if (lr == 0) s_red[gw][w][lg * 4 + i] = l;
+        }
+    }
+    __syncthreads();
+    if (live) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int h = lg * 4 + i;
-            const float tile_max = fmaxf(fmaxf(s_red[0][h], s_red[1][h]), fmaxf(s_red[2][h], s_red[3][h]));
-            const float m_new = fmaxf(m_run[i], tile_max);
-            alpha[i] = m_new == -INFINITY ? 1.f : __expf(m_run[i] - m_new);
-            m_run[i] = m_new;
-            const float pr = m_new == -INFINITY ? 0.f : __expf(lg_v[i] - m_new);
-            const uint16_t pb = bf16_bits(pr);
-            l_part[i] = l_part[i] * alpha[i] + pr;
-            s_p[h * kPPitch + w * 16 + lr] = pb;
+            l_tot[i] = s_red[gw][0][h] + s_red[gw][1][h] + s_red[gw][2][h] + s_red[gw][3][h];
         }
-        __syncthreads();
-
-        // Value product for features 128 w .. 128 w + 127 (8 MFMA columns of 16).
+        if (splits > 1) {
+            float* ws = p.workspace + ((static_cast<size_t>(r) * groups + grp) * splits + sp) * kPartial;
+            if (w == 0 && lr == 0) {
 #pragma unroll
-        for (int t = 0; t < 8; ++t) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) acc[t][i] *= alpha[i];
-        }
-#pragma unroll
-        for (int ks = 0; ks < kSaTile / 32; ++ks) {
-            const bf16x8 pa = as_bf16x8(*reinterpret_cast<const v4i*>(s_p + lr * kPPitch + ks * 32 + lg * 8));
-            const uint16_t* vr = s_k + (ks * 32 + lg * 8) * kPitch + w * 128 + lr;
-#pragma unroll
-            for (int t = 0; t < 8; ++t) {
-                uint32_t pk[4];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    pk[j] = static_cast<uint32_t>(vr[(2 * j) * kPitch + t * 16]) |
-                            (static_cast<uint32_t>(vr[(2 * j + 1) * kPitch + t * 16]) << 16);
+                for (int i = 0; i < 4; ++i) {
+                    ws[lg * 4 + i] = m_run[i];
+                    ws[kSaHeads + lg * 4 + i] = l_tot[i];
                 }
-                const v4i vb = v4i{static_cast<int>(pk[0]), static_cast<int>(pk[1]), static_cast<int>(pk[2]),
-                                   static_cast<int>(pk[3])};
-                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, as_bf16x8(vb), acc[t], 0, 0, 0);
             }
-        }
-        __syncthreads();  // s_k, s_p and s_red are rewritten by the next tile
-    }
-
-    // Row sums: over the 16 lanes of a group, then over the waves.
-    float l_tot[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        float l = l_part[i];
-#pragma unroll
-        for (int o = 1; o < 16; o <<= 1) l += __shfl_xor(l, o);
-        if (lr == 0) s_red[w][lg * 4 + i] = l;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int h = lg * 4 + i;
-        l_tot[i] = s_red[0][h] + s_red[1][h] + s_red[2][h] + s_red[3][h];
-    }
-    if (splits > 1) {  // partial of this split: max and sum per head, unnormalised output
-        float* ws = p.workspace + ((static_cast<size_t>(r) * groups + hg) * splits + sp) * kPartial;
-        if (w == 0 && lr == 0) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                ws[lg * 4 + i] = m_run[i];
-                ws[kSaHeads + lg * 4 + i] = l_tot[i];
+                float* o = ws + 2 * kSaHeads + (lg * 4 + i) * kValueDim + w * 128 + lr;
+#pragma unroll
+                for (int t = 0; t < 8; ++t) o[t * 16] = acc[t][i];
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int h = grp * kSaHeads + lg * 4 + i;
+                if (h >= p.heads) continue;
+                const float inv = l_tot[i] > 0.f ? 1.f / l_tot[i] : 0.f;
+                float* o = p.output + (static_cast<size_t>(r) * p.heads + h) * kValueDim + w * 128 + lr;
+#pragma unroll
+                for (int t = 0; t < 8; ++t) o[t * 16] = acc[t][i] * inv;
             }
         }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            float* o = ws + 2 * kSaHeads + (lg * 4 + i) * kValueDim + w * 128 + lr;
-#pragma unroll
-            for (int t = 0; t < 8; ++t) o[t * 16] = acc[t][i];
-        }
-        report(p.status, err);
-        return;
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int h = h0 + lg * 4 + i;
-        if (h >= p.heads) continue;
-        const float inv = l_tot[i] > 0.f ? 1.f / l_tot[i] : 0.f;
-        float* o = p.output + (static_cast<size_t>(r) * p.heads + h) * kValueDim + w * 128 + lr;
-#pragma unroll
-        for (int t = 0; t < 8; ++t) o[t * 16] = acc[t][i] * inv;
     }
     report(p.status, err);
 }
@@ -300,7 +376,7 @@ __global__ __launch_bounds__(kSaThreads) void sparse_attention_merge_kernel(cons
     __shared__ float s_w[kMaxSplits][kSaHeads];
     __shared__ float s_inv[kSaHeads];
     const int groups = (p.heads + kSaHeads - 1) / kSaHeads;
-    const int splits = sa_splits(p.rows, groups);
+    const int splits = sa_splits(p.rows, sa_sets(p.heads));
     const int unit = blockIdx.x / 8, part = blockIdx.x % 8;
     const int r = unit / groups, h0 = (unit % groups) * kSaHeads;
     const float* ws = p.workspace + static_cast<size_t>(unit) * splits * kPartial;
@@ -335,7 +411,7 @@ __global__ __launch_bounds__(kSaThreads) void sparse_attention_merge_kernel(cons
 uint64_t sparse_attention_workspace_bytes(int rows, int heads) {
     if (rows < 1 || heads < 1) return 0;
     const int groups = (heads + kSaHeads - 1) / kSaHeads;
-    const int splits = sa_splits(rows, groups);
+    const int splits = sa_splits(rows, sa_sets(heads));
     return splits > 1 ? static_cast<uint64_t>(rows) * groups * splits * kPartial * sizeof(float) : 0;
 }
 
@@ -344,7 +420,8 @@ uint32_t validate_sparse_attention(const KvipSparseAttnArgs* a) {
     const bool ok = a->query && a->kv_cache && a->block_table && a->indices && a->output && a->rows >= 1 &&
                     a->rows_per_request >= 1 && a->rows % a->rows_per_request == 0 && a->heads >= 1 &&
                     a->heads <= 128 && a->max_blocks >= 1 && a->max_blocks <= (1 << 24) / kBlockTokens &&
-                    a->num_blocks >= 1 && a->row_stride >= KVIP_KV_ROW_BYTES && a->row_stride % 16 == 0 &&
+                    a->num_blocks >= 1 && a->num_blocks < (1 << 24) && a->row_stride >= KVIP_KV_ROW_BYTES &&
+                    a->row_stride % 16 == 0 &&
                     a->kv_block_stride % 16 == 0 &&
                     a->kv_block_stride >= static_cast<int64_t>(kBlockTokens) * a->row_stride &&
                     (reinterpret_cast<uintptr_t>(a->kv_cache) & 15u) == 0 &&
@@ -359,10 +436,15 @@ extern "C" uint32_t kvip_hip_sparse_attention(const KvipSparseAttnArgs* args, vo
     const uint32_t rc = kvip::validate_sparse_attention(args);
     if (rc != KVIP_OK) return rc;
     const int groups = (args->heads + kvip::kSaHeads - 1) / kvip::kSaHeads;
-    const int splits = kvip::sa_splits(args->rows, groups);
+    const int sets = kvip::sa_sets(args->heads);
+    const int splits = kvip::sa_splits(args->rows, sets);
     const hipStream_t s = static_cast<hipStream_t>(stream);
-    hipLaunchKernelGGL(kvip::sparse_attention_kernel, dim3(((args->rows + 7) / 8) * 8 * groups * splits),
-                       dim3(kvip::kSaThreads), 0, s, *args);
+    const dim3 grid(((args->rows + 7) / 8) * 8 * sets * splits);
+    if (kvip::sa_group_set(args->heads) == 2) {
+        hipLaunchKernelGGL(kvip::sparse_attention_kernel<2>, grid, dim3(2 * kvip::kSaThreads), 0, s, *args);
+    } else {
+        hipLaunchKernelGGL(kvip::sparse_attention_kernel<1>, grid, dim3(kvip::kSaThreads), 0, s, *args);
+    }
     if (splits > 1) {
         hipLaunchKernelGGL(kvip::sparse_attention_merge_kernel, dim3(args->rows * groups * 8), dim3(kvip::kSaThreads),
                            0, s, *args);
