@@ -57,7 +57,7 @@ KVIP_DEVICE void wave_hist_add(uint32_t* hist, uint32_t bin, bool live) {
     unsigned long long pending = __ballot(live);
     while (pending) {
         const int leader = __ffsll(pending) - 1;
-        const uint32_t lead_bin = __shfl(bin, leader);
+        const uint32_t lead_bin = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(bin), leader));
         const bool same = live && bin == lead_bin;
         const unsigned long long group = __ballot(same);
         if (lane_id() == leader) atomicAdd(&hist[lead_bin], static_cast<uint32_t>(__popcll(group)));
@@ -66,14 +66,38 @@ KVIP_DEVICE void wave_hist_add(uint32_t* hist, uint32_t bin, bool live) {
     }
 }
 
+// Value of the lane `CTRL` selects within each row of 16 lanes (a DPP row shift); lanes
+// whose source falls outside their row read 0.
+template <int CTRL>
+KVIP_DEVICE uint32_t dpp_row(uint32_t v) {
+    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, 0xF, 0xF, true));
+}
+
+// Inclusive prefix sum over the 64 lanes: Hillis-Steele inside each 16-lane row by DPP row
+// shifts (no LDS round trip), then the totals of the lower rows by readlane.
 KVIP_DEVICE uint32_t wave_inclusive_scan(uint32_t v) {
-    const int lane = lane_id();
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        const uint32_t t = __shfl_up(v, d);
-        if (lane >= d) v += t;
-    }
-    return v;
+    v += dpp_row<0x111>(v);  // row_shr:1
+    v += dpp_row<0x112>(v);  // row_shr:2
+    v += dpp_row<0x114>(v);  // row_shr:4
+    v += dpp_row<0x118>(v);  // row_shr:8
+    const uint32_t r0 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 15));
+    const uint32_t r1 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 31));
+    const uint32_t r2 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 47));
+    const int row = lane_id() >> 4;
+    return v + (row >= 1 ? r0 : 0u) + (row >= 2 ? r1 : 0u) + (row >= 3 ? r2 : 0u);
+}
+
+// Inclusive suffix sum over the 64 lanes (lane l gets the sum of lanes l..63).
+KVIP_DEVICE uint32_t wave_inclusive_suffix_scan(uint32_t v) {
+    v += dpp_row<0x101>(v);  // row_shl:1
+    v += dpp_row<0x102>(v);  // row_shl:2
+    v += dpp_row<0x104>(v);  // row_shl:4
+    v += dpp_row<0x108>(v);  // row_shl:8
+    const uint32_t r1 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 16));
+    const uint32_t r2 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 32));
+    const uint32_t r3 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 48));
+    const int row = lane_id() >> 4;
+    return v + (row <= 0 ? r1 : 0u) + (row <= 1 ? r2 : 0u) + (row <= 2 ? r3 : 0u);
 }
 
 // Exclusive prefix sum over the whole workgroup (blockDim.x a multiple of 64, at most

@@ -161,7 +161,8 @@ KVIP_DEVICE void ss_select(const KvipTopkArgs& t, int b, int v, uint32_t* rec, u
     int hb;
     uint32_t gt_hi;
     wave_select_bin(h, kTopK, hb, gt_hi);
-    const uint32_t hist_total = __shfl(wave_inclusive_scan(h[0] + h[1] + h[2] + h[3]), 63);
+    const uint32_t hist_total =
+        static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(wave_inclusive_scan(h[0] + h[1] + h[2] + h[3])), 63));
     if (tid == 0 && hist_total != static_cast<uint32_t>(v)) err |= KVIP_STATUS_HISTOGRAM;
     __syncthreads();
     const RowSelection sel =

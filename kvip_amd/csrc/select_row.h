@@ -28,8 +28,7 @@ namespace kvip {
 KVIP_DEVICE void wave_select_bin(const uint32_t (&h)[4], uint32_t target, int& sel, uint32_t& above) {
     const int lane = lane_id();
     const uint32_t mine = h[0] + h[1] + h[2] + h[3];
-    // Suffix sums over lanes: an inclusive scan of the reversed lane order.
-    const uint32_t suffix_incl = __shfl(wave_inclusive_scan(__shfl(mine, 63 - lane)), 63 - lane);
+    const uint32_t suffix_incl = wave_inclusive_suffix_scan(mine);
     uint32_t ge = suffix_incl - mine;  // keys in bins of higher lanes
     int best = -1;
     uint32_t best_above = 0;
@@ -44,8 +43,8 @@ KVIP_DEVICE void wave_select_bin(const uint32_t (&h)[4], uint32_t target, int& s
     }
     const unsigned long long cand = __ballot(best >= 0);
     const int top = cand ? 63 - __clzll(cand) : 0;
-    sel = cand ? __shfl(best, top) : -1;
-    above = __shfl(best_above, top);
+    sel = cand ? __builtin_amdgcn_readlane(best, top) : -1;
+    above = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(best_above), top));
 }
 
 struct RowSelection {

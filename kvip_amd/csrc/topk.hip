@@ -215,7 +215,8 @@ __global__ __launch_bounds__(kTopkThreads) void topk_regs_kernel(const KvipTopkA
     wave_select_bin(h, kTopK, hb, gt_hi);
     // The scoring histogram counts every visible key once: a total other than `valid`
     // means the scoring launch skipped or repeated tiles.
-    const uint32_t hist_total = __shfl(wave_inclusive_scan(h[0] + h[1] + h[2] + h[3]), 63);
+    const uint32_t hist_total =
+        static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(wave_inclusive_scan(h[0] + h[1] + h[2] + h[3])), 63));
     const bool counted = hist_total == static_cast<uint32_t>(valid);
     if (tid < 256) s_hist[tid] = 0u;
     reinterpret_cast<int2*>(s_out)[tid] = int2{-1, -1};
