@@ -95,7 +95,7 @@ __global__ __launch_bounds__(kGatherThreads) void fetch_gather_kernel(const Kvip
             const int idx = it * 64 + lane;
             const int r = idx / PIECES;
             const int piece = idx - r * PIECES;
-            const int64_t base = __shfl(src, min(r, kRowsPerWave - 1));
+            const int64_t base = row_value<PIECES, kRowsPerWave>(src, it, r);
             val[it] = v4i{0, 0, 0, 0};
             if (idx < total && base >= 0) {
                 val[it] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(p.kv_cache + base + piece * 16));

@@ -66,6 +66,29 @@ KVIP_DEVICE void wave_hist_add(uint32_t* hist, uint32_t bin, bool live) {
     }
 }
 
+// 64-bit value of lane l (l uniform).
+KVIP_DEVICE int64_t readlane64(int64_t v, int l) {
+    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), l));
+    const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v >> 32), l));
+    return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+// Row copies with a wave-wide 16-byte piece index: piece idx = it * 64 + lane of a list of
+// rows of PIECES pieces belongs to row idx / PIECES. For a compile-time `it` that row is one
+// of at most three consecutive rows, so the row's value (held by lane `row` of v) is picked
+// from three readlanes instead of an LDS shuffle.
+template <int PIECES, int ROWS>
+KVIP_DEVICE int64_t row_value(int64_t v, int it, int row) {
+    const int lo = min((it * 64) / PIECES, ROWS - 1);
+    const int hi = min((it * 64 + 63) / PIECES, ROWS - 1);
+    int64_t out = readlane64(v, lo);
+#pragma unroll
+    for (int q = 1; q <= 2; ++q) {
+        if (lo + q <= hi && row == lo + q) out = readlane64(v, lo + q);
+    }
+    return out;
+}
+
 // Value of the lane `CTRL` selects within each row of 16 lanes (a DPP row shift); lanes
 // whose source falls outside their row read 0.
 template <int CTRL>

@@ -569,7 +569,7 @@ __global__ __launch_bounds__(256) void resident_fetch_kernel(const KvipResidentA
                 const int idx = it * 64 + lane;
                 const int r = idx / PIECES;
                 const int piece = idx - r * PIECES;
-                const int64_t s = __shfl(src, min(r, kFetchRows - 1));
+                const int64_t s = row_value<PIECES, kFetchRows>(src, it, r);
                 val[it] = v4i{0, 0, 0, 0};
                 if (idx < n && s >= 0) {
                     val[it] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(p.host_pool + s + piece * 16));
@@ -580,7 +580,7 @@ __global__ __launch_bounds__(256) void resident_fetch_kernel(const KvipResidentA
                 const int idx = it * 64 + lane;
                 const int r = idx / PIECES;
                 const int piece = idx - r * PIECES;
-                const int64_t d = __shfl(dst, min(r, kFetchRows - 1));
+                const int64_t d = row_value<PIECES, kFetchRows>(dst, it, r);
                 if (idx < n && d >= 0) *reinterpret_cast<v4i*>(p.hot_cache + d + piece * 16) = val[it];
             }
         } else {
