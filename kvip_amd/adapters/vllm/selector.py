@@ -108,6 +108,40 @@ class PagedIndexer:
         return selected.view(rows, 1, TOPK)
 
 
+class _StepLayout:
+    """Host view of one scheduler step: its plans split by kind, the decode requests' query
+    layout, and the step kind ("decode": no plan or decode plans only; "prefill": prefill
+    plans only; "mixed")."""
+
+    __slots__ = ("plans", "decodes", "prefills", "kind")
+
+    def __init__(self, plans=()):
+        self.plans = tuple(plans)
+        self.decodes = tuple(p for p in self.plans if p.decode)
+        self.prefills = tuple((row, p) for row, p in enumerate(self.plans) if not p.decode)
+        if self.prefills:
+            self.kind = "mixed" if self.decodes else "prefill"
+        else:
+            self.kind = "decode"
+
+    def query_layout(self):
+        """(query counts, first flat token, owner row) of every decode request, in order."""
+        counts, begins, owners = [], [], []
+        for p in self.decodes:
+            counts.append(int(p.stop - p.begin))
+            begins.append(int(p.begin))
+            owners.append(int(p.owner))
+        return counts, begins, owners
+
+    def shared_decode_owners(self):
+        """Owner rows named by more than one decode request that has tokens this step."""
+        seen, shared = set(), set()
+        for p in self.decodes:
+            if p.stop > p.begin:
+                (shared if p.owner in seen else seen).add(p.owner)
+        return sorted(shared)
+
+
 class VllmIndexSelector:
     def __init__(self, torch, *, inputs, rotating, update, logical_ids, row_owners, prefix_workspace=None,
                  storage=None, forward_factory=LIFetchForward, unique_active_owners=False):
@@ -132,67 +166,85 @@ class VllmIndexSelector:
             problems.append("the Index update must publish token-order outputs of these QueryInputs")
         if problems:
             raise ValueError("VllmIndexSelector: " + "; ".join(problems))
-        self.torch, self.inputs, self.rotating, self.update = torch, inputs, rotating, update
-        self.forward = forward_factory(rotating, update)
+        self.torch, self.inputs, self.rotating, self.update, self.storage = torch, inputs, rotating, update, storage
+        self.logical_ids, self.row_owners, self.prefix_workspace = logical_ids, row_owners, prefix_workspace
         self.unique_active_owners = unique_active_owners
-        self.logical_ids, self.row_owners = logical_ids, row_owners
-        self.prefix_workspace = prefix_workspace
-        self.storage, self.positions = storage, None
+        self.forward = forward_factory(rotating, update)
         self.history = int(logical_ids.shape[1])
         self.topk = rotating.topk.view(inputs.batch, QUERIES_PER_REQUEST, TOPK)
-        self.attention_indices = None
-        # ABC tail bounds of the step ([batch, 2] int32 {begin, end}, e.g. columns 2:4 of the
-        # serving policy's ABC descriptors), copied into the update's tail_bounds before each
-        # decode forward (selector.py:42, :115-116 of the reference).
+        # A row-owner tensor of its own is refreshed from the inputs' row by every prepare.
+        self._owners_copied = row_owners.data_ptr() != inputs.row_owners.data_ptr()
+        self._step = _StepLayout()
+        self._selection = None  # hot-cache slots of the last decode selection, token order
+        # Caller-set per step: positions of the step's tokens (the prefill Index ingest
+        # reads them), and the ABC tail bounds ([batch, 2] int32 {begin, end}, e.g. columns
+        # 2:4 of the serving policy's ABC descriptors) copied into the update's tail_bounds
+        # before each decode forward (selector.py:42, :115-116 of the reference).
+        self.positions = None
         self.tail_source = None
-        self.plans = None
-        self.decodes = ()
-        self.prefills = ()
+
+    # The step's plans as the reference's selector exposes them.
+    plans = property(lambda self: self._step.plans or None)
+    decodes = property(lambda self: self._step.decodes)
+    prefills = property(lambda self: self._step.prefills)
+    attention_indices = property(lambda self: self._selection)
 
     def prepare(self, plans, *, prepare_inputs=True):
         """Host layout of one scheduler step, no device read: the Index owners of new
         requests are reset and the decode requests' query rows laid out."""
-        self.plans = tuple(plans)
-        self.decodes = tuple(p for p in self.plans if p.decode)
-        self.prefills = tuple((row, p) for row, p in enumerate(self.plans) if not p.decode)
+        step = _StepLayout(plans)
         if self.unique_active_owners:
-            live = [p.owner for p in self.decodes if p.stop > p.begin]
-            if len(set(live)) != len(live):
-                raise ValueError(f"decode requests share an owner row: {sorted(live)}")
+            shared = step.shared_decode_owners()
+            if shared:
+                raise ValueError(f"decode requests share an owner row: {shared}")
+        self._step = step
         if self.storage is not None:
-            self.storage.prepare(self.plans)
+            self.storage.prepare(step.plans)
         if prepare_inputs:
-            self.inputs.prepare([int(p.stop - p.begin) for p in self.decodes],
-                                query_starts=[int(p.begin) for p in self.decodes],
-                                query_owners=[int(p.owner) for p in self.decodes])
-        if self.row_owners.data_ptr() != self.inputs.row_owners.data_ptr():
+            counts, begins, owners = step.query_layout()
+            self.inputs.prepare(counts, query_starts=begins, query_owners=owners)
+        if self._owners_copied:
             self.row_owners.copy_(self.inputs.row_owners)
 
     def __call__(self, query, weights, indexer, metadata, query_scale):
         """TopK-2048 logical positions of the step's tokens, int32 [tokens, 1, 2048]; the
         slots of the decode tokens' selections are kept for `slots`."""
-        mixed = bool(self.decodes) and bool(self.prefills)
-        if self.storage is not None:
-            cache = indexer.k_cache.kv_cache
-            if self.prefills:
-                self.storage.ingest_prefill(cache, metadata, self.plans, self.positions)
-            else:
-                self.storage.ingest_decode(cache, metadata, self.inputs, self.row_owners)
-        if self.plans and not self.decodes:
+        step = self._step
+        self._ingest(step, indexer, metadata)
+        if step.kind == "prefill":
             return indexer.select_topk_native(query, weights, metadata, query_scale)
+        tokens = int(weights.shape[0])
+        logical = self._decode(query, weights, query_scale, step, tokens)
+        if step.kind == "decode":
+            return logical
+        return self._mixed(query, weights, query_scale, indexer, metadata, logical, tokens)
+
+    def _ingest(self, step, indexer, metadata):
+        """Index rows of the step's new tokens: the prefill list (restored prefixes first)
+        when the step holds prefill requests, else the decode rows of the packed inputs."""
+        if self.storage is None:
+            return
+        cache = indexer.k_cache.kv_cache
+        if step.prefills:
+            self.storage.ingest_prefill(cache, metadata, step.plans, self.positions)
+        else:
+            self.storage.ingest_decode(cache, metadata, self.inputs, self.row_owners)
+
+    def _decode(self, query, weights, query_scale, step, tokens):
+        """The resident LIFetch forward over the packed decode rows; its token-order outputs
+        (logical positions returned, hot-cache slots kept for `slots`)."""
         self.inputs.pack(query, weights, query_scale)
         if self.tail_source is not None:
             if self.update.tail_bounds is None:
                 raise ValueError("tail_source needs a ResidentIndexUpdate bound with tail_bounds")
             self.update.tail_bounds.copy_(self.tail_source)
         self.forward()
-        tokens = int(weights.shape[0])
-        live = self.inputs.token_count if mixed or tokens > self.inputs.capacity else tokens
-        logical = self.update.logical_output[:live]
-        self.attention_indices = self.update.slot_output[:live]
-        if not mixed:
-            return logical
-        return self._mixed(query, weights, query_scale, indexer, metadata, logical, tokens)
+        # A decode-only batch that fits the packed capacity publishes one row per token; a
+        # mixed or larger batch publishes the packed decode tokens first.
+        packed = step.kind == "mixed" or tokens > self.inputs.capacity
+        live = self.inputs.token_count if packed else tokens
+        self._selection = self.update.slot_output.narrow(0, 0, live)
+        return self.update.logical_output.narrow(0, 0, live)
 
     def _mixed(self, query, weights, query_scale, indexer, metadata, logical, tokens):
         """Token-order result of a mixed step: the decode tokens' published rows and one
@@ -230,9 +282,10 @@ class VllmIndexSelector:
     def slots(self, token_count):
         """Hot-cache slots of the last selection's first `token_count` decode tokens (the
         indices the sparse attention reads)."""
-        if self.attention_indices is None:
+        held = self._selection
+        if held is None:
             raise RuntimeError("slots() needs a selection: call the selector for this step first")
-        if token_count > self.attention_indices.shape[0]:
-            raise ValueError(f"{token_count} tokens requested, the last selection holds "
-                             f"{self.attention_indices.shape[0]}")
-        return self.attention_indices[:token_count]
+        available = int(held.shape[0])
+        if not 0 <= token_count <= available:
+            raise ValueError(f"{token_count} tokens requested, the last selection holds {available}")
+        return held.narrow(0, 0, token_count)
