@@ -677,14 +677,16 @@ uint32_t kvip_hip_resident_finish(const KvipResidentArgs* args, void* stream);
 uint32_t kvip_hip_resident_resolve(const KvipResidentArgs* args, void* stream);
 uint32_t kvip_hip_resident_fetch(const KvipResidentArgs* args, void* stream);
 uint32_t kvip_hip_resident_update(const KvipResidentArgs* args, void* stream);
-/* The first half of kvip_hip_resident_forward with the round's initialisation: owner block
- * table, scoring of the owners' Index rows, then kvip_hip_resident_begin. A prefetching
- * forward follows it with kvip_hip_resident_prefix + kvip_hip_resident_prefetch (possibly
- * on a second stream), the final kvip_hip_topk, then kvip_hip_resident_finish. */
+/* The first half of kvip_hip_resident_forward with the round's initialisation: the
+ * initialisation of kvip_hip_resident_begin together with the owner block table (one
+ * launch), then the scoring of the owners' Index rows. A prefetching forward follows it
+ * with kvip_hip_resident_prefix + kvip_hip_resident_prefetch (possibly on a second stream),
+ * the final kvip_hip_topk, then kvip_hip_resident_finish. */
 uint32_t kvip_hip_resident_score(const KvipIndexerArgs* indexer, const KvipTopkArgs* topk,
                                  const KvipResidentArgs* resident, void* stream);
-/* One resident-cache LIFetch step: block_table[b][j] = row_owners[b] * (history / 128) + j,
- * scoring of the owners' Index rows, TopK-2048, then kvip_hip_resident_round. */
+/* One resident-cache LIFetch step: the round's initialisation with block_table[b][j] =
+ * row_owners[b] * (history / 128) + j, scoring of the owners' Index rows, TopK-2048, then
+ * kvip_hip_resident_finish (the same round as kvip_hip_resident_round). */
 uint32_t kvip_hip_resident_forward(const KvipIndexerArgs* indexer, const KvipTopkArgs* topk,
                                    const KvipResidentArgs* resident, void* stream);
 /* Sparse attention of the selected rows (no reference entry point: the consumer the

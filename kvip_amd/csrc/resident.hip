@@ -105,11 +105,21 @@ __global__ void resident_prepare_kernel(const KvipResidentArgs p) {
 
 // Round initialisation of request b. A hot slot named by two candidates fails the request
 // (KVIP_RESIDENT_ERR_CANDIDATE): both ordinals would otherwise see it free and receive it.
-__global__ __launch_bounds__(kRsThreads) void resident_init_kernel(const KvipResidentArgs p) {
+// With `table` set it also writes request b's row of the scoring block table (entry j =
+// row_owners[b] * blocks_per_owner + j for j < blocks_per_owner, else 0), so that a resident
+// forward initialises its round and its owner table in one launch ahead of the scoring.
+__global__ __launch_bounds__(kRsThreads) void resident_init_kernel(const KvipResidentArgs p, int32_t* table,
+                                                                   int max_blocks, int blocks_per_owner) {
     __shared__ uint32_t s_seen[kMaxWords];
     __shared__ uint32_t s_dup;
     const int b = blockIdx.x;
     const int tid = threadIdx.x;
+    if (table != nullptr) {
+        const int o = p.row_owners[b];
+        for (int j = tid; j < max_blocks; j += kRsThreads) {
+            table[static_cast<size_t>(b) * max_blocks + j] = j < blocks_per_owner ? o * blocks_per_owner + j : 0;
+        }
+    }
     const int words = (p.resident + 31) / 32;
     int32_t* reserved = p.reserved_hot + static_cast<size_t>(b) * p.resident;
     for (int s = tid; s < p.resident; s += kRsThreads) reserved[s] = -1;
@@ -789,16 +799,6 @@ __global__ __launch_bounds__(kRsThreads) void resident_update_kernel(const KvipR
     if (tid == 0 && s_err != 0u) atomicOr(&p.status[b], static_cast<int32_t>(s_err));
 }
 
-__global__ void owner_table_kernel(int32_t* table, const int32_t* owners, int batch, int max_blocks,
-                                   int blocks_per_owner) {
-    const int b = blockIdx.y;
-    const int j = blockIdx.x * blockDim.x + threadIdx.x;
-    if (b < batch && j < max_blocks) {
-        const int o = owners[b];
-        table[static_cast<size_t>(b) * max_blocks + j] = j < blocks_per_owner ? o * blocks_per_owner + j : 0;
-    }
-}
-
 bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 
 }  // namespace
@@ -837,8 +837,10 @@ void launch_resident_fetch(const KvipResidentArgs& a, hipStream_t s) {
     }
 }
 
-hipError_t launch_resident_begin(const KvipResidentArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL(resident_init_kernel, dim3(a.batch), dim3(kRsThreads), 0, s, a);
+hipError_t launch_resident_begin(const KvipResidentArgs& a, hipStream_t s, int32_t* table = nullptr,
+                                 int max_blocks = 0) {
+    hipLaunchKernelGGL(resident_init_kernel, dim3(a.batch), dim3(kRsThreads), 0, s, a, table, max_blocks,
+                       a.history / kBlockTokens);
     return hipGetLastError();
 }
 
@@ -934,18 +936,16 @@ extern "C" uint32_t kvip_hip_resident_prefetch(const KvipResidentArgs* args, con
 }
 
 namespace kvip {
-// Owner block table, then the scoring of the owners' Index rows (the first half of
-// kvip_hip_resident_forward); KVIP_ERR_INVALID when the three argument blocks do not chain.
+// Round initialisation with the owner block table (one launch), then the scoring of the
+// owners' Index rows (the first half of kvip_hip_resident_forward); KVIP_ERR_INVALID when
+// the three argument blocks do not chain.
 static uint32_t resident_score(const KvipIndexerArgs* indexer, const KvipTopkArgs* topk,
                                const KvipResidentArgs* resident, hipStream_t s);
 }  // namespace kvip
 
 extern "C" uint32_t kvip_hip_resident_score(const KvipIndexerArgs* indexer, const KvipTopkArgs* topk,
                                             const KvipResidentArgs* resident, void* stream) {
-    const hipStream_t s = static_cast<hipStream_t>(stream);
-    const uint32_t rc = kvip::resident_score(indexer, topk, resident, s);
-    if (rc != KVIP_OK) return rc;
-    return static_cast<uint32_t>(kvip::launch_resident_begin(*resident, s));
+    return kvip::resident_score(indexer, topk, resident, static_cast<hipStream_t>(stream));
 }
 
 extern "C" uint32_t kvip_hip_resident_forward(const KvipIndexerArgs* indexer, const KvipTopkArgs* topk,
@@ -955,7 +955,7 @@ extern "C" uint32_t kvip_hip_resident_forward(const KvipIndexerArgs* indexer, co
     if (rc != KVIP_OK) return rc;
     const hipError_t e = kvip::launch_topk(*topk, s);
     if (e != hipSuccess) return static_cast<uint32_t>(e);
-    return static_cast<uint32_t>(kvip::launch_resident_round(*resident, s));
+    return static_cast<uint32_t>(kvip::launch_resident_finish(*resident, s));
 }
 
 uint32_t kvip::resident_score(const KvipIndexerArgs* indexer, const KvipTopkArgs* topk,
@@ -977,9 +977,8 @@ uint32_t kvip::resident_score(const KvipIndexerArgs* indexer, const KvipTopkArgs
                          li.scale_block_stride == kvip::kBlockTokens && li.max_blocks >= blocks_per_owner &&
                          li.num_blocks == ra.owners * blocks_per_owner && li.qk_dtype == KVIP_DTYPE_FP8_E4M3;
     if (!chained) return KVIP_ERR_INVALID;
-    hipLaunchKernelGGL(kvip::owner_table_kernel, dim3((li.max_blocks + 255) / 256, li.batch), dim3(256), 0, s,
-                       const_cast<int32_t*>(li.block_table), ra.row_owners, li.batch, li.max_blocks, blocks_per_owner);
-    hipError_t e = hipGetLastError();
+    // The round's initialisation (it reads only the candidates) writes the owner table too.
+    hipError_t e = kvip::launch_resident_begin(ra, s, const_cast<int32_t*>(li.block_table), li.max_blocks);
     if (e != hipSuccess) return static_cast<uint32_t>(e);
     return static_cast<uint32_t>(kvip::launch_indexer(li, s));
 }

@@ -344,8 +344,10 @@ __global__ __launch_bounds__(kSplitThreads) void topk_emit_kernel(const KvipTopk
         return;
     }
     const uint32_t gt_hi = recs[258];
-    // Row histogram of the low byte within hb, and this segment's share of earlier counts.
+    // Row histogram of the low byte within hb, and this segment's share of earlier counts
+    // (8 records requested per round trip).
     uint32_t all = 0, before = 0;
+#pragma unroll 8
     for (int s = 0; s < nseg; ++s) {
         const uint32_t c = recs[s * kSegWords + tid];
         all += c;
