@@ -4,7 +4,7 @@
 // Work split: the (request, 32-token tile) pairs of the batch are flattened and every
 // wave of a grid that fills the GPU once takes one balanced, contiguous range of them.
 // Each wave owns a 4-slot LDS ring (4 KiB of K rows + 128 bytes of key scales per slot):
-// direct-to-LDS loads (global_load_lds_dwordx4) bring tile i+3 while tile i is scored.
+// direct-to-LDS loads (global_load_lds_dwordx4) bring tiles i+1..i+3 while tile i is scored.
 // The loads apply the fragment swizzle on the global side (LDS row r, 16-byte slot s
 // holds piece s ^ (r & 7) of token r's row), so the MFMA B fragments are read straight
 // from the ring, bank-conflict free, with no transposition and no barrier (the ring is
@@ -46,7 +46,15 @@ constexpr int kVmcntZero = 0x0F70;
 // Cache policy of the K-tile loads: nt (each index-K byte is read once per step; streamed
 // past the caches, reads run at ~7.0 TB/s on MI355X against ~6.3 TB/s with the default policy).
 constexpr int kNonTemporal = 2;
-constexpr int kVmcnt15 = 0x0F7F;  // vmcnt(15)
+// Tiles in flight per wave while one is scored (at most kRgSlots - 1). One: with ~2000
+// waves the HBM queues stay full, and deeper rings only delay the first tiles of the
+// workgroups dispatched last (their waves then finish last).
+constexpr int kRgDepth = 1;
+// Relative tile shares of the waves of the first dispatch round (the first workgroup on
+// each CU) and of the later rounds: the later workgroups' first tiles queue behind the
+// first round's and land ~2 us later at config-2 sizes, so they get ~18 % fewer tiles.
+constexpr int kRgLeadWeight = 22;
+constexpr int kRgLagWeight = 18;
 
 // Stands in for a missing key-scale array (stride 0): 128 unit scales.
 __device__ __align__(16) float kRingUnitScale[kBlockTokens] = {
@@ -85,7 +93,7 @@ KVIP_DEVICE int rg_valid(const KvipIndexerArgs& p, int b) {
 }
 
 template <int HEADS, bool W_BF16>
-__global__ __launch_bounds__(kRgThreads, 2) void indexer_ring_kernel(const KvipIndexerArgs p) {
+__global__ __launch_bounds__(kRgThreads, 2) void indexer_ring_kernel(const KvipIndexerArgs p, int lead_blocks) {
     constexpr int MT = HEADS / 32;
     __shared__ __align__(16) uint8_t s_ring[kRgWaves][kRgSlots][kRgSlotBytes];
     __shared__ __align__(16) uint32_t s_hist[kRgWaves][256];
@@ -112,12 +120,18 @@ __global__ __launch_bounds__(kRgThreads, 2) void indexer_ring_kernel(const KvipI
     for (int i = tid; i < kRgWaves * 256; i += kRgThreads) (&s_hist[0][0])[i] = 0u;
     __syncthreads();
 
-    // This wave's balanced share [t, t_end) of the flattened tile list.
+    // This wave's share [t, t_end) of the flattened tile list: the waves of the first
+    // lead_blocks workgroups weigh kRgLeadWeight, the others kRgLagWeight.
     const int total_tiles = s_prefix[p.batch];
+    const int64_t lead = static_cast<int64_t>(min(lead_blocks, static_cast<int>(gridDim.x))) * kRgWaves;
+    auto weight_before = [&](int64_t v) {
+        return kRgLeadWeight * min(v, lead) + kRgLagWeight * max(v - lead, static_cast<int64_t>(0));
+    };
     const int64_t nw = static_cast<int64_t>(gridDim.x) * kRgWaves;
     const int64_t w = static_cast<int64_t>(blockIdx.x) * kRgWaves + wave;
-    int t = static_cast<int>(total_tiles * w / nw);
-    const int t_end = static_cast<int>(total_tiles * (w + 1) / nw);
+    const int64_t weight_total = weight_before(nw);
+    int t = static_cast<int>(total_tiles * weight_before(w) / weight_total);
+    const int t_end = static_cast<int>(total_tiles * weight_before(w + 1) / weight_total);
     if (t >= t_end) return;  // no barrier follows: waves run independently from here
 
     uint8_t* ring = &s_ring[wave][0][0];
@@ -272,14 +286,13 @@ __global__ __launch_bounds__(kRgThreads, 2) void indexer_ring_kernel(const KvipI
             load_q(b_first);
             qb = b_first;
         }
-        issue(0);
-        issue(1);
-        issue(2);
-        __builtin_amdgcn_s_waitcnt(kVmcnt15);
-        // Pipeline: loads of tiles i+1..i+3 stay in flight while tile i is scored. The
-        // vmcnt of each wait counts the vector memory instructions issued after tile i's
-        // loads (3 tile loads of kRgOps instructions plus the key stores in between);
-        // a Q reload or histogram flush in between only makes a wait longer.
+#pragma unroll
+        for (int j = 0; j < kRgDepth; ++j) issue(j);
+        wait_vmcnt<kRgDepth * kRgOps>();
+        // Pipeline: loads of tiles i+1..i+kRgDepth stay in flight while tile i is scored.
+        // The vmcnt of each wait counts the vector memory instructions issued after tile
+        // i's loads (kRgDepth tile loads of kRgOps instructions plus the key stores in
+        // between); a Q reload or histogram flush in between only makes a wait longer.
         int i = 0;
         while (i < cnt) {  // runs of one request
             const int b = __builtin_amdgcn_readlane(d_b, i);
@@ -291,15 +304,15 @@ __global__ __launch_bounds__(kRgThreads, 2) void indexer_ring_kernel(const KvipI
             const uint64_t later = run_ends >> i;
             const int run_end = i + static_cast<int>(__builtin_ctzll(later)) + 1;
             for (; i < run_end; ++i) {
-                issue(i + 3);
-                if (i >= 3) {
-                    wait_vmcnt<3 * kRgOps + 3>();
+                issue(i + kRgDepth);
+                if (i >= kRgDepth) {
+                    wait_vmcnt<kRgDepth * kRgOps + kRgDepth>();
                 } else if (i == 2) {
-                    wait_vmcnt<3 * kRgOps + 2>();
+                    wait_vmcnt<kRgDepth * kRgOps + 2>();
                 } else if (i == 1) {
-                    wait_vmcnt<3 * kRgOps + 1>();
+                    wait_vmcnt<kRgDepth * kRgOps + 1>();
                 } else {
-                    wait_vmcnt<3 * kRgOps>();
+                    wait_vmcnt<kRgDepth * kRgOps>();
                 }
                 score(i);
             }
@@ -311,18 +324,24 @@ __global__ __launch_bounds__(kRgThreads, 2) void indexer_ring_kernel(const KvipI
     report(p.status, err);
 }
 
-// Workgroups per CU the kernel keeps resident times the CU count.
+// Grid = workgroups per CU the kernel keeps resident times the CU count; the first
+// dispatch round is one workgroup per CU.
+struct RingGrid {
+    int blocks;
+    int lead_blocks;
+};
+
 template <typename K>
-int ring_grid(K kernel) {
-    static int grid = 0;
-    if (grid == 0) {
+RingGrid ring_grid(K kernel) {
+    static RingGrid grid{0, 0};
+    if (grid.blocks == 0) {
         int dev = 0, cus = 0, per_cu = 0;
         if (hipGetDevice(&dev) != hipSuccess ||
             hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
             hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kRgThreads, 0) != hipSuccess) {
-            return 0;
+            return grid;
         }
-        grid = max(1, cus * max(per_cu, 1));
+        grid = RingGrid{max(1, cus * max(per_cu, 1)), max(1, cus)};
     }
     return grid;
 }
@@ -330,9 +349,9 @@ int ring_grid(K kernel) {
 template <int HEADS, bool W_BF16>
 hipError_t launch_ring_kernel(const KvipIndexerArgs& a, hipStream_t stream) {
     auto kernel = indexer_ring_kernel<HEADS, W_BF16>;
-    const int grid = ring_grid(kernel);
-    if (grid == 0) return hipErrorInvalidDevice;
-    hipLaunchKernelGGL(kernel, dim3(grid), dim3(kRgThreads), 0, stream, a);
+    const RingGrid grid = ring_grid(kernel);
+    if (grid.blocks == 0) return hipErrorInvalidDevice;
+    hipLaunchKernelGGL(kernel, dim3(grid.blocks), dim3(kRgThreads), 0, stream, a, grid.lead_blocks);
     return hipGetLastError();
 }
 
