@@ -2,9 +2,10 @@
 // decode step): a streaming kernel that feeds MFMA straight from a per-wave LDS ring.
 //
 // Work split: the (request, 32-token tile) pairs of the batch are flattened and every
-// wave of a grid that fills the GPU once takes one balanced, contiguous range of them.
-// Each wave owns a 4-slot LDS ring (4 KiB of K rows + 128 bytes of key scales per slot):
-// direct-to-LDS loads (global_load_lds_dwordx4) bring tiles i+1..i+3 while tile i is scored.
+// wave of a grid that fills the GPU once takes one contiguous range of them (weighted by
+// dispatch round, see kRgLeadWeight). Each wave owns a 4-slot LDS ring (4 KiB of K rows +
+// 128 bytes of key scales per slot): direct-to-LDS loads (global_load_lds_dwordx4) bring
+// the next kRgDepth tiles while tile i is scored.
 // The loads apply the fragment swizzle on the global side (LDS row r, 16-byte slot s
 // holds piece s ^ (r & 7) of token r's row), so the MFMA B fragments are read straight
 // from the ring, bank-conflict free, with no transposition and no barrier (the ring is
