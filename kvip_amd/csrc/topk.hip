@@ -426,14 +426,16 @@ hipError_t launch_topk(const KvipTopkArgs& a, hipStream_t stream) {
         hipLaunchKernelGGL(topk_emit_kernel, split, dim3(kSplitThreads), 0, stream, a);
         return hipGetLastError();
     }
-    // Rows that fit 1024*KPT keys use the register-resident select.
-    if (a.key_stride <= kTopkThreads * 8) {
+    // Rows that fit 1024*KPT keys use the register-resident select; a limit (the resident
+    // prefix of a longer row) bounds the keys a row can have.
+    const int64_t span = a.limit > 0 ? std::min<int64_t>(a.key_stride, (a.limit + 7) / 8 * 8) : a.key_stride;
+    if (span <= kTopkThreads * 8) {
         hipLaunchKernelGGL(topk_regs_kernel<8>, grid, block, 0, stream, a);
-    } else if (a.key_stride <= kTopkThreads * 16) {
+    } else if (span <= kTopkThreads * 16) {
         hipLaunchKernelGGL(topk_regs_kernel<16>, grid, block, 0, stream, a);
-    } else if (a.key_stride <= kTopkThreads * 32) {
+    } else if (span <= kTopkThreads * 32) {
         hipLaunchKernelGGL(topk_regs_kernel<32>, grid, block, 0, stream, a);
-    } else if (a.key_stride <= kTopkThreads * 64) {
+    } else if (span <= kTopkThreads * 64) {
         hipLaunchKernelGGL(topk_regs_kernel<64>, grid, block, 0, stream, a);
     } else {
         hipLaunchKernelGGL(topk_kernel, grid, block, 0, stream, a);

@@ -518,23 +518,25 @@ def test_resident_forward_graph_replay(torch_gpu, prefetch):
         assert not upd.status.any()
 
 
-def test_resident_prefix_matches_oracle(torch_gpu):
+@pytest.mark.parametrize("ctx,ends,resident", [
+    ([20000, 9000], [20000, 19990, 9000, 1500], 4096),
+    # Rows longer than the register select's 65536 keys, prefix of 16384 (config 4's shape).
+    ([70000, 40000], [70000, 69000, 40000, 16000], 16384),
+])
+def test_resident_prefix_matches_oracle(torch_gpu, ctx, ends, resident):
     """Resident TopK, threshold and hit bits on the device keys of a scored step equal the
     oracle's on the same keys (bit-exact), including short and query-bounded rows."""
     torch = torch_gpu
     from kvip_amd import synthetic
 
-    ctx = [20000, 9000, 3000, 1500]
-    wl = synthetic.decode_workload(torch, batch=2, ctx=ctx[:2], device="cuda", seed=21, rows_per_request=2)
-    ends = [20000, 19990, 9000, 1500]
+    wl = synthetic.decode_workload(torch, batch=2, ctx=ctx, device="cuda", seed=21, rows_per_request=2)
     rot, upd, fwd = synthetic.bind(torch, kvip_amd, wl, query_ends=ends)
     fwd.score()
-    resident = 4096
     rng = np.random.default_rng(21)
     lru = np.stack([rng.permutation(resident)[:2048] for _ in range(2)]).astype(np.int32)
     lru[0, :2] = [resident + 3, -1]
     pre = kvip_amd.ResidentPrefix(torch, rot, torch.from_numpy(lru).cuda(), resident)
-    say("case resident prefix")
+    say(f"case resident prefix ctx {ctx} resident {resident}")
     pre()
     torch.cuda.synchronize()
     keys = rot.score_keys.cpu().numpy().view(np.uint16)
