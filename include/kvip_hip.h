@@ -86,7 +86,7 @@
 extern "C" {
 #endif
 
-#define KVIP_HIP_ABI_VERSION 12u
+#define KVIP_HIP_ABI_VERSION 13u
 
 #define KVIP_TOPK 2048
 #define KVIP_BLOCK_TOKENS 128
@@ -516,11 +516,14 @@ typedef struct KvipResidentArgs {
  * This is the reference's service when every window is serviced after scoring has passed
  * the window's end (it caps each progress snapshot at the window boundary,
  * op_kernel/prefetch.h:609-627); the final round repairs whatever was not prefetched. */
+#define KVIP_PREFETCH_MAX_WINDOWS 32
 typedef struct KvipPrefetchArgs {
     const uint32_t* victim_hits;  /* [batch * rows_per_request, 64], kvip_hip_resident_prefix */
     const uint32_t* cold_hits;    /* [batch * rows_per_request, cold_words] */
+    int32_t* window_counts;       /* [batch, KVIP_PREFETCH_MAX_WINDOWS] prefetch count after each window
+                                     (windowed entry points), or NULL */
     int32_t cold_words;           /* >= (history - resident) / 32 */
-    int32_t windows;              /* 1..32, fewer than cold_tiles */
+    int32_t windows;              /* 1..KVIP_PREFETCH_MAX_WINDOWS, fewer than cold_tiles */
     int32_t window_limit;         /* 1..480 */
     int32_t prefetch_limit;       /* 0..2048 */
 } KvipPrefetchArgs;
@@ -607,6 +610,13 @@ typedef struct KvipPrefixClassifyArgs {
 
 uint32_t kvip_hip_abi_version(void);
 uint32_t kvip_hip_indexer_decode(const KvipIndexerArgs* args, void* stream);
+/* kvip_hip_indexer_decode of the token positions [token_begin, token_end) only (token_begin
+ * a multiple of 128; token_end a multiple of 128 or at least key_stride; the histogram
+ * accumulates, so windows covering the row give the whole row's keys and histogram). fp8
+ * Q/K with one row per request (others: KVIP_ERR_INVALID). No reference counterpart: it
+ * lets a caller start on the first positions' scores while later ones are scored. */
+uint32_t kvip_hip_indexer_decode_window(const KvipIndexerArgs* args, int32_t token_begin, int32_t token_end,
+                                        void* stream);
 uint32_t kvip_hip_topk(const KvipTopkArgs* args, void* stream);
 uint32_t kvip_hip_fetch_gather(const KvipFetchArgs* args, void* stream);
 uint32_t kvip_hip_indexer_prefill(const KvipPrefillArgs* args, void* stream);
@@ -658,6 +668,12 @@ uint32_t kvip_hip_ingest_index(const KvipIngestArgs* args, void* stream);
 /* Resident TopK (kvip_hip_topk of `topk`, whose limit must equal cls->resident and whose
  * output must be cls->prefix_topk) followed by the prefix classification. */
 uint32_t kvip_hip_resident_prefix(const KvipTopkArgs* topk, const KvipPrefixClassifyArgs* cls, void* stream);
+/* kvip_hip_resident_prefix in parts, for a prefetch that follows the scoring window by
+ * window: the resident TopK and classification (thresholds, victim bits), then the cold
+ * hit bits of the cold words [word_begin, word_end) once those positions are scored. */
+uint32_t kvip_hip_resident_threshold(const KvipTopkArgs* topk, const KvipPrefixClassifyArgs* cls, void* stream);
+uint32_t kvip_hip_resident_cold_hits(const KvipPrefixClassifyArgs* cls, int32_t word_begin, int32_t word_end,
+                                     void* stream);
 uint64_t kvip_hip_resident_workspace_bytes(int32_t batch, int32_t history);
 uint32_t kvip_hip_resident_prepare(const KvipResidentArgs* args, void* stream);
 uint32_t kvip_hip_resident_round(const KvipResidentArgs* args, void* stream);
@@ -667,6 +683,20 @@ uint32_t kvip_hip_resident_round(const KvipResidentArgs* args, void* stream);
  * prefix classification; finish must follow both. */
 uint32_t kvip_hip_resident_begin(const KvipResidentArgs* args, void* stream);
 uint32_t kvip_hip_resident_prefetch(const KvipResidentArgs* args, const KvipPrefetchArgs* prefetch, void* stream);
+/* kvip_hip_resident_prefetch window by window (no reference entry point: the reference's
+ * service walks the windows as scoring passes them, op_kernel/prefetch.h:578-832):
+ * _windows takes the candidates of windows [window_begin, window_end) (window 0 first,
+ * each range continuing from the count the earlier ranges left in prefetch_counts) and
+ * records the count after each window in prefetch->window_counts; _copy copies the host
+ * rows of the ordinals those windows took. Calling _windows over consecutive ranges
+ * covering [0, windows) and _copy for each range equals kvip_hip_resident_prefetch. A
+ * range's copy may run beside later ranges' decisions (it reads only their earlier window
+ * counts); resolve and Index update need only the decisions, kvip_hip_resident_fetch must
+ * follow every copy (a final miss may take a slot a copy writes). */
+uint32_t kvip_hip_resident_prefetch_windows(const KvipResidentArgs* args, const KvipPrefetchArgs* prefetch,
+                                            int32_t window_begin, int32_t window_end, void* stream);
+uint32_t kvip_hip_resident_prefetch_copy(const KvipResidentArgs* args, const KvipPrefetchArgs* prefetch,
+                                         int32_t window_begin, int32_t window_end, void* stream);
 uint32_t kvip_hip_resident_finish(const KvipResidentArgs* args, void* stream);
 /* kvip_hip_resident_finish = resolve, then Fetch, then update. The Fetch copies the resolve's
  * misses (it reads fetch_sources/fetch_slots/miss_counts and writes hot_cache only) and the
@@ -684,6 +714,14 @@ uint32_t kvip_hip_resident_update(const KvipResidentArgs* args, void* stream);
  * the final kvip_hip_topk, then kvip_hip_resident_finish. */
 uint32_t kvip_hip_resident_score(const KvipIndexerArgs* indexer, const KvipTopkArgs* topk,
                                  const KvipResidentArgs* resident, void* stream);
+/* kvip_hip_resident_score over the token positions [token_begin, token_end) of every row
+ * (token_begin a multiple of 128; token_end a multiple of 128 or at least key_stride); the
+ * round's initialisation runs with the window that starts at 0. Windows covering
+ * [0, key_stride) give the keys and histograms of kvip_hip_resident_score. fp8 indexers with
+ * one row per request (others: KVIP_ERR_INVALID). */
+uint32_t kvip_hip_resident_score_window(const KvipIndexerArgs* indexer, const KvipTopkArgs* topk,
+                                        const KvipResidentArgs* resident, int32_t token_begin, int32_t token_end,
+                                        void* stream);
 /* One resident-cache LIFetch step: the round's initialisation with block_table[b][j] =
  * row_owners[b] * (history / 128) + j, scoring of the owners' Index rows, TopK-2048, then
  * kvip_hip_resident_finish (the same round as kvip_hip_resident_round). */

@@ -30,7 +30,8 @@ namespace kvip {
 
 // fp8 decode with one row per request: the LDS-ring kernel (indexer_ring.hip).
 bool ring_eligible(const KvipIndexerArgs& a);
-hipError_t launch_indexer_ring(const KvipIndexerArgs& a, hipStream_t stream);
+hipError_t launch_indexer_ring(const KvipIndexerArgs& a, hipStream_t stream, int tile_lo = 0,
+                               int tile_hi = 1 << 30);
 
 namespace {
 
@@ -511,4 +512,17 @@ extern "C" uint32_t kvip_hip_indexer_decode(const KvipIndexerArgs* args, void* s
     const uint32_t rc = kvip::validate_indexer(args);
     if (rc != KVIP_OK) return rc;
     return static_cast<uint32_t>(kvip::launch_indexer(*args, static_cast<hipStream_t>(stream)));
+}
+
+extern "C" uint32_t kvip_hip_indexer_decode_window(const KvipIndexerArgs* args, int32_t token_begin,
+                                                   int32_t token_end, void* stream) {
+    const uint32_t rc = kvip::validate_indexer(args);
+    if (rc != KVIP_OK) return rc;
+    if (!kvip::ring_eligible(*args) || token_begin < 0 || token_end <= token_begin || token_begin % 128 != 0 ||
+        (token_end % 128 != 0 && token_end < args->key_stride)) {
+        return KVIP_ERR_INVALID;
+    }
+    const int end = static_cast<int>(std::min<int64_t>(token_end, args->key_stride));
+    return static_cast<uint32_t>(
+        kvip::launch_indexer_ring(*args, static_cast<hipStream_t>(stream), token_begin / 32, (end + 31) / 32));
 }

@@ -94,7 +94,8 @@ KVIP_DEVICE int rg_valid(const KvipIndexerArgs& p, int b) {
 }
 
 template <int HEADS, bool W_BF16>
-__global__ __launch_bounds__(kRgThreads, 2) void indexer_ring_kernel(const KvipIndexerArgs p, int lead_blocks) {
+__global__ __launch_bounds__(kRgThreads, 2) void indexer_ring_kernel(const KvipIndexerArgs p, int lead_blocks,
+                                                                     int tile_lo, int tile_hi) {
     constexpr int MT = HEADS / 32;
     __shared__ __align__(16) uint8_t s_ring[kRgWaves][kRgSlots][kRgSlotBytes];
     __shared__ __align__(16) uint32_t s_hist[kRgWaves][256];
@@ -107,11 +108,12 @@ __global__ __launch_bounds__(kRgThreads, 2) void indexer_ring_kernel(const KvipI
     const int n = lane & 31;
     const int g = lane >> 5;
 
-    // Tile counts per request -> prefix sums (whole workgroup, before any ring load).
+    // Tile counts per request inside the window [tile_lo, tile_hi) of 32-token tiles ->
+    // prefix sums (whole workgroup, before any ring load).
     int running = 0;
     for (int base = 0; base < p.batch; base += kRgThreads) {
         const int b = base + tid;
-        const int c = b < p.batch ? (rg_valid(p, b) + 31) / 32 : 0;
+        const int c = b < p.batch ? max(0, min((rg_valid(p, b) + 31) / 32, tile_hi) - tile_lo) : 0;
         uint32_t total;
         const uint32_t excl = block_exclusive_scan(static_cast<uint32_t>(c), s_scan, &total);
         if (b < p.batch) s_prefix[b] = running + static_cast<int>(excl);
@@ -198,7 +200,7 @@ __global__ __launch_bounds__(kRgThreads, 2) void indexer_ring_kernel(const KvipI
                 if (s_prefix[mid] <= tt) lo = mid; else hi = mid - 1;
             }
             d_b = lo;
-            d_k = tt - s_prefix[lo];
+            d_k = tt - s_prefix[lo] + tile_lo;
             const int id = p.block_table[static_cast<size_t>(d_b) * p.max_blocks + (d_k >> 2)];
             const bool ok = static_cast<unsigned>(id) < static_cast<unsigned>(p.num_blocks);
             d_page = ok ? id : 0;
@@ -348,11 +350,11 @@ RingGrid ring_grid(K kernel) {
 }
 
 template <int HEADS, bool W_BF16>
-hipError_t launch_ring_kernel(const KvipIndexerArgs& a, hipStream_t stream) {
+hipError_t launch_ring_kernel(const KvipIndexerArgs& a, int tile_lo, int tile_hi, hipStream_t stream) {
     auto kernel = indexer_ring_kernel<HEADS, W_BF16>;
     const RingGrid grid = ring_grid(kernel);
     if (grid.blocks == 0) return hipErrorInvalidDevice;
-    hipLaunchKernelGGL(kernel, dim3(grid.blocks), dim3(kRgThreads), 0, stream, a, grid.lead_blocks);
+    hipLaunchKernelGGL(kernel, dim3(grid.blocks), dim3(kRgThreads), 0, stream, a, grid.lead_blocks, tile_lo, tile_hi);
     return hipGetLastError();
 }
 
@@ -370,13 +372,14 @@ bool ring_eligible(const KvipIndexerArgs& a) {
             ((reinterpret_cast<uintptr_t>(a.key_scale) & 15u) == 0 && a.scale_block_stride % 4 == 0));
 }
 
-hipError_t launch_indexer_ring(const KvipIndexerArgs& a, hipStream_t stream) {
+// Scores the 32-token tiles [tile_lo, tile_hi) of every row's visible positions.
+hipError_t launch_indexer_ring(const KvipIndexerArgs& a, hipStream_t stream, int tile_lo, int tile_hi) {
     if (a.heads == 64) {
-        return a.weight_dtype == KVIP_DTYPE_BF16 ? launch_ring_kernel<64, true>(a, stream)
-                                                 : launch_ring_kernel<64, false>(a, stream);
+        return a.weight_dtype == KVIP_DTYPE_BF16 ? launch_ring_kernel<64, true>(a, tile_lo, tile_hi, stream)
+                                                 : launch_ring_kernel<64, false>(a, tile_lo, tile_hi, stream);
     }
-    return a.weight_dtype == KVIP_DTYPE_BF16 ? launch_ring_kernel<32, true>(a, stream)
-                                             : launch_ring_kernel<32, false>(a, stream);
+    return a.weight_dtype == KVIP_DTYPE_BF16 ? launch_ring_kernel<32, true>(a, tile_lo, tile_hi, stream)
+                                             : launch_ring_kernel<32, false>(a, tile_lo, tile_hi, stream);
 }
 
 }  // namespace kvip

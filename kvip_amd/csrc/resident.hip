@@ -28,6 +28,8 @@ namespace kvip {
 uint32_t validate_indexer(const KvipIndexerArgs* a);
 uint32_t validate_topk(const KvipTopkArgs* a);
 hipError_t launch_indexer(const KvipIndexerArgs& a, hipStream_t stream);
+bool ring_eligible(const KvipIndexerArgs& a);
+hipError_t launch_indexer_ring(const KvipIndexerArgs& a, hipStream_t stream, int tile_lo, int tile_hi);
 hipError_t launch_topk(const KvipTopkArgs& a, hipStream_t stream);
 
 namespace {
@@ -424,7 +426,8 @@ __global__ __launch_bounds__(kRsThreads) void resident_resolve_kernel(const Kvip
 // Records go to prefetch_tokens / the ordinal change records / the workspace map; the
 // rows are copied by resident_fetch_kernel<., true>.
 __global__ __launch_bounds__(kRsThreads) void resident_prefetch_kernel(const KvipResidentArgs p,
-                                                                       const KvipPrefetchArgs f) {
+                                                                       const KvipPrefetchArgs f, int e_begin,
+                                                                       int e_end) {
     __shared__ uint32_t s_wave[kRsThreads / 64];
     __shared__ uint32_t s_err;
     const int b = blockIdx.x;
@@ -438,6 +441,7 @@ __global__ __launch_bounds__(kRsThreads) void resident_prefetch_kernel(const Kvi
         return;
     }
     const Tail tail = tail_of(p, b);
+    const int o = p.row_owners[b];
     const int32_t* lru = p.lru_slots + static_cast<size_t>(b) * kLru;
     int32_t* map = workspace_of(p).map + static_cast<size_t>(b) * H;
     int32_t* tokens = p.prefetch_tokens + static_cast<size_t>(b) * kLru;
@@ -446,21 +450,36 @@ __global__ __launch_bounds__(kRsThreads) void resident_prefetch_kernel(const Kvi
     if (tid == 0) s_err = 0u;
     __syncthreads();
     auto mapped_tail = [&](int t) { return t >= tail.begin && t < tail.mapped; };
-    // Takes ordinal k for token t.
+    // Takes ordinal k for token t. The row's host source is checked here, so that a bad
+    // source is in the status word before the round's resolve whenever the copy runs.
     auto take = [&](int k, int t) {
         const int s = lru[k];
         if (s < 0 || s >= R) atomicOr(&s_err, KVIP_RESIDENT_ERR_CANDIDATE);
+        const int64_t off = p.addresses[static_cast<size_t>(o) * H + t];
+        if (off < 0 || off > p.host_pool_bytes - p.row_bytes || (off & 15) != 0) {
+            atomicOr(&s_err, KVIP_RESIDENT_ERR_SOURCE);
+        }
         tokens[k] = t;
         map[t] = k;
         changes[k] = t;
     };
-    int used = 0;  // uniform
+    // Windows [e_begin, e_end) continue from the count the earlier windows left.
+    int used = e_begin == 0 ? 0 : p.prefetch_counts[b];  // uniform
     const int cold_tiles = (H - R) / kBlockTokens;
-    int lo = R;
-    for (int e = 0; e < f.windows; ++e) {
+    auto window_end = [&](int e) {
+        return R + kBlockTokens * static_cast<int>(static_cast<int64_t>(cold_tiles) * e / max(1, f.windows - 1));
+    };
+    int lo = e_begin <= 1 ? R : window_end(e_begin - 1);
+    int32_t* counts = f.window_counts != nullptr ? f.window_counts + static_cast<size_t>(b) * KVIP_PREFETCH_MAX_WINDOWS
+                                                 : nullptr;
+    for (int e = e_begin; e < e_end; ++e) {
         const int available = min(f.window_limit, min(kLru - used, f.prefetch_limit - used));
-        const int hi = R + kBlockTokens * static_cast<int>(static_cast<int64_t>(cold_tiles) * e / max(1, f.windows - 1));
-        if (available <= 0) break;
+        const int hi = window_end(e);
+        if (available <= 0) {
+            if (counts != nullptr && tid == 0) counts[e] = used;
+            if (e > 0) lo = hi;
+            continue;
+        }
         int taken = 0;
         if (e == 0) {
             // Victim coordinates i = 2 tid + k, in ordinal order; candidate token lru[i].
@@ -514,6 +533,7 @@ __global__ __launch_bounds__(kRsThreads) void resident_prefetch_kernel(const Kvi
             lo = hi;
         }
         used += taken;
+        if (counts != nullptr && tid == 0) counts[e] = used;
         __syncthreads();
     }
     if (tid == 0) {
@@ -533,7 +553,8 @@ __global__ __launch_bounds__(kRsThreads) void resident_prefetch_kernel(const Kvi
 constexpr int kFetchRows = 32;
 constexpr int kFetchWaves = 64;
 template <int PIECES, bool PREFETCH>
-__global__ __launch_bounds__(256) void resident_fetch_kernel(const KvipResidentArgs p) {
+__global__ __launch_bounds__(256) void resident_fetch_kernel(const KvipResidentArgs p, const int32_t* window_counts,
+                                                             int e_begin, int e_end) {
     const int b = blockIdx.y;
     const int lane = threadIdx.x & 63;
     // The prefetch copy runs before the resolve and skips a failed round. The miss copy
@@ -541,11 +562,20 @@ __global__ __launch_bounds__(256) void resident_fetch_kernel(const KvipResidentA
     // was checked by the resolve), never the status words that a concurrent Index update
     // may set: the copy and the update can run side by side.
     if (PREFETCH && p.status[b] != 0) return;
-    const int total = PREFETCH ? p.prefetch_counts[b] : p.miss_counts[b * 5 + 4];
+    // Rows [first, total): the prefetch rows of windows [e_begin, e_end) with window counts,
+    // else every prefetched row or every miss.
+    int first = 0, total;
+    if (PREFETCH && window_counts != nullptr) {
+        const int32_t* counts = window_counts + static_cast<size_t>(b) * KVIP_PREFETCH_MAX_WINDOWS;
+        first = e_begin > 0 ? counts[e_begin - 1] : 0;
+        total = counts[e_end - 1];
+    } else {
+        total = PREFETCH ? p.prefetch_counts[b] : p.miss_counts[b * 5 + 4];
+    }
     const int o = p.row_owners[b];
     const int pieces = PIECES > 0 ? PIECES : p.row_bytes / 16;
     uint32_t err = 0;
-    for (int r0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * kFetchRows; r0 < total;
+    for (int r0 = first + (blockIdx.x * 4 + (threadIdx.x >> 6)) * kFetchRows; r0 < total;
          r0 += gridDim.x * 4 * kFetchRows) {
         const int rows = min(kFetchRows, total - r0);
         int64_t src = -1, dst = -1;
@@ -825,15 +855,18 @@ uint32_t validate_resident(const KvipResidentArgs* a) {
 }
 
 template <bool PREFETCH>
-void launch_resident_fetch(const KvipResidentArgs& a, hipStream_t s) {
+void launch_resident_fetch(const KvipResidentArgs& a, hipStream_t s, const int32_t* window_counts = nullptr,
+                           int e_begin = 0, int e_end = 0) {
     // Up to kFetchWaves waves in all (at least one workgroup per request).
     const int rows = PREFETCH ? kLru : a.rows_per_request * kTopK;
     const int per_request = max(1, kFetchWaves / (4 * a.batch));
     const dim3 fgrid(min((rows + 4 * kFetchRows - 1) / (4 * kFetchRows), per_request), a.batch);
     if (a.row_bytes == KVIP_KV_ROW_BYTES) {
-        hipLaunchKernelGGL((resident_fetch_kernel<KVIP_KV_ROW_BYTES / 16, PREFETCH>), fgrid, dim3(256), 0, s, a);
+        hipLaunchKernelGGL((resident_fetch_kernel<KVIP_KV_ROW_BYTES / 16, PREFETCH>), fgrid, dim3(256), 0, s, a,
+                           window_counts, e_begin, e_end);
     } else {
-        hipLaunchKernelGGL((resident_fetch_kernel<0, PREFETCH>), fgrid, dim3(256), 0, s, a);
+        hipLaunchKernelGGL((resident_fetch_kernel<0, PREFETCH>), fgrid, dim3(256), 0, s, a, window_counts, e_begin,
+                           e_end);
     }
 }
 
@@ -930,8 +963,40 @@ extern "C" uint32_t kvip_hip_resident_prefetch(const KvipResidentArgs* args, con
                     static_cast<int64_t>(f->cold_words) * 32 >= static_cast<int64_t>(args->history) - args->resident;
     if (!ok) return KVIP_ERR_INVALID;
     const hipStream_t s = static_cast<hipStream_t>(stream);
-    hipLaunchKernelGGL(kvip::resident_prefetch_kernel, dim3(args->batch), dim3(kvip::kRsThreads), 0, s, *args, *f);
+    hipLaunchKernelGGL(kvip::resident_prefetch_kernel, dim3(args->batch), dim3(kvip::kRsThreads), 0, s, *args, *f, 0,
+                       f->windows);
     kvip::launch_resident_fetch<true>(*args, s);
+    return static_cast<uint32_t>(hipGetLastError());
+}
+
+namespace kvip {
+// Arguments of the windowed prefetch entry points: a valid prefetch, window counts, and a
+// window range inside [0, windows).
+static bool prefetch_windows_ok(const KvipResidentArgs* args, const KvipPrefetchArgs* f, int e_begin, int e_end) {
+    if (validate_resident(args) != KVIP_OK || f == nullptr || args->prefetch_tokens == nullptr) return false;
+    const int cold_tiles = (args->history - args->resident) / kBlockTokens;
+    return f->victim_hits != nullptr && f->cold_hits != nullptr && f->window_counts != nullptr &&
+           args->resident % kBlockTokens == 0 && f->windows >= 1 && f->windows <= KVIP_PREFETCH_MAX_WINDOWS &&
+           cold_tiles > f->windows && f->window_limit >= 1 && f->window_limit <= 480 && f->prefetch_limit >= 0 &&
+           f->prefetch_limit <= kLru &&
+           static_cast<int64_t>(f->cold_words) * 32 >= static_cast<int64_t>(args->history) - args->resident &&
+           e_begin >= 0 && e_end > e_begin && e_end <= f->windows;
+}
+}  // namespace kvip
+
+extern "C" uint32_t kvip_hip_resident_prefetch_windows(const KvipResidentArgs* args, const KvipPrefetchArgs* f,
+                                                       int32_t window_begin, int32_t window_end, void* stream) {
+    if (!kvip::prefetch_windows_ok(args, f, window_begin, window_end)) return KVIP_ERR_INVALID;
+    hipLaunchKernelGGL(kvip::resident_prefetch_kernel, dim3(args->batch), dim3(kvip::kRsThreads), 0,
+                       static_cast<hipStream_t>(stream), *args, *f, window_begin, window_end);
+    return static_cast<uint32_t>(hipGetLastError());
+}
+
+extern "C" uint32_t kvip_hip_resident_prefetch_copy(const KvipResidentArgs* args, const KvipPrefetchArgs* f,
+                                                    int32_t window_begin, int32_t window_end, void* stream) {
+    if (!kvip::prefetch_windows_ok(args, f, window_begin, window_end)) return KVIP_ERR_INVALID;
+    kvip::launch_resident_fetch<true>(*args, static_cast<hipStream_t>(stream), f->window_counts, window_begin,
+                                      window_end);
     return static_cast<uint32_t>(hipGetLastError());
 }
 
@@ -940,12 +1005,23 @@ namespace kvip {
 // owners' Index rows (the first half of kvip_hip_resident_forward); KVIP_ERR_INVALID when
 // the three argument blocks do not chain.
 static uint32_t resident_score(const KvipIndexerArgs* indexer, const KvipTopkArgs* topk,
-                               const KvipResidentArgs* resident, hipStream_t s);
+                               const KvipResidentArgs* resident, hipStream_t s, int token_begin = 0,
+                               int token_end = -1);
 }  // namespace kvip
 
 extern "C" uint32_t kvip_hip_resident_score(const KvipIndexerArgs* indexer, const KvipTopkArgs* topk,
                                             const KvipResidentArgs* resident, void* stream) {
     return kvip::resident_score(indexer, topk, resident, static_cast<hipStream_t>(stream));
+}
+
+extern "C" uint32_t kvip_hip_resident_score_window(const KvipIndexerArgs* indexer, const KvipTopkArgs* topk,
+                                                   const KvipResidentArgs* resident, int32_t token_begin,
+                                                   int32_t token_end, void* stream) {
+    if (indexer == nullptr || !kvip::ring_eligible(*indexer) || token_begin < 0 || token_end <= token_begin ||
+        token_begin % 128 != 0) {
+        return KVIP_ERR_INVALID;
+    }
+    return kvip::resident_score(indexer, topk, resident, static_cast<hipStream_t>(stream), token_begin, token_end);
 }
 
 extern "C" uint32_t kvip_hip_resident_forward(const KvipIndexerArgs* indexer, const KvipTopkArgs* topk,
@@ -959,7 +1035,7 @@ extern "C" uint32_t kvip_hip_resident_forward(const KvipIndexerArgs* indexer, co
 }
 
 uint32_t kvip::resident_score(const KvipIndexerArgs* indexer, const KvipTopkArgs* topk,
-                              const KvipResidentArgs* resident, hipStream_t s) {
+                              const KvipResidentArgs* resident, hipStream_t s, int token_begin, int token_end) {
     if (indexer == nullptr || topk == nullptr || resident == nullptr) return KVIP_ERR_INVALID;
     if (kvip::validate_indexer(indexer) != KVIP_OK || kvip::validate_topk(topk) != KVIP_OK ||
         kvip::validate_resident(resident) != KVIP_OK) {
@@ -977,10 +1053,16 @@ uint32_t kvip::resident_score(const KvipIndexerArgs* indexer, const KvipTopkArgs
                          li.scale_block_stride == kvip::kBlockTokens && li.max_blocks >= blocks_per_owner &&
                          li.num_blocks == ra.owners * blocks_per_owner && li.qk_dtype == KVIP_DTYPE_FP8_E4M3;
     if (!chained) return KVIP_ERR_INVALID;
-    // The round's initialisation (it reads only the candidates) writes the owner table too.
-    hipError_t e = kvip::launch_resident_begin(ra, s, const_cast<int32_t*>(li.block_table), li.max_blocks);
-    if (e != hipSuccess) return static_cast<uint32_t>(e);
-    return static_cast<uint32_t>(kvip::launch_indexer(li, s));
+    // The round's initialisation (it reads only the candidates) writes the owner table too;
+    // a window that starts past position 0 continues a round already initialised.
+    if (token_begin == 0) {
+        const hipError_t e = kvip::launch_resident_begin(ra, s, const_cast<int32_t*>(li.block_table), li.max_blocks);
+        if (e != hipSuccess) return static_cast<uint32_t>(e);
+    }
+    if (token_end < 0) return static_cast<uint32_t>(kvip::launch_indexer(li, s));
+    const int end = static_cast<int>(std::min<int64_t>(token_end, li.key_stride));
+    if (end % 128 != 0 && end < li.key_stride) return KVIP_ERR_INVALID;
+    return static_cast<uint32_t>(kvip::launch_indexer_ring(li, s, token_begin / 32, (end + 31) / 32));
 }
 
 namespace kvip {
@@ -1034,11 +1116,12 @@ __global__ __launch_bounds__(kPcThreads) void prefix_classify_kernel(const KvipP
 // Cold bits of query row blockIdx.y, words [256 x, 256 x + 256): position resident + 32 w + k
 // above the row's threshold. One word per thread, its 32 keys read as four 16-byte pieces
 // when the word is aligned and complete.
-__global__ __launch_bounds__(kPcThreads) void cold_hits_kernel(const KvipPrefixClassifyArgs p) {
+__global__ __launch_bounds__(kPcThreads) void cold_hits_kernel(const KvipPrefixClassifyArgs p, int word_begin,
+                                                               int word_end) {
     const int row = blockIdx.y;
     const int b = row / p.rows_per_request;
-    const int w = blockIdx.x * kPcThreads + threadIdx.x;
-    if (w >= p.cold_words) return;
+    const int w = word_begin + blockIdx.x * kPcThreads + threadIdx.x;
+    if (w >= word_end) return;
     int valid = max(p.seq_lens[b], 0);
     if (p.query_ends != nullptr) valid = min(valid, p.query_ends[row]);
     valid = min(max(valid, 0), p.key_stride);
@@ -1071,17 +1154,47 @@ __global__ __launch_bounds__(kPcThreads) void cold_hits_kernel(const KvipPrefixC
 }  // namespace
 }  // namespace kvip
 
-extern "C" uint32_t kvip_hip_resident_prefix(const KvipTopkArgs* topk, const KvipPrefixClassifyArgs* cls, void* stream) {
-    if (topk == nullptr || cls == nullptr || kvip::validate_topk(topk) != KVIP_OK) return KVIP_ERR_INVALID;
+namespace kvip {
+static bool prefix_args_ok(const KvipTopkArgs* topk, const KvipPrefixClassifyArgs* cls) {
+    if (topk == nullptr || cls == nullptr || validate_topk(topk) != KVIP_OK) return false;
     const KvipPrefixClassifyArgs& c = *cls;
-    const bool ok = c.score_keys && c.prefix_topk && c.seq_lens && c.lru_slots && c.thresholds && c.victim_hits &&
-                    c.cold_hits && c.batch == topk->batch && c.rows_per_request == topk->rows_per_request &&
-                    c.key_stride == topk->key_stride && c.score_keys == topk->score_keys &&
-                    c.prefix_topk == topk->topk && c.seq_lens == topk->seq_lens && c.query_ends == topk->query_ends &&
-                    topk->limit == c.resident && c.resident >= 1 && c.resident <= c.key_stride &&
-                    static_cast<int64_t>(c.cold_words) * 32 >= static_cast<int64_t>(c.key_stride) - c.resident &&
-                    c.cold_words >= 0;
-    if (!ok) return KVIP_ERR_INVALID;
+    return c.score_keys && c.prefix_topk && c.seq_lens && c.lru_slots && c.thresholds && c.victim_hits &&
+           c.cold_hits && c.batch == topk->batch && c.rows_per_request == topk->rows_per_request &&
+           c.key_stride == topk->key_stride && c.score_keys == topk->score_keys && c.prefix_topk == topk->topk &&
+           c.seq_lens == topk->seq_lens && c.query_ends == topk->query_ends && topk->limit == c.resident &&
+           c.resident >= 1 && c.resident <= c.key_stride &&
+           static_cast<int64_t>(c.cold_words) * 32 >= static_cast<int64_t>(c.key_stride) - c.resident &&
+           c.cold_words >= 0;
+}
+}  // namespace kvip
+
+extern "C" uint32_t kvip_hip_resident_threshold(const KvipTopkArgs* topk, const KvipPrefixClassifyArgs* cls,
+                                                void* stream) {
+    if (!kvip::prefix_args_ok(topk, cls)) return KVIP_ERR_INVALID;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    const hipError_t e = kvip::launch_topk(*topk, s);
+    if (e != hipSuccess) return static_cast<uint32_t>(e);
+    hipLaunchKernelGGL(kvip::prefix_classify_kernel, dim3(cls->batch * cls->rows_per_request), dim3(kvip::kPcThreads),
+                       0, s, *cls);
+    return static_cast<uint32_t>(hipGetLastError());
+}
+
+extern "C" uint32_t kvip_hip_resident_cold_hits(const KvipPrefixClassifyArgs* cls, int32_t word_begin,
+                                                int32_t word_end, void* stream) {
+    if (cls == nullptr || cls->cold_hits == nullptr || cls->score_keys == nullptr || cls->thresholds == nullptr ||
+        cls->seq_lens == nullptr || word_begin < 0 || word_end <= word_begin || word_end > cls->cold_words) {
+        return KVIP_ERR_INVALID;
+    }
+    const int words = word_end - word_begin;
+    hipLaunchKernelGGL(kvip::cold_hits_kernel,
+                       dim3((words + kvip::kPcThreads - 1) / kvip::kPcThreads, cls->batch * cls->rows_per_request),
+                       dim3(kvip::kPcThreads), 0, static_cast<hipStream_t>(stream), *cls, word_begin, word_end);
+    return static_cast<uint32_t>(hipGetLastError());
+}
+
+extern "C" uint32_t kvip_hip_resident_prefix(const KvipTopkArgs* topk, const KvipPrefixClassifyArgs* cls, void* stream) {
+    if (!kvip::prefix_args_ok(topk, cls)) return KVIP_ERR_INVALID;
+    const KvipPrefixClassifyArgs& c = *cls;
     const hipStream_t s = static_cast<hipStream_t>(stream);
     hipError_t e = kvip::launch_topk(*topk, s);
     if (e != hipSuccess) return static_cast<uint32_t>(e);
@@ -1090,7 +1203,7 @@ extern "C" uint32_t kvip_hip_resident_prefix(const KvipTopkArgs* topk, const Kvi
     if (c.cold_words > 0) {
         hipLaunchKernelGGL(kvip::cold_hits_kernel,
                            dim3((c.cold_words + kvip::kPcThreads - 1) / kvip::kPcThreads, c.batch * c.rows_per_request),
-                           dim3(kvip::kPcThreads), 0, s, c);
+                           dim3(kvip::kPcThreads), 0, s, c, 0, c.cold_words);
     }
     return static_cast<uint32_t>(hipGetLastError());
 }

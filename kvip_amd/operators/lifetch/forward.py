@@ -56,15 +56,40 @@ class LIFetchForward:
                 torch = self.torch
                 self.prefix = ResidentPrefix(torch, rotating, update.lru_slots, update.resident)
                 pf = update.prefetch
+                self.window_counts = torch.zeros((rotating.batch, abi.PREFETCH_MAX_WINDOWS), dtype=torch.int32,
+                                                 device=rotating.device)
                 self.prefetch_args = abi.PrefetchArgs(
                     victim_hits=abi.ptr(self.prefix.victim_hits), cold_hits=abi.ptr(self.prefix.cold_hits),
-                    cold_words=self.prefix.cold_words, windows=pf.windows, window_limit=pf.window_limit,
-                    prefetch_limit=pf.prefetch_limit)
+                    window_counts=abi.ptr(self.window_counts), cold_words=self.prefix.cold_words,
+                    windows=pf.windows, window_limit=pf.window_limit, prefetch_limit=pf.prefetch_limit)
                 self._prefetch_ref = ctypes.byref(self.prefetch_args)
                 # The prefetch branch: its own stream (default priority), forked after the
                 # scoring and joined before the final round.
                 self.side = torch.cuda.Stream(device=rotating.device)
                 self.scored, self.prefetched = torch.cuda.Event(), torch.cuda.Event()
+                # Windowed prefetch (opt-in; fp8 scoring with one row per request): the
+                # scoring runs window by window on the main stream; each scored window's cold
+                # hits and prefetch decisions follow on the side stream and its host copies
+                # on a third stream, so the copies overlap the scoring of later windows, the
+                # final TopK, resolve and Index update; only the final Fetch waits for them.
+                self.windowed = (pf.windowed and rotating.qk_name == "fp8" and rotating.rows_per_request == 1 and
+                                 rotating.batch <= 512)
+                if self.windowed:
+                    self.copy = torch.cuda.Stream(device=rotating.device)
+                    self.window_scored = [torch.cuda.Event() for _ in range(pf.windows)]
+                    self.window_decided = [torch.cuda.Event() for _ in range(pf.windows)]
+                    self.copies_done = torch.cuda.Event()
+                    resident, history = update.resident, update.history
+                    cold_tiles = (history - resident) // 128
+                    # Scoring window e covers [bounds[e], bounds[e + 1]) (the last one runs to
+                    # the row's end); prefetch window e >= 1 reads its cold hit words.
+                    ends = [resident + 128 * (cold_tiles * e // max(1, pf.windows - 1)) for e in range(pf.windows)]
+                    self.score_bounds = [0, resident] + ends[1:]
+                    self.score_bounds[-1] = max(self.score_bounds[-1], rotating.key_stride)
+                    self.hit_words = [None] + [((ends[e - 1] if e > 1 else resident) - resident) // 32
+                                               for e in range(1, pf.windows)]
+                    self.hit_words_end = [None] + [min((ends[e] - resident) // 32, self.prefix.cold_words)
+                                                   for e in range(1, pf.windows)]
             return
         self.args = abi.LIFetchArgs(rotating.indexer_args(), rotating.topk_args(), update.fetch_args(),
                                     abi.ptr(rotating.round_work) if fused else 0)
@@ -111,6 +136,9 @@ class LIFetchForward:
                 return
             torch, lib = self.torch, self.library
             main = torch.cuda.current_stream(self.rotating.device)
+            if self.windowed:
+                self._windowed_prefetch_forward(torch, lib, main)
+                return
             abi.check(lib.kvip_hip_resident_score(*self._refs, main.cuda_stream), "resident scoring")
             self.scored.record(main)
             self.side.wait_event(self.scored)
@@ -124,6 +152,42 @@ class LIFetchForward:
             upd.finish()
             return
         abi.check(self.library.kvip_hip_lifetch_forward(self._args_ref, self._stream()), "LIFetch forward")
+
+    def _windowed_prefetch_forward(self, torch, lib, main):
+        """The prefetching resident forward with the scoring in prefetch windows (same
+        outputs as scoring first and prefetching after: every window's decisions see the
+        same scores and run in window order)."""
+        upd, pf = self.update, self.update.prefetch
+        side, copy = self.side, self.copy
+        bounds = self.score_bounds
+        # Window 0: the resident prefix (with the round's initialisation); its TopK gives the
+        # thresholds, then window 0's decisions (the victim candidates).
+        abi.check(lib.kvip_hip_resident_score_window(*self._refs[:3], bounds[0], bounds[1], main.cuda_stream),
+                  "resident scoring (prefix)")
+        self.window_scored[0].record(main)
+        side.wait_event(self.window_scored[0])
+        abi.check(lib.kvip_hip_resident_threshold(ctypes.byref(self.prefix.topk_args), ctypes.byref(self.prefix.args),
+                                                  side.cuda_stream), "resident threshold")
+        for e in range(pf.windows):
+            if e > 0:
+                abi.check(lib.kvip_hip_indexer_decode_window(self._refs[0], bounds[e], bounds[e + 1],
+                                                             main.cuda_stream), "resident scoring (window)")
+                self.window_scored[e].record(main)
+                side.wait_event(self.window_scored[e])
+                if self.hit_words_end[e] > self.hit_words[e]:
+                    abi.check(lib.kvip_hip_resident_cold_hits(ctypes.byref(self.prefix.args), self.hit_words[e],
+                                                              self.hit_words_end[e], side.cuda_stream),
+                              "resident cold hits")
+            abi.check(lib.kvip_hip_resident_prefetch_windows(self._refs[2], self._prefetch_ref, e, e + 1,
+                                                             side.cuda_stream), "resident prefetch decisions")
+            self.window_decided[e].record(side)
+            copy.wait_event(self.window_decided[e])
+            abi.check(lib.kvip_hip_resident_prefetch_copy(self._refs[2], self._prefetch_ref, e, e + 1,
+                                                          copy.cuda_stream), "resident prefetch copy")
+        self.copies_done.record(copy)
+        abi.check(lib.kvip_hip_topk(self._refs[1], main.cuda_stream), "TopK")
+        main.wait_event(self.window_decided[-1])
+        upd.finish(copies_done=self.copies_done)
 
     # Individual stages (same kernels as the fused forward).
     def score(self):

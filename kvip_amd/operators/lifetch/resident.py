@@ -47,7 +47,13 @@ class ResidentPrefetch:
     boundaries), at most `window_limit` fetches per window (default prefetch_limit //
     windows) and `prefetch_limit` per request and round."""
 
-    def __init__(self, windows=8, prefetch_limit=512, window_limit=None):
+    def __init__(self, windows=8, prefetch_limit=512, window_limit=None, windowed=False):
+        """windowed: score the Index window by window and make each window's prefetch
+        decisions and host copies on other streams as soon as it is scored (fp8 scoring with
+        one query row per request; same results). Off by default: on MI355X the scoring of
+        a C4 round split into 8 launches takes ~140 us against ~73 us in one, and the
+        decision kernels wait for CUs behind each scoring launch, so the round is slower
+        than scoring first and prefetching after."""
         if type(windows) is not int or not 1 <= windows <= 32:
             raise ValueError("Prefetch requires 1..32 windows")
         if window_limit is None:
@@ -55,6 +61,7 @@ class ResidentPrefetch:
         if not 0 <= prefetch_limit <= LRU_SLOTS or not 1 <= window_limit <= 480:
             raise ValueError("Invalid prefetch budgets: total must be 0..2048 and window 1..480")
         self.windows, self.prefetch_limit, self.window_limit = windows, int(prefetch_limit), int(window_limit)
+        self.windowed = bool(windowed)
 
 
 class ResidentIndexUpdate:
@@ -176,15 +183,24 @@ class ResidentIndexUpdate:
         self.lru = chains
         self.commit_rows = self.slot_output.view(self.rotating.batch, -1)
 
-    def finish(self):
+    def finish(self, copies_done=None):
         """The round after its TopK (and prefetch): resolve, then the Fetch of the misses and
         the Index update (+ the attached LRU commit), enqueued on the current stream; with
         overlap the update branch runs on the second stream and is joined before return.
-        Capturable: no allocation, synchronisation or read-back."""
+        copies_done: an event the Fetch of the misses waits for (the last prefetch copy of a
+        windowed prefetch, which may still be writing slots the final misses take); resolve
+        and update need only the prefetch decisions. Capturable: no allocation,
+        synchronisation or read-back."""
         torch, lib = self.torch, self.library
         main = torch.cuda.current_stream(self.device)
         if not self.overlap:
-            abi.check(lib.kvip_hip_resident_finish(self._ref, main.cuda_stream), "resident round")
+            if copies_done is None:
+                abi.check(lib.kvip_hip_resident_finish(self._ref, main.cuda_stream), "resident round")
+            else:
+                abi.check(lib.kvip_hip_resident_resolve(self._ref, main.cuda_stream), "resident resolve")
+                main.wait_event(copies_done)
+                abi.check(lib.kvip_hip_resident_fetch(self._ref, main.cuda_stream), "resident Fetch")
+                abi.check(lib.kvip_hip_resident_update(self._ref, main.cuda_stream), "resident Index update")
             if self.lru is not None:
                 self.lru.commit(self.commit_rows)
             return
@@ -196,6 +212,8 @@ class ResidentIndexUpdate:
             with torch.cuda.stream(self.side):
                 self.lru.commit(self.commit_rows)
         self.updated.record(self.side)
+        if copies_done is not None:
+            main.wait_event(copies_done)
         abi.check(lib.kvip_hip_resident_fetch(self._ref, main.cuda_stream), "resident Fetch")
         main.wait_event(self.updated)
 

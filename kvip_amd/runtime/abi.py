@@ -9,7 +9,7 @@ import ctypes
 from pathlib import Path
 
 LIBRARY = Path(__file__).resolve().parents[1] / "_lib" / "libkvip_hip.so"
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 KVIP_OK = 0
 KVIP_ERR_INVALID = 100000
@@ -170,10 +170,13 @@ class PrefixClassifyArgs(ctypes.Structure):
     ]
 
 
+PREFETCH_MAX_WINDOWS = 32  # KVIP_PREFETCH_MAX_WINDOWS
+
+
 class PrefetchArgs(ctypes.Structure):
     _fields_ = [
-        ("victim_hits", _p), ("cold_hits", _p), ("cold_words", _i32), ("windows", _i32), ("window_limit", _i32),
-        ("prefetch_limit", _i32),
+        ("victim_hits", _p), ("cold_hits", _p), ("window_counts", _p), ("cold_words", _i32), ("windows", _i32),
+        ("window_limit", _i32), ("prefetch_limit", _i32),
     ]
 
 
@@ -200,6 +203,7 @@ PROTOTYPES = {
     "kvip_hip_sparse_attention_workspace_bytes": ([_i32, _i32], ctypes.c_uint64),
     "kvip_hip_publish_pages": ([ctypes.POINTER(PageArgs), _p], ctypes.c_uint32),
     "kvip_hip_indexer_decode": ([ctypes.POINTER(IndexerArgs), _p], ctypes.c_uint32),
+    "kvip_hip_indexer_decode_window": ([ctypes.POINTER(IndexerArgs), _i32, _i32, _p], ctypes.c_uint32),
     "kvip_hip_indexer_prefill": ([ctypes.POINTER(PrefillArgs), _p], ctypes.c_uint32),
     "kvip_hip_topk": ([ctypes.POINTER(TopkArgs), _p], ctypes.c_uint32),
     "kvip_hip_fetch_gather": ([ctypes.POINTER(FetchArgs), _p], ctypes.c_uint32),
@@ -230,6 +234,14 @@ PROTOTYPES = {
     "kvip_hip_resident_fetch": ([ctypes.POINTER(ResidentArgs), _p], ctypes.c_uint32),
     "kvip_hip_resident_update": ([ctypes.POINTER(ResidentArgs), _p], ctypes.c_uint32),
     "kvip_hip_resident_prefetch": ([ctypes.POINTER(ResidentArgs), ctypes.POINTER(PrefetchArgs), _p], ctypes.c_uint32),
+    "kvip_hip_resident_prefetch_windows": ([ctypes.POINTER(ResidentArgs), ctypes.POINTER(PrefetchArgs), _i32, _i32, _p],
+                                           ctypes.c_uint32),
+    "kvip_hip_resident_prefetch_copy": ([ctypes.POINTER(ResidentArgs), ctypes.POINTER(PrefetchArgs), _i32, _i32, _p],
+                                        ctypes.c_uint32),
+    "kvip_hip_resident_threshold": ([ctypes.POINTER(TopkArgs), ctypes.POINTER(PrefixClassifyArgs), _p], ctypes.c_uint32),
+    "kvip_hip_resident_cold_hits": ([ctypes.POINTER(PrefixClassifyArgs), _i32, _i32, _p], ctypes.c_uint32),
+    "kvip_hip_resident_score_window": ([ctypes.POINTER(IndexerArgs), ctypes.POINTER(TopkArgs),
+                                        ctypes.POINTER(ResidentArgs), _i32, _i32, _p], ctypes.c_uint32),
     "kvip_hip_resident_score": ([ctypes.POINTER(IndexerArgs), ctypes.POINTER(TopkArgs), ctypes.POINTER(ResidentArgs),
                                  _p], ctypes.c_uint32),
     "kvip_hip_resident_forward": ([ctypes.POINTER(IndexerArgs), ctypes.POINTER(TopkArgs), ctypes.POINTER(ResidentArgs),

@@ -416,8 +416,8 @@ def oracle_prefetch(st, keys, lru, pf):
     return out
 
 
-@pytest.mark.parametrize("q_rows,ring", [(1, 0), (2, 512)])
-def test_resident_prefetch_forward_matches_oracle(torch_gpu, q_rows, ring):
+@pytest.mark.parametrize("q_rows,ring,windowed", [(1, 0, False), (1, 0, True), (2, 512, False)])
+def test_resident_prefetch_forward_matches_oracle(torch_gpu, q_rows, ring, windowed):
     """The forward with the speculative windowed prefetch (prefix TopK and hit bits, the
     window scan and budgets, the prefetch Fetch on a second stream, the final round with
     prefetched tokens resolved to their slots and the prefetch applied first in the Index
@@ -426,8 +426,8 @@ def test_resident_prefetch_forward_matches_oracle(torch_gpu, q_rows, ring):
     to round so that each round prefetches, hits and misses."""
     torch = torch_gpu
     batch, history, resident = 3, 16384, 4096
-    pf = kvip_amd.ResidentPrefetch(windows=4, prefetch_limit=600, window_limit=200)
-    say(f"case resident prefetch q={q_rows} ring={ring}")
+    pf = kvip_amd.ResidentPrefetch(windows=4, prefetch_limit=600, window_limit=200, windowed=windowed)
+    say(f"case resident prefetch q={q_rows} ring={ring} windowed={windowed}")
     st = Setup(torch, batch=batch, owners=batch, history=history, resident=resident, q_rows=q_rows, seed=13 + ring,
                invalid=0.03, ring=ring, prefetch=pf)
     rot, upd = st.rot, st.upd
@@ -443,6 +443,7 @@ def test_resident_prefetch_forward_matches_oracle(torch_gpu, q_rows, ring):
         p.resize(resident, resident)
         policies.append(p)
     fwd = kvip_amd.LIFetch(rot, upd)
+    assert fwd.windowed == windowed
     for rnd in range(3):
         say(f"  round {rnd}")
         q = base + 0.4 * rnd * torch.randn(base.shape, generator=gen, device="cuda")
@@ -473,14 +474,18 @@ def test_resident_prefetch_forward_matches_oracle(torch_gpu, q_rows, ring):
             p.commit(s_out[(s_out >= 0) & (s_out < resident)])
 
 
-@pytest.mark.parametrize("prefetch", [False, True])
-def test_resident_forward_graph_replay(torch_gpu, prefetch):
+@pytest.mark.parametrize("prefetch,q_rows,windowed", [(False, 2, False), (True, 2, False), (True, 1, True)])
+def test_resident_forward_graph_replay(torch_gpu, prefetch, q_rows, windowed):
     """The resident forward captured once and replayed: each replay equals the same step
     run eagerly on a copy of the state (tables and outputs); with the prefetch, the capture
-    forks the prefetch onto its second stream and joins it before the final round."""
+    forks the prefetch onto its second stream and joins it before the final round (one
+    query row: the windowed prefetch, scoring window by window with the decisions on a
+    second stream and the host copies on a third)."""
     torch = torch_gpu
-    st = Setup(torch, batch=2, owners=2, history=8192, resident=4096, q_rows=2, seed=12,
-               prefetch=kvip_amd.ResidentPrefetch(windows=3, prefetch_limit=300) if prefetch else None)
+    say(f"case resident graph replay prefetch={prefetch} q={q_rows} windowed={windowed}")
+    st = Setup(torch, batch=2, owners=2, history=8192, resident=4096, q_rows=q_rows, seed=12,
+               prefetch=kvip_amd.ResidentPrefetch(windows=3, prefetch_limit=300, windowed=windowed)
+               if prefetch else None)
     rot, upd = st.rot, st.upd
     gen = torch.Generator(device="cuda")
     gen.manual_seed(5)
@@ -488,6 +493,7 @@ def test_resident_forward_graph_replay(torch_gpu, prefetch):
     rot.weights.copy_(torch.randn(rot.weights.shape, generator=gen, device="cuda") / 8)
     upd.set_candidates(torch.stack([torch.arange(2048), torch.arange(2048, 4096)]).int().cuda())
     fwd = kvip_amd.LIFetch(rot, upd)
+    assert not prefetch or fwd.windowed == windowed
     state = (st.keys, st.scales, st.addresses, st.logical, st.valid, st.hot)
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
