@@ -150,28 +150,30 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const KvipTopkArgs p
 }
 
 
-// Register-resident variant for rows of at most 1024*KPT keys (KPT <= 64): thread t holds keys
-// [t*KPT, (t+1)*KPT) (packed two per register), loaded in one batch; the high-byte bin
-// comes from the scoring histogram (each wave reads it) or a histogram built here, and
+// Register-resident variant for rows of at most THREADS*KPT keys (KPT <= 64): thread t
+// holds keys [t*KPT, (t+1)*KPT) (packed two per register), loaded in one batch; the high-byte
+// bin comes from the scoring histogram (each wave reads it) or a histogram built here, and
 // the rest is select_row.h (low-byte histogram, bitmask counts, one workgroup scan,
-// emission of the selected keys only).
-template <int KPT>
-__global__ __launch_bounds__(kTopkThreads) void topk_regs_kernel(const KvipTopkArgs p) {
+// emission of the selected keys only). Rows of at most 8192 keys take 256-thread workgroups
+// (32 keys each), so that a batch of short rows keeps several rows per CU in flight.
+template <int KPT, int THREADS = kTopkThreads>
+__global__ __launch_bounds__(THREADS) void topk_regs_kernel(const KvipTopkArgs p) {
     constexpr int W = KPT / 2;  // packed registers per thread
+    static_assert(THREADS >= 256 && THREADS % 64 == 0 && kTopK % (2 * THREADS) == 0, "whole int2 output pairs");
     __shared__ __align__(16) uint32_t s_hist[256];
-    __shared__ uint32_t s_wave[kTopkThreads / 64];
+    __shared__ uint32_t s_wave[THREADS / 64];
     __shared__ __align__(16) int32_t s_out[kTopK];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int row = blockIdx.x;
-    const int valid = min(topk_row_valid(p, row), kTopkThreads * KPT);
+    const int valid = min(topk_row_valid(p, row), THREADS * KPT);
     int32_t* out = p.topk + static_cast<size_t>(row) * kTopK;
     const uint16_t* keys = p.score_keys + static_cast<size_t>(row) * p.key_stride;
     uint32_t* ghist = p.histogram != nullptr ? p.histogram + static_cast<size_t>(row) * 256 : nullptr;
 
     if (valid < kTopK) {
-        for (int i = tid; i < kTopK; i += kTopkThreads) out[i] = i < valid ? i : -1;
+        for (int i = tid; i < kTopK; i += THREADS) out[i] = i < valid ? i : -1;
         if (ghist != nullptr && tid < 256) ghist[tid] = 0u;
         return;
     }
@@ -219,15 +221,14 @@ __global__ __launch_bounds__(kTopkThreads) void topk_regs_kernel(const KvipTopkA
         static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(wave_inclusive_scan(h[0] + h[1] + h[2] + h[3])), 63));
     const bool counted = hist_total == static_cast<uint32_t>(valid);
     if (tid < 256) s_hist[tid] = 0u;
-    reinterpret_cast<int2*>(s_out)[tid] = int2{-1, -1};
+    for (int i = tid; i < kTopK / 2; i += THREADS) reinterpret_cast<int2*>(s_out)[i] = int2{-1, -1};
     __syncthreads();
     if (ghist != nullptr && tid < 256) ghist[tid] = 0u;  // read by every wave: ready for the next scoring launch
 
     const RowSelection sel =
         select_row<KPT>(kk, count, first, hb, gt_hi, s_hist, s_wave, [&](int pos, int tok) { s_out[pos] = tok; });
     __syncthreads();
-    static_assert(kTopK == 2 * kTopkThreads, "one int2 per thread");
-    reinterpret_cast<int2*>(out)[tid] = reinterpret_cast<const int2*>(s_out)[tid];
+    for (int i = tid; i < kTopK / 2; i += THREADS) reinterpret_cast<int2*>(out)[i] = reinterpret_cast<const int2*>(s_out)[i];
     if (tid == 0 && !(sel.ok && counted)) report(p.status, KVIP_STATUS_HISTOGRAM);
 }
 
@@ -429,8 +430,8 @@ hipError_t launch_topk(const KvipTopkArgs& a, hipStream_t stream) {
     // Rows that fit 1024*KPT keys use the register-resident select; a limit (the resident
     // prefix of a longer row) bounds the keys a row can have.
     const int64_t span = a.limit > 0 ? std::min<int64_t>(a.key_stride, (a.limit + 7) / 8 * 8) : a.key_stride;
-    if (span <= kTopkThreads * 8) {
-        hipLaunchKernelGGL(topk_regs_kernel<8>, grid, block, 0, stream, a);
+    if (span <= 256 * 32) {
+        hipLaunchKernelGGL((topk_regs_kernel<32, 256>), grid, dim3(256), 0, stream, a);
     } else if (span <= kTopkThreads * 16) {
         hipLaunchKernelGGL(topk_regs_kernel<16>, grid, block, 0, stream, a);
     } else if (span <= kTopkThreads * 32) {

@@ -107,6 +107,7 @@ def keys_case(kind, n, rng):
 
 @pytest.mark.parametrize("kind,ctx", [
     ("random", [32768, 20000, 2048, 2047, 0, 8193]),
+    ("random", [8192, 5000, 2049, 100]),  # rows of at most 8192 keys: 256-thread workgroups
     ("few_levels", [16384, 30000]),
     ("all_equal", [4096, 2048]),
     ("all_equal", [65536, 4096]),  # a full register row of equal keys: the eq total reaches 65536
