@@ -132,12 +132,13 @@ def cpu_baseline(torch, wl, rot, budget_s):
                       f"has {physical} physical cores, {logical} logical CPUs"}
 
 
-def lidu_leg(torch, kvip_amd, device, seed, iters=50):
+def lidu_leg(torch, kvip_amd, device, seed, iters=50, reps=7):
     """Device time of one kvip.lidu call at the BASELINE config-4 shape (16 MTP requests x
     4 query rows, resident budget 16384 of a 131072-token history, ~80 % hits). Each call
     must start from the same maps, so two graphs are replayed back to back `iters` times:
     one restores the maps, the other restores them and runs lidu; the difference of the
-    two is lidu's time with host launch latency hidden behind the queued replays."""
+    two (medians over `reps` alternations) is lidu's time with host launch latency hidden
+    behind the queued replays."""
     from kvip_amd import synthetic
 
     dev, outs, args = synthetic.lidu_workload(torch, device, seed=seed)
@@ -156,8 +157,7 @@ def lidu_leg(torch, kvip_amd, device, seed, iters=50):
         with torch.cuda.graph(g):
             body()
         graphs.append(g)
-    times = []
-    for g in graphs:
+    def timed(g):
         for _ in range(3):
             g.replay()
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -166,13 +166,20 @@ def lidu_leg(torch, kvip_amd, device, seed, iters=50):
             g.replay()
         end.record()
         end.synchronize()
-        times.append(start.elapsed_time(end) * 1e3 / iters)
+        return start.elapsed_time(end) * 1e3 / iters
+
+    # The two graphs alternate `reps` times; the medians damp clock and queue drift.
+    samples = [[], []]
+    for _ in range(reps):
+        for k, g in enumerate(graphs):
+            samples[k].append(timed(g))
+    times = [float(np.median(x)) for x in samples]
     counts = outs["miss_counts"].cpu().numpy()
     if (counts[:-1] < 0).any():
         raise RuntimeError(f"lidu rejected a request: {counts.tolist()}")
     return {"workload": "c4 shape: 16 requests x 4 MTP rows, budget 16384, history 131072, ~80% hits",
             "us_per_call": round(times[1] - times[0], 2), "restore_us": round(times[0], 2),
-            "unique_misses_per_request": round(float(counts[:-1].mean()), 1), "calls": iters}
+            "unique_misses_per_request": round(float(counts[:-1].mean()), 1), "calls": iters * reps}
 
 
 def _query_walk(torch, base, sets, seed, step=0.3):

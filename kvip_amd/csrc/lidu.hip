@@ -9,11 +9,13 @@
 // hot_slot_selection.h, validation :264-295 + :1743-1797, clear/install/refill :350-449,
 // descriptors :451-545 + :2198-2261, batch outputs :2111-2196).
 //
-// Two launches, one 1024-thread workgroup per request in each:
+// Three launches: lidu_lookup_kernel gathers the token_to_slot entries of every TopK token
+// (16 workgroups per request), then one 1024-thread workgroup per request in each of:
 //   lidu_prepare_kernel reads the maps only. It checks the request's query range and
 //     whether its pool row aliases an earlier request's, classifies its 1-4 TopK rows
-//     (token_to_slot gathers, membership bits in LDS), compacts them with block scans,
-//     dedups the misses with LDS bitmaps over 2^18-token source tiles, selects slots
+//     (token_to_slot values from the lookup launch, membership bits in LDS), compacts them
+//     with block scans, dedups the misses with LDS bitmaps over 2^18-token source tiles,
+//     selects slots
 //     (miss_slots, then a ring scan of the unprotected bitmap), validates them, writes the
 //     hit suffixes, and leaves unique tokens, slots, miss prefixes and a control block in
 //     the workspace.
@@ -71,6 +73,16 @@ KVIP_DEVICE int32_t* request_ws(const KvipLiduArgs& p, int b) {
     return static_cast<int32_t*>(p.workspace) + head_words(p.batch) + static_cast<int64_t>(b) * kWsWords;
 }
 
+// Slot-table lookups of request b after the request blocks: token_to_slot of every TopK
+// entry of its query rows [kMaxQueries][2048] (kNoLookup where the entry is not looked up).
+constexpr int kNoLookup = INT32_MIN;
+constexpr int kLookupThreads = 256;
+constexpr int kLookupParts = kMaxQueries * kTopK / (2 * kLookupThreads);  // workgroups per request
+KVIP_DEVICE int32_t* request_lookups(const KvipLiduArgs& p, int b) {
+    return static_cast<int32_t*>(p.workspace) + head_words(p.batch) + static_cast<int64_t>(p.batch) * kWsWords +
+           static_cast<int64_t>(b) * kMaxQueries * kTopK;
+}
+
 // Graph padding rows (:1303-1320): reserved pool entry, no resident budget, no source.
 KVIP_DEVICE bool padding_row(const KvipLiduArgs& p, int r) {
     return p.cache_tokens[r] == 0 && p.candidate_lens[r] == 0 && p.logical_seq_lengths[r] == 1 &&
@@ -108,9 +120,43 @@ KVIP_DEVICE uint32_t ring_word(const uint32_t* protect, uint32_t o, uint32_t fir
     return ~protect[w] & mask;
 }
 
+// The token_to_slot gathers of the classification, spread over kLookupParts workgroups per
+// request (8192 scattered 4-byte reads per request are bound by one CU's outstanding misses
+// when its prepare workgroup makes them). Workgroup L serves request
+// (L / (8 * kLookupParts)) * 8 + L % 8, so that all of a request's lookups run on the XCD
+// (L % 8) of its prepare and commit workgroups and leave the token_to_slot lines they read in
+// that XCD's L2. Same query layout, validity and dummy-mode token substitution as the
+// prepare pass, which reads the results only for requests it classifies.
+__global__ __launch_bounds__(kLookupThreads) void lidu_lookup_kernel(const KvipLiduArgs p) {
+    const int l = blockIdx.x;
+    const int b = (l / (8 * kLookupParts)) * 8 + l % 8;
+    const int part = (l / 8) % kLookupParts;
+    if (b >= p.batch) return;
+    const int q0 = b == 0 ? 0 : p.actual_seq_lengths_query[b - 1];
+    const int q_end = p.actual_seq_lengths_query[b];
+    const int qn = q_end - q0;
+    if (q0 < 0 || q_end < q0 || q_end > p.packed_queries || qn < 1 || qn > kMaxQueries || padding_row(p, b)) return;
+    const int pool = p.req_pool_entries[b];
+    const int cand = p.candidate_lens[b];
+    if (pool < 0 || pool >= p.pool_size || cand < 1 || cand > p.source_capacity) return;
+    const int e = 2 * (part * kLookupThreads + static_cast<int>(threadIdx.x));  // pair of TopK entries
+    if (e >= qn * kTopK) return;
+    const bool dummy = p.profile_enabled[0] == kProfileGraphDummy;
+    const int32_t* t2s = p.token_to_slot + static_cast<int64_t>(pool) * p.source_capacity;
+    const int2 t2 = reinterpret_cast<const int2*>(p.topk + static_cast<int64_t>(q0) * kTopK)[e >> 1];
+    int t[2] = {t2.x, t2.y};
+    int m[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        if (dummy && (t[j] < 0 || t[j] >= cand)) t[j] = 0;
+        m[j] = t[j] >= 0 && t[j] < cand ? t2s[t[j]] : kNoLookup;
+    }
+    reinterpret_cast<int2*>(request_lookups(p, b))[e >> 1] = make_int2(m[0], m[1]);
+}
+
 __global__ __launch_bounds__(kThreads) void lidu_prepare_kernel(const KvipLiduArgs p) {
     __shared__ uint32_t s_member[kBitmapWords];   // miss-slot membership (zero in graph-dummy mode)
-    __shared__ uint32_t s_protect[kBitmapWords];  // membership | every hit slot
+    __shared__ uint32_t s_protect[kBitmapWords];  // membership | every hit slot (ring scan only)
     __shared__ int32_t s_miss[kMaxQueries][kTopK];
     __shared__ uint4 s_seen[kTileWords / 4];
     __shared__ uint4 s_cur[kTileWords / 4];       // reused as the slot list after dedup
@@ -172,19 +218,23 @@ __global__ __launch_bounds__(kThreads) void lidu_prepare_kernel(const KvipLiduAr
     const bool dummy = p.profile_enabled[0] == kProfileGraphDummy;
     const uint32_t* bitmap = reinterpret_cast<const uint32_t*>(p.miss_slot_bitmap) + static_cast<int64_t>(b) * kBitmapWords;
     for (int i = tid; i < kBitmapWords; i += kThreads) {
-        const uint32_t m = dummy ? 0u : bitmap[i];
-        s_member[i] = m;
-        s_protect[i] = m;
+        s_member[i] = dummy ? 0u : bitmap[i];
     }
     for (int i = tid; i < kTileWords / 4; i += kThreads) s_cur[i] = make_uint4(0, 0, 0, 0);
     __syncthreads();
 
-    const int32_t* t2s = p.token_to_slot + static_cast<int64_t>(pool) * p.source_capacity;
+    // token_to_slot values from the lookup launch (lidu_lookup_kernel).
+    const int32_t* looked = request_lookups(p, b);
     int tok[kMaxQueries][2], slot[kMaxQueries][2];
+    int2 lk[kMaxQueries];
 #pragma unroll
     for (int q = 0; q < kMaxQueries; ++q) {
         int2 v = make_int2(0, 0);
-        if (q < qn) v = reinterpret_cast<const int2*>(p.topk + static_cast<int64_t>(q0 + q) * kTopK)[tid];
+        lk[q] = make_int2(kNoLookup, kNoLookup);
+        if (q < qn) {
+            v = reinterpret_cast<const int2*>(p.topk + static_cast<int64_t>(q0 + q) * kTopK)[tid];
+            lk[q] = reinterpret_cast<const int2*>(looked + q * kTopK)[tid];
+        }
         tok[q][0] = v.x;
         tok[q][1] = v.y;
     }
@@ -197,34 +247,49 @@ __global__ __launch_bounds__(kThreads) void lidu_prepare_kernel(const KvipLiduAr
             tok[q][j] = t;
             int s = -1;
             if (q < qn && t >= 0 && t < cand) {
-                const int m = t2s[t];
+                const int m = j == 0 ? lk[q].x : lk[q].y;
                 if (m >= 0 && m < budget && !((s_member[m >> 5] >> (m & 31)) & 1u)) s = m;
             }
             slot[q][j] = s;
         }
     }
+    // Miss positions: one block scan per query pair, the two queries' counts in the 16-bit
+    // halves of one word (each total is at most 2048).
     int pos[kMaxQueries][2];
     int miss_count[kMaxQueries];
     int bad_token = 0;
 #pragma unroll
-    for (int q = 0; q < kMaxQueries; ++q) {
-        miss_count[q] = 0;
-        if (q >= qn) continue;
-        const uint32_t m0 = slot[q][0] < 0 ? 1u : 0u;
-        const uint32_t m1 = slot[q][1] < 0 ? 1u : 0u;
-        uint32_t total;
-        const uint32_t pre = block_exclusive_scan(m0 + m1, s_wave, &total);
-        miss_count[q] = static_cast<int>(total);
-        const int i0 = 2 * tid;
-        pos[q][0] = m0 ? pre : total + (i0 - pre);
-        pos[q][1] = m1 ? pre + m0 : total + (i0 + 1 - pre - m0);
+    for (int h = 0; h < kMaxQueries / 2; ++h) {
+        if (2 * h >= qn) {
+            miss_count[2 * h] = miss_count[2 * h + 1] = 0;
+            continue;
+        }
+        uint32_t packed = 0;
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            if (slot[q][j] < 0) {
-                s_miss[q][pos[q][j]] = tok[q][j];
-                bad_token |= (tok[q][j] < 0 || tok[q][j] >= cand) ? 1 : 0;
-            } else {
-                atomicOr(&s_protect[slot[q][j] >> 5], 1u << (slot[q][j] & 31));
+        for (int k = 0; k < 2; ++k) {
+            const int q = 2 * h + k;
+            const uint32_t misses = q < qn ? (slot[q][0] < 0 ? 1u : 0u) + (slot[q][1] < 0 ? 1u : 0u) : 0u;
+            packed |= misses << (16 * k);
+        }
+        uint32_t totals;
+        const uint32_t pres = block_exclusive_scan(packed, s_wave, &totals);
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int q = 2 * h + k;
+            const uint32_t pre = (pres >> (16 * k)) & 0xFFFFu;
+            const uint32_t total = (totals >> (16 * k)) & 0xFFFFu;
+            miss_count[q] = q < qn ? static_cast<int>(total) : 0;
+            if (q >= qn) continue;
+            const uint32_t m0 = slot[q][0] < 0 ? 1u : 0u;
+            const int i0 = 2 * tid;
+            pos[q][0] = m0 ? pre : total + (i0 - pre);
+            pos[q][1] = slot[q][1] < 0 ? pre + m0 : total + (i0 + 1 - pre - m0);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                if (slot[q][j] < 0) {
+                    s_miss[q][pos[q][j]] = tok[q][j];
+                    bad_token |= (tok[q][j] < 0 || tok[q][j] >= cand) ? 1 : 0;
+                }
             }
         }
     }
@@ -306,6 +371,17 @@ __global__ __launch_bounds__(kThreads) void lidu_prepare_kernel(const KvipLiduAr
         const int32_t* preferred = p.miss_slots + static_cast<int64_t>(b) * kTopK;
         for (int i = tid; i < n_in; i += kThreads) s_slots[i] = preferred[i];
         if (unique > static_cast<uint32_t>(kTopK)) {
+            // Slots the scan must skip: membership and every hit slot.
+            for (int i = tid; i < kBitmapWords; i += kThreads) s_protect[i] = s_member[i];
+            __syncthreads();
+#pragma unroll
+            for (int q = 0; q < kMaxQueries; ++q) {
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    if (q < qn && slot[q][j] >= 0) atomicOr(&s_protect[slot[q][j] >> 5], 1u << (slot[q][j] & 31));
+                }
+            }
+            __syncthreads();
             const uint32_t extra = unique - kTopK;
             const int cursor_in = p.eviction_cursors[pool];
             const uint32_t ubudget = static_cast<uint32_t>(budget);
@@ -517,7 +593,9 @@ __global__ __launch_bounds__(kThreads) void lidu_commit_kernel(const KvipLiduArg
 
 extern "C" uint64_t kvip_hip_lidu_workspace_bytes(int32_t batch) {
     if (batch < 1) return 0;
-    return static_cast<uint64_t>(kvip::head_words(batch) + static_cast<int64_t>(batch) * kvip::kWsWords) * 4u;
+    return static_cast<uint64_t>(kvip::head_words(batch) +
+                                 static_cast<int64_t>(batch) * (kvip::kWsWords + kvip::kMaxQueries * kvip::kTopK)) *
+           4u;
 }
 
 extern "C" uint32_t kvip_hip_lidu(const KvipLiduArgs* a, void* stream) {
@@ -550,6 +628,8 @@ extern "C" uint32_t kvip_hip_lidu(const KvipLiduArgs* a, void* stream) {
         return KVIP_ERR_INVALID;
     }
     const hipStream_t s = static_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(kvip::lidu_lookup_kernel, dim3((a->batch + 7) / 8 * 8 * kvip::kLookupParts),
+                       dim3(kvip::kLookupThreads), 0, s, *a);
     hipLaunchKernelGGL(kvip::lidu_prepare_kernel, dim3(a->batch), dim3(kvip::kThreads), 0, s, *a);
     hipLaunchKernelGGL(kvip::lidu_commit_kernel, dim3(a->batch), dim3(kvip::kThreads), 0, s, *a);
     return static_cast<uint32_t>(hipGetLastError());
