@@ -3,7 +3,9 @@
 One step = one decode round of the hot path over one batch of synthetic input that
 is already resident in HBM: lightning-indexer scoring of every context token of the
 64 requests, TopK-2048 per request, and the Fetch gather of the 2048 selected
-656-byte KV rows per request into a contiguous [64, 2048, 656] buffer.
+656-byte KV rows per request into a contiguous [64, 2048, 656] buffer. Rounds run as
+kernel nodes of captured hipGraphs, 8 rounds per graph by default (--rounds-per-graph;
+graph_ms_per_step reports one graph launch per round beside it).
 
 Prints one JSON line (rank 0): queries/s, per-kernel HIP-event timings, the roofline
 of the dominant kernel against MI355X's 8 TB/s HBM peak, the CPU baseline (the
@@ -36,6 +38,9 @@ def parse():
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--config", default="c2", choices=["c1", "c2"])
+    p.add_argument("--rounds-per-graph", type=int, default=8,
+                   help="decode rounds captured back to back in one hipGraph (as inside a model's decode "
+                        "graph); 1 = one graph launch per round; 1 or even")
     p.add_argument("--seed", type=int, default=2026)
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU-baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -677,8 +682,14 @@ def main():
             raise RuntimeError(f"device status {int(r.status.item())} after warm-up")
 
     stream = torch.cuda.current_stream()
-    # Timed region: the decode round captured as one hipGraph per input set, replayed
-    # alternately (the forward is graph-capturable: no allocation, sync or memset).
+    # Timed region: `rounds_per_graph` decode rounds captured back to back in one hipGraph
+    # (input sets alternating, kernel nodes with no host launch between them, as the
+    # indexer runs inside a model's captured decode step), replayed until exactly
+    # args.steps rounds have run; a remainder runs as one-round graphs. The forward is
+    # graph-capturable: no allocation, sync or memset.
+    per_graph = args.rounds_per_graph
+    if per_graph < 1 or (per_graph > 1 and per_graph % 2):
+        raise SystemExit("--rounds-per-graph must be 1 or even (the two input sets alternate)")
     graphs = []
     side = torch.cuda.Stream()
     side.wait_stream(stream)
@@ -692,45 +703,56 @@ def main():
         with torch.cuda.graph(g):
             f()
         graphs.append(g)
+    multi = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(multi):
+        for j in range(per_graph):
+            sets[j % 2][3]()
     for i in range(4):
         graphs[i % 2].replay()
+    multi.replay()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for s in range(args.steps):
+    for _ in range(args.steps // per_graph):
+        multi.replay()
+    for s in range(args.steps - args.steps % per_graph, args.steps):
         graphs[s % 2].replay()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_per_step = wall * 1e3 / args.steps
     steps_bytes = sum(step_bytes[s % 2] for s in range(args.steps))
 
-    # Per-kernel durations: HIP events on the launch stream around back-to-back graph
-    # replays (no host gap between launches), same alternating inputs: scoring from
+    # Per-kernel durations: HIP events on the launch stream around replays of graphs of
+    # `rounds_per_graph` back-to-back calls, same alternating inputs: scoring from
     # score-only graphs, TopK as score+TopK graphs minus scoring, the gather as the full
     # three-launch round minus score+TopK. The XCD-local round (scoring with in-launch
-    # selection, then the gather) is timed beside it on the same inputs.
+    # selection, then the gather) is timed beside it on the same inputs. graph_ms_per_step
+    # is the default round with one graph launch per round.
     plan = fwd.plan
     threes = [kvip_amd.LIFetch(r, u, fused=False) for w, r, u, f in sets]
     rounds = [kvip_amd.LIFetch(r, u, fused=True) for w, r, u, f in sets]
 
     def capture(calls):
         gs = []
-        for c in calls:
+        for k in range(1 if per_graph > 1 else len(calls)):
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g):
-                c()
+                for j in range(per_graph):
+                    calls[(k + j) % 2]()
             gs.append(g)
         return gs
 
     def replay_ms(gs):
+        per = per_graph if len(gs) == 1 else 1
+        reps = max(1, args.steps // per)
         for i in range(4):
-            gs[i % 2].replay()
+            gs[i % len(gs)].replay()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(stream)
-        for s in range(args.steps):
-            gs[s % 2].replay()
+        for s in range(reps):
+            gs[s % len(gs)].replay()
         e1.record(stream)
         e1.synchronize()
-        return e0.elapsed_time(e1) / args.steps
+        return e0.elapsed_time(e1) / (reps * per)
 
     with torch.cuda.stream(side):
         for t in threes + rounds:
@@ -782,6 +804,7 @@ def main():
         "hbm_frac_step": round(steps_bytes / wall / 1e9 / HBM_PEAK_GBS, 4),
         "step_bytes": step_bytes,
         "plan": plan,
+        "rounds_per_graph": per_graph,
         "graph_ms_per_step": round(full_ms, 4),
         "three_launch_graph_ms_per_step": round(three_ms, 4),
         "xcd_round_graph_ms_per_step": None if round_ms is None else round(round_ms, 4),
