@@ -272,6 +272,43 @@ def test_graph_replay_matches_eager(torch_gpu):
         assert torch.equal(g_out, upd.output), step
 
 
+def test_graph_of_alternating_rounds_matches_eager(torch_gpu):
+    """Four decode rounds captured in one graph over two bound input sets (set 0, 1, 0, 1),
+    the way bench.py times the step: every replay leaves each set's TopK and gathered rows
+    equal to an eager round on that set."""
+    torch = torch_gpu
+    bound = [synthetic.bind(torch, kvip_amd, synthetic.decode_workload(
+        torch, batch=6, ctx_low=3000, ctx_high=12000, device="cuda", seed=seed)) for seed in (11, 12)]
+    want = []
+    for rot, upd, fwd in bound:
+        fwd()
+        torch.cuda.synchronize()
+        assert int(rot.status.item()) == 0
+        want.append((rot.topk.clone(), upd.output.clone()))
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for _, _, fwd in bound:
+            fwd()  # warm-up on the capture stream
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for j in range(4):
+            bound[j % 2][2]()
+    for rep in range(3):
+        for rot, upd, _ in bound:
+            rot.topk.fill_(-7)
+            upd.output.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for k, ((rot, upd, _), (topk, out)) in enumerate(zip(bound, want)):
+            assert int(rot.status.item()) == 0, (rep, k)
+            assert torch.equal(rot.topk, topk), (rep, k)
+            assert torch.equal(upd.output, out), (rep, k)
+
+
 def test_bad_block_id_is_reported_not_faulted(torch_gpu):
     torch = torch_gpu
     wl = synthetic.decode_workload(torch, batch=2, ctx=[4096, 4096], device="cuda", seed=1)
