@@ -57,6 +57,7 @@ def check_case(torch, case, tag):
     (5, (4,), dict(hot_tokens=2048, hit_share=1.0)),
     (6, (4, 2), dict(hot_tokens=8192, hit_share=0.0, budget=12288, cand=40000)),
     (10, (1,) * 16, dict(budget=(1 << 17) + 2560, cand=300000, hot_tokens=2500)),
+    (12, (1, 2, 3, 4, 4, 3, 2, 1, 2, 4, 3), {}),  # 11 requests: a partial second group of 8
 ])
 def test_lidu_matches_oracle(torch_gpu, seed, queries, kw):
     check_case(torch_gpu, lc.random_case(seed, queries=queries, **kw), f"seed{seed}")
