@@ -49,8 +49,6 @@ def parse():
     p.add_argument("--no-prefill", action="store_true", help="skip the config-3 prefill timing leg")
     p.add_argument("--no-mixed", action="store_true", help="skip the config-5 mixed-round timing leg")
     p.add_argument("--no-sfa", action="store_true", help="skip the sparse-attention consumer timing leg")
-    p.add_argument("--coissue", action="store_true",
-                   help="also run the MFMA/VALU co-issue probe (the prefill scoring's ceiling at its VALU density)")
     p.add_argument("--copy-calibration", action="store_true",
                    help="also run a plain 1 GiB device copy (for rocprof FETCH/WRITE_SIZE scaling)")
     return p.parse_args()
@@ -618,36 +616,6 @@ def mixed_leg(torch, kvip_amd, device, seed, rounds=20, warm=4):
             "decode_hit_fraction": round(1.0 - miss / (nd * TOPK), 4), "rounds": rounds}
 
 
-def coissue_leg(torch, device, iters=2000):
-    """MFMA / VALU co-issue probe (kvip_hip_probe_coissue): every wave retires 4 fp8
-    32x32x64 MFMAs per iteration with V independent fp32 FMAs interleaved; one or two waves
-    per SIMD on every CU. Reports each V's time and the fraction of the dense fp8 peak
-    (5 PFLOP/s) its MFMAs reach. The prefill indexer issues 22 VALU instructions per MFMA
-    (V = 88 per 4 MFMAs), so the V = 88 fraction is the ceiling of its epilogue density."""
-    from kvip_amd.runtime import abi
-    lib = abi.load_library()
-    cus = torch.cuda.get_device_properties(device).multi_processor_count
-    out = torch.empty(cus * 2 * 256, dtype=torch.float32, device=device)
-    stream = torch.cuda.current_stream()
-    result = {"workload": f"{cus} CUs x 4 SIMDs, {iters} iterations of 4 MFMAs + V FMAs per wave", "iters": iters}
-    for waves in (1, 2):
-        blocks = cus * waves
-        row = {}
-        for v in (0, 32, 64, 88, 96):
-            abi.check(lib.kvip_hip_probe_coissue(v, blocks, 10, abi.ptr(out), stream.cuda_stream), "co-issue probe")
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record(stream)
-            abi.check(lib.kvip_hip_probe_coissue(v, blocks, iters, abi.ptr(out), stream.cuda_stream), "co-issue probe")
-            e1.record(stream)
-            e1.synchronize()
-            ms = e0.elapsed_time(e1)
-            flops = blocks * 4 * iters * 4 * (32 * 32 * 64 * 2)
-            tflops = flops / (ms * 1e-3) / 1e12
-            row[str(v)] = {"us": round(ms * 1e3, 1), "tflops": round(tflops, 1), "frac": round(tflops / 5000.0, 4)}
-        result[f"waves_per_simd_{waves}"] = row
-    return result
-
-
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -724,12 +692,10 @@ def main():
     # Per-kernel durations: HIP events on the launch stream around replays of graphs of
     # `rounds_per_graph` back-to-back calls, same alternating inputs: scoring from
     # score-only graphs, TopK as score+TopK graphs minus scoring, the gather as the full
-    # three-launch round minus score+TopK. The XCD-local round (scoring with in-launch
-    # selection, then the gather) is timed beside it on the same inputs. graph_ms_per_step
-    # is the default round with one graph launch per round.
+    # three-launch round minus score+TopK. graph_ms_per_step is the default round with one
+    # graph launch per round.
     plan = fwd.plan
-    threes = [kvip_amd.LIFetch(r, u, fused=False) for w, r, u, f in sets]
-    rounds = [kvip_amd.LIFetch(r, u, fused=True) for w, r, u, f in sets]
+    threes = [kvip_amd.LIFetch(r, u) for w, r, u, f in sets]
 
     def capture(calls):
         gs = []
@@ -755,7 +721,7 @@ def main():
         return e0.elapsed_time(e1) / (reps * per)
 
     with torch.cuda.stream(side):
-        for t in threes + rounds:
+        for t in threes:
             t()
     stream.wait_stream(side)
     torch.cuda.synchronize()
@@ -766,7 +732,6 @@ def main():
     st_ms = replay_ms(capture([lambda t=t: (t.score(), t.select()) for t in threes]))
     three_ms = replay_ms(capture(threes))
     times = {"indexer": score_ms, "topk": st_ms - score_ms, "fetch": three_ms - st_ms}
-    round_ms = replay_ms(capture(rounds)) if rounds[0].plan == "round" else None
     for w, r, u, f in sets:
         if int(r.status.item()) != 0:
             raise RuntimeError(f"device status {int(r.status.item())} after the timed steps")
@@ -807,7 +772,6 @@ def main():
         "rounds_per_graph": per_graph,
         "graph_ms_per_step": round(full_ms, 4),
         "three_launch_graph_ms_per_step": round(three_ms, 4),
-        "xcd_round_graph_ms_per_step": None if round_ms is None else round(round_ms, 4),
         "kernels": {k: {"ms": round(v, 5), "bytes": int(mean_bytes[k]),
                         "gbs": round(mean_bytes[k] / (v * 1e-3) / 1e9, 1)} for k, v in times.items()},
         "roofline": {"kernel": dominant, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
@@ -820,7 +784,6 @@ def main():
             ("prefill", args.no_prefill, lambda: prefill_leg(torch, kvip_amd, device, args.seed)),
             ("mixed", args.no_mixed, lambda: mixed_leg(torch, kvip_amd, device, args.seed)),
             ("sfa", args.no_sfa, lambda: sfa_leg(torch, kvip_amd, device, args.seed)),
-            ("coissue", not args.coissue, lambda: coissue_leg(torch, device)),
             ("cpu_baseline", args.no_cpu_baseline, lambda: cpu_baseline(torch, wl, rot, args.cpu_seconds))]
     print(f"bench: decode steps done ({result['ms_per_step']} ms/step)", file=sys.stderr, flush=True)
     for name, skip, leg in legs:

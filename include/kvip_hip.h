@@ -86,7 +86,7 @@
 extern "C" {
 #endif
 
-#define KVIP_HIP_ABI_VERSION 13u
+#define KVIP_HIP_ABI_VERSION 14u
 
 #define KVIP_TOPK 2048
 #define KVIP_BLOCK_TOKENS 128
@@ -108,10 +108,6 @@ extern "C" {
 #define KVIP_STATUS_BAD_BLOCK 1u     /* a block-table entry outside [0, num_blocks) */
 #define KVIP_STATUS_HISTOGRAM 2u     /* TopK histogram inconsistent with the row length */
 #define KVIP_STATUS_BAD_TOKEN 4u     /* a TopK token id outside the block table */
-#define KVIP_STATUS_STALLED 8u       /* XCD-local round only: a request went unselected or the
-                                        dispatcher did not place each group of workgroups on
-                                        one XCD; that round's outputs are unusable (rerun it
-                                        with the three-launch plan) */
 
 /* Lightning-indexer scoring over a paged index-K cache.
  *
@@ -223,29 +219,13 @@ typedef struct KvipFetchArgs {
     int32_t num_blocks;
 } KvipFetchArgs;
 
-/* One decode round: scoring -> TopK-2048 -> Fetch gather, stream-ordered. With the
- * scoring histogram and segment work memory in `topk`, TopK and Fetch run as one fused
- * launch (kvip_hip_select_fetch). With `round_work` (KVIP_ROUND_WORK_WORDS(rows) words,
- * 128-byte aligned, zero before the first launch; every round leaves it zero), fp8 Q/K,
- * one row per request, at most KVIP_ROUND_MAX_ROWS requests, key rows of at most 32768
- * keys on 128-byte boundaries and the scoring histogram, the round is two launches: scoring
- * with the requests dealt to XCDs, each request selected inside that launch by the
- * workgroup that finishes scoring it, then the gather, which also checks the first launch
- * (KVIP_STATUS_STALLED if a request went unselected or the dispatcher did not deal
- * workgroups round-robin over the XCDs) and zeroes the work memory. Score keys are then
- * written only for rows of at least 2048 tokens. Layout: 16 lines of per-XCD masks, a
- * completion line per request, one word per request. Rounds that share one work memory
- * must not overlap. */
-#define KVIP_ROUND_MAX_ROWS 256
-#define KVIP_ROUND_MAX_XCDS 16
-#define KVIP_ROUND_LINE_WORDS 32
-#define KVIP_ROUND_WORK_WORDS(rows) \
-    (KVIP_ROUND_MAX_XCDS * KVIP_ROUND_LINE_WORDS + (2 * KVIP_ROUND_LINE_WORDS + 256) * (rows))
+/* One decode round: scoring -> TopK-2048 -> Fetch gather, stream-ordered (three
+ * launches; the stages must be chained: TopK reads the scoring's keys and histogram, the
+ * gather the TopK's ids). */
 typedef struct KvipLIFetchArgs {
     KvipIndexerArgs indexer;
     KvipTopkArgs topk;
     KvipFetchArgs fetch;
-    uint32_t* round_work;        /* XCD-local round work memory, or NULL */
 } KvipLIFetchArgs;
 
 /* ABC ring maps: token_to_slot / slot_to_token are int32 [layers, pool, tokens];
@@ -622,13 +602,11 @@ uint32_t kvip_hip_fetch_gather(const KvipFetchArgs* args, void* stream);
 uint32_t kvip_hip_indexer_prefill(const KvipPrefillArgs* args, void* stream);
 uint32_t kvip_hip_lifetch_forward(const KvipLIFetchArgs* args, void* stream);
 /* The launch plan kvip_hip_lifetch_forward takes for these arguments (no launch, no device
- * access): KVIP_LIFETCH_PLAN_ROUND (with the round work memory: XCD-local scoring with
- * in-launch selection, then the checked gather) or _THREE (scoring, TopK, gather; rows of
- * at most KVIP_TOPK_REGS_MAX_KEYS keys use the register-resident TopK);
- * KVIP_ERR_INVALID when the forward would reject them. A host query with no counterpart in
- * the reference, for callers and tests that need to know which kernels a round runs. */
+ * access): KVIP_LIFETCH_PLAN_THREE (scoring, TopK, gather; rows of at most
+ * KVIP_TOPK_REGS_MAX_KEYS keys use the register-resident TopK), or KVIP_ERR_INVALID when
+ * the forward would reject them. A host query with no counterpart in the reference, for
+ * callers and tests that need to know which kernels a round runs. */
 #define KVIP_LIFETCH_PLAN_THREE 0u
-#define KVIP_LIFETCH_PLAN_ROUND 2u
 #define KVIP_TOPK_REGS_MAX_KEYS 65536
 uint32_t kvip_hip_lifetch_plan(const KvipLIFetchArgs* args);
 /* kvip_hip_lifetch_forward without caller scratch, for callers that cannot allocate device
@@ -636,7 +614,7 @@ uint32_t kvip_hip_lifetch_plan(const KvipLIFetchArgs* args);
  * No counterpart in the reference. The score keys and histograms come from one
  * library-owned array of KVIP_LIFETCH_STATIC_SCRATCH_BYTES per GPU (held until the process
  * ends): indexer.score_keys, indexer.histogram, topk.score_keys, topk.histogram,
- * topk.segments and round_work must be NULL, and rows * 1024 (rounded up to 256) + rows *
+ * and topk.segments must be NULL, and rows * 1024 (rounded up to 256) + rows *
  * key_stride * 2 bytes must fit the array (rows = batch * rows_per_request), else
  * KVIP_ERR_INVALID and nothing is launched. Same outputs as kvip_hip_lifetch_forward's
  * three-launch plan (plus one small fill launch that clears the histograms first); no
@@ -733,11 +711,6 @@ uint32_t kvip_hip_sparse_attention(const KvipSparseAttnArgs* args, void* stream)
 uint64_t kvip_hip_sparse_attention_workspace_bytes(int32_t rows, int32_t heads);
 /* Page publication of one step (PageUpdates.submit, python/kvip/cache/page_updates.py:27-62). */
 uint32_t kvip_hip_publish_pages(const KvipPageArgs* args, void* stream);
-/* Measurement probe, no reference counterpart (bench.py --coissue): `blocks` workgroups of
- * 256 threads each retire `iters` x 4 fp8 32x32x64 MFMAs interleaved with
- * valu_per_4_mfma (0, 32, 64, 88 or 96) independent fp32 FMAs, then write one float per
- * thread to out [blocks * 256]; timing it prices a VALU epilogue against the MFMA rate. */
-uint32_t kvip_hip_probe_coissue(int32_t valu_per_4_mfma, int32_t blocks, int32_t iters, float* out, void* stream);
 
 #ifdef __cplusplus
 }

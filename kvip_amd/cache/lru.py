@@ -46,7 +46,7 @@ class SlotLRU:
     def resize(self, capacity, committed):
         """Grow storage and append newly committed slots, preserving LRU order (lru.py:33-83)."""
         if not 0 <= committed <= capacity:
-            raise ValueError("Committed slots must fit HBM capacity")
+            raise ValueError(f"cannot commit {committed} slots into a capacity of {capacity}")
         torch = self.torch
         changed = False
         if capacity > self.capacity:

@@ -9,10 +9,6 @@
 // from FetchQueryGroup, op_kernel/streaming.cpp:365-500, :445; UBmem form
 // patches/kvaf-ubmem-device-get.patch:41-90; row layout
 // tests/operators/lifetch/support/workloads.py:493-515).
-//
-// As the second launch of the XCD-local round (score_select.hip) the first workgroup also
-// checks that launch: every scored request was selected and every virtual XCD ran on one
-// physical XCD (else KVIP_STATUS_STALLED), and zeroes its work memory for the next round.
 #include "kvip_device.h"
 
 namespace kvip {
@@ -22,47 +18,16 @@ constexpr int kGatherThreads = 256;
 constexpr int kRowsPerWave = 32;
 constexpr int kRowsPerBlock = kRowsPerWave * (kGatherThreads / 64);
 
-// Work memory of the XCD-local round (layout in score_select.hip): line v < 16 word 0 is
-// the physical-XCD mask of virtual XCD v, line 16 + b request b's record (completion count,
-// selected flag), then one word per request (1 if scored). Whole workgroup.
-KVIP_DEVICE void round_check(const RoundCheck& rc, uint32_t& err) {
-    constexpr int kLine = KVIP_ROUND_LINE_WORDS;
-    uint32_t* records = rc.work + 16 * kLine;
-    uint32_t* scored = records + static_cast<size_t>(rc.rows) * kLine;
-    for (int b = threadIdx.x; b < rc.rows; b += blockDim.x) {
-        uint32_t* rec = records + static_cast<size_t>(b) * kLine;
-        if (scored[b] != rec[1]) {
-            err |= KVIP_STATUS_STALLED;
-            uint32_t* h = rc.histogram + static_cast<size_t>(b) * 256;
-            for (int i = 0; i < 256; ++i) h[i] = 0u;  // the unselected request's counts
-        }
-        rec[0] = 0u;
-        rec[1] = 0u;
-        scored[b] = 0u;
-    }
-    if (threadIdx.x < 16) {
-        uint32_t* m = rc.work + threadIdx.x * kLine;
-        if (__popc(*m) > 1) err |= KVIP_STATUS_STALLED;
-        *m = 0u;
-    }
-}
-
 // One wave moves 32 consecutive selected rows: lanes 0..31 translate the token ids to
 // source rows (token id -> block table -> byte offset), then all 64 lanes copy the
 // 32*PIECES 16-byte pieces (21 loads in flight per lane for 656-byte rows). Because the
 // destination rows are consecutive, the wave's output
 // is one contiguous range written with fully coalesced 16-byte stores.
 template <int PIECES>
-__global__ __launch_bounds__(kGatherThreads) void fetch_gather_kernel(const KvipFetchArgs p, uint32_t selections,
-                                                                      const RoundCheck rc) {
+__global__ __launch_bounds__(kGatherThreads) void fetch_gather_kernel(const KvipFetchArgs p, uint32_t selections) {
     const int pieces = PIECES > 0 ? PIECES : p.row_bytes / 16;
     const int lane = threadIdx.x & 63;
     uint32_t err = 0;
-    if (rc.work != nullptr && blockIdx.x == 0) {
-        round_check(rc, err);
-        report(p.status, err);
-        err = 0;
-    }
     const uint32_t sel0 = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6) * kRowsPerWave;
     if (sel0 >= selections) return;
     const int capacity = p.max_blocks * kBlockTokens;
@@ -139,20 +104,16 @@ uint32_t validate_fetch(const KvipFetchArgs* a) {
     return ok ? KVIP_OK : KVIP_ERR_INVALID;
 }
 
-hipError_t launch_fetch_checked(const KvipFetchArgs& a, const RoundCheck& rc, hipStream_t stream) {
+hipError_t launch_fetch(const KvipFetchArgs& a, hipStream_t stream) {
     const uint32_t selections = static_cast<uint32_t>(a.batch) * a.rows_per_request * kTopK;
     const dim3 grid((selections + kRowsPerBlock - 1) / kRowsPerBlock);
     if (a.row_bytes == KVIP_KV_ROW_BYTES) {
         hipLaunchKernelGGL(fetch_gather_kernel<KVIP_KV_ROW_BYTES / 16>, grid, dim3(kGatherThreads), 0, stream, a,
-                           selections, rc);
+                           selections);
     } else {
-        hipLaunchKernelGGL(fetch_gather_kernel<0>, grid, dim3(kGatherThreads), 0, stream, a, selections, rc);
+        hipLaunchKernelGGL(fetch_gather_kernel<0>, grid, dim3(kGatherThreads), 0, stream, a, selections);
     }
     return hipGetLastError();
-}
-
-hipError_t launch_fetch(const KvipFetchArgs& a, hipStream_t stream) {
-    return launch_fetch_checked(a, RoundCheck{nullptr, nullptr, 0}, stream);
 }
 
 }  // namespace kvip

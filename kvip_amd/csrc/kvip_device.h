@@ -22,14 +22,6 @@ typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 
 KVIP_DEVICE int lane_id() { return __lane_id(); }
 
-// The gather launch's check of the XCD-local round (score_select.hip): its work memory
-// (NULL: no check), the scoring histogram and the row count.
-struct RoundCheck {
-    uint32_t* work;       // round work memory of the scoring launch, or NULL
-    uint32_t* histogram;  // [rows, 256] scoring histogram
-    int rows;
-};
-
 // fp32 -> bf16 bits, rounding half away from zero on the magnitude (the Ascend
 // CAST_ROUND mode the reference scores use: tests/operators/lifetch/support/
 // workloads.py:233-235, op_kernel/indexer/indexer_score.h:105-140).

@@ -6,9 +6,7 @@
 // gather (fetch_gather.hip). Measured at BASELINE config 2 this beats TopK fused with the
 // gather (select_fetch.hip, still exported as kvip_hip_select_fetch): the separate gather
 // launch is balanced by the hardware dispatcher, while the fused one waits for its
-// slowest workgroup. With the round work memory the round is two launches: XCD-local
-// scoring in which each request is selected by the workgroup that finishes scoring it
-// (score_select.hip), then the gather, which also checks that launch.
+// slowest workgroup.
 //
 // Replaces kvip_lifetch_streaming_forward (csrc/operators/lightning_indexer_with_fetch/
 // include/api.h:7, op_host/launch.cpp:76-83), whose init -> LI -> resolve/update/fetch
@@ -22,9 +20,6 @@ uint32_t validate_fetch(const KvipFetchArgs* a);
 hipError_t launch_indexer(const KvipIndexerArgs& a, hipStream_t stream);
 hipError_t launch_topk(const KvipTopkArgs& a, hipStream_t stream);
 hipError_t launch_fetch(const KvipFetchArgs& a, hipStream_t stream);
-bool score_select_eligible(const KvipIndexerArgs& a, const KvipTopkArgs& t, const uint32_t* work);
-hipError_t launch_score_select(const KvipIndexerArgs& a, const KvipTopkArgs& t, uint32_t* work, hipStream_t stream);
-hipError_t launch_fetch_checked(const KvipFetchArgs& a, const RoundCheck& rc, hipStream_t stream);
 }  // namespace kvip
 
 extern "C" uint32_t kvip_hip_abi_version(void) { return KVIP_HIP_ABI_VERSION; }
@@ -48,10 +43,6 @@ uint32_t lifetch_plan(const KvipLIFetchArgs* args) {
                          tk.rows_per_request == li.rows_per_request && fe.topk == tk.topk &&
                          fe.batch == li.batch && fe.rows_per_request == li.rows_per_request;
     if (!chained) return KVIP_ERR_INVALID;
-    // With the round work memory: scoring with in-launch selection, then the gather.
-    if (args->round_work != nullptr && kvip::score_select_eligible(li, tk, args->round_work)) {
-        return KVIP_LIFETCH_PLAN_ROUND;
-    }
     return KVIP_LIFETCH_PLAN_THREE;
 }
 }  // namespace
@@ -65,12 +56,6 @@ extern "C" uint32_t kvip_hip_lifetch_forward(const KvipLIFetchArgs* args, void* 
     const KvipIndexerArgs& li = args->indexer;
     const KvipTopkArgs& tk = args->topk;
     const KvipFetchArgs& fe = args->fetch;
-    if (plan == KVIP_LIFETCH_PLAN_ROUND) {
-        const hipError_t e = kvip::launch_score_select(li, tk, args->round_work, s);
-        if (e != hipSuccess) return static_cast<uint32_t>(e);
-        const kvip::RoundCheck rc{args->round_work, tk.histogram, li.batch * li.rows_per_request};
-        return static_cast<uint32_t>(kvip::launch_fetch_checked(fe, rc, s));
-    }
     hipError_t e = kvip::launch_indexer(li, s);
     if (e != hipSuccess) return static_cast<uint32_t>(e);
     // Rows that fit the register-resident TopK take it even when the split select's work

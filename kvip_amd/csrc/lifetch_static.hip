@@ -53,10 +53,10 @@ extern "C" uint32_t kvip_hip_lifetch_forward_static(const KvipLIFetchArgs* args,
     if (args == nullptr) return KVIP_ERR_INVALID;
     const KvipIndexerArgs& li = args->indexer;
     const KvipTopkArgs& tk = args->topk;
-    // The library supplies the scratch; the split select and the XCD-local round (which
-    // need more work memory) are not offered here.
+    // The library supplies the scratch; the split select (which needs more work memory) is
+    // not offered here.
     if (li.score_keys != nullptr || li.histogram != nullptr || tk.score_keys != nullptr || tk.histogram != nullptr ||
-        tk.segments != nullptr || args->round_work != nullptr) {
+        tk.segments != nullptr) {
         return KVIP_ERR_INVALID;
     }
     if (li.batch < 1 || li.rows_per_request < 1 || li.key_stride < 8) return KVIP_ERR_INVALID;

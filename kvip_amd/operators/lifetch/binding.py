@@ -77,8 +77,6 @@ class LIFetchBinding:
         self.topk_segments = torch.zeros((self.rows, segments, TOPK_SEGMENT_WORDS), dtype=torch.int32, device=dev)
         self.topk = torch.full((self.rows, TOPK), -1, dtype=torch.int32, device=dev)
         self.status = torch.zeros(1, dtype=torch.int32, device=dev)
-        # Work memory of the XCD-local round (zero; every round leaves it so).
-        self.round_work = torch.zeros(abi.round_work_words(self.rows), dtype=torch.int32, device=dev)
         self.keys = None
         self.key_scale = None
         self.query_inputs = None

@@ -23,15 +23,11 @@ class LIFetchForward:
     ResidentIndexUpdate (hot-cache round: resolve, Fetch of the misses from host memory,
     Index update)."""
 
-    def __init__(self, rotating, update, *, q_workers=2, fused=False):
+    def __init__(self, rotating, update, *, q_workers=2):
         """q_workers: the reference's per-request Fetch worker count
         (python/kvip/operators/lifetch/forward.py:8); accepted for call compatibility (a
         positive int). On MI355X the Fetch work is spread by the hardware dispatcher over
-        every CU, so it selects nothing here.
-        fused: hand the round work memory to the contiguous-Fetch forward, which then
-        runs the XCD-local round where it applies (fp8, one row per request: scoring with
-        each request selected inside that launch, then the gather); False (the default)
-        keeps three launches: scoring, TopK, gather."""
+        every CU, so it selects nothing here."""
         if type(q_workers) is not int or q_workers < 1:
             raise ValueError(f"q_workers must be a positive int (got {q_workers!r})")
         self.q_workers = q_workers
@@ -91,8 +87,7 @@ class LIFetchForward:
                     self.hit_words_end = [None] + [min((ends[e] - resident) // 32, self.prefix.cold_words)
                                                    for e in range(1, pf.windows)]
             return
-        self.args = abi.LIFetchArgs(rotating.indexer_args(), rotating.topk_args(), update.fetch_args(),
-                                    abi.ptr(rotating.round_work) if fused else 0)
+        self.args = abi.LIFetchArgs(rotating.indexer_args(), rotating.topk_args(), update.fetch_args())
         self._args_ref = ctypes.byref(self.args)
         # Stage-wise argument blocks for score()/select()/fetch().
         self._indexer = ctypes.byref(self.args.indexer)
@@ -110,8 +105,7 @@ class LIFetchForward:
 
     @property
     def plan(self):
-        """The launch plan of a contiguous-Fetch forward: "round" (XCD-local scoring with
-        in-launch selection, then the gather) or "three" (scoring, TopK, gather);
+        """The launch plan of a contiguous-Fetch forward: "three" (scoring, TopK, gather);
         "resident" for the resident-cache forward."""
         if self.resident:
             return "resident"

@@ -187,10 +187,13 @@ class ResidentIndexUpdate:
         """The round after its TopK (and prefetch): resolve, then the Fetch of the misses and
         the Index update (+ the attached LRU commit), enqueued on the current stream; with
         overlap the update branch runs on the second stream and is joined before return.
-        copies_done: an event the Fetch of the misses waits for (the last prefetch copy of a
-        windowed prefetch, which may still be writing slots the final misses take); resolve
-        and update need only the prefetch decisions. Capturable: no allocation,
-        synchronisation or read-back."""
+        copies_done: the event of the last prefetch copy of a windowed prefetch, still
+        running on its own stream. The resolve needs only the prefetch decisions, but the
+        copies read what the Index update and the LRU commit rewrite (each prefetched
+        token's host address in `addresses`, its candidate slot in `lru_slots`) and write
+        slots the final misses may take, so the Fetch of the misses, the Index update and
+        the LRU commit all wait for it. Capturable: no allocation, synchronisation or
+        read-back."""
         torch, lib = self.torch, self.library
         main = torch.cuda.current_stream(self.device)
         if not self.overlap:
@@ -198,7 +201,7 @@ class ResidentIndexUpdate:
                 abi.check(lib.kvip_hip_resident_finish(self._ref, main.cuda_stream), "resident round")
             else:
                 abi.check(lib.kvip_hip_resident_resolve(self._ref, main.cuda_stream), "resident resolve")
-                main.wait_event(copies_done)
+                main.wait_event(copies_done)  # before the Fetch, the update and the LRU commit
                 abi.check(lib.kvip_hip_resident_fetch(self._ref, main.cuda_stream), "resident Fetch")
                 abi.check(lib.kvip_hip_resident_update(self._ref, main.cuda_stream), "resident Index update")
             if self.lru is not None:
@@ -207,6 +210,8 @@ class ResidentIndexUpdate:
         abi.check(lib.kvip_hip_resident_resolve(self._ref, main.cuda_stream), "resident resolve")
         self.resolved.record(main)
         self.side.wait_event(self.resolved)
+        if copies_done is not None:
+            self.side.wait_event(copies_done)
         abi.check(lib.kvip_hip_resident_update(self._ref, self.side.cuda_stream), "resident Index update")
         if self.lru is not None:
             with torch.cuda.stream(self.side):

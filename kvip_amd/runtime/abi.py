@@ -9,7 +9,7 @@ import ctypes
 from pathlib import Path
 
 LIBRARY = Path(__file__).resolve().parents[1] / "_lib" / "libkvip_hip.so"
-ABI_VERSION = 13
+ABI_VERSION = 14
 
 KVIP_OK = 0
 KVIP_ERR_INVALID = 100000
@@ -21,7 +21,6 @@ DTYPE_FP32 = 2
 STATUS_BAD_BLOCK = 1
 STATUS_HISTOGRAM = 2
 STATUS_BAD_TOKEN = 4
-STATUS_STALLED = 8
 
 _p = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -68,17 +67,7 @@ class FetchArgs(ctypes.Structure):
 
 
 class LIFetchArgs(ctypes.Structure):
-    _fields_ = [("indexer", IndexerArgs), ("topk", TopkArgs), ("fetch", FetchArgs), ("round_work", _p)]
-
-
-ROUND_MAX_ROWS = 256
-ROUND_MAX_XCDS = 16
-ROUND_LINE_WORDS = 32
-
-
-def round_work_words(rows):
-    """Words of the XCD-local round work memory (KVIP_ROUND_WORK_WORDS)."""
-    return ROUND_MAX_XCDS * ROUND_LINE_WORDS + (2 * ROUND_LINE_WORDS + 256) * rows
+    _fields_ = [("indexer", IndexerArgs), ("topk", TopkArgs), ("fetch", FetchArgs)]
 
 
 class AbcArgs(ctypes.Structure):
@@ -119,7 +108,7 @@ class QueryPackArgs(ctypes.Structure):
 
 
 # kvip_hip_lifetch_plan results.
-LIFETCH_PLANS = {0: "three", 2: "round"}
+LIFETCH_PLANS = {0: "three"}
 TOPK_REGS_MAX_KEYS = 65536  # KVIP_TOPK_REGS_MAX_KEYS
 LIFETCH_STATIC_SCRATCH_BYTES = 16 << 20  # KVIP_LIFETCH_STATIC_SCRATCH_BYTES
 
@@ -229,7 +218,6 @@ PROTOTYPES = {
     "kvip_hip_resident_round": ([ctypes.POINTER(ResidentArgs), _p], ctypes.c_uint32),
     "kvip_hip_resident_begin": ([ctypes.POINTER(ResidentArgs), _p], ctypes.c_uint32),
     "kvip_hip_resident_finish": ([ctypes.POINTER(ResidentArgs), _p], ctypes.c_uint32),
-    "kvip_hip_probe_coissue": ([ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, _p, _p], ctypes.c_uint32),
     "kvip_hip_resident_resolve": ([ctypes.POINTER(ResidentArgs), _p], ctypes.c_uint32),
     "kvip_hip_resident_fetch": ([ctypes.POINTER(ResidentArgs), _p], ctypes.c_uint32),
     "kvip_hip_resident_update": ([ctypes.POINTER(ResidentArgs), _p], ctypes.c_uint32),

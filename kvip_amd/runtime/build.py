@@ -11,6 +11,7 @@ import hashlib
 import os
 import shutil
 import subprocess
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 PACKAGE = Path(__file__).resolve().parents[1]
@@ -18,6 +19,7 @@ ROOT = PACKAGE.parent
 SOURCES = PACKAGE / "csrc"
 INCLUDE = ROOT / "include"
 OUTPUT = PACKAGE / "_lib" / "libkvip_hip.so"
+OBJECTS = PACKAGE / "_lib" / "_build"
 ARCH = "gfx950"
 
 # Packed-FP32 instructions are disabled for every HIP file (hipcc's host pass warns
@@ -28,7 +30,6 @@ HIPCC_FLAGS = [
     "-std=c++17",
     "-mcode-object-version=5",
     "-fPIC",
-    "-shared",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-command-line-argument",
     # MFMA accumulators in VGPRs (gfx950 has a unified register file): the epilogue then
@@ -70,8 +71,19 @@ def files_digest(paths) -> str:
     return digest.hexdigest()
 
 
+def _compile(source: Path, jobs_dir: Path) -> Path:
+    obj = jobs_dir / (source.stem + ".o")
+    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{SOURCES}", "-c", str(source), "-o", str(obj)]
+    result = subprocess.run(cmd, capture_output=True, text=True)
+    if result.returncode != 0:
+        raise RuntimeError(f"hipcc failed on {source.name} ({result.returncode}):\n{result.stderr[-6000:]}")
+    return obj
+
+
 def build_libraries(force: bool = True, verbose: bool = False) -> Path:
-    """Compile every HIP source into kvip_amd/_lib/libkvip_hip.so.
+    """Compile every HIP source into kvip_amd/_lib/libkvip_hip.so: one object per source,
+    compiled in parallel (each translation unit carries its own gfx950 code object), then
+    one shared-library link.
 
     force=False skips the compile when the stamped source digest matches."""
     OUTPUT.parent.mkdir(parents=True, exist_ok=True)
@@ -79,13 +91,22 @@ def build_libraries(force: bool = True, verbose: bool = False) -> Path:
     digest = source_digest()
     if not force and OUTPUT.exists() and stamp.exists() and stamp.read_text() == digest:
         return OUTPUT
-    tmp = OUTPUT.with_name(OUTPUT.name + f".tmp{os.getpid()}")
-    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{SOURCES}", *map(str, source_files()), "-o", str(tmp)]
-    result = subprocess.run(cmd, capture_output=True, text=True)
-    if result.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({result.returncode}):\n{result.stderr[-6000:]}")
-    if verbose and result.stderr:
-        print(result.stderr)
-    os.replace(tmp, OUTPUT)
+    jobs_dir = OBJECTS / f"p{os.getpid()}"
+    jobs_dir.mkdir(parents=True, exist_ok=True)
+    try:
+        sources = source_files()
+        workers = max(1, min(len(sources), int(os.environ.get("MAX_JOBS", os.cpu_count() or 1))))
+        with ThreadPoolExecutor(workers) as pool:
+            objects = list(pool.map(lambda src: _compile(src, jobs_dir), sources))
+        tmp = OUTPUT.with_name(OUTPUT.name + f".tmp{os.getpid()}")
+        cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objects), "-o", str(tmp)]
+        result = subprocess.run(cmd, capture_output=True, text=True)
+        if result.returncode != 0:
+            raise RuntimeError(f"hipcc link failed ({result.returncode}):\n{result.stderr[-6000:]}")
+        if verbose and result.stderr:
+            print(result.stderr)
+        os.replace(tmp, OUTPUT)
+    finally:
+        shutil.rmtree(jobs_dir, ignore_errors=True)
     stamp.write_text(digest)
     return OUTPUT

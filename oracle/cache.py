@@ -81,7 +81,7 @@ class SlotLRU:
     def resize(self, capacity, committed):
         """lru.py:33-83."""
         if not 0 <= committed <= capacity:
-            raise ValueError("Committed slots must fit HBM capacity")
+            raise ValueError(f"cannot commit {committed} slots into a capacity of {capacity}")
         changed = False
         if capacity > len(self.next):
             capacity = max(capacity, 2 * len(self.next))

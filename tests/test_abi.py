@@ -162,7 +162,7 @@ def test_lifetch_plan_query():
     assert lib.kvip_hip_lifetch_plan(None) == abi.KVIP_ERR_INVALID
 
     def make(**over):
-        o = dict(qk=abi.DTYPE_FP8_E4M3, rpr=1, batch=64, work=0x9000, segments=0x8000, histogram=0x7000)
+        o = dict(qk=abi.DTYPE_FP8_E4M3, rpr=1, batch=64, segments=0x8000, histogram=0x7000)
         o.update(over)
         li = abi.IndexerArgs(query=0x1000, weights=0x1100, keys=0x2000, block_table=0x3000, seq_lens=0x4000,
                              score_keys=0x5000, histogram=o["histogram"], key_block_stride=128 * 128 * 2, batch=o["batch"],
@@ -173,21 +173,14 @@ def test_lifetch_plan_query():
         fe = abi.FetchArgs(topk=0x6000, kv_cache=0xA000, block_table=0x3000, output=0xB000,
                            kv_block_stride=128 * 656, row_stride=656, row_bytes=656, batch=o["batch"],
                            rows_per_request=o["rpr"], max_blocks=256, num_blocks=1024)
-        return abi.LIFetchArgs(li, tk, fe, o["work"])
+        return abi.LIFetchArgs(li, tk, fe)
 
     plan = lambda a: abi.LIFETCH_PLANS.get(lib.kvip_hip_lifetch_plan(ctypes.byref(a)), "invalid")  # noqa: E731
-    # The XCD-local round also needs a device whose grid splits evenly over its XCDs.
-    torch = pytest.importorskip("torch")
-    assert plan(make()) == ("round" if torch.cuda.is_available() else "three")
-    assert plan(make(work=0)) == "three"
-    assert plan(make(work=0, segments=0)) == "three"
-    assert plan(make(qk=abi.DTYPE_BF16)) == "three"             # the round is fp8 only
-    assert plan(make(rpr=2)) == "three"                         # and one row per request
-    assert plan(make(batch=257)) == "three"                     # and at most 256 requests
+    assert plan(make()) == "three"
+    assert plan(make(segments=0)) == "three"
+    assert plan(make(qk=abi.DTYPE_BF16)) == "three"
+    assert plan(make(rpr=2)) == "three"
     assert plan(make(histogram=0)) == "invalid"                 # decode scoring always fills a histogram
-    unaligned = make()
-    unaligned.indexer.score_keys = unaligned.topk.score_keys = 0x5010  # key rows off 128-byte lines
-    assert plan(unaligned) == "three"
     bad = make()
     bad.fetch.topk = 0x6100                                     # stages not chained
     assert plan(bad) == "invalid"

@@ -28,7 +28,6 @@ def static_args(fwd):
     a.topk.score_keys = 0
     a.topk.histogram = 0
     a.topk.segments = 0
-    a.round_work = 0
     return a
 
 
