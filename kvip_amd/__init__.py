@@ -29,6 +29,8 @@ __all__ = [
     "update_abc",
     "lidu",
     "lidu_prepare",
+    "lidu_reserve",
+    "register_torch_ops",
     "build_libraries",
     "load_library",
 ]
@@ -56,6 +58,8 @@ _EXPORTS = {
     "update_abc": ("cache.abc", "update_abc"),
     "lidu": ("operators.lidu", "lidu"),
     "lidu_prepare": ("operators.lidu", "lidu_prepare"),
+    "lidu_reserve": ("operators.lidu", "lidu_reserve"),
+    "register_torch_ops": ("operators.lidu", "register_torch_ops"),
     "build_libraries": ("runtime.build", "build_libraries"),
     "load_library": ("runtime.abi", "load_library"),
 }

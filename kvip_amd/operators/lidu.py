@@ -6,10 +6,22 @@ the out-variant op ``lidu_fused_batch_get_prepare_mtp_out``
 20 tensors and four integers in the reference's order, the six outputs returned. The
 tensor checks mirror the reference host op (:41-190) and raise ValueError. The work is
 enqueued on torch's current stream of the tensors' device through ``kvip_hip_lidu``
-(libkvip_hip.so); the per-batch workspace is allocated once per (device, batch) and
-reused, so the call can be captured in a CUDA graph after a first eager call.
+(libkvip_hip.so).
+
+Workspace: the kernels need per-request scratch (kvip_hip_lidu_workspace_bytes). It comes
+from the caller (``workspace=``), from the device's reserved buffer (``lidu_reserve(device,
+max_batch)`` at bind time: one buffer serves every batch up to max_batch), or, for an
+eager call with neither, from a buffer the module grows on first use. A call under hipGraph
+capture never allocates: without a caller or reserved workspace large enough it raises.
 
 `lidu_prepare` is the allocating variant ``lidu_fused_batch_get_prepare_mtp`` (:272-300).
+
+`register_torch_ops()` (run when this module is imported) defines the reference's two
+operators in the ``nanovllm_dsa`` namespace with the reference's schemas (:374-399), for
+callers that look them up as ``torch.ops.nanovllm_dsa.*`` (the reference's harness,
+tests/operators/lifetch/support/execution.py:678-683): the CUDA (HIP) kernels are this
+module's `lidu` / `lidu_prepare`, and the Meta kernels give the output shapes for tracing
+(as the reference's Meta implementation does, :320-372).
 """
 from __future__ import annotations
 
@@ -26,7 +38,7 @@ PROFILE_LANES = 8
 PROFILE_FIELDS = 32
 INT32_MAX = (1 << 31) - 1
 
-_WORKSPACES = {}
+_WORKSPACES = {}  # device -> int32 workspace tensor (reserved or grown eagerly)
 
 
 def _torch():
@@ -35,14 +47,38 @@ def _torch():
     return torch
 
 
-def _workspace(torch, lib, device, batch):
-    key = (str(device), batch)
-    ws = _WORKSPACES.get(key)
-    if ws is None:
-        nbytes = int(lib.kvip_hip_lidu_workspace_bytes(batch))
-        ws = torch.empty(nbytes // 4, dtype=torch.int32, device=device)
-        _WORKSPACES[key] = ws
+def workspace_bytes(batch):
+    """Bytes of LIDU workspace a batch of `batch` requests needs."""
+    return int(abi.load_library().kvip_hip_lidu_workspace_bytes(int(batch)))
+
+
+def lidu_reserve(device, max_batch):
+    """Allocate (once) the device's LIDU workspace for batches of up to `max_batch`
+    requests, so that later calls, captured ones included, allocate nothing. Returns it."""
+    torch = _torch()
+    device = abi.device_of(torch, device)
+    nbytes = workspace_bytes(max_batch)
+    ws = _WORKSPACES.get(str(device))
+    if ws is None or ws.numel() * 4 < nbytes:
+        ws = torch.empty((nbytes + 3) // 4, dtype=torch.int32, device=device)
+        _WORKSPACES[str(device)] = ws
     return ws
+
+
+def _workspace(torch, device, batch, workspace):
+    need = workspace_bytes(batch)
+    if workspace is not None:
+        if (workspace.dtype != torch.int32 or workspace.device != device or not workspace.is_contiguous()
+                or workspace.numel() * 4 < need):
+            raise ValueError(f"lidu: workspace must be a contiguous int32 tensor of at least {need} bytes on {device}")
+        return workspace
+    ws = _WORKSPACES.get(str(device))
+    if ws is not None and ws.numel() * 4 >= need:
+        return ws
+    if torch.cuda.is_current_stream_capturing():
+        raise RuntimeError(f"lidu: no workspace of {need} bytes is reserved for this batch on {device}; call "
+                           f"kvip_amd.lidu_reserve(device, max_batch) before capture or pass workspace=")
+    return lidu_reserve(device, batch)
 
 
 def _check_inputs(torch, topk, query_ends, pool_entries, t2s, s2t, cursors, cache_tokens, candidate_lens,
@@ -108,10 +144,11 @@ def _check_outputs(torch, topk, batch, dest, counts, indices, offsets, output_in
 def lidu(topk_indices, actual_seq_lengths_query, req_pool_entries, token_to_slot_pool, slot_to_token_pool,
          eviction_cursors, cache_tokens, candidate_lens, miss_slots, miss_slot_bitmap, resident_block_table,
          logical_seq_lengths, profile_enabled, destination_slots, miss_counts, indices, offsets, output_indices,
-         resident_seq_lengths, profiling, layer_id, num_layers, max_num_reqs, qcap):
+         resident_seq_lengths, profiling, layer_id, num_layers, max_num_reqs, qcap, *, workspace=None):
     """Run the LIDU transaction; token_to_slot_pool, slot_to_token_pool, eviction_cursors and the
     outputs are written in place. Returns (destination_slots, miss_counts, indices, offsets,
-    output_indices, resident_seq_lengths)."""
+    output_indices, resident_seq_lengths). workspace: an optional caller-owned int32 tensor of
+    at least workspace_bytes(B) bytes."""
     torch = _torch()
     batch, packed = _check_inputs(
         torch, topk_indices, actual_seq_lengths_query, req_pool_entries, token_to_slot_pool, slot_to_token_pool,
@@ -121,7 +158,7 @@ def lidu(topk_indices, actual_seq_lengths_query, req_pool_entries, token_to_slot
                    resident_seq_lengths, profiling)
     lib = abi.load_library()
     device = abi.device_of(torch, topk_indices.device)
-    ws = _workspace(torch, lib, device, batch)
+    ws = _workspace(torch, device, batch, workspace)
     p = abi.ptr
     args = abi.LiduArgs(
         topk=p(topk_indices), actual_seq_lengths_query=p(actual_seq_lengths_query),
@@ -158,3 +195,58 @@ def lidu_prepare(topk_indices, actual_seq_lengths_query, req_pool_entries, token
     return lidu(topk_indices, actual_seq_lengths_query, req_pool_entries, token_to_slot_pool, slot_to_token_pool,
                 eviction_cursors, cache_tokens, candidate_lens, miss_slots, miss_slot_bitmap, resident_block_table,
                 logical_seq_lengths, profile_enabled, *outs, profiling, layer_id, num_layers, max_num_reqs, qcap)
+
+
+# The reference operators' schemas (lidu_fused_batch_get_prepare_mtp_ops.cpp:374-399).
+_SCHEMA = (
+    "lidu_fused_batch_get_prepare_mtp(Tensor topk_indices, Tensor actual_seq_lengths_query, "
+    "Tensor req_pool_entries, Tensor(a!) token_to_slot_pool, Tensor(b!) slot_to_token_pool, "
+    "Tensor(c!) eviction_cursors, Tensor cache_tokens, Tensor candidate_lens, Tensor miss_slots, "
+    "Tensor miss_slot_bitmap, Tensor resident_block_table, Tensor logical_seq_lengths, Tensor profile_enabled, "
+    "int layer_id, int num_layers, int max_num_reqs, int qcap) -> (Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)")
+_SCHEMA_OUT = (
+    "lidu_fused_batch_get_prepare_mtp_out(Tensor topk_indices, Tensor actual_seq_lengths_query, "
+    "Tensor req_pool_entries, Tensor(a!) token_to_slot_pool, Tensor(b!) slot_to_token_pool, "
+    "Tensor(c!) eviction_cursors, Tensor cache_tokens, Tensor candidate_lens, Tensor miss_slots, "
+    "Tensor miss_slot_bitmap, Tensor resident_block_table, Tensor logical_seq_lengths, Tensor profile_enabled, "
+    "Tensor(d!) destination_slots, Tensor(e!) miss_counts, Tensor(f!) indices, Tensor(g!) offsets, "
+    "Tensor(h!) output_indices, Tensor(i!) resident_seq_lengths, Tensor(j!) profiling, int layer_id, "
+    "int num_layers, int max_num_reqs, int qcap) -> (Tensor(d!), Tensor(e!), Tensor(f!), Tensor(g!), "
+    "Tensor(h!), Tensor(i!))")
+_TORCH_LIBRARY = None
+
+
+def _prepare_meta(topk_indices, actual_seq_lengths_query, *rest):
+    torch = _torch()
+    batch = actual_seq_lengths_query.shape[0]
+    cap = batch * MISS_CAPACITY
+    dev = topk_indices.device
+    return (torch.empty(topk_indices.shape, dtype=torch.int32, device=dev),
+            torch.empty(batch + 1, dtype=torch.int32, device=dev), torch.empty(cap, dtype=torch.int32, device=dev),
+            torch.empty(cap, dtype=torch.int32, device=dev), torch.empty(cap, dtype=torch.int32, device=dev),
+            torch.empty(batch, dtype=torch.int32, device=dev))
+
+
+def _out_meta(*args):
+    return tuple(args[13:19])
+
+
+def register_torch_ops():
+    """Define nanovllm_dsa::lidu_fused_batch_get_prepare_mtp and _out with the reference's
+    schemas, with CUDA (HIP) and Meta kernels. Idempotent."""
+    global _TORCH_LIBRARY
+    if _TORCH_LIBRARY is not None:
+        return _TORCH_LIBRARY
+    torch = _torch()
+    lib = torch.library.Library("nanovllm_dsa", "FRAGMENT")
+    lib.define(_SCHEMA)
+    lib.define(_SCHEMA_OUT)
+    lib.impl("lidu_fused_batch_get_prepare_mtp", lidu_prepare, "CUDA")
+    lib.impl("lidu_fused_batch_get_prepare_mtp_out", lidu, "CUDA")
+    lib.impl("lidu_fused_batch_get_prepare_mtp", _prepare_meta, "Meta")
+    lib.impl("lidu_fused_batch_get_prepare_mtp_out", _out_meta, "Meta")
+    _TORCH_LIBRARY = lib
+    return lib
+
+
+register_torch_ops()

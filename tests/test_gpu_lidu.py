@@ -191,3 +191,44 @@ def test_lidu_prepare_allocating_variant(torch_gpu):
         if k in ("indices", "offsets", "output_indices"):
             got, want = got[:total], want[:total]
         assert np.array_equal(got, want), k
+
+
+def test_torch_op_out_variant_in_a_graph_matches_oracle(torch_gpu):
+    """torch.ops.nanovllm_dsa.lidu_fused_batch_get_prepare_mtp_out (the registered operator the
+    reference's harness looks up) with the workspace reserved at bind time: captured in a
+    hipGraph before any eager call, then replayed on fresh TopK rows; every replay is checked
+    against the oracle run on the previous round's state."""
+    torch = torch_gpu
+    case = lc.random_case(21, queries=(4, 1, 3), hot_tokens=5000, hit_share=0.6, budget=8192, cand=60000)
+    rng = np.random.default_rng(9)
+    dev = upload(torch, case)
+    outs = device_outputs(torch, case)
+    batch = len(case["actual_seq_lengths_query"])
+    kvip_amd.lidu_reserve("cuda", max_batch=8)
+    profiling = torch.zeros((batch, 8, 32), dtype=torch.int64, device="cuda")
+    op = torch.ops.nanovllm_dsa.lidu_fused_batch_get_prepare_mtp_out
+    args = [dev[k] for k in lc.INPUTS] + [outs[k] for k in lc.OUTPUTS] + [profiling, case["layer_id"],
+                                                                          case["num_layers"], case["max_num_reqs"],
+                                                                          case["qcap"]]
+    graph = torch.cuda.CUDAGraph()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            res = op(*args)
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    assert all(r.data_ptr() == outs[k].data_ptr() for r, k in zip(res, lc.OUTPUTS))
+    for i in range(3):
+        for q in range(case["topk"].shape[0]):
+            r = int(np.searchsorted(case["actual_seq_lengths_query"], q, side="right"))
+            case["topk"][q, 0] = rng.choice(int(case["candidate_lens"][r]), 2048, replace=False)
+        dev["topk"].copy_(torch.from_numpy(case["topk"]))
+        expect_state, expect = lc.run_oracle(case)
+        for k, v in lc.empty_outputs(case["topk"].shape[0], batch).items():
+            outs[k].copy_(torch.from_numpy(v))
+        graph.replay()
+        torch.cuda.synchronize()
+        compare(dev, outs, expect_state, expect, f"op replay{i}")
+        for k in lc.STATE:
+            case[k] = expect_state[k]

@@ -1,5 +1,10 @@
 """GPU parity at the BASELINE configurations' own shapes, through the C ABI.
 
+C1  batch 4, ctx 4096, bf16 Q/K, fp32 weights, no scales (the bench's c1 workload): the
+    decode forward end to end. Every row scored by the oracle (1e-2 relative, > 99 %
+    identical keys), TopK bit-exact against the oracle's TopK of the GPU's keys and inside
+    the oracle's one-ulp cutoff band; the GPU TopK fed the oracle's own keys bit-exact
+    against the oracle's TopK; the gather byte-exact.
 C2  batch 64, ctx U[8192, 32768], fp8 (the bench workload, same seed): the decode forward;
     every row's TopK bit-exact against the oracle's TopK of the GPU's keys, both single pass
     and in the reference's trunk-merge order for this batch (trunk 8192: more than 16
@@ -44,6 +49,48 @@ def assert_close_row(got, want, rtol, what):
     w = ref.score_values(want).astype(np.float64)
     bad = np.abs(g - w) > rtol * np.abs(w) + rtol * np.abs(w).max()
     assert not bad.any(), f"{what}: {int(bad.sum())} scores outside rtol {rtol}"
+
+
+def test_c1_end_to_end_against_oracle(torch_gpu):
+    torch = torch_gpu
+    import ctypes
+    from kvip_amd.runtime import abi
+
+    say("case C1 batch 4 ctx 4096 bf16 (bench c1 workload)")
+    wl = synthetic.config_workload(torch, "c1", "cuda", seed=2026)
+    rot, upd, fwd = synthetic.bind(torch, kvip_amd, wl)
+    fwd()
+    torch.cuda.synchronize()
+    assert int(rot.status.item()) == 0
+    keys = rot.score_keys.cpu().numpy().view(np.uint16)
+    topk = rot.topk.cpu().numpy()
+    table = wl.block_table.cpu().numpy()
+    q = wl.query.float().cpu().numpy()
+    w = wl.weights.float().cpu().numpy()
+    want_keys = np.zeros_like(keys)
+    for r, v in enumerate(wl.ctx):
+        v = int(v)
+        k = rows_of_pages(torch, wl.keys.float(), table[r], v)
+        want = ref.li_keys(q[r], k, w[r], None, None)
+        want_keys[r, :v] = want
+        assert_close_row(keys[r, :v], want, 1e-2, f"row {r}")
+        assert np.array_equal(topk[r], ref.topk_reference(keys[r], v)), r
+        assert ref.validate_topk_band(topk[r], ref.score_values(want)), r
+    same = ref.identical_share(keys, want_keys, [int(v) for v in wl.ctx])
+    say(f"  identical keys: {same:.5f}")
+    assert same > 0.99
+    say("  gather of the 4 rows")
+    assert np.array_equal(upd.output.cpu().numpy(), ref.fetch_gather(wl.kv_cache.cpu().numpy(), table, topk))
+    say("  TopK fed the oracle's keys")
+    rot.score_keys.copy_(torch.from_numpy(want_keys.view(np.int16)))
+    rot.topk.fill_(-5)
+    args = rot.topk_args(use_histogram=False)
+    abi.check(abi.load_library().kvip_hip_topk(ctypes.byref(args), abi.stream_handle(torch, rot.device)), "topk")
+    torch.cuda.synchronize()
+    got = rot.topk.cpu().numpy()
+    for r, v in enumerate(wl.ctx):
+        assert np.array_equal(got[r], ref.topk_reference(want_keys[r], int(v))), r
+    assert int(rot.status.item()) == 0
 
 
 def test_c2_full_shape_against_oracle(torch_gpu):
