@@ -44,11 +44,18 @@ def parse():
     p.add_argument("--seed", type=int, default=2026)
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU-baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-mtp", action="store_true", help="skip the 4-rows-per-request (MTP) decode leg")
     p.add_argument("--no-lidu", action="store_true", help="skip the kvip.lidu timing leg")
     p.add_argument("--no-resident", action="store_true", help="skip the resident-cache round timing leg")
     p.add_argument("--no-prefill", action="store_true", help="skip the config-3 prefill timing leg")
     p.add_argument("--no-mixed", action="store_true", help="skip the config-5 mixed-round timing leg")
     p.add_argument("--no-sfa", action="store_true", help="skip the sparse-attention consumer timing leg")
+    p.add_argument("--only", default=None,
+                   help="run just this leg (mtp, lidu, resident, cache_ops, prefill, mixed, sfa) and print its JSON "
+                        "(profiling runs; no headline line)")
+    p.add_argument("--sequential", action="store_true",
+                   help="resident and mixed legs on one stream (Fetch after the Index update, prefill after the "
+                        "decode; no speculative-prefetch loop): each kernel runs alone, for per-kernel profiles")
     p.add_argument("--copy-calibration", action="store_true",
                    help="also run a plain 1 GiB device copy (for rocprof FETCH/WRITE_SIZE scaling)")
     return p.parse_args()
@@ -308,7 +315,7 @@ def cache_ops_leg(torch, kvip_amd, device, seed, iters=20):
     return out
 
 
-def resident_leg(torch, kvip_amd, device, seed, rounds=24, warm=4):
+def resident_leg(torch, kvip_amd, device, seed, rounds=24, warm=4, sequential=False):
     """BASELINE config 4 on the resident cache: 16 requests, history 131072, 16384 hot
     slots, misses fetched from a pinned host pool, the device LRU chains (one per request)
     committed by every round inside the graph. Two loops of consecutive rounds, each one
@@ -320,13 +327,15 @@ def resident_leg(torch, kvip_amd, device, seed, rounds=24, warm=4):
                three stages in sequence on one stream (`sequential_us_per_round`);
       forward: the whole resident forward (LI over 16 x 131072 Index rows, TopK-2048, the
                round, LRU commit) on query sets along a random walk (consecutive rounds
-               select overlapping, drifting positions)."""
+               select overlapping, drifting positions).
+    sequential: every loop on one stream (upd.overlap False) and no speculative-prefetch
+    loop (its prefix TopK runs on a forked stream)."""
     from kvip_amd import synthetic
 
     batch, history, resident = 16, 131072, 16384
     n = warm + rounds + 1  # + the eager round before capture
     rot, upd, fwd = synthetic.resident_workload(torch, kvip_amd, device, seed=seed, batch=batch,
-                                                history=history, resident=resident)
+                                                history=history, resident=resident, overlap=not sequential)
     rng = np.random.default_rng(seed)
     picks = torch.from_numpy(synthetic.resident_selections(torch, rng, steps=n, batch=batch, q_rows=1,
                                                            history=history, resident=resident)).to(device)
@@ -355,7 +364,7 @@ def resident_leg(torch, kvip_amd, device, seed, rounds=24, warm=4):
     trace.zero_()
     upd.overlap = False
     seq_us = _cursor_rounds(torch, round_body, warm, rounds, n)
-    upd.overlap = True
+    upd.overlap = not sequential
     if upd.status.any():
         raise RuntimeError(f"resident round failed: {upd.status.cpu().tolist()}")
     seq_miss = trace[warm:warm + rounds].sum(1).float().mean().item()
@@ -372,6 +381,20 @@ def resident_leg(torch, kvip_amd, device, seed, rounds=24, warm=4):
     if upd.status.any() or rot.status.any():
         raise RuntimeError(f"resident forward failed: {upd.status.cpu().tolist()} {int(rot.status.item())}")
     fwd_miss = trace[warm:warm + rounds].sum(1).float().mean().item()
+    out = {"workload": "c4 shape: 16 requests x 1 row, history 131072, resident 16384, misses fetched from pinned "
+                       "host memory, LRU chains committed in the graph; round: TopK rows drawn ~80% hot (Zipf 1.1), "
+                       "a fresh draw per round; forward: LI + TopK + round on query sets along a random walk",
+           "us_per_round": round(round_us, 2), "misses_per_round": round(round_miss, 1),
+           "sequential_us_per_round": round(seq_us, 2), "sequential_misses_per_round": round(seq_miss, 1),
+           "hit_fraction": round(1.0 - round_miss / (batch * TOPK), 4),
+           "fetch_gbs_lower_bound": round(round_miss * 656 / (round_us * 1e-6) / 1e9, 2),
+           "forward_us": round(fwd_us, 2), "forward_misses_per_round": round(fwd_miss, 1),
+           "forward_hit_fraction": round(1.0 - fwd_miss / (batch * TOPK), 4),
+           "forward_index_gbs": round(batch * history * 132 / (fwd_us * 1e-6) / 1e9, 1), "rounds": rounds,
+           "streams": "one" if sequential else "Fetch beside the Index update"}
+    if sequential:
+        return out
+    del rot, upd, fwd, picks, picks_now  # the second workload reuses the first one's pinned pool block
 
     # The same forward loop with the speculative windowed prefetch (default budgets), on a
     # fresh copy of the workload so that both loops start from the same state.
@@ -391,20 +414,10 @@ def resident_leg(torch, kvip_amd, device, seed, rounds=24, warm=4):
     if upd2.status.any() or rot2.status.any():
         raise RuntimeError(f"resident prefetch forward failed: {upd2.status.cpu().tolist()}")
     pf_trace = trace2[warm:warm + rounds].sum(2).float().mean(0).tolist()
-    host_gbs = host_read_gbs(torch, device)
-    return {"workload": "c4 shape: 16 requests x 1 row, history 131072, resident 16384, misses fetched from pinned "
-                        "host memory, LRU chains committed in the graph; round: TopK rows drawn ~80% hot (Zipf 1.1), "
-                        "a fresh draw per round; forward: LI + TopK + round on query sets along a random walk",
-            "us_per_round": round(round_us, 2), "misses_per_round": round(round_miss, 1),
-            "sequential_us_per_round": round(seq_us, 2), "sequential_misses_per_round": round(seq_miss, 1),
-            "hit_fraction": round(1.0 - round_miss / (batch * TOPK), 4),
-            "fetch_gbs_lower_bound": round(round_miss * 656 / (round_us * 1e-6) / 1e9, 2),
-            "host_read_ceiling_gbs": round(host_gbs, 1),
-            "forward_us": round(fwd_us, 2), "forward_misses_per_round": round(fwd_miss, 1),
-            "forward_hit_fraction": round(1.0 - fwd_miss / (batch * TOPK), 4),
-            "forward_index_gbs": round(batch * history * 132 / (fwd_us * 1e-6) / 1e9, 1),
-            "prefetch_forward_us": round(pf_us, 2), "prefetch_final_misses_per_round": round(pf_trace[0], 1),
-            "prefetched_per_round": round(pf_trace[1], 1), "rounds": rounds}
+    out.update({"host_read_ceiling_gbs": round(host_read_gbs(torch, device), 1),
+                "prefetch_forward_us": round(pf_us, 2), "prefetch_final_misses_per_round": round(pf_trace[0], 1),
+                "prefetched_per_round": round(pf_trace[1], 1)})
+    return out
 
 
 def prefill_leg(torch, kvip_amd, device, seed, iters=5):
@@ -576,7 +589,7 @@ def sfa_leg(torch, kvip_amd, device, seed, iters=20):
     return out
 
 
-def mixed_leg(torch, kvip_amd, device, seed, rounds=20, warm=4):
+def mixed_leg(torch, kvip_amd, device, seed, rounds=20, warm=4, sequential=False):
     """one continuous-batching round captured as a single hipGraph:
     Index ingest of all new tokens (32 decode + 2048 + 1536 prefill rows), resident decode
     LIFetch for 32 requests (ctx ~U[4096, 65536], 16384 hot slots, misses from pinned host
@@ -586,7 +599,7 @@ def mixed_leg(torch, kvip_amd, device, seed, rounds=20, warm=4):
     walk (overlapping, drifting selections) and records its misses."""
     from kvip_amd import synthetic
 
-    wl = synthetic.mixed_workload(torch, kvip_amd, device, seed=seed, lru=True)
+    wl = synthetic.mixed_workload(torch, kvip_amd, device, seed=seed, lru=True, overlap=not sequential)
     rnd = wl.round
     nd = len(wl.decode_ctx)
     n = warm + rounds + 1
@@ -613,7 +626,89 @@ def mixed_leg(torch, kvip_amd, device, seed, rounds=20, warm=4):
             "us_per_round": round(us, 1), "decode_rows": nd, "prefill_rows": pf_rows,
             "rows_per_s": round((nd + pf_rows) / (us * 1e-6), 1),
             "decode_misses_per_round": round(miss, 1),
-            "decode_hit_fraction": round(1.0 - miss / (nd * TOPK), 4), "rounds": rounds}
+            "decode_hit_fraction": round(1.0 - miss / (nd * TOPK), 4), "rounds": rounds,
+            "streams": "one" if sequential else "prefill beside the decode, Fetch beside the Index update"}
+
+
+def _stage_times(torch, pairs, per_graph=8, reps=25):
+    """Per-stage device times of the three-launch round, in ms per round: graphs of
+    `per_graph` back-to-back calls alternating over the `pairs` (LIFetch forwards of the two
+    input sets), timed with HIP events on the launch stream. Scoring from score-only graphs,
+    TopK as score+TopK minus scoring, the gather as the whole round minus score+TopK."""
+    stream = torch.cuda.current_stream()
+    side = torch.cuda.Stream()
+    side.wait_stream(stream)
+    with torch.cuda.stream(side):
+        for f in pairs:
+            f()
+    stream.wait_stream(side)
+    torch.cuda.synchronize()
+
+    def graph_of(calls):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for j in range(per_graph):
+                calls[j % 2]()
+        return g
+
+    def ms(g):
+        for _ in range(3):
+            g.replay()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            g.replay()
+        e1.record(stream)
+        e1.synchronize()
+        return e0.elapsed_time(e1) / (reps * per_graph)
+
+    full = ms(graph_of(pairs))
+    score = ms(graph_of([f.score for f in pairs]))
+    for f in pairs:
+        f.rotating.histogram.zero_()  # score-only replays keep adding to the histograms
+    score_topk = ms(graph_of([lambda f=f: (f.score(), f.select()) for f in pairs]))
+    return {"round": full, "indexer": score, "topk": score_topk - score, "fetch": full - score_topk}
+
+
+def mtp_leg(torch, kvip_amd, device, seed):
+    """The decode step as the vLLM selector runs it: 4 query rows per request (the MTP rows,
+    python/kvip/adapters/vllm/inputs.py:11), at config-2 sizes (64 requests, ctx U[8192,
+    32768], fp8, 64 heads, key scales, 656-byte KV rows). Row q of request b sees its first
+    ctx_b - 3 + q tokens. Every index-K tile of a request is read once and scored for its 4
+    rows, so a tile carries 4 x 2 x 64 x 128 flops per token against 132 bytes (496 flop/B
+    against MI355X's fp8 ridge of 625 flop/B: HBM-bound, with the MFMA roof 1.26x away). Bytes
+    count each index-K row once per request; the gather moves 4 x 2048 rows per request."""
+    from kvip_amd import synthetic
+
+    sets = []
+    for k in range(2):
+        wl = synthetic.decode_workload(torch, batch=64, ctx_low=8192, ctx_high=32768, device=device, qk="fp8",
+                                       key_scale=True, rows_per_request=4, seed=seed + k, max_context=32768)
+        ends = np.stack([wl.ctx - 3 + q for q in range(4)], axis=1).reshape(-1)
+        sets.append((wl, *synthetic.bind(torch, kvip_amd, wl, query_ends=ends)))
+    heads = int(sets[0][0].query.shape[1])
+    per = [algorithmic_bytes(w, heads, False) for w, *_ in sets]
+    mean = {k: (per[0][k] + per[1][k]) / 2 for k in per[0]}
+    flops = float(np.mean([2 * heads * 128 * (np.minimum(w.ctx[:, None], np.stack([w.ctx - 3 + q for q in range(4)], 1))
+                                             .sum()) for w, *_ in sets]))
+    t = _stage_times(torch, [f for *_, f in sets])
+    for w, r, u, f in sets:
+        if int(r.status.item()) != 0:
+            raise RuntimeError(f"MTP leg: device status {int(r.status.item())}")
+    score_s = t["indexer"] * 1e-3
+    hbm = mean["indexer"] / score_s / 1e9
+    tflops = flops / score_s / 1e12
+    step_bytes = sum(mean.values())
+    rows = 64 * 4
+    return {"workload": "c2 sizes with 4 MTP rows per request: 64 requests x 4 rows, ctx U[8192,32768], fp8, "
+                        "64 heads x 128, key scales, KV rows 656 B, row q sees ctx - 3 + q tokens",
+            "us_per_step": round(t["round"] * 1e3, 2), "queries_per_s": round(rows / (t["round"] * 1e-3), 1),
+            "hbm_frac_step": round(step_bytes / (t["round"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "kernels_us": {k: round(v * 1e3, 2) for k, v in t.items() if k != "round"},
+            "step_bytes": int(step_bytes), "score_flops": int(flops),
+            "score_roofline": {"bound": "hbm", "achieved": round(hbm, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                               "frac": round(hbm / HBM_PEAK_GBS, 4),
+                               "mfma_tflops": round(tflops, 1), "mfma_frac": round(tflops / FP8_MFMA_PEAK_TFLOPS, 4)}}
 
 
 def main():
@@ -629,6 +724,20 @@ def main():
 
     device = "cuda:0"
     torch.cuda.set_device(0)
+    only_legs = {"mtp": lambda: mtp_leg(torch, kvip_amd, device, args.seed),
+                 "lidu": lambda: lidu_leg(torch, kvip_amd, device, args.seed),
+                 "resident": lambda: resident_leg(torch, kvip_amd, device, args.seed, sequential=args.sequential),
+                 "cache_ops": lambda: cache_ops_leg(torch, kvip_amd, device, args.seed),
+                 "prefill": lambda: prefill_leg(torch, kvip_amd, device, args.seed),
+                 "mixed": lambda: mixed_leg(torch, kvip_amd, device, args.seed, sequential=args.sequential),
+                 "sfa": lambda: sfa_leg(torch, kvip_amd, device, args.seed)}
+    if args.only is not None:
+        if args.only not in only_legs:
+            raise SystemExit(f"--only: unknown leg {args.only!r} ({', '.join(only_legs)})")
+        print(f"bench: {args.only} leg starts", file=sys.stderr, flush=True)
+        print(json.dumps({"leg": args.only, args.only: only_legs[args.only]()}), flush=True)
+        print(f"bench: {args.only} leg done", file=sys.stderr, flush=True)
+        return
     # Two independent input sets, alternated step by step: a step touches ~346 MB and
     # MI355X's 256 MB Infinity Cache would otherwise keep part of the same inputs
     # between consecutive steps, so every step streams its inputs from HBM.
@@ -778,11 +887,14 @@ def main():
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(dominant) if args.config == "c2" else None},
     }
-    legs = [("lidu", args.no_lidu, lambda: lidu_leg(torch, kvip_amd, device, args.seed)),
-            ("resident", args.no_resident, lambda: resident_leg(torch, kvip_amd, device, args.seed)),
+    legs = [("mtp", args.no_mtp, lambda: mtp_leg(torch, kvip_amd, device, args.seed)),
+            ("lidu", args.no_lidu, lambda: lidu_leg(torch, kvip_amd, device, args.seed)),
+            ("resident", args.no_resident, lambda: resident_leg(torch, kvip_amd, device, args.seed,
+                                                                sequential=args.sequential)),
             ("cache_ops", args.no_resident, lambda: cache_ops_leg(torch, kvip_amd, device, args.seed)),
             ("prefill", args.no_prefill, lambda: prefill_leg(torch, kvip_amd, device, args.seed)),
-            ("mixed", args.no_mixed, lambda: mixed_leg(torch, kvip_amd, device, args.seed)),
+            ("mixed", args.no_mixed, lambda: mixed_leg(torch, kvip_amd, device, args.seed,
+                                                       sequential=args.sequential)),
             ("sfa", args.no_sfa, lambda: sfa_leg(torch, kvip_amd, device, args.seed)),
             ("cpu_baseline", args.no_cpu_baseline, lambda: cpu_baseline(torch, wl, rot, args.cpu_seconds))]
     print(f"bench: decode steps done ({result['ms_per_step']} ms/step)", file=sys.stderr, flush=True)

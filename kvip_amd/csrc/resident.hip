@@ -421,6 +421,290 @@ __global__ __launch_bounds__(kRsThreads) void resident_resolve_kernel(const Kvip
     }
 }
 
+// The resolve of a request with one query row (the plain decode step): the same outcome
+// as resident_resolve_kernel, with the row's first occurrences and miss ranks kept in an
+// LDS hash set of its tokens instead of the workspace tables, and every global value the
+// resolve needs (hot_valid, reserved, the LRU candidates, the tokens' KV addresses and
+// logical ids) requested together at the start: one round trip to memory instead of a chain
+// of them.
+constexpr int kHashSlots = 2 * kTopK;  // at most kTopK keys: load factor <= 1/2
+
+KVIP_DEVICE uint32_t token_hash(int t) { return (static_cast<uint32_t>(t) * 0x9E3779B9u) >> 20; }  // 12 bits
+
+__global__ __launch_bounds__(kRsThreads) void resident_resolve_one_kernel(const KvipResidentArgs p) {
+    static_assert(kHashSlots == 4096, "12-bit token hash");
+    __shared__ int32_t s_slots[kTopK];             // slot of each miss rank
+    __shared__ int32_t s_ord[kTopK];               // its candidate ordinal (reserved_hot of the slot), or -1
+    __shared__ uint32_t s_bitmap[kMaxWords];       // protected or allocated hot slots
+    __shared__ int32_t s_hkey[kHashSlots];         // tokens of the row's unresolved entries
+    __shared__ uint32_t s_hfirst[kHashSlots];      // lowest entry index of each token
+    __shared__ int32_t s_hrank[kHashSlots];        // miss rank of each token
+    __shared__ uint32_t s_wave[kRsThreads / 64];
+    __shared__ uint32_t s_err;
+    __shared__ int s_dest;
+
+    const int b = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int R = p.resident;
+    const int H = p.history;
+    const int words = (R + 31) / 32;
+    const int o = p.row_owners[b];
+    const bool good_owner = owner_ok(p, o);
+    const int oo = good_owner ? o : 0;
+    const int32_t* reserved = p.reserved_hot + static_cast<size_t>(b) * R;
+    const int32_t* lru = p.lru_slots + static_cast<size_t>(b) * kLru;
+    const int32_t* hot_valid = p.hot_valid + static_cast<size_t>(oo) * R;
+    const Tail tail = tail_of(p, b);
+    const bool prefetched = p.prefetch_counts != nullptr;
+    const int used = prefetched ? p.prefetch_counts[b] : p.used;
+    const int32_t* pmap = workspace_of(p).map + static_cast<size_t>(b) * H;
+    const int nchg = kLru + kTopK;
+
+    // Entries i = 2 tid + k, and every global value they need, requested at once.
+    int tok[2], cand[2], hv[2], rsv[2], pk[2];
+    int64_t addr[2], logical[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int i = 2 * tid + k;
+        const int t = p.topk[static_cast<size_t>(b) * kTopK + i];
+        tok[k] = t;
+        cand[k] = lru[i];
+        const bool in = good_owner && t >= 0 && t < H;
+        const int tc = in ? t : 0;
+        const int th = in && t < R ? t : 0;
+        hv[k] = hot_valid[th];
+        rsv[k] = reserved[th];
+        pk[k] = prefetched ? pmap[tc] : -1;
+        addr[k] = p.addresses[static_cast<size_t>(oo) * H + tc];
+        logical[k] = p.logical_ids[static_cast<size_t>(oo) * H + tc];
+    }
+    for (int w = tid; w < words; w += kRsThreads) s_bitmap[w] = 0u;
+    for (int h = tid; h < kHashSlots; h += kRsThreads) {
+        s_hkey[h] = -1;
+        s_hfirst[h] = kNoFirst;
+    }
+    if (tid == 0) {
+        s_err = static_cast<uint32_t>(p.status[b]) | (good_owner && tail.ok ? 0u : static_cast<uint32_t>(KVIP_RESIDENT_ERR_TOKEN));
+        s_dest = -1;
+    }
+    __syncthreads();
+
+    // Classification (as resident_resolve_kernel's, one row).
+    int loc[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int t = tok[k];
+        loc[k] = -1;
+        if (t >= H) {
+            atomicOr(&s_err, KVIP_RESIDENT_ERR_TOKEN);
+        } else if (good_owner && t >= 0) {
+            const bool in_tail = t >= tail.begin && t < tail.end;
+            if (in_tail && t < tail.mapped) {
+                loc[k] = R + t % tail.ring;
+            } else if (!in_tail && t < R && hv[k] != 0 && rsv[k] < 0) {
+                loc[k] = t;
+                atomicOr(&s_bitmap[t >> 5], 1u << (t & 31));
+            } else if (prefetched) {
+                const int s = pk[k] >= 0 && pk[k] < used ? lru[pk[k]] : -1;
+                if (s >= 0 && s < R) {
+                    loc[k] = s;
+                    atomicOr(&s_bitmap[s >> 5], 1u << (s & 31));
+                }
+            }
+        }
+    }
+    // (a) first occurrence of every unresolved token (LDS hash set, linear probing).
+    bool unresolved[2];
+    int slot_of[2] = {0, 0};
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int t = tok[k];
+        unresolved[k] = t >= 0 && t < H && loc[k] < 0;
+        if (unresolved[k]) {
+            uint32_t h = token_hash(t);
+            for (int probe = 0; probe < kHashSlots; ++probe) {
+                const int prev = atomicCAS(&s_hkey[h], -1, t);
+                if (prev == -1 || prev == t) break;
+                h = (h + 1) & (kHashSlots - 1);
+            }
+            slot_of[k] = static_cast<int>(h);
+            atomicMin(&s_hfirst[h], static_cast<uint32_t>(2 * tid + k));
+        }
+    }
+    __syncthreads();
+    const bool run = s_err == 0u;  // uniform: read after a barrier
+    int need = 0;
+    bool fresh[2] = {false, false};
+    if (run) {
+        // (b) new misses in index order -> ranks.
+        uint32_t nnew = 0;
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            fresh[k] = unresolved[k] && s_hfirst[slot_of[k]] == static_cast<uint32_t>(2 * tid + k);
+            nnew += fresh[k] ? 1u : 0u;
+        }
+        uint32_t need_u;
+        uint32_t r = block_exclusive_scan(nnew, s_wave, &need_u);
+        need = static_cast<int>(need_u);
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            if (fresh[k]) s_hrank[slot_of[k]] = static_cast<int32_t>(r++);
+        }
+        // (c) slots: free candidates in ordinal order, pass 0 = ordinals >= used.
+        int allocated = 0;
+        if (need > 0) {
+            for (int pass = 0; pass < 2 && allocated < need; ++pass) {
+                bool ok[2];
+                uint32_t avail = 0;
+#pragma unroll
+                for (int k = 0; k < 2; ++k) {
+                    const int ord = 2 * tid + k;
+                    const int s = cand[k];
+                    ok[k] = false;
+                    if ((ord >= used) == (pass == 0)) {
+                        if (s < 0 || s >= R) {
+                            atomicOr(&s_err, KVIP_RESIDENT_ERR_CANDIDATE);
+                        } else {
+                            ok[k] = ((s_bitmap[s >> 5] >> (s & 31)) & 1u) == 0u;
+                        }
+                    }
+                    avail += ok[k] ? 1u : 0u;
+                }
+                uint32_t n_avail;
+                uint32_t rank = block_exclusive_scan(avail, s_wave, &n_avail);
+                const int take = min(static_cast<int>(n_avail), need - allocated);
+#pragma unroll
+                for (int k = 0; k < 2; ++k) {
+                    if (ok[k]) {
+                        if (rank < static_cast<uint32_t>(take)) {
+                            // reserved_hot of a candidate's slot is its ordinal (round init)
+                            s_slots[allocated + rank] = cand[k];
+                            s_ord[allocated + rank] = 2 * tid + k;
+                        }
+                        ++rank;
+                    }
+                }
+                __syncthreads();
+                for (int j = tid; j < take; j += kRsThreads) {
+                    const int s = s_slots[allocated + j];
+                    atomicOr(&s_bitmap[s >> 5], 1u << (s & 31));
+                }
+                allocated += take;
+                __syncthreads();
+            }
+            if (allocated < need && s_err == 0u) {
+                // Fallback: every known slot is protected, then the free hot slots in
+                // ascending order (none is a candidate's: every free candidate was taken).
+#pragma unroll
+                for (int k = 0; k < 2; ++k) {
+                    if (loc[k] >= 0 && loc[k] < R) atomicOr(&s_bitmap[loc[k] >> 5], 1u << (loc[k] & 31));
+                }
+                __syncthreads();
+                const int per = (words + kRsThreads - 1) / kRsThreads;
+                const int w0 = min(tid * per, words);
+                const int w1 = min(w0 + per, words);
+                uint32_t free_bits = 0;
+                for (int w = w0; w < w1; ++w) {
+                    const int bits = min(32, R - 32 * w);
+                    const uint32_t live = bits == 32 ? 0xFFFFFFFFu : ((1u << bits) - 1u);
+                    free_bits += __popc(~s_bitmap[w] & live);
+                }
+                uint32_t n_free;
+                uint32_t rank = block_exclusive_scan(free_bits, s_wave, &n_free);
+                const int want = need - allocated;
+                if (n_free < static_cast<uint32_t>(want)) {
+                    if (tid == 0) atomicOr(&s_err, KVIP_RESIDENT_ERR_CANDIDATE);
+                } else {
+                    for (int w = w0; w < w1 && rank < static_cast<uint32_t>(want); ++w) {
+                        const int bits = min(32, R - 32 * w);
+                        const uint32_t live = bits == 32 ? 0xFFFFFFFFu : ((1u << bits) - 1u);
+                        uint32_t m = ~s_bitmap[w] & live;
+                        while (m != 0u && rank < static_cast<uint32_t>(want)) {
+                            const int bit = __ffs(m) - 1;
+                            s_slots[allocated + rank] = 32 * w + bit;
+                            s_ord[allocated + rank] = -1;
+                            ++rank;
+                            m &= m - 1u;
+                        }
+                    }
+                }
+                __syncthreads();
+                if (s_err == 0u) {
+                    for (int j = tid; j < want; j += kRsThreads) {
+                        const int s = s_slots[allocated + j];
+                        atomicOr(&s_bitmap[s >> 5], 1u << (s & 31));
+                    }
+                    allocated = need;
+                }
+                __syncthreads();
+            }
+        }
+        __syncthreads();
+        if (s_err == 0u) {
+            // (d) locations, change records and Fetch descriptors of the misses.
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                if (unresolved[k]) loc[k] = s_slots[s_hrank[slot_of[k]]];
+                if (fresh[k]) {
+                    const int rk = s_hrank[slot_of[k]];
+                    const int s = s_slots[rk];
+                    const int ord = s_ord[rk];
+                    const int rec = ord >= 0 ? ord : kLru + rk;
+                    p.change_slots[static_cast<size_t>(b) * nchg + rec] = s;
+                    p.changes[static_cast<size_t>(b) * nchg + rec] = tok[k];
+                    const size_t d = static_cast<size_t>(b) * kTopK + rk;
+                    const int64_t off = addr[k];
+                    if (off < 0 || off > p.host_pool_bytes - p.row_bytes || (off & 15) != 0) {
+                        atomicOr(&s_err, KVIP_RESIDENT_ERR_SOURCE);
+                    }
+                    p.fetch_slots[d] = s;
+                    p.fetch_positions[d] = tok[k];
+                    p.fetch_sources[d] = off;
+                }
+            }
+            if (tid == 0) p.miss_counts[b * 5] = need;
+        }
+        __syncthreads();
+    }
+
+    // Outputs (-1 throughout for a failed request) and the miss total; in token order as in
+    // resident_resolve_kernel.
+    const bool failed = s_err != 0u;
+    const bool tnd = p.unpack_indices != nullptr;
+    int dest = b;
+    if (tnd) {
+        const int rows = p.batch * kMaxQ;
+        for (int r = tid; r < rows; r += kRsThreads) {
+            const bool active = p.output_valid[r] != 0;
+            if (active && p.unpack_indices[r] == static_cast<int64_t>(b) * kMaxQ) s_dest = r;
+        }
+        for (int e = tid; e < kMaxQ * kTopK; e += kRsThreads) {
+            const int r = b * kMaxQ + e / kTopK;
+            if (p.output_valid[r] == 0) {
+                const size_t at = static_cast<size_t>(r) * kTopK + e % kTopK;
+                p.slot_output[at] = -1;
+                p.logical_output[at] = -1;
+            }
+        }
+        __syncthreads();
+        dest = s_dest;
+    }
+    if (dest >= 0) {
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const size_t at = static_cast<size_t>(dest) * kTopK + 2 * tid + k;
+            const int t = tok[k];
+            const bool live = !failed && t >= 0 && t < H;
+            p.slot_output[at] = live ? loc[k] : -1;
+            p.logical_output[at] = live ? static_cast<int32_t>(logical[k]) : -1;
+        }
+    }
+    if (tid == 0) {
+        p.miss_counts[b * 5 + 4] = failed ? 0 : need;
+        p.status[b] = static_cast<int32_t>(s_err);
+    }
+}
+
 // Speculative windowed prefetch of request b (one 1024-thread workgroup): the window
 // candidates in order, the first `available` of each window taken as the next ordinals.
 // Records go to prefetch_tokens / the ordinal change records / the workspace map; the
@@ -878,7 +1162,11 @@ hipError_t launch_resident_begin(const KvipResidentArgs& a, hipStream_t s, int32
 }
 
 hipError_t launch_resident_resolve(const KvipResidentArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL(resident_resolve_kernel, dim3(a.batch), dim3(kRsThreads), 0, s, a);
+    if (a.rows_per_request == 1) {
+        hipLaunchKernelGGL(resident_resolve_one_kernel, dim3(a.batch), dim3(kRsThreads), 0, s, a);
+    } else {
+        hipLaunchKernelGGL(resident_resolve_kernel, dim3(a.batch), dim3(kRsThreads), 0, s, a);
+    }
     return hipGetLastError();
 }
 

@@ -158,7 +158,7 @@ def _filled_pool(torch, gen, owners, history, resident, device):
 
 
 def mixed_workload(torch, kvip, device, *, seed=2026, decode_ctx=None, history=65536, resident=16384,
-                   prefill=((2048, 8192), (1536, 1536)), heads=64, lru=False, fill_pool=False):
+                   prefill=((2048, 8192), (1536, 1536)), heads=64, lru=False, fill_pool=False, overlap=True):
     """BASELINE config 5 round: decode requests (one row each, contexts `decode_ctx`, default
     32 requests ~U[4096, 65536]) on the resident cache (owner Index rows of `history`
     positions, `resident` hot slots, misses from a pinned host pool) plus prefill chunks
@@ -228,7 +228,8 @@ def mixed_workload(torch, kvip, device, *, seed=2026, decode_ctx=None, history=6
     ctx_t = torch.from_numpy(decode_ctx.astype(np.int32)).to(dev)
     rot.seq_lens.copy_(ctx_t)
     rot.query_ends.copy_(ctx_t)
-    upd = kvip.ResidentIndexUpdate(torch, keys=keys, scales=scales, addresses=addresses, logical_ids=logical,
+    upd = kvip.ResidentIndexUpdate(torch, overlap=overlap, keys=keys, scales=scales, addresses=addresses,
+                                   logical_ids=logical,
                                    row_owners=torch.arange(nd, dtype=torch.int32, device=dev), rotating=rot,
                                    hot_valid=valid, hot_cache=hot, host_pool=pool, resident=resident)
     chains = None
@@ -249,7 +250,8 @@ def mixed_workload(torch, kvip, device, *, seed=2026, decode_ctx=None, history=6
     pidx.bind(pf_query, pf_weights, pf_qscale, cache_keys, cache_scales, cu, kl, table)
     forward = kvip.LIFetch(rot, upd)
     rnd = kvip.MixedRound(torch, decode=forward, prefill=pidx, storage_keys=keys, storage_scales=scales,
-                          cache_keys=cache_keys, cache_scales=cache_scales, new_tokens=len(sources), lru=chains)
+                          cache_keys=cache_keys, cache_scales=cache_scales, new_tokens=len(sources), lru=chains,
+                          overlap=overlap)
     rnd.sources.copy_(torch.tensor(sources, dtype=torch.int64))
     rnd.targets.copy_(torch.tensor(targets, dtype=torch.int64))
     return SimpleNamespace(round=rnd, rot=rot, update=upd, forward=forward, prefill=pidx, lru=chains, keys=keys,
@@ -351,7 +353,7 @@ def lidu_workload(torch, device, *, seed=2026, batch=16, queries=4, budget=16384
 
 
 def resident_workload(torch, kvip, device, *, seed=2026, batch=16, history=131072, resident=16384, q_rows=1,
-                      heads=64, fill_pool=False, prefetch=None):
+                      heads=64, fill_pool=False, prefetch=None, overlap=True):
     """BASELINE config 4 shape for the resident-cache round: `batch` requests, each owning
     `history` Index rows (fp8 keys ~ random finite codes, scales U(0.5, 2)) and a hot
     cache of `resident` slots holding positions 0..resident-1; every row's KV lives in a
@@ -381,7 +383,7 @@ def resident_workload(torch, kvip, device, *, seed=2026, batch=16, history=13107
     upd = kvip.ResidentIndexUpdate(torch, keys=keys, scales=scales, addresses=addresses, logical_ids=logical,
                                    row_owners=torch.arange(batch, dtype=torch.int32, device=device), rotating=rot,
                                    hot_valid=valid, hot_cache=hot, host_pool=pool, resident=resident,
-                                   prefetch=prefetch)
+                                   prefetch=prefetch, overlap=overlap)
     return rot, upd, kvip.LIFetch(rot, upd)
 
 

@@ -154,14 +154,17 @@ def mtp_selection(rng, q_rows, history, resident, hot_frac, n=None, hot_pool=Non
     return out
 
 
-@pytest.mark.parametrize("batch,owners,q_rows,history,resident,seed", [
-    (2, 2, 1, 8192, 4096, 1),
-    (3, 4, 4, 16384, 8192, 2),
-    (4, 4, 2, 12288, 2048, 3),
+@pytest.mark.parametrize("batch,owners,q_rows,history,resident,seed,dups", [
+    (2, 2, 1, 8192, 4096, 1, False),
+    (3, 3, 1, 16384, 4096, 4, True),   # one row per request, with repeated tokens inside rows
+    (3, 4, 4, 16384, 8192, 2, False),
+    (4, 4, 2, 12288, 2048, 3, True),
 ])
-def test_resident_round_matches_oracle_over_rounds(torch_gpu, batch, owners, q_rows, history, resident, seed):
+def test_resident_round_matches_oracle_over_rounds(torch_gpu, batch, owners, q_rows, history, resident, seed, dups):
+    """Consecutive rounds against the oracle. dups: 5 % of every row's entries repeat another
+    entry of the same row (the first occurrence takes the miss rank, the repeats its slot)."""
     torch = torch_gpu
-    say(f"case resident round b={batch} o={owners} q={q_rows} h={history} r={resident} seed={seed}")
+    say(f"case resident round b={batch} o={owners} q={q_rows} h={history} r={resident} seed={seed} dups={dups}")
     owners_of = np.random.default_rng(seed).permutation(owners)[:batch]
     st = Setup(torch, batch=batch, owners=owners, history=history, resident=resident, q_rows=q_rows, seed=seed,
                invalid=0.05, row_owners=owners_of)
@@ -174,6 +177,11 @@ def test_resident_round_matches_oracle_over_rounds(torch_gpu, batch, owners, q_r
     for rnd in range(3):
         say(f"  round {rnd}")
         selected = np.concatenate([mtp_selection(rng, q_rows, history, resident, 0.6) for _ in range(batch)])
+        if dups:
+            for row in selected:
+                n = int((row >= 0).sum())
+                at = rng.choice(n, n // 20, replace=False)
+                row[at] = row[rng.integers(0, n, len(at))]
         lru = np.stack([p.slots.astype(np.int64) for p in policies])
         outs = st.oracle_round(selected, lru)
         st.run_round(selected, lru)
