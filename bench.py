@@ -589,17 +589,19 @@ def sfa_leg(torch, kvip_amd, device, seed, iters=20):
     return out
 
 
-def mixed_leg(torch, kvip_amd, device, seed, rounds=20, warm=4, sequential=False):
+def mixed_leg(torch, kvip_amd, device, seed, rounds=20, warm=4, sequential=False, prefill_after=None):
     """one continuous-batching round captured as a single hipGraph:
     Index ingest of all new tokens (32 decode + 2048 + 1536 prefill rows), resident decode
     LIFetch for 32 requests (ctx ~U[4096, 65536], 16384 hot slots, misses from pinned host
     memory, the LRU chains committed inside the graph) and prefill LI + TopK for the two
     chunks (k_len 8192 and 1536). Consecutive replays are consecutive serving rounds on the
     evolving cache state: each picks its decode queries by a device cursor from a random
-    walk (overlapping, drifting selections) and records its misses."""
+    walk (overlapping, drifting selections) and records its misses. prefill_after: where
+    the prefill stage forks off (MixedRound's default when None)."""
     from kvip_amd import synthetic
 
-    wl = synthetic.mixed_workload(torch, kvip_amd, device, seed=seed, lru=True, overlap=not sequential)
+    wl = synthetic.mixed_workload(torch, kvip_amd, device, seed=seed, lru=True, overlap=not sequential,
+                                  prefill_after=prefill_after)
     rnd = wl.round
     nd = len(wl.decode_ctx)
     n = warm + rounds + 1
@@ -627,7 +629,9 @@ def mixed_leg(torch, kvip_amd, device, seed, rounds=20, warm=4, sequential=False
             "rows_per_s": round((nd + pf_rows) / (us * 1e-6), 1),
             "decode_misses_per_round": round(miss, 1),
             "decode_hit_fraction": round(1.0 - miss / (nd * TOPK), 4), "rounds": rounds,
-            "streams": "one" if sequential else "prefill beside the decode, Fetch beside the Index update"}
+            "streams": "one" if sequential else (f"prefill forked after the decode's {rnd.prefill_after}"
+                                                 if rnd.prefill_after != "start" else "prefill forked at the start")
+                       + ("" if sequential else ", Fetch beside the Index update")}
 
 
 def _stage_times(torch, pairs, per_graph=8, reps=25):
@@ -711,6 +715,16 @@ def mtp_leg(torch, kvip_amd, device, seed):
                                "mfma_tflops": round(tflops, 1), "mfma_frac": round(tflops / FP8_MFMA_PEAK_TFLOPS, 4)}}
 
 
+def copy_calibration(torch, device):
+    """Three plain 1 GiB device-to-device copies: the kernel whose rocprofv3 FETCH_SIZE and
+    WRITE_SIZE per dispatch scale those counters to bytes moved."""
+    src = torch.empty(1 << 30, dtype=torch.uint8, device=device)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+
+
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -737,6 +751,8 @@ def main():
         print(f"bench: {args.only} leg starts", file=sys.stderr, flush=True)
         print(json.dumps({"leg": args.only, args.only: only_legs[args.only]()}), flush=True)
         print(f"bench: {args.only} leg done", file=sys.stderr, flush=True)
+        if args.copy_calibration:
+            copy_calibration(torch, device)
         return
     # Two independent input sets, alternated step by step: a step touches ~346 MB and
     # MI355X's 256 MB Infinity Cache would otherwise keep part of the same inputs
@@ -846,11 +862,7 @@ def main():
             raise RuntimeError(f"device status {int(r.status.item())} after the timed steps")
 
     if args.copy_calibration:
-        src = torch.empty(1 << 30, dtype=torch.uint8, device=device)
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            dst.copy_(src)
-        torch.cuda.synchronize()
+        copy_calibration(torch, device)
 
     rows = rot.rows
     # The dominant kernel of the default three-launch round: the longest launch.

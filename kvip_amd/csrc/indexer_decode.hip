@@ -32,6 +32,9 @@ namespace kvip {
 bool ring_eligible(const KvipIndexerArgs& a);
 hipError_t launch_indexer_ring(const KvipIndexerArgs& a, hipStream_t stream, int tile_lo = 0,
                                int tile_hi = 1 << 30);
+// fp8 decode with 2 or 4 rows per request: the shared-ring kernel (indexer_ring.hip).
+bool ring_rows_eligible(const KvipIndexerArgs& a);
+hipError_t launch_indexer_ring_rows(const KvipIndexerArgs& a, hipStream_t stream);
 
 namespace {
 
@@ -448,6 +451,7 @@ int stream_grid(K kernel) {
 template <int ELEM, int HEADS, int RPR, bool W_BF16>
 hipError_t launch_kernel(const KvipIndexerArgs& a, hipStream_t stream) {
     if (ring_eligible(a)) return launch_indexer_ring(a, stream);
+    if (ring_rows_eligible(a)) return launch_indexer_ring_rows(a, stream);
     if (a.batch <= kStreamMaxBatch) {
         auto kernel = indexer_stream_kernel<ELEM, HEADS, RPR, W_BF16>;
         const int grid = stream_grid(kernel);

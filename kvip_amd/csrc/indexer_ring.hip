@@ -86,11 +86,79 @@ KVIP_DEVICE v4f rg_weights4(const KvipIndexerArgs& p, int row, int h, bool qscal
     return w;
 }
 
-// Visible tokens of request b's single query row.
-KVIP_DEVICE int rg_valid(const KvipIndexerArgs& p, int b) {
+// Visible tokens of query row `row` of request b.
+KVIP_DEVICE int rg_valid(const KvipIndexerArgs& p, int b, int row) {
     int v = max(p.seq_lens[b], 0);
-    if (p.query_ends != nullptr) v = min(v, p.query_ends[b]);
+    if (p.query_ends != nullptr) v = min(v, p.query_ends[row]);
     return min(max(v, 0), p.max_blocks * kBlockTokens);
+}
+
+// Q fragments (A operand: head mt*32 + n, bytes [64*g, +64)) and per-lane weights of
+// query row `row`, in the MFMA output layout (wr[mt*16 + r] weighs head
+// mt*32 + 8*(r/4) + 4*g + r%4).
+template <int HEADS, bool W_BF16>
+KVIP_DEVICE void rg_load_q(const KvipIndexerArgs& p, int row, int n, int g, bool qscale,
+                           v4i (&qa)[HEADS / 32][4], float (&wr)[HEADS / 2]) {
+#pragma unroll
+    for (int mt = 0; mt < HEADS / 32; ++mt) {
+        const v4i* src = reinterpret_cast<const v4i*>(static_cast<const uint8_t*>(p.query) +
+                                                      (static_cast<size_t>(row) * HEADS + mt * 32 + n) * kIndexDim +
+                                                      g * (kIndexDim / 2));
+#pragma unroll
+        for (int v = 0; v < 4; ++v) qa[mt][v] = src[v];
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+            const v4f w4 = rg_weights4<HEADS, W_BF16>(p, row, mt * 32 + r4 * 8 + g * 4, qscale);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) wr[mt * 16 + r4 * 4 + j] = w4[j];
+        }
+    }
+}
+
+// Sortable key of token n for one query row from the tile's B fragments kb and the
+// token's key scale ks (same value in both lane halves): fp8 MFMA over the heads, ReLU
+// (integer max: negative floats map to +0), head weights, head reduction (4 FMA chains,
+// then v_permlane32_swap adds the other lane half's heads), key scale, bf16 half-away
+// rounding, sortable transform. The next head tile's MFMAs are interleaved with the
+// current tile's epilogue.
+template <int MT>
+KVIP_DEVICE uint32_t rg_key(const v4i (&qa)[MT][4], const float (&wr)[MT * 16], const v4i (&kb)[4], float ks,
+                            int g) {
+    float pj[4] = {0.f, 0.f, 0.f, 0.f};
+    v16f acc[2];
+    acc[0] = v16f{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    Mma<1>::step(0, qa[0], kb, acc[0]);
+    Mma<1>::step(1, qa[0], kb, acc[0]);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        v16f& cur = acc[mt & 1];
+        if (mt + 1 < MT) {
+            v16f& nxt = acc[(mt + 1) & 1];
+            nxt = v16f{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            Mma<1>::step(0, qa[mt + 1], kb, nxt);
+            Mma<1>::step(1, qa[mt + 1], kb, nxt);
+        }
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float relu = __int_as_float(max(__float_as_int(cur[r4 * 4 + j]), 0));
+                pj[j] = fmaf(relu, wr[mt * 16 + r4 * 4 + j], pj[j]);
+            }
+        }
+        if (mt + 1 < MT) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    float part = (pj[0] + pj[1]) + (pj[2] + pj[3]);
+    const auto swapped = __builtin_amdgcn_permlane32_swap(__float_as_int(part), __float_as_int(part), false, false);
+    part += __int_as_float(g == 0 ? swapped[1] : swapped[0]);
+    return sortable_key(bf16_bits_half_away(part * ks));
 }
 
 template <int HEADS, bool W_BF16>
@@ -113,7 +181,7 @@ __global__ __launch_bounds__(kRgThreads, 2) void indexer_ring_kernel(const KvipI
     int running = 0;
     for (int base = 0; base < p.batch; base += kRgThreads) {
         const int b = base + tid;
-        const int c = b < p.batch ? max(0, min((rg_valid(p, b) + 31) / 32, tile_hi) - tile_lo) : 0;
+        const int c = b < p.batch ? max(0, min((rg_valid(p, b, b) + 31) / 32, tile_hi) - tile_lo) : 0;
         uint32_t total;
         const uint32_t excl = block_exclusive_scan(static_cast<uint32_t>(c), s_scan, &total);
         if (b < p.batch) s_prefix[b] = running + static_cast<int>(excl);
@@ -157,22 +225,7 @@ __global__ __launch_bounds__(kRgThreads, 2) void indexer_ring_kernel(const KvipI
     float wr[MT * 16];
     int qb = -1;  // request whose Q fragments and weights are loaded
     const bool qscale = p.query_scale != nullptr;
-    auto load_q = [&](int b) {
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-            const v4i* src = reinterpret_cast<const v4i*>(static_cast<const uint8_t*>(p.query) +
-                                                          (static_cast<size_t>(b) * HEADS + mt * 32 + n) * kIndexDim +
-                                                          g * (kIndexDim / 2));
-#pragma unroll
-            for (int v = 0; v < 4; ++v) qa[mt][v] = src[v];
-#pragma unroll
-            for (int r4 = 0; r4 < 4; ++r4) {
-                const v4f w4 = rg_weights4<HEADS, W_BF16>(p, b, mt * 32 + r4 * 8 + g * 4, qscale);
-#pragma unroll
-                for (int j = 0; j < 4; ++j) wr[mt * 16 + r4 * 4 + j] = w4[j];
-            }
-        }
-    };
+    auto load_q = [&](int b) { rg_load_q<HEADS, W_BF16>(p, b, n, g, qscale, qa, wr); };
 
     // The run's histogram (one request) in LDS, added to the global row at the run's end.
     auto flush = [&](int req) {
@@ -206,7 +259,7 @@ __global__ __launch_bounds__(kRgThreads, 2) void indexer_ring_kernel(const KvipI
             d_page = ok ? id : 0;
             d_ok = ok ? 1.0f : 0.0f;
             if (!ok) err |= KVIP_STATUS_BAD_BLOCK;
-            d_valid = rg_valid(p, d_b);
+            d_valid = rg_valid(p, d_b, d_b);
         }
         // Tiles whose request differs from the next tile's end a run (lane cnt - 1 always).
         const int next_b = __shfl_down(d_b, 1);
@@ -234,45 +287,8 @@ __global__ __launch_bounds__(kRgThreads, 2) void indexer_ring_kernel(const KvipI
             v4i kb[4];
             float ks_raw;
             lds_read_tile(ka[0] + so, ka[1] + so, ka[2] + so, ka[3] + so, ksa + so, kb, ks_raw);
-            float pj[4] = {0.f, 0.f, 0.f, 0.f};
-            v16f acc[2];
-            acc[0] = v16f{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-            Mma<1>::step(0, qa[0], kb, acc[0]);
-            Mma<1>::step(1, qa[0], kb, acc[0]);
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt) {
-                v16f& cur = acc[mt & 1];
-                if (mt + 1 < MT) {
-                    v16f& nxt = acc[(mt + 1) & 1];
-                    nxt = v16f{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-                    Mma<1>::step(0, qa[mt + 1], kb, nxt);
-                    Mma<1>::step(1, qa[mt + 1], kb, nxt);
-                }
-#pragma unroll
-                for (int r4 = 0; r4 < 4; ++r4) {
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        // ReLU as an integer max: negative floats (sign bit set) map to +0.
-                        const float relu = __int_as_float(max(__float_as_int(cur[r4 * 4 + j]), 0));
-                        pj[j] = fmaf(relu, wr[mt * 16 + r4 * 4 + j], pj[j]);
-                    }
-                }
-                if (mt + 1 < MT) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);
-                    __builtin_amdgcn_sched_barrier(0);
-                }
-            }
-            float part = (pj[0] + pj[1]) + (pj[2] + pj[3]);
-            // Add the other lane half's heads (v_permlane32_swap: lane l <-> lane l ^ 32).
-            const auto swapped =
-                __builtin_amdgcn_permlane32_swap(__float_as_int(part), __float_as_int(part), false, false);
-            part += __int_as_float(g == 0 ? swapped[1] : swapped[0]);
             const float ks = ks_raw * __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, d_ok), i));
-            const uint32_t key = sortable_key(bf16_bits_half_away(part * ks));
+            const uint32_t key = rg_key<MT>(qa, wr, kb, ks, g);
             const int b = __builtin_amdgcn_readlane(d_b, i);
             const int tok = __builtin_amdgcn_readlane(d_k, i) * 32 + n;
             if (g == 0) {  // lanes 0-31: one store instruction per tile
@@ -327,6 +343,206 @@ __global__ __launch_bounds__(kRgThreads, 2) void indexer_ring_kernel(const KvipI
     report(p.status, err);
 }
 
+// Decode with ROWS = 2 or 4 query rows per request (the MTP rows): one workgroup of ROWS
+// waves per tile stream, wave w scoring row w of each tile's request. The workgroup shares
+// one LDS ring: every wave loads its share of each tile (4 / ROWS KiB of K rows and 128 /
+// ROWS bytes of key scales, same fragment swizzle as above), waits for its own loads with
+// an exact vmcnt and meets the others at a barrier, after which every wave reads the whole
+// tile. A tile is thus read from HBM once for all rows of its request, and each wave keeps
+// the Q fragments and weights of one row in registers, as the one-row kernel does.
+// Slots: kRrDepth tiles are in flight while tile i is scored, and the loads of tile
+// i + kRrDepth are issued while slow waves may still read tile i - 1, so the ring needs
+// kRrDepth + 2 slots (rounded up to a power of two; a full pass of kRgPass tiles then ends
+// on the last slot and the next pass starts on slot 0, away from the one still read).
+// Every wave of a workgroup walks the same tiles, runs and passes, so all of them reach
+// the same barriers.
+constexpr int kRrDepth = 1;
+constexpr int kRrSlots = kRrDepth + 2 <= 4 ? 4 : 8;
+static_assert(kRgPass % kRrSlots == 0, "a full pass ends on the last slot");
+static_assert(kRrDepth >= 1 && kRrDepth <= 4, "the waits below cover up to 4 tiles in flight");
+
+template <int ROWS, int HEADS, bool W_BF16>
+__global__ __launch_bounds__(ROWS * 64) void indexer_rows_kernel(const KvipIndexerArgs p, int lead_blocks) {
+    constexpr int MT = HEADS / 32;
+    constexpr int kThreads = ROWS * 64;
+    constexpr int kChunks = 4 / ROWS;  // KiB of K rows each wave loads per tile
+    constexpr int kScaleLanes = 8 / ROWS;
+    constexpr int kOps = kChunks + 1;  // vector memory instructions per tile and wave
+    __shared__ __align__(16) uint8_t s_ring[kRrSlots][kRgSlotBytes];
+    __shared__ __align__(16) uint32_t s_hist[ROWS][256];
+    __shared__ int s_prefix[kRgMaxBatch + 1];
+    __shared__ uint32_t s_scan[ROWS];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n = lane & 31;
+    const int g = lane >> 5;
+
+    // Tiles per request (the longest of its rows) -> prefix sums.
+    int running = 0;
+    for (int base = 0; base < p.batch; base += kThreads) {
+        const int b = base + tid;
+        int c = 0;
+        if (b < p.batch) {
+            int vmax = 0;
+#pragma unroll
+            for (int q = 0; q < ROWS; ++q) vmax = max(vmax, rg_valid(p, b, b * ROWS + q));
+            c = (vmax + 31) / 32;
+        }
+        uint32_t total;
+        const uint32_t excl = block_exclusive_scan(static_cast<uint32_t>(c), s_scan, &total);
+        if (b < p.batch) s_prefix[b] = running + static_cast<int>(excl);
+        running += static_cast<int>(total);
+    }
+    if (tid == 0) s_prefix[p.batch] = running;
+    for (int i = tid; i < ROWS * 256; i += kThreads) (&s_hist[0][0])[i] = 0u;
+    __syncthreads();
+
+    // The workgroup's share [t, t_end) of the flattened tile list (first dispatch round
+    // weighted kRgLeadWeight, later ones kRgLagWeight).
+    const int total_tiles = s_prefix[p.batch];
+    const int64_t lead = min(lead_blocks, static_cast<int>(gridDim.x));
+    auto weight_before = [&](int64_t v) {
+        return kRgLeadWeight * min(v, lead) + kRgLagWeight * max(v - lead, static_cast<int64_t>(0));
+    };
+    const int64_t weight_total = weight_before(gridDim.x);
+    int t = static_cast<int>(total_tiles * weight_before(blockIdx.x) / weight_total);
+    const int t_end = static_cast<int>(total_tiles * weight_before(blockIdx.x + 1) / weight_total);
+    if (t >= t_end) return;  // uniform for the workgroup
+
+    uint8_t* ring = &s_ring[0][0];
+    const uint32_t ring_lds = lds_addr(ring);
+    uint32_t ka[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) ka[u] = ring_lds + n * kIndexDim + (((g * 4 + u) ^ (n & 7)) * 16);
+    const uint32_t ksa = ring_lds + kRgTileBytes + n * 4;
+    const uint32_t hist_lds = lds_addr(&s_hist[wave][0]);
+    const int src_lane = (lane >> 3) * kIndexDim + (((lane & 7) ^ (lane >> 3)) * 16);
+    const uint8_t* kbase = static_cast<const uint8_t*>(p.keys);
+    const float* kscale = p.key_scale != nullptr ? p.key_scale : kRingUnitScale;
+    const int64_t kscale_stride = p.key_scale != nullptr ? p.scale_block_stride : 0;
+    uint32_t err = 0;
+
+    v4i qa[MT][4];
+    float wr[MT * 16];
+    int qb = -1;
+    const bool qscale = p.query_scale != nullptr;
+
+    auto flush = [&](int row) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t a = hist_lds + (k * 64 + lane) * 4;
+            const uint32_t c = lds_read_b32(a);
+            if (c != 0u) {
+                atomicAdd(&p.histogram[static_cast<size_t>(row) * 256 + k * 64 + lane], c);
+                lds_write_b32(a, 0u);
+            }
+        }
+    };
+
+    while (t < t_end) {
+        const int cnt = min(t_end - t, kRgPass);
+        // Lane i describes tile t + i (every wave computes the same descriptors).
+        int d_b = 0, d_k = 0, d_page = 0, d_valid = 0;
+        float d_ok = 0.0f;
+        if (lane < cnt) {
+            const int tt = t + lane;
+            int lo = 0, hi = p.batch - 1;
+            while (lo < hi) {
+                const int mid = (lo + hi + 1) >> 1;
+                if (s_prefix[mid] <= tt) lo = mid; else hi = mid - 1;
+            }
+            d_b = lo;
+            d_k = tt - s_prefix[lo];
+            const int id = p.block_table[static_cast<size_t>(d_b) * p.max_blocks + (d_k >> 2)];
+            const bool ok = static_cast<unsigned>(id) < static_cast<unsigned>(p.num_blocks);
+            d_page = ok ? id : 0;
+            d_ok = ok ? 1.0f : 0.0f;
+            if (!ok && wave == 0) err |= KVIP_STATUS_BAD_BLOCK;
+            d_valid = rg_valid(p, d_b, d_b * ROWS + wave);
+        }
+        const int next_b = __shfl_down(d_b, 1);
+        const uint64_t run_ends = __ballot(lane < cnt && (lane == cnt - 1 || next_b != d_b));
+
+        // This wave's share of tile j's loads (tiles past the pass end repeat its last tile).
+        auto issue = [&](int j) {
+            const int jj = min(j, cnt - 1);
+            const int page = __builtin_amdgcn_readlane(d_page, jj);
+            const int k = __builtin_amdgcn_readlane(d_k, jj);
+            uint8_t* dst = ring + (j & (kRrSlots - 1)) * kRgSlotBytes;
+            const uint8_t* src = kbase + static_cast<size_t>(page) * p.key_block_stride + (k & 3) * kRgTileBytes + src_lane;
+#pragma unroll
+            for (int c = 0; c < kChunks; ++c) {
+                const int v = wave * kChunks + c;
+                __builtin_amdgcn_global_load_lds(src + v * 1024, LDS_PTR(dst + v * 1024), 16, 0, kNonTemporal);
+            }
+            if (lane < kScaleLanes) {
+                const float* ssrc = kscale + static_cast<size_t>(page) * kscale_stride + (k & 3) * 32 +
+                                    (wave * kScaleLanes + lane) * 4;
+                __builtin_amdgcn_global_load_lds(ssrc, LDS_PTR(dst + kRgTileBytes + wave * kScaleLanes * 16), 16, 0,
+                                                 kNonTemporal);
+            }
+        };
+
+        auto score = [&](int i) {
+            const uint32_t so = (i & (kRrSlots - 1)) * kRgSlotBytes;
+            v4i kb[4];
+            float ks_raw;
+            lds_read_tile(ka[0] + so, ka[1] + so, ka[2] + so, ka[3] + so, ksa + so, kb, ks_raw);
+            const float ks = ks_raw * __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, d_ok), i));
+            const uint32_t key = rg_key<MT>(qa, wr, kb, ks, g);
+            const int row = __builtin_amdgcn_readlane(d_b, i) * ROWS + wave;
+            const int tok = __builtin_amdgcn_readlane(d_k, i) * 32 + n;
+            if (g == 0) {
+                p.score_keys[static_cast<size_t>(row) * p.key_stride + tok] = static_cast<uint16_t>(key);
+                if (tok < __builtin_amdgcn_readlane(d_valid, i)) lds_add_u32(hist_lds + (key >> 8) * 4, 1u);
+            }
+        };
+
+        const int b_first = __builtin_amdgcn_readlane(d_b, 0);
+        if (b_first != qb) {
+            rg_load_q<HEADS, W_BF16>(p, b_first * ROWS + wave, n, g, qscale, qa, wr);
+            qb = b_first;
+        }
+#pragma unroll
+        for (int j = 0; j < kRrDepth; ++j) issue(j);
+        int i = 0;
+        while (i < cnt) {  // runs of one request
+            const int b = __builtin_amdgcn_readlane(d_b, i);
+            if (b != qb) {
+                rg_load_q<HEADS, W_BF16>(p, b * ROWS + wave, n, g, qscale, qa, wr);
+                qb = b;
+                __builtin_amdgcn_s_waitcnt(kVmcntZero);
+            }
+            const uint64_t later = run_ends >> i;
+            const int run_end = i + static_cast<int>(__builtin_ctzll(later)) + 1;
+            for (; i < run_end; ++i) {
+                issue(i + kRrDepth);
+                // Own share of tile i landed: after its loads come those of the next
+                // kRrDepth tiles and the key stores of the (at most kRrDepth) tiles before i.
+                if (i >= kRrDepth) {
+                    wait_vmcnt<kRrDepth * kOps + kRrDepth>();
+                } else if (kRrDepth > 3 && i == 3) {
+                    wait_vmcnt<kRrDepth * kOps + (kRrDepth > 3 ? 3 : 0)>();
+                } else if (kRrDepth > 2 && i == 2) {
+                    wait_vmcnt<kRrDepth * kOps + (kRrDepth > 2 ? 2 : 0)>();
+                } else if (kRrDepth > 1 && i == 1) {
+                    wait_vmcnt<kRrDepth * kOps + (kRrDepth > 1 ? 1 : 0)>();
+                } else {
+                    wait_vmcnt<kRrDepth * kOps>();
+                }
+                __builtin_amdgcn_s_barrier();  // every wave's share of tile i landed
+                score(i);
+            }
+            flush(b * ROWS + wave);
+        }
+        wait_vmcnt<0>();  // the repeated tail load lands before the ring is reused
+        t += cnt;
+    }
+    report(p.status, err);
+}
+
 // Grid = workgroups per CU the kernel keeps resident times the CU count; the first
 // dispatch round is one workgroup per CU.
 struct RingGrid {
@@ -358,6 +574,33 @@ hipError_t launch_ring_kernel(const KvipIndexerArgs& a, int tile_lo, int tile_hi
     return hipGetLastError();
 }
 
+template <int ROWS, int HEADS, bool W_BF16>
+hipError_t launch_rows_kernel(const KvipIndexerArgs& a, hipStream_t stream) {
+    auto kernel = indexer_rows_kernel<ROWS, HEADS, W_BF16>;
+    static RingGrid grid{0, 0};
+    if (grid.blocks == 0) {
+        int dev = 0, cus = 0, per_cu = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, ROWS * 64, 0) != hipSuccess) {
+            return hipErrorInvalidDevice;
+        }
+        grid = RingGrid{max(1, cus * max(per_cu, 1)), max(1, cus)};
+    }
+    hipLaunchKernelGGL(kernel, dim3(grid.blocks), dim3(ROWS * 64), 0, stream, a, grid.lead_blocks);
+    return hipGetLastError();
+}
+
+template <int ROWS>
+hipError_t launch_rows(const KvipIndexerArgs& a, hipStream_t stream) {
+    if (a.heads == 64) {
+        return a.weight_dtype == KVIP_DTYPE_BF16 ? launch_rows_kernel<ROWS, 64, true>(a, stream)
+                                                 : launch_rows_kernel<ROWS, 64, false>(a, stream);
+    }
+    return a.weight_dtype == KVIP_DTYPE_BF16 ? launch_rows_kernel<ROWS, 32, true>(a, stream)
+                                             : launch_rows_kernel<ROWS, 32, false>(a, stream);
+}
+
 }  // namespace
 
 // fp8, one row per request, batch within the LDS prefix table, 16-byte aligned key-scale
@@ -370,6 +613,20 @@ bool ring_eligible(const KvipIndexerArgs& a) {
            (a.query_scale == nullptr || (reinterpret_cast<uintptr_t>(a.query_scale) & 15u) == 0) &&
            (a.key_scale == nullptr ||
             ((reinterpret_cast<uintptr_t>(a.key_scale) & 15u) == 0 && a.scale_block_stride % 4 == 0));
+}
+
+// fp8 with 2 or 4 rows per request, same batch and alignment limits as the one-row kernel.
+bool ring_rows_eligible(const KvipIndexerArgs& a) {
+    const uintptr_t wal = a.weight_dtype == KVIP_DTYPE_BF16 ? 7u : 15u;
+    return a.qk_dtype == KVIP_DTYPE_FP8_E4M3 && (a.rows_per_request == 2 || a.rows_per_request == 4) &&
+           a.batch <= kRgMaxBatch && (reinterpret_cast<uintptr_t>(a.weights) & wal) == 0 &&
+           (a.query_scale == nullptr || (reinterpret_cast<uintptr_t>(a.query_scale) & 15u) == 0) &&
+           (a.key_scale == nullptr ||
+            ((reinterpret_cast<uintptr_t>(a.key_scale) & 15u) == 0 && a.scale_block_stride % 4 == 0));
+}
+
+hipError_t launch_indexer_ring_rows(const KvipIndexerArgs& a, hipStream_t stream) {
+    return a.rows_per_request == 2 ? launch_rows<2>(a, stream) : launch_rows<4>(a, stream);
 }
 
 // Scores the 32-token tiles [tile_lo, tile_hi) of every row's visible positions.

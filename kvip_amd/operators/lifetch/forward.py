@@ -41,6 +41,10 @@ class LIFetchForward:
             raise ValueError("Fetch and Index update must use the same device")
         self.rotating, self.update, self.torch = rotating, update, rotating.torch
         self.library = abi.load_library()
+        # Called with the launch stream right after the round's scoring is enqueued; None:
+        # nothing (the point from which a caller may fork work that should overlap the TopK
+        # and what follows rather than the HBM-bound scoring).
+        self.after_scoring = None
         self.resident = isinstance(update, ResidentIndexUpdate)
         if self.resident:
             self.indexer_args, self.topk_args = rotating.indexer_args(), rotating.topk_args()
@@ -118,13 +122,14 @@ class LIFetchForward:
         if self.resident:
             upd = self.update
             if self.prefix is None:
-                if not upd.overlap and upd.lru is None:
+                if not upd.overlap and upd.lru is None and self.after_scoring is None and upd.after_resolve is None:
                     abi.check(self.library.kvip_hip_resident_forward(*self._refs, self._stream()),
                               "resident LIFetch forward")
                     return
                 # Scoring + round initialisation, TopK, then the round's resolve / Fetch /
                 # Index update (the update beside the Fetch with overlap).
                 abi.check(self.library.kvip_hip_resident_score(*self._refs, self._stream()), "resident scoring")
+                self._scored()
                 abi.check(self.library.kvip_hip_topk(self._refs[1], self._stream()), "TopK")
                 upd.finish()
                 return
@@ -134,6 +139,7 @@ class LIFetchForward:
                 self._windowed_prefetch_forward(torch, lib, main)
                 return
             abi.check(lib.kvip_hip_resident_score(*self._refs, main.cuda_stream), "resident scoring")
+            self._scored()
             self.scored.record(main)
             self.side.wait_event(self.scored)
             abi.check(lib.kvip_hip_resident_prefix(ctypes.byref(self.prefix.topk_args), ctypes.byref(self.prefix.args),
@@ -145,7 +151,17 @@ class LIFetchForward:
             main.wait_event(self.prefetched)
             upd.finish()
             return
+        if self.after_scoring is not None:
+            self.score()
+            self._scored()
+            self.select()
+            self.fetch()
+            return
         abi.check(self.library.kvip_hip_lifetch_forward(self._args_ref, self._stream()), "LIFetch forward")
+
+    def _scored(self):
+        if self.after_scoring is not None:
+            self.after_scoring(self.torch.cuda.current_stream(self.rotating.device))
 
     def _windowed_prefetch_forward(self, torch, lib, main):
         """The prefetching resident forward with the scoring in prefetch windows (same
@@ -179,6 +195,7 @@ class LIFetchForward:
             abi.check(lib.kvip_hip_resident_prefetch_copy(self._refs[2], self._prefetch_ref, e, e + 1,
                                                           copy.cuda_stream), "resident prefetch copy")
         self.copies_done.record(copy)
+        self._scored()
         abi.check(lib.kvip_hip_topk(self._refs[1], main.cuda_stream), "TopK")
         main.wait_event(self.window_decided[-1])
         upd.finish(copies_done=self.copies_done)

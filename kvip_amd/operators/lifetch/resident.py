@@ -162,6 +162,10 @@ class ResidentIndexUpdate:
         self.library = lib
         abi.check(lib.kvip_hip_resident_prepare(self._ref, abi.stream_handle(torch, dev)), "resident workspace")
         self.lru = self.commit_rows = None
+        # Called with the launch stream right after each round's resolve is enqueued (the
+        # point from which a caller may fork work that should not compete with the scoring,
+        # TopK and resolve for compute units); None: nothing.
+        self.after_resolve = None
         self.overlap = bool(overlap)
         if self.overlap:
             # The Index-update branch: its own stream (default priority), forked after the
@@ -197,17 +201,22 @@ class ResidentIndexUpdate:
         torch, lib = self.torch, self.library
         main = torch.cuda.current_stream(self.device)
         if not self.overlap:
-            if copies_done is None:
+            if copies_done is None and self.after_resolve is None:
                 abi.check(lib.kvip_hip_resident_finish(self._ref, main.cuda_stream), "resident round")
             else:
                 abi.check(lib.kvip_hip_resident_resolve(self._ref, main.cuda_stream), "resident resolve")
-                main.wait_event(copies_done)  # before the Fetch, the update and the LRU commit
+                if self.after_resolve is not None:
+                    self.after_resolve(main)
+                if copies_done is not None:
+                    main.wait_event(copies_done)  # before the Fetch, the update and the LRU commit
                 abi.check(lib.kvip_hip_resident_fetch(self._ref, main.cuda_stream), "resident Fetch")
                 abi.check(lib.kvip_hip_resident_update(self._ref, main.cuda_stream), "resident Index update")
             if self.lru is not None:
                 self.lru.commit(self.commit_rows)
             return
         abi.check(lib.kvip_hip_resident_resolve(self._ref, main.cuda_stream), "resident resolve")
+        if self.after_resolve is not None:
+            self.after_resolve(main)
         self.resolved.record(main)
         self.side.wait_event(self.resolved)
         if copies_done is not None:

@@ -21,10 +21,14 @@ buffers bound once, so the whole round is one hipGraph:
      packed chunks (cumulative query lengths) and TopK-2048 per row.
 
 The prefill stage reads only the paged cache and its own buffers, so it runs on a second
-stream forked at the round's start and joined at its end (`overlap=True`, the default):
-its MFMA-bound scoring then overlaps the decode's HBM-bound scoring and PCIe-bound Fetch
-instead of following them. The fork and join are events, so the round stays one capturable
-sequence on the caller's stream.
+stream joined at the round's end (`overlap=True`, the default), forked at the point
+`prefill_after` names: "resolve" (default for a resident decode: once the decode's scoring,
+TopK and resolve are enqueued, so its MFMA-bound scoring overlaps the PCIe-bound Fetch, the
+Index update and the LRU commit and leaves the compute units to the short decode kernels
+before them; two prefill workgroups fill a CU's LDS, so a decode kernel queued behind them
+would wait for whole prefill workgroups), "scoring" (after the decode's scoring) or "start"
+(at the round's start, beside everything). The fork and join are events, so the round
+stays one capturable sequence on the caller's stream.
 
 The caller fills the per-round inputs in place before a launch or replay: decode Q /
 weights / lengths, the prefill buffers it bound, and `sources` / `targets` of the new
@@ -41,7 +45,7 @@ INDEX_DIM = 128
 
 class MixedRound:
     def __init__(self, torch, *, decode, prefill, storage_keys, storage_scales, cache_keys, cache_scales,
-                 new_tokens, status=None, lru=None, overlap=True):
+                 new_tokens, status=None, lru=None, overlap=True, prefill_after=None):
         """decode: a LIFetch forward; prefill: a PrefillIndexer after `bind(...)`;
         storage_keys [owners, history, 128] (fp8 or uint8) and storage_scales
         [owners, history] float32: the persistent Index rows; cache_keys
@@ -85,6 +89,17 @@ class MixedRound:
             # Committed by the decode round itself, right after its Index update.
             decode.update.attach_lru(lru)
         self.overlap = overlap
+        resident = getattr(decode, "resident", False)
+        if prefill_after is None:
+            prefill_after = "resolve" if resident else "scoring"
+        if prefill_after not in ("start", "scoring", "resolve"):
+            raise ValueError(f"prefill_after must be 'start', 'scoring' or 'resolve' (got {prefill_after!r})")
+        if prefill_after == "resolve" and not resident:
+            raise ValueError("prefill_after='resolve' needs a resident decode update")
+        if prefill_after != "start" and not hasattr(decode, "after_scoring"):
+            raise ValueError("the decode forward has no stage hooks: use prefill_after='start'")
+        self.prefill_after = prefill_after
+        self._forks = 0
         if overlap:
             # The prefill branch: its own stream (default priority) and the fork/join events.
             self.side = torch.cuda.Stream(device=dev)
@@ -94,20 +109,39 @@ class MixedRound:
         abi.check(self.library.kvip_hip_ingest_index(ctypes.byref(self.ingest_args),
                                                      abi.stream_handle(self.torch, self.device)), "mixed ingest")
 
+    def _fork(self, main):
+        """Enqueue the prefill stage on the second stream, after what `main` holds so far."""
+        self.forked.record(main)
+        self.side.wait_event(self.forked)
+        with self.torch.cuda.stream(self.side):
+            self.prefill.score()
+            self.prefill.select()
+        self.joined.record(self.side)
+        self._forks += 1
+
     def __call__(self):
         torch = self.torch
-        if self.overlap:
-            main = torch.cuda.current_stream(self.device)
-            self.forked.record(main)
-            self.side.wait_event(self.forked)
-            with torch.cuda.stream(self.side):
-                self.prefill.score()
-                self.prefill.select()
-            self.joined.record(self.side)
-        self.ingest()
-        self.decode()
-        if self.overlap:
-            torch.cuda.current_stream(self.device).wait_event(self.joined)
-            return self.prefill.topk[:self.prefill._rows]
-        self.prefill.score()
-        return self.prefill.select()
+        if not self.overlap:
+            self.ingest()
+            self.decode()
+            self.prefill.score()
+            return self.prefill.select()
+        main = torch.cuda.current_stream(self.device)
+        self._forks = 0
+        if self.prefill_after == "start":
+            self._fork(main)
+            self.ingest()
+            self.decode()
+        else:
+            owner = self.decode.update if self.prefill_after == "resolve" else self.decode
+            name = "after_resolve" if self.prefill_after == "resolve" else "after_scoring"
+            setattr(owner, name, self._fork)
+            try:
+                self.ingest()
+                self.decode()
+            finally:
+                setattr(owner, name, None)
+        if self._forks != 1:
+            raise RuntimeError(f"mixed round: the prefill stage was enqueued {self._forks} times")
+        torch.cuda.current_stream(self.device).wait_event(self.joined)
+        return self.prefill.topk[:self.prefill._rows]

@@ -84,6 +84,41 @@ def test_indexer_scores_match_oracle(torch_gpu, name, qk, heads, wdt, kscale, qs
         assert np.array_equal(hist[r], np.bincount(gpu_keys(rot)[r, :v] >> 8, minlength=256)), r
 
 
+MTP_CASES = [
+    # name, rows per request, heads, weight dtype, key scale, query scale, ctx
+    ("rows4_h64_fp32w", 4, 64, "f32", True, True, [9000, 4100, 33, 12000, 1, 2049]),
+    ("rows2_h64_bf16w", 2, 64, "bf16", True, False, [5000, 31, 7000]),
+    ("rows4_h32_noscale", 4, 32, "f32", False, False, [3000, 4096, 130]),
+]
+
+
+@pytest.mark.parametrize("name,rows,heads,wdt,kscale,qscale,ctx", MTP_CASES, ids=[c[0] for c in MTP_CASES])
+def test_indexer_mtp_rows_match_oracle(torch_gpu, name, rows, heads, wdt, kscale, qscale, ctx):
+    """fp8 decode scoring with 2 or 4 query rows per request (the shared-ring kernel): row q
+    of request b sees its own visible bound (ctx - rows + 1 + q, with a padding row and rows
+    shorter than one tile); keys against the oracle and every row's histogram against its
+    keys."""
+    torch = torch_gpu
+    say(f"case {name}")
+    wl = synthetic.decode_workload(torch, batch=len(ctx), ctx=ctx, device="cuda", heads=heads, qk="fp8",
+                                   weight_dtype=torch.float32 if wdt == "f32" else torch.bfloat16,
+                                   key_scale=kscale, query_scale=qscale, rows_per_request=rows, seed=13)
+    ends = []
+    for c in ctx:
+        ends += [max(c - rows + 1 + q, 0) for q in range(rows)]
+    ends[1] = 0  # a padding row
+    rot, upd, fwd = synthetic.bind(torch, kvip_amd, wl, query_ends=ends)
+    fwd.score()
+    torch.cuda.synchronize()
+    assert int(rot.status.item()) == 0
+    want, valid = oracle_keys(torch, wl, rot)
+    assert list(valid) == [min(e, c) for e, c in zip(ends, np.repeat(ctx, rows))]
+    assert_scores_close(gpu_keys(rot), want, valid, 3e-2)
+    hist = rot.histogram.cpu().numpy()
+    for r, v in enumerate(valid):
+        assert np.array_equal(hist[r], np.bincount(gpu_keys(rot)[r, :v] >> 8, minlength=256)), r
+
+
 def run_topk(torch, rot, use_histogram, split=True):
     lib = abi.load_library()
     args = rot.topk_args(use_histogram, split=split)

@@ -26,9 +26,10 @@ def host(torch, t):
     return t.float().cpu().numpy()
 
 
-def small(torch):
+def small(torch, prefill_after=None):
     return synthetic.mixed_workload(torch, kvip_amd, "cuda", seed=7, decode_ctx=[8000, 5000, 6200, 3000],
-                                    history=8192, resident=4096, prefill=((40, 3000), (25, 25)))
+                                    history=8192, resident=4096, prefill=((40, 3000), (25, 25)),
+                                    prefill_after=prefill_after)
 
 
 def state(wl):
@@ -57,9 +58,11 @@ def test_mixed_round_ingest_is_byte_exact(torch_gpu):
     assert np.array_equal(dst_s[t], src_s[s])
 
 
-def test_mixed_round_graph_replay_matches_eager_and_oracle(torch_gpu):
+@pytest.mark.parametrize("prefill_after", ["resolve", "scoring", "start"])
+def test_mixed_round_graph_replay_matches_eager_and_oracle(torch_gpu, prefill_after):
     torch = torch_gpu
-    wl = small(torch)
+    wl = small(torch, prefill_after)
+    assert wl.round.prefill_after == prefill_after
     start = [x.clone() for x in state(wl)]
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
@@ -71,7 +74,7 @@ def test_mixed_round_graph_replay_matches_eager_and_oracle(torch_gpu):
     with torch.cuda.graph(graph):
         wl.round()
     for step in range(2):
-        say(f"case mixed graph replay step {step}")
+        say(f"case mixed graph replay step {step} (prefill after {prefill_after})")
         for x, s in zip(state(wl), start):
             x.copy_(s)
         graph.replay()

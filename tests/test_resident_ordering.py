@@ -77,6 +77,7 @@ def make_update(overlap):
     upd.torch, upd.library, upd.device, upd._ref = torch, FakeLibrary(log), "cuda:0", None
     upd.overlap = overlap
     upd.lru, upd.commit_rows = FakeLru(log, torch), None
+    upd.after_resolve = None
     if overlap:
         upd.side = FakeStream(log, "side")
         upd.resolved, upd.updated = FakeEvent(log, "resolved"), FakeEvent(log, "updated")
@@ -120,3 +121,18 @@ def test_finish_without_prefetch_copies_waits_for_nothing():
     upd, log = make_update(overlap=True)
     upd.finish()
     assert not any(x[0] == "wait" and x[1] == "copies_done" for x in log.entries)
+
+
+def test_after_resolve_hook_runs_between_the_resolve_and_the_fetch():
+    """A caller's fork point (MixedRound forks its prefill stage there): the hook sees the
+    main stream right after the resolve is enqueued, before the Fetch, in both modes and
+    with or without the prefetch copies."""
+    for overlap in (True, False):
+        for copies in (False, True):
+            upd, log = make_update(overlap)
+            upd.after_resolve = lambda stream, log=log: log.entries.append(("hook", stream.name))
+            upd.finish(copies_done=FakeEvent(log, "copies_done") if copies else None)
+            e = log.entries
+            assert e.count(("hook", "main")) == 1, e
+            hook = position(e, ("hook", "main"))
+            assert position(e, ("launch", "resolve", "main")) < hook < position(e, ("launch", "fetch", "main")), e
