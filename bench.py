@@ -1,4 +1,4 @@
-"""Decode LI+TopK+Fetch throughput on one MI355X (BASELINE config 2 by default).
+"""Decode LI+TopK+Fetch throughput on one MI355X (config 2 by default).
 
 One step = one decode round of the hot path over one batch of synthetic input that
 is already resident in HBM: lightning-indexer scoring of every context token of the
@@ -30,6 +30,8 @@ HBM_PEAK_GBS = 8000.0
 FP8_MFMA_PEAK_TFLOPS = 5000.0
 BF16_MFMA_PEAK_TFLOPS = 2500.0
 TOPK = 2048
+# Rounds captured back to back in one hipGraph by the resident and mixed legs.
+CURSOR_ROUNDS_PER_GRAPH = 4
 
 
 def parse():
@@ -143,7 +145,7 @@ def cpu_baseline(torch, wl, rot, budget_s):
 
 
 def lidu_leg(torch, kvip_amd, device, seed, iters=50, reps=7):
-    """Device time of one kvip.lidu call at the BASELINE config-4 shape (16 MTP requests x
+    """Device time of one kvip.lidu call at the config-4 shape (16 MTP requests x
     4 query rows, resident budget 16384 of a 131072-token history, ~80 % hits). Each call
     must start from the same maps, so two graphs are replayed back to back `iters` times:
     one restores the maps, the other restores them and runs lidu; the difference of the
@@ -209,15 +211,20 @@ def _query_walk(torch, base, sets, seed, step=0.3):
     return out
 
 
-def _cursor_rounds(torch, body, warm, rounds, sets):
-    """Consecutive rounds from one captured hipGraph: body(cursor) enqueues round `cursor`
-    (a device int64 [1] that the graph then advances), reading that round's inputs and
-    recording its outcome by device indexing. One eager call on a side stream (code-object
-    loading), cursor reset, capture; `warm` untimed replays, then `rounds` back-to-back
-    replays timed with HIP events on the launch stream; the cursor stays below `sets`, the
-    number of input sets the body indexes. Returns us per round."""
+def _cursor_rounds(torch, body, warm, rounds, sets, per_graph=None):
+    """Consecutive rounds from one captured hipGraph of `per_graph` rounds: body(cursor)
+    enqueues round `cursor` (a device int64 [1] that the graph then advances), reading that
+    round's inputs and recording its outcome by device indexing. One eager round on a side
+    stream (code-object loading), cursor reset, capture; warm / per_graph untimed replays,
+    then rounds / per_graph back-to-back replays timed with HIP events on the launch stream
+    (the rounds of a graph follow each other with no host launch between them, as a model's
+    layers do inside its captured decode step); the cursor stays below `sets`, the number of
+    input sets the body indexes. Returns us per round."""
+    per_graph = CURSOR_ROUNDS_PER_GRAPH if per_graph is None else per_graph
     if warm + rounds > sets:
         raise ValueError(f"{warm} + {rounds} rounds need as many input sets (have {sets})")
+    if warm % per_graph or rounds % per_graph:
+        raise ValueError(f"warm-up ({warm}) and timed rounds ({rounds}) must be multiples of {per_graph}")
     stream = torch.cuda.current_stream()
     cursor = torch.zeros(1, dtype=torch.int64, device=stream.device)
 
@@ -234,19 +241,25 @@ def _cursor_rounds(torch, body, warm, rounds, sets):
     cursor.zero_()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
-        step()
+        for _ in range(per_graph):
+            step()
     cursor.zero_()
     torch.cuda.synchronize()
-    for _ in range(warm):
+    for _ in range(warm // per_graph):
         graph.replay()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(stream)
-    for _ in range(rounds):
+    for _ in range(rounds // per_graph):
         graph.replay()
     e1.record(stream)
     e1.synchronize()
     return e0.elapsed_time(e1) * 1e3 / rounds
+
+
+def _pick(torch, inputs, cursor, dst):
+    """dst <- inputs[cursor] in one gather launch (dst is the bound input buffer)."""
+    torch.index_select(inputs, 0, cursor, out=dst.view(1, *dst.shape))
 
 
 def host_read_gbs(torch, device, nbytes=256 << 20):
@@ -316,11 +329,12 @@ def cache_ops_leg(torch, kvip_amd, device, seed, iters=20):
 
 
 def resident_leg(torch, kvip_amd, device, seed, rounds=24, warm=4, sequential=False):
-    """BASELINE config 4 on the resident cache: 16 requests, history 131072, 16384 hot
+    """config 4 on the resident cache: 16 requests, history 131072, 16384 hot
     slots, misses fetched from a pinned host pool, the device LRU chains (one per request)
-    committed by every round inside the graph. Two loops of consecutive rounds, each one
-    captured hipGraph replayed back to back (HIP events around the timed replays), every
-    round on inputs of its own (picked by a device cursor) and recording its misses:
+    committed by every round inside the graph. Two loops of consecutive rounds, each a
+    captured hipGraph of CURSOR_ROUNDS_PER_GRAPH rounds replayed back to back (HIP events
+    around the timed replays), every round on inputs of its own (picked by a device cursor)
+    and recording its misses:
       round:   the resident round alone (init, resolve, then the Fetch of the misses beside
                the Index update and LRU commit on a second stream) on TopK rows drawn ~80 %
                hot under Zipf(1.1) popularity, a fresh draw per round; timed again with the
@@ -348,7 +362,7 @@ def resident_leg(torch, kvip_amd, device, seed, rounds=24, warm=4, sequential=Fa
         trace.index_copy_(0, cursor, upd.miss_counts[:, 4].view(1, batch))
 
     def round_body(cursor):
-        rot.topk.copy_(torch.index_select(picks_now[0], 0, cursor)[0])
+        _pick(torch, picks_now[0], cursor, rot.topk)
         upd.round()
         record(cursor)
 
@@ -373,7 +387,7 @@ def resident_leg(torch, kvip_amd, device, seed, rounds=24, warm=4, sequential=Fa
     trace.zero_()
 
     def forward_body(cursor):
-        q_bytes.copy_(torch.index_select(queries, 0, cursor)[0])
+        _pick(torch, queries, cursor, q_bytes)
         fwd()
         record(cursor)
 
@@ -391,6 +405,7 @@ def resident_leg(torch, kvip_amd, device, seed, rounds=24, warm=4, sequential=Fa
            "forward_us": round(fwd_us, 2), "forward_misses_per_round": round(fwd_miss, 1),
            "forward_hit_fraction": round(1.0 - fwd_miss / (batch * TOPK), 4),
            "forward_index_gbs": round(batch * history * 132 / (fwd_us * 1e-6) / 1e9, 1), "rounds": rounds,
+           "rounds_per_graph": CURSOR_ROUNDS_PER_GRAPH,
            "streams": "one" if sequential else "Fetch beside the Index update"}
     if sequential:
         return out
@@ -406,7 +421,7 @@ def resident_leg(torch, kvip_amd, device, seed, rounds=24, warm=4, sequential=Fa
     trace2 = torch.zeros((n, 2, batch), dtype=torch.int32, device=device)
 
     def prefetch_body(cursor):
-        q2.copy_(torch.index_select(queries, 0, cursor)[0])
+        _pick(torch, queries, cursor, q2)
         fwd2()
         trace2.index_copy_(0, cursor, torch.stack([upd2.miss_counts[:, 4], upd2.prefetch_counts]).view(1, 2, batch))
 
@@ -421,7 +436,7 @@ def resident_leg(torch, kvip_amd, device, seed, rounds=24, warm=4, sequential=Fa
 
 
 def prefill_leg(torch, kvip_amd, device, seed, iters=5):
-    """one 4096-row prefill chunk against a 65536-token context, right-
+    """config 3: one 4096-row prefill chunk against a 65536-token context, right-
     down causal. Times, with HIP events on the launch stream, the MFMA scoring launch, the
     TopK-2048 launch and the Index update of the 4096 new rows (VllmIndexCacheStorage.
     ingest_prefill, one list launch after the first call imported the restored prefix).
@@ -590,8 +605,8 @@ def sfa_leg(torch, kvip_amd, device, seed, iters=20):
 
 
 def mixed_leg(torch, kvip_amd, device, seed, rounds=20, warm=4, sequential=False, prefill_after=None):
-    """one continuous-batching round captured as a single hipGraph:
-    Index ingest of all new tokens (32 decode + 2048 + 1536 prefill rows), resident decode
+    """config 5: continuous-batching rounds captured as hipGraphs (CURSOR_ROUNDS_PER_GRAPH
+    rounds per graph), each round: Index ingest of all new tokens (32 decode + 2048 + 1536 prefill rows), resident decode
     LIFetch for 32 requests (ctx ~U[4096, 65536], 16384 hot slots, misses from pinned host
     memory, the LRU chains committed inside the graph) and prefill LI + TopK for the two
     chunks (k_len 8192 and 1536). Consecutive replays are consecutive serving rounds on the
@@ -610,7 +625,7 @@ def mixed_leg(torch, kvip_amd, device, seed, rounds=20, warm=4, sequential=False
     trace = torch.zeros((n, nd), dtype=torch.int32, device=device)
 
     def body(cursor):
-        q_bytes.copy_(torch.index_select(queries, 0, cursor)[0])
+        _pick(torch, queries, cursor, q_bytes)
         rnd()
         trace.index_copy_(0, cursor, wl.update.miss_counts[:, 4].view(1, nd))
 
@@ -624,11 +639,12 @@ def mixed_leg(torch, kvip_amd, device, seed, rounds=20, warm=4, sequential=False
                         f"{wl.decode_ctx.mean():.0f}; resident {wl.resident} hot slots, misses from pinned host "
                         f"memory, LRU chains committed in the graph, queries along a random walk) + prefill "
                         f"chunks {[list(c) for c in wl.chunks]} (q_len, k_len); Index ingest of "
-                        f"{len(wl.sources)} new tokens; one hipGraph per round",
+                        f"{len(wl.sources)} new tokens; each round one captured sequence, 4 rounds per hipGraph",
             "us_per_round": round(us, 1), "decode_rows": nd, "prefill_rows": pf_rows,
             "rows_per_s": round((nd + pf_rows) / (us * 1e-6), 1),
             "decode_misses_per_round": round(miss, 1),
             "decode_hit_fraction": round(1.0 - miss / (nd * TOPK), 4), "rounds": rounds,
+            "rounds_per_graph": CURSOR_ROUNDS_PER_GRAPH,
             "streams": "one" if sequential else (f"prefill forked after the decode's {rnd.prefill_after}"
                                                  if rnd.prefill_after != "start" else "prefill forked at the start")
                        + ("" if sequential else ", Fetch beside the Index update")}
@@ -729,7 +745,7 @@ def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the path shards by request with no "
-              "exchange; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+              "exchange between GPUs). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
     import torch
 

@@ -3,7 +3,7 @@
 // memset), so the whole round can be captured into a single hipGraph. The default plan is
 // three launches: scoring (indexer_ring.hip), TopK with the row's keys in registers
 // (topk.hip; rows above 65536 keys take the multi-workgroup split select) and the
-// gather (fetch_gather.hip). Measured at BASELINE config 2 this beats TopK fused with the
+// gather (fetch_gather.hip). Measured at config 2 this beats TopK fused with the
 // gather (select_fetch.hip, still exported as kvip_hip_select_fetch): the separate gather
 // launch is balanced by the hardware dispatcher, while the fused one waits for its
 // slowest workgroup.

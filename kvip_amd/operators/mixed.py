@@ -4,7 +4,7 @@ The reference's vLLM selector runs a mixed batch as: Index ingest of the round's
 (python/kvip/adapters/vllm/selector.py:102-106 -> index_import.py:17-56), the fused LIFetch
 forward for the decode rows (:110-112) and the native prefill indexer for each prefill
 chunk (:126-154). `MixedRound` enqueues the same three stages on the current stream with
-buffers bound once, so the whole round is one hipGraph:
+buffers bound once, so the whole round is one hipGraph (config 5):
 
   1. one list-mode `kvip_hip_ingest_index` launch copies every new token's index-K row and
      scale from the paged cache (`sources`: cache row = block * 128 + offset) to its Index
@@ -22,13 +22,13 @@ buffers bound once, so the whole round is one hipGraph:
 
 The prefill stage reads only the paged cache and its own buffers, so it runs on a second
 stream joined at the round's end (`overlap=True`, the default), forked at the point
-`prefill_after` names: "resolve" (default for a resident decode: once the decode's scoring,
-TopK and resolve are enqueued, so its MFMA-bound scoring overlaps the PCIe-bound Fetch, the
-Index update and the LRU commit and leaves the compute units to the short decode kernels
-before them; two prefill workgroups fill a CU's LDS, so a decode kernel queued behind them
-would wait for whole prefill workgroups), "scoring" (after the decode's scoring) or "start"
-(at the round's start, beside everything). The fork and join are events, so the round
-stays one capturable sequence on the caller's stream.
+`prefill_after` names: "start" (default: at the round's start, beside everything), "scoring"
+(after the decode's scoring is enqueued) or "resolve" (resident decode: after its scoring,
+TopK and resolve, so that the prefill overlaps only the PCIe-bound Fetch, the Index update
+and the LRU commit). On MI355X at config 5 the three measured 304, 310 and 312-320
+us per round: two prefill workgroups fill a CU's LDS, so the later fork points leave the
+short decode kernels alone but serialise the prefill behind them. The fork and join are
+events, so the round stays one capturable sequence on the caller's stream.
 
 The caller fills the per-round inputs in place before a launch or replay: decode Q /
 weights / lengths, the prefill buffers it bound, and `sources` / `targets` of the new
@@ -91,7 +91,7 @@ class MixedRound:
         self.overlap = overlap
         resident = getattr(decode, "resident", False)
         if prefill_after is None:
-            prefill_after = "resolve" if resident else "scoring"
+            prefill_after = "start"
         if prefill_after not in ("start", "scoring", "resolve"):
             raise ValueError(f"prefill_after must be 'start', 'scoring' or 'resolve' (got {prefill_after!r})")
         if prefill_after == "resolve" and not resident:

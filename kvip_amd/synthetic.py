@@ -5,7 +5,7 @@ reads: request context lengths, a shuffled block table, a paged index-K cache wi
 per-token scales, the index queries and head weights, and a paged KV cache of
 656-byte rows filled with random bytes (any misplaced byte is detectable).
 
-Configurations:
+Configurations (the benchmark configurations):
   c1: batch 4, ctx 4096, bf16 Q/K ~N(0,1), fp32 weights ~N(0,1)/8, no scales.
   c2: batch 64, ctx ~U{8192..32768}, fp8 e4m3 Q/K from N(0,1) (saturating cast),
       per-token key scale ~U(0.5, 2), fp32 weights ~N(0,1)/8, KV rows of 656 bytes.
@@ -160,7 +160,7 @@ def _filled_pool(torch, gen, owners, history, resident, device):
 def mixed_workload(torch, kvip, device, *, seed=2026, decode_ctx=None, history=65536, resident=16384,
                    prefill=((2048, 8192), (1536, 1536)), heads=64, lru=False, fill_pool=False, overlap=True,
                    prefill_after=None):
-    """BASELINE config 5 round: decode requests (one row each, contexts `decode_ctx`, default
+    """config 5 round: decode requests (one row each, contexts `decode_ctx`, default
     32 requests ~U[4096, 65536]) on the resident cache (owner Index rows of `history`
     positions, `resident` hot slots, misses from a pinned host pool) plus prefill chunks
     (q_len, k_len) packed TND-style against a paged index-K cache; every new token (the
@@ -293,7 +293,7 @@ def _bitmap_words(torch, slots, words):
 
 def lidu_workload(torch, device, *, seed=2026, batch=16, queries=4, budget=16384, cand=131072, hit=0.8,
                   query_overlap=0.9, num_layers=61, layer_id=7):
-    """Inputs of one kvip.lidu call in the reference argument order (BASELINE config 4
+    """Inputs of one kvip.lidu call in the reference argument order (config 4
     shape: `batch` MTP requests of `queries` rows, resident budget `budget` of a
     `cand`-token history). Every request owns a pool row holding a random resident set
     of `budget` history tokens; each TopK row takes `hit` of its tokens from the resident
@@ -355,7 +355,7 @@ def lidu_workload(torch, device, *, seed=2026, batch=16, queries=4, budget=16384
 
 def resident_workload(torch, kvip, device, *, seed=2026, batch=16, history=131072, resident=16384, q_rows=1,
                       heads=64, fill_pool=False, prefetch=None, overlap=True):
-    """BASELINE config 4 shape for the resident-cache round: `batch` requests, each owning
+    """config 4 shape for the resident-cache round: `batch` requests, each owning
     `history` Index rows (fp8 keys ~ random finite codes, scales U(0.5, 2)) and a hot
     cache of `resident` slots holding positions 0..resident-1; every row's KV lives in a
     pinned host pool (random bytes with fill_pool, the hot cache then holding each owner's

@@ -1,4 +1,4 @@
-"""GPU parity of the mixed continuous-batching round (kvip.MixedRound
+"""GPU parity of the mixed continuous-batching round (kvip.MixedRound, config 5
 shape at test size): Index ingest of the round's new tokens, resident decode LIFetch and
 prefill LI + TopK, captured as one hipGraph.
 

@@ -1,4 +1,4 @@
-"""GPU parity at the BASELINE configurations' own shapes, through the C ABI.
+"""GPU parity at the benchmark configurations' own shapes, through the C ABI.
 
 C1  batch 4, ctx 4096, bf16 Q/K, fp32 weights, no scales (the bench's c1 workload): the
     decode forward end to end. Every row scored by the oracle (1e-2 relative, > 99 %
