@@ -86,7 +86,7 @@
 extern "C" {
 #endif
 
-#define KVIP_HIP_ABI_VERSION 14u
+#define KVIP_HIP_ABI_VERSION 15u
 
 #define KVIP_TOPK 2048
 #define KVIP_BLOCK_TOKENS 128
@@ -600,6 +600,12 @@ uint32_t kvip_hip_indexer_decode_window(const KvipIndexerArgs* args, int32_t tok
 uint32_t kvip_hip_topk(const KvipTopkArgs* args, void* stream);
 uint32_t kvip_hip_fetch_gather(const KvipFetchArgs* args, void* stream);
 uint32_t kvip_hip_indexer_prefill(const KvipPrefillArgs* args, void* stream);
+/* kvip_hip_indexer_prefill on a grid of at most `workgroups` workgroups (0: one per work unit
+ * of 8 query rows x 4096 key positions, as kvip_hip_indexer_prefill) that stride over the
+ * units; same results. No reference counterpart: a launch shape for callers that run the
+ * prefill beside other kernels (a mixed decode + prefill round), where a grid of twice the
+ * CU count leaves the CUs that finish their units to the other kernels. */
+uint32_t kvip_hip_indexer_prefill_grid(const KvipPrefillArgs* args, int32_t workgroups, void* stream);
 uint32_t kvip_hip_lifetch_forward(const KvipLIFetchArgs* args, void* stream);
 /* The launch plan kvip_hip_lifetch_forward takes for these arguments (no launch, no device
  * access): KVIP_LIFETCH_PLAN_THREE (scoring, TopK, gather; rows of at most

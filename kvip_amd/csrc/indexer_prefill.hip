@@ -3,7 +3,8 @@
 // or bf16 Q/K.
 //
 // Work unit = (query block, context segment): 8 consecutive query rows of one sequence
-// against 4096 key positions. The workgroup's 4 waves own 2 query rows each and keep their
+// against 4096 key positions (one unit per workgroup, or a bounded grid whose workgroups
+// stride over the units, kvip_hip_indexer_prefill_grid). The workgroup's 4 waves own 2 query rows each and keep their
 // Q fragments and per-lane head weights (w'_h = w_h * qscale_h for the 32 heads a lane
 // reduces) in registers. The segment streams through LDS in 32 KiB chunks (256 fp8 or 128
 // bf16 tokens), double buffered: every wave issues direct-to-LDS 16-byte loads
@@ -22,6 +23,8 @@
 // sparse_mode 3) that the vLLM selector runs for prefill rows (python/kvip/adapters/vllm/
 // selector.py:126-154); the score formula is the decode one (op_kernel/indexer/
 // indexer_cube.h:161-322, indexer_score.h:384-426, score_common.h:66-97).
+#include <algorithm>
+
 #include "indexer_tile.h"
 #include "lds_async.h"
 
@@ -93,8 +96,18 @@ __global__ __launch_bounds__(kPfThreads, 3 - ELEM) void indexer_prefill_kernel(c
     if (tid == 0) s_prefix[p.sequences] = running;
     for (int i = tid; i < kPfBlockRows * 128; i += kPfThreads) (&s_hist[0][0])[i] = 0u;
     __syncthreads();
-    const int block = blockIdx.x;
-    if (block >= s_prefix[p.sequences]) return;  // uniform
+    // Work items (query block, segment), block-fastest: the launch holds one workgroup per
+    // item, or fewer that stride over them (a bounded grid, for callers that run other
+    // kernels beside the prefill: workgroups that run out of items free their CU instead
+    // of queueing more items behind the other kernels).
+    const int nb_items = p.rows / kPfBlockRows + p.sequences;
+    const int64_t n_items =
+        static_cast<int64_t>(nb_items) * ((p.max_blocks * kBlockTokens + kPfSegment - 1) / kPfSegment);
+    uint32_t err = 0;
+    for (int64_t item = blockIdx.x; item < n_items; item += gridDim.x) {
+    const int block = static_cast<int>(item) % nb_items;  // n_items <= 2^31 - 1 (validated)
+    const int segi = static_cast<int>(item) / nb_items;
+    if (block >= s_prefix[p.sequences]) continue;  // uniform
     int lo = 0, hi = p.sequences - 1;            // largest s with s_prefix[s] <= block
     while (lo < hi) {
         const int mid = (lo + hi + 1) >> 1;
@@ -115,13 +128,13 @@ __global__ __launch_bounds__(kPfThreads, 3 - ELEM) void indexer_prefill_kernel(c
         const bool live = j < q_len;
         rowi[q] = q0 + min(j, q_len - 1);
         vis[q] = live ? min(max(k_len - q_len + j + 1, 0), k_len) : 0;
-        if (live && blockIdx.y == 0 && lane == 0) p.row_valid[q0 + j] = vis[q];
+        if (live && segi == 0 && lane == 0) p.row_valid[q0 + j] = vis[q];
     }
     const int last = min(j0 + kPfBlockRows, q_len) - 1;
     const int vis_max = min(max(k_len - q_len + last + 1, 0), k_len);
-    const int seg0 = blockIdx.y * kPfSegment;
+    const int seg0 = segi * kPfSegment;
     const int seg_end = min(seg0 + kPfSegment, vis_max);
-    if (seg0 >= seg_end) return;  // uniform: nothing visible in this segment
+    if (seg0 >= seg_end) continue;  // uniform: nothing visible in this segment
     const int nchunks = (seg_end - seg0 + kPfChunk - 1) / kPfChunk;
 
     // Q fragments and head weights of the wave's rows.
@@ -152,7 +165,6 @@ __global__ __launch_bounds__(kPfThreads, 3 - ELEM) void indexer_prefill_kernel(c
     const int pages_k = (k_len + kBlockTokens - 1) / kBlockTokens;
     int my_page = 0;
     float my_ok = 0.0f;
-    uint32_t err = 0;
     if (lane < kPfPages) {
         const int pi = min(seg0 / kBlockTokens + lane, max(pages_k - 1, 0));
         const int id = p.block_table[static_cast<size_t>(seq) * p.max_blocks + pi];
@@ -312,13 +324,25 @@ __global__ __launch_bounds__(kPfThreads, 3 - ELEM) void indexer_prefill_kernel(c
         const uint32_t c = (s_hist[rq][bin >> 1] >> (16 * (bin & 1))) & 0xFFFFu;
         if (j < q_len && c != 0u) atomicAdd(&p.histogram[static_cast<size_t>(q0 + j) * 256 + bin], c);
     }
+    if (item + gridDim.x < n_items) {  // uniform: clear the row histograms for the next item
+        __syncthreads();
+        for (int i = tid; i < kPfBlockRows * 128; i += kPfThreads) (&s_hist[0][0])[i] = 0u;
+        __syncthreads();
+    }
+    }
     report(p.status, err);
 }
 
+// Work items: (query blocks bound) x (segments of the bound context).
+int64_t prefill_items(const KvipPrefillArgs& a) {
+    const int64_t blocks = a.rows / kPfBlockRows + a.sequences;  // bound on the per-sequence blocks
+    return blocks * ((static_cast<int64_t>(a.max_blocks) * kBlockTokens + kPfSegment - 1) / kPfSegment);
+}
+
 template <int ELEM, int HEADS>
-hipError_t launch_heads(const KvipPrefillArgs& a, hipStream_t stream) {
-    const int blocks = a.rows / kPfBlockRows + a.sequences;  // bound on the per-sequence blocks
-    const dim3 grid(blocks, (a.max_blocks * kBlockTokens + kPfSegment - 1) / kPfSegment);
+hipError_t launch_heads(const KvipPrefillArgs& a, int workgroups, hipStream_t stream) {
+    const int64_t items = prefill_items(a);
+    const dim3 grid(static_cast<unsigned>(workgroups > 0 ? std::min<int64_t>(items, workgroups) : items));
     if (a.weight_dtype == KVIP_DTYPE_BF16) {
         hipLaunchKernelGGL((indexer_prefill_kernel<ELEM, HEADS, true>), grid, dim3(kPfThreads), 0, stream, a);
     } else {
@@ -349,15 +373,15 @@ uint32_t validate_prefill(const KvipPrefillArgs* a) {
         (a->key_scale == nullptr || (a->scale_block_stride >= kBlockTokens && a->scale_block_stride % 4 == 0 &&
                                      (reinterpret_cast<uintptr_t>(a->key_scale) & 15u) == 0)) &&
         aligned16(a->query) && aligned16(a->keys) && aligned16(a->score_keys) &&
-        static_cast<int64_t>(a->rows / kPfBlockRows + a->sequences) <= 0x7FFFFFFF;
+        prefill_items(*a) <= 0x7FFFFFFF;
     return ok ? KVIP_OK : KVIP_ERR_INVALID;
 }
 
-hipError_t launch_prefill(const KvipPrefillArgs& a, hipStream_t stream) {
+hipError_t launch_prefill(const KvipPrefillArgs& a, hipStream_t stream, int workgroups) {
     if (a.qk_dtype == KVIP_DTYPE_BF16) {
-        return a.heads == 64 ? launch_heads<2, 64>(a, stream) : launch_heads<2, 32>(a, stream);
+        return a.heads == 64 ? launch_heads<2, 64>(a, workgroups, stream) : launch_heads<2, 32>(a, workgroups, stream);
     }
-    return a.heads == 64 ? launch_heads<1, 64>(a, stream) : launch_heads<1, 32>(a, stream);
+    return a.heads == 64 ? launch_heads<1, 64>(a, workgroups, stream) : launch_heads<1, 32>(a, workgroups, stream);
 }
 
 }  // namespace kvip
@@ -365,5 +389,12 @@ hipError_t launch_prefill(const KvipPrefillArgs& a, hipStream_t stream) {
 extern "C" uint32_t kvip_hip_indexer_prefill(const KvipPrefillArgs* args, void* stream) {
     const uint32_t rc = kvip::validate_prefill(args);
     if (rc != KVIP_OK) return rc;
-    return static_cast<uint32_t>(kvip::launch_prefill(*args, static_cast<hipStream_t>(stream)));
+    return static_cast<uint32_t>(kvip::launch_prefill(*args, static_cast<hipStream_t>(stream), 0));
+}
+
+extern "C" uint32_t kvip_hip_indexer_prefill_grid(const KvipPrefillArgs* args, int32_t workgroups, void* stream) {
+    const uint32_t rc = kvip::validate_prefill(args);
+    if (rc != KVIP_OK) return rc;
+    if (workgroups < 0) return KVIP_ERR_INVALID;
+    return static_cast<uint32_t>(kvip::launch_prefill(*args, static_cast<hipStream_t>(stream), workgroups));
 }

@@ -45,7 +45,7 @@ INDEX_DIM = 128
 
 class MixedRound:
     def __init__(self, torch, *, decode, prefill, storage_keys, storage_scales, cache_keys, cache_scales,
-                 new_tokens, status=None, lru=None, overlap=True, prefill_after=None):
+                 new_tokens, status=None, lru=None, overlap=True, prefill_after=None, prefill_workgroups=None):
         """decode: a LIFetch forward; prefill: a PrefillIndexer after `bind(...)`;
         storage_keys [owners, history, 128] (fp8 or uint8) and storage_scales
         [owners, history] float32: the persistent Index rows; cache_keys
@@ -99,6 +99,15 @@ class MixedRound:
         if prefill_after != "start" and not hasattr(decode, "after_scoring"):
             raise ValueError("the decode forward has no stage hooks: use prefill_after='start'")
         self.prefill_after = prefill_after
+        # The prefill's scoring grid beside the decode: twice the CU count (two prefill
+        # workgroups fill a CU's LDS), so that CUs whose workgroups run out of work units go
+        # to the decode kernels instead of to queued prefill workgroups; 0 = one workgroup
+        # per unit. In sequence (overlap=False) the prefill runs alone on its full grid.
+        if prefill_workgroups is None:
+            prefill_workgroups = 2 * torch.cuda.get_device_properties(dev).multi_processor_count if overlap else 0
+        if int(prefill_workgroups) < 0:
+            raise ValueError("prefill_workgroups must be >= 0")
+        self.prefill_workgroups = int(prefill_workgroups)
         self._forks = 0
         if overlap:
             # The prefill branch: its own stream (default priority) and the fork/join events.
@@ -114,7 +123,7 @@ class MixedRound:
         self.forked.record(main)
         self.side.wait_event(self.forked)
         with self.torch.cuda.stream(self.side):
-            self.prefill.score()
+            self.prefill.score(workgroups=self.prefill_workgroups)
             self.prefill.select()
         self.joined.record(self.side)
         self._forks += 1
@@ -124,7 +133,7 @@ class MixedRound:
         if not self.overlap:
             self.ingest()
             self.decode()
-            self.prefill.score()
+            self.prefill.score(workgroups=self.prefill_workgroups)
             return self.prefill.select()
         main = torch.cuda.current_stream(self.device)
         self._forks = 0

@@ -48,6 +48,10 @@ class PrefillIndexer:
         self.topk = torch.full((max_rows, TOPK), -1, dtype=torch.int32, device=dev)
         self.status = torch.zeros(1, dtype=torch.int32, device=dev)
         self.library = abi.load_library()
+        # Scoring grid: 0 = one workgroup per work unit (8 query rows x 4096 key positions);
+        # n > 0 = at most n workgroups striding over the units (kvip_hip_indexer_prefill_grid),
+        # for rounds that run other kernels beside the prefill.
+        self.workgroups = 0
 
     def __call__(self, query, weights, query_scale, key, key_scale, cu_seqlens_q, seq_lens_k, block_table):
         """query [rows, heads, 128] fp8 e4m3 or bf16; weights [rows, heads]; query_scale
@@ -108,10 +112,18 @@ class PrefillIndexer:
         self._bound = (query, weights, query_scale, key, key_scale, cu_seqlens_q, seq_lens_k, block_table)
         self._args, self._topk_args, self._rows = args, topk, rows
 
-    def score(self):
-        """Scoring launch: score keys, per-row visible lengths and high-byte histograms."""
-        abi.check(self.library.kvip_hip_indexer_prefill(ctypes.byref(self._args),
-                                                        abi.stream_handle(self.torch, self.device)), "prefill LI")
+    def score(self, workgroups=None):
+        """Scoring launch: score keys, per-row visible lengths and high-byte histograms.
+        workgroups: grid bound for this launch (None: self.workgroups)."""
+        stream = abi.stream_handle(self.torch, self.device)
+        workgroups = self.workgroups if workgroups is None else int(workgroups)
+        if workgroups < 0:
+            raise ValueError("workgroups must be >= 0")
+        if workgroups:
+            abi.check(self.library.kvip_hip_indexer_prefill_grid(ctypes.byref(self._args), workgroups, stream),
+                      "prefill LI")
+        else:
+            abi.check(self.library.kvip_hip_indexer_prefill(ctypes.byref(self._args), stream), "prefill LI")
 
     def select(self):
         """TopK-2048 launch over the scored rows (consumes and re-zeroes the histograms)."""

@@ -9,7 +9,7 @@ import ctypes
 from pathlib import Path
 
 LIBRARY = Path(__file__).resolve().parents[1] / "_lib" / "libkvip_hip.so"
-ABI_VERSION = 14
+ABI_VERSION = 15
 
 KVIP_OK = 0
 KVIP_ERR_INVALID = 100000
@@ -194,6 +194,7 @@ PROTOTYPES = {
     "kvip_hip_indexer_decode": ([ctypes.POINTER(IndexerArgs), _p], ctypes.c_uint32),
     "kvip_hip_indexer_decode_window": ([ctypes.POINTER(IndexerArgs), _i32, _i32, _p], ctypes.c_uint32),
     "kvip_hip_indexer_prefill": ([ctypes.POINTER(PrefillArgs), _p], ctypes.c_uint32),
+    "kvip_hip_indexer_prefill_grid": ([ctypes.POINTER(PrefillArgs), ctypes.c_int32, _p], ctypes.c_uint32),
     "kvip_hip_topk": ([ctypes.POINTER(TopkArgs), _p], ctypes.c_uint32),
     "kvip_hip_fetch_gather": ([ctypes.POINTER(FetchArgs), _p], ctypes.c_uint32),
     "kvip_hip_lifetch_forward": ([ctypes.POINTER(LIFetchArgs), _p], ctypes.c_uint32),

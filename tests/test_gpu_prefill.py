@@ -133,6 +133,38 @@ def test_prefill_histogram_before_topk(torch_gpu):
         assert np.array_equal(hist[r], np.bincount(keys[r, :v] >> 8, minlength=256)), r
 
 
+@pytest.mark.parametrize("qk,workgroups", [("fp8", 3), ("fp8", 64), ("bf16", 5)])
+def test_prefill_bounded_grid_equals_full_grid(torch_gpu, qk, workgroups):
+    """kvip_hip_indexer_prefill_grid: workgroups striding over the work units (fewer than the
+    units, several units each, across sequences and segments) give the full grid's keys,
+    visible lengths, histograms and TopK bit for bit."""
+    torch = torch_gpu
+    say(f"case prefill grid {qk} workgroups={workgroups}")
+    c = make_case(torch, q_lens=[37, 100, 9], k_lens=[3000, 9000, 40], heads=64, wdt=torch.float32, qscale=True,
+                  kscale=True, seed=23, qk=qk)
+    idx = kvip_amd.PrefillIndexer(torch, max_rows=c["rows"], max_context=c["max_ctx"], max_sequences=3,
+                                  device="cuda")
+    idx.bind(c["query"], c["weights"], c["query_scale"], c["keys"], c["key_scale"], c["cu"], c["kl"], c["table"])
+    results = []
+    for wg in (0, workgroups):
+        idx.score_keys.fill_(-1)
+        idx.row_valid.fill_(-1)
+        idx.score(workgroups=wg)
+        torch.cuda.synchronize()
+        vis = idx.row_valid.cpu().numpy()
+        keys = idx.score_keys.cpu().numpy().view(np.uint16)
+        hist = idx.histogram.cpu().numpy().copy()
+        top = idx.select().cpu().numpy()
+        torch.cuda.synchronize()
+        assert int(idx.status.item()) == 0
+        results.append((vis, [keys[r, :v].copy() for r, v in enumerate(vis)], hist, top))
+    (v0, k0, h0, t0), (v1, k1, h1, t1) = results
+    assert np.array_equal(v0, v1)
+    assert all(np.array_equal(a, b) for a, b in zip(k0, k1))
+    assert np.array_equal(h0, h1) and np.array_equal(t0, t1)
+    assert h0.sum() == v0.sum()
+
+
 def test_quant_lightning_indexer_wrapper(torch_gpu):
     """The native-call surface: TND rows, cumulative query lengths, [blocks,128,1,128] keys."""
     torch = torch_gpu
