@@ -604,7 +604,8 @@ def sfa_leg(torch, kvip_amd, device, seed, iters=20):
     return out
 
 
-def mixed_leg(torch, kvip_amd, device, seed, rounds=20, warm=4, sequential=False, prefill_after=None):
+def mixed_leg(torch, kvip_amd, device, seed, rounds=20, warm=4, sequential=False, prefill_after=None,
+              prefill_workgroups=None):
     """config 5: continuous-batching rounds captured as hipGraphs (CURSOR_ROUNDS_PER_GRAPH
     rounds per graph), each round: Index ingest of all new tokens (32 decode + 2048 + 1536 prefill rows), resident decode
     LIFetch for 32 requests (ctx ~U[4096, 65536], 16384 hot slots, misses from pinned host
@@ -612,11 +613,12 @@ def mixed_leg(torch, kvip_amd, device, seed, rounds=20, warm=4, sequential=False
     chunks (k_len 8192 and 1536). Consecutive replays are consecutive serving rounds on the
     evolving cache state: each picks its decode queries by a device cursor from a random
     walk (overlapping, drifting selections) and records its misses. prefill_after: where
-    the prefill stage forks off (MixedRound's default when None)."""
+    the prefill stage forks off; prefill_workgroups: its scoring grid (MixedRound's defaults
+    when None)."""
     from kvip_amd import synthetic
 
     wl = synthetic.mixed_workload(torch, kvip_amd, device, seed=seed, lru=True, overlap=not sequential,
-                                  prefill_after=prefill_after)
+                                  prefill_after=prefill_after, prefill_workgroups=prefill_workgroups)
     rnd = wl.round
     nd = len(wl.decode_ctx)
     n = warm + rounds + 1
@@ -645,6 +647,7 @@ def mixed_leg(torch, kvip_amd, device, seed, rounds=20, warm=4, sequential=False
             "decode_misses_per_round": round(miss, 1),
             "decode_hit_fraction": round(1.0 - miss / (nd * TOPK), 4), "rounds": rounds,
             "rounds_per_graph": CURSOR_ROUNDS_PER_GRAPH,
+            "prefill_workgroups": rnd.prefill_workgroups,
             "streams": "one" if sequential else (f"prefill forked after the decode's {rnd.prefill_after}"
                                                  if rnd.prefill_after != "start" else "prefill forked at the start")
                        + ("" if sequential else ", Fetch beside the Index update")}

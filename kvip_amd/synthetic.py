@@ -159,7 +159,7 @@ def _filled_pool(torch, gen, owners, history, resident, device):
 
 def mixed_workload(torch, kvip, device, *, seed=2026, decode_ctx=None, history=65536, resident=16384,
                    prefill=((2048, 8192), (1536, 1536)), heads=64, lru=False, fill_pool=False, overlap=True,
-                   prefill_after=None):
+                   prefill_after=None, prefill_workgroups=None):
     """config 5 round: decode requests (one row each, contexts `decode_ctx`, default
     32 requests ~U[4096, 65536]) on the resident cache (owner Index rows of `history`
     positions, `resident` hot slots, misses from a pinned host pool) plus prefill chunks
@@ -252,7 +252,7 @@ def mixed_workload(torch, kvip, device, *, seed=2026, decode_ctx=None, history=6
     forward = kvip.LIFetch(rot, upd)
     rnd = kvip.MixedRound(torch, decode=forward, prefill=pidx, storage_keys=keys, storage_scales=scales,
                           cache_keys=cache_keys, cache_scales=cache_scales, new_tokens=len(sources), lru=chains,
-                          overlap=overlap, prefill_after=prefill_after)
+                          overlap=overlap, prefill_after=prefill_after, prefill_workgroups=prefill_workgroups)
     rnd.sources.copy_(torch.tensor(sources, dtype=torch.int64))
     rnd.targets.copy_(torch.tensor(targets, dtype=torch.int64))
     return SimpleNamespace(round=rnd, rot=rot, update=upd, forward=forward, prefill=pidx, lru=chains, keys=keys,
