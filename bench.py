@@ -211,7 +211,7 @@ def _query_walk(torch, base, sets, seed, step=0.3):
     return out
 
 
-def _cursor_rounds(torch, body, warm, rounds, sets, per_graph=None):
+def _cursor_rounds(torch, body, warm, rounds, sets, per_graph=None, label="rounds"):
     """Consecutive rounds from one captured hipGraph of `per_graph` rounds: body(cursor)
     enqueues round `cursor` (a device int64 [1] that the graph then advances), reading that
     round's inputs and recording its outcome by device indexing. One eager round on a side
@@ -219,7 +219,8 @@ def _cursor_rounds(torch, body, warm, rounds, sets, per_graph=None):
     then rounds / per_graph back-to-back replays timed with HIP events on the launch stream
     (the rounds of a graph follow each other with no host launch between them, as a model's
     layers do inside its captured decode step); the cursor stays below `sets`, the number of
-    input sets the body indexes. Returns us per round."""
+    input sets the body indexes. Prints a progress line (`label`) to stderr. Returns us per
+    round."""
     per_graph = CURSOR_ROUNDS_PER_GRAPH if per_graph is None else per_graph
     if warm + rounds > sets:
         raise ValueError(f"{warm} + {rounds} rounds need as many input sets (have {sets})")
@@ -254,7 +255,9 @@ def _cursor_rounds(torch, body, warm, rounds, sets, per_graph=None):
         graph.replay()
     e1.record(stream)
     e1.synchronize()
-    return e0.elapsed_time(e1) * 1e3 / rounds
+    us = e0.elapsed_time(e1) * 1e3 / rounds
+    print(f"bench: {label} loop done ({us:.1f} us per round)", file=sys.stderr, flush=True)
+    return us
 
 
 def _pick(torch, inputs, cursor, dst):
@@ -366,7 +369,7 @@ def resident_leg(torch, kvip_amd, device, seed, rounds=24, warm=4, sequential=Fa
         upd.round()
         record(cursor)
 
-    round_us = _cursor_rounds(torch, round_body, warm, rounds, n)
+    round_us = _cursor_rounds(torch, round_body, warm, rounds, n, label="resident round")
     if upd.status.any():
         raise RuntimeError(f"resident round failed: {upd.status.cpu().tolist()}")
     round_miss = trace[warm:warm + rounds].sum(1).float().mean().item()
@@ -377,7 +380,7 @@ def resident_leg(torch, kvip_amd, device, seed, rounds=24, warm=4, sequential=Fa
         resident=resident)).to(device)
     trace.zero_()
     upd.overlap = False
-    seq_us = _cursor_rounds(torch, round_body, warm, rounds, n)
+    seq_us = _cursor_rounds(torch, round_body, warm, rounds, n, label="resident round in sequence")
     upd.overlap = not sequential
     if upd.status.any():
         raise RuntimeError(f"resident round failed: {upd.status.cpu().tolist()}")
@@ -391,7 +394,7 @@ def resident_leg(torch, kvip_amd, device, seed, rounds=24, warm=4, sequential=Fa
         fwd()
         record(cursor)
 
-    fwd_us = _cursor_rounds(torch, forward_body, warm, rounds, n)
+    fwd_us = _cursor_rounds(torch, forward_body, warm, rounds, n, label="resident forward")
     if upd.status.any() or rot.status.any():
         raise RuntimeError(f"resident forward failed: {upd.status.cpu().tolist()} {int(rot.status.item())}")
     fwd_miss = trace[warm:warm + rounds].sum(1).float().mean().item()
@@ -425,7 +428,7 @@ def resident_leg(torch, kvip_amd, device, seed, rounds=24, warm=4, sequential=Fa
         fwd2()
         trace2.index_copy_(0, cursor, torch.stack([upd2.miss_counts[:, 4], upd2.prefetch_counts]).view(1, 2, batch))
 
-    pf_us = _cursor_rounds(torch, prefetch_body, warm, rounds, n)
+    pf_us = _cursor_rounds(torch, prefetch_body, warm, rounds, n, label="resident prefetch forward")
     if upd2.status.any() or rot2.status.any():
         raise RuntimeError(f"resident prefetch forward failed: {upd2.status.cpu().tolist()}")
     pf_trace = trace2[warm:warm + rounds].sum(2).float().mean(0).tolist()
@@ -631,7 +634,7 @@ def mixed_leg(torch, kvip_amd, device, seed, rounds=20, warm=4, sequential=False
         rnd()
         trace.index_copy_(0, cursor, wl.update.miss_counts[:, 4].view(1, nd))
 
-    us = _cursor_rounds(torch, body, warm, rounds, n)
+    us = _cursor_rounds(torch, body, warm, rounds, n, label="mixed round")
     for st in (wl.update.status, wl.rot.status, wl.prefill.status, rnd.status):
         if st.any():
             raise RuntimeError(f"mixed round: device status {st.cpu().tolist()}")
