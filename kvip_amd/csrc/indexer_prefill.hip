@@ -16,7 +16,7 @@
 // epilogue is the decode kernel's: ReLU, head weights, head reduction, key scale, bf16
 // half-away rounding, sortable key; keys go through a per-wave LDS strip to coalesced
 // stores, and a per-workgroup 256-bin histogram of the key high byte (two 16-bit counters
-// per word) is added to the row histograms at the end. bf16 holds twice the Q fragment
+// per word: bins b and b + 128) is added to the row histograms at the end. bf16 holds twice the Q fragment
 // registers, so its kernel runs one workgroup (one wave per SIMD) per CU.
 //
 // Reference: the native prefill LI (torch_npu.npu_quant_lightning_indexer, TND layout,
@@ -73,7 +73,7 @@ __global__ __launch_bounds__(kPfThreads, 3 - ELEM) void indexer_prefill_kernel(c
     __shared__ __align__(16) uint8_t s_k[2][kPfChunkBytes];
     __shared__ __align__(16) float s_ks[2][kPfChunk];
     __shared__ __align__(16) uint16_t s_keys[kPfWaves][kPfRowsPerWave][kPfChunk];
-    __shared__ uint32_t s_hist[kPfBlockRows][128];  // two 16-bit counters per word
+    __shared__ uint32_t s_hist[kPfBlockRows][128];  // bins b (low half) and b + 128 (high half)
     __shared__ int s_prefix[kPfMaxSeq + 1];
     __shared__ uint32_t s_scan[kPfWaves];
 
@@ -296,8 +296,10 @@ __global__ __launch_bounds__(kPfThreads, 3 - ELEM) void indexer_prefill_kernel(c
             const uint32_t key = sortable_key(bf16_bits_half_away(total * ks));
             lds_write_b16(keya + k * 64, key);
             if (t0 + n < vis_mine) {
+                // Bins b and b ^ 128 share a word: the populated bins of a row are adjacent
+                // and would otherwise serialise on one word's atomics.
                 const uint32_t bin = key >> 8;
-                lds_add_u32(hista + (bin >> 1) * 4, 1u << (16 * (bin & 1)));
+                lds_add_u32(hista + (bin & 127) * 4, 1u << (16 * (bin >> 7)));
             }
         }
         // Flush the chunk's keys of the wave's rows (8-byte stores, inside the row stride).
@@ -321,7 +323,7 @@ __global__ __launch_bounds__(kPfThreads, 3 - ELEM) void indexer_prefill_kernel(c
         const int rq = i >> 8;
         const int bin = i & 255;
         const int j = j0 + rq;
-        const uint32_t c = (s_hist[rq][bin >> 1] >> (16 * (bin & 1))) & 0xFFFFu;
+        const uint32_t c = (s_hist[rq][bin & 127] >> (16 * (bin >> 7))) & 0xFFFFu;
         if (j < q_len && c != 0u) atomicAdd(&p.histogram[static_cast<size_t>(q0 + j) * 256 + bin], c);
     }
     if (item + gridDim.x < n_items) {  // uniform: clear the row histograms for the next item
