@@ -62,8 +62,9 @@ KVIP_DEVICE RowSelection select_row(const uint32_t (&kk)[KPT / 2], int count, in
     constexpr int M = (KPT + 31) / 32;  // 32-key mask words per thread
     const int lane = lane_id();
     auto key_at = [&](int j) -> uint32_t { return (j & 1) ? (kk[j >> 1] >> 16) : (kk[j >> 1] & 0xFFFFu); };
-    // 1. Low-byte histogram of the live keys in bin hb.
-    if (hb >= 0) {
+    // 1. Low-byte histogram of the live keys in bin hb (threads past the row's end skip
+    // their key loops).
+    if (hb >= 0 && count > 0) {
 #pragma unroll
         for (int j = 0; j < KPT; ++j) {
             const uint32_t k = key_at(j);
@@ -92,12 +93,14 @@ KVIP_DEVICE RowSelection select_row(const uint32_t (&kk)[KPT / 2], int count, in
         gtm[m] = 0u;
         eqm[m] = 0u;
     }
+    if (count > 0) {
 #pragma unroll
-    for (int j = 0; j < KPT; ++j) {
-        const uint32_t k = key_at(j);
-        const bool live = j < count;
-        gtm[j >> 5] |= (live && k > r.kth) ? (1u << (j & 31)) : 0u;
-        eqm[j >> 5] |= (live && k == r.kth) ? (1u << (j & 31)) : 0u;
+        for (int j = 0; j < KPT; ++j) {
+            const uint32_t k = key_at(j);
+            const bool live = j < count;
+            gtm[j >> 5] |= (live && k > r.kth) ? (1u << (j & 31)) : 0u;
+            eqm[j >> 5] |= (live && k == r.kth) ? (1u << (j & 31)) : 0u;
+        }
     }
     uint32_t ngt = 0, neq = 0;
 #pragma unroll

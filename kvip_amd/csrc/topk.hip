@@ -178,52 +178,67 @@ __global__ __launch_bounds__(THREADS) void topk_regs_kernel(const KvipTopkArgs p
         return;
     }
 
-    // Keys of this thread; positions >= valid are excluded by `count`. Every vector load
-    // is unconditional: its start is clamped into the row (the row stride is a multiple
-    // of 8 keys).
+    // Keys of this thread; positions >= valid are excluded by `count`, and threads whose
+    // keys all lie past the row's end load nothing (a row's valid length is often well
+    // below the stride the kernel is sized for). A load's start is clamped into the row
+    // (the row stride is a multiple of 8 keys).
     const int first = tid * KPT;
     const int count = max(0, min(KPT, valid - first));
     uint32_t kk[W];
 #pragma unroll
-    for (int v = 0; v < W / 4; ++v) {
-        const int at = min(first + v * 8, p.key_stride - 8);
-        const v4i x = *reinterpret_cast<const v4i*>(keys + at);
-        kk[4 * v] = x[0];
-        kk[4 * v + 1] = x[1];
-        kk[4 * v + 2] = x[2];
-        kk[4 * v + 3] = x[3];
+    for (int v = 0; v < W; ++v) kk[v] = 0u;
+    if (count > 0) {
+#pragma unroll
+        for (int v = 0; v < W / 4; ++v) {
+            const int at = min(first + v * 8, p.key_stride - 8);
+            const v4i x = *reinterpret_cast<const v4i*>(keys + at);
+            kk[4 * v] = x[0];
+            kk[4 * v + 1] = x[1];
+            kk[4 * v + 2] = x[2];
+            kk[4 * v + 3] = x[3];
+        }
     }
 
-    // High-byte bin of the 2048th largest key.
-    v4i hv;
-    if (ghist != nullptr) {
-        hv = *reinterpret_cast<const v4i*>(ghist + lane * 4);  // every wave reads all 256 bins
-    } else {
+    // High-byte bin of the 2048th largest key: wave 0 reads the 256 bins (from the
+    // scoring histogram, or one built here) and shares the bin through LDS.
+    __shared__ uint32_t s_bin[3];
+    if (ghist == nullptr) {
         if (tid < 256) s_hist[tid] = 0u;
         __syncthreads();
+        if (count > 0) {
 #pragma unroll
-        for (int j = 0; j < KPT; ++j) {
-            const uint32_t k = (j & 1) ? (kk[j >> 1] >> 16) : (kk[j >> 1] & 0xFFFFu);
-            wave_hist_add(s_hist, k >> 8, j < count);
+            for (int j = 0; j < KPT; ++j) {
+                const uint32_t k = (j & 1) ? (kk[j >> 1] >> 16) : (kk[j >> 1] & 0xFFFFu);
+                wave_hist_add(s_hist, k >> 8, j < count);
+            }
         }
         __syncthreads();
-        hv = *reinterpret_cast<const v4i*>(s_hist + lane * 4);
-        __syncthreads();  // every wave has its copy before the bins are cleared below
     }
-    const uint32_t h[4] = {static_cast<uint32_t>(hv[0]), static_cast<uint32_t>(hv[1]), static_cast<uint32_t>(hv[2]),
-                           static_cast<uint32_t>(hv[3])};
-    int hb;
-    uint32_t gt_hi;
-    wave_select_bin(h, kTopK, hb, gt_hi);
-    // The scoring histogram counts every visible key once: a total other than `valid`
-    // means the scoring launch skipped or repeated tiles.
-    const uint32_t hist_total =
-        static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(wave_inclusive_scan(h[0] + h[1] + h[2] + h[3])), 63));
-    const bool counted = hist_total == static_cast<uint32_t>(valid);
+    if (tid < 64) {
+        const v4i hv = *reinterpret_cast<const v4i*>((ghist != nullptr ? ghist : s_hist) + lane * 4);
+        const uint32_t h[4] = {static_cast<uint32_t>(hv[0]), static_cast<uint32_t>(hv[1]),
+                               static_cast<uint32_t>(hv[2]), static_cast<uint32_t>(hv[3])};
+        int hb0;
+        uint32_t gt0;
+        wave_select_bin(h, kTopK, hb0, gt0);
+        // The scoring histogram counts every visible key once: a total other than
+        // `valid` means the scoring launch skipped or repeated tiles.
+        const uint32_t hist_total = static_cast<uint32_t>(
+            __builtin_amdgcn_readlane(static_cast<int>(wave_inclusive_scan(h[0] + h[1] + h[2] + h[3])), 63));
+        if (lane == 0) {
+            s_bin[0] = static_cast<uint32_t>(hb0);
+            s_bin[1] = gt0;
+            s_bin[2] = hist_total == static_cast<uint32_t>(valid) ? 1u : 0u;
+        }
+    }
+    if (ghist == nullptr) __syncthreads();  // wave 0 has read the bins before they are cleared
     if (tid < 256) s_hist[tid] = 0u;
     for (int i = tid; i < kTopK / 2; i += THREADS) reinterpret_cast<int2*>(s_out)[i] = int2{-1, -1};
     __syncthreads();
-    if (ghist != nullptr && tid < 256) ghist[tid] = 0u;  // read by every wave: ready for the next scoring launch
+    if (ghist != nullptr && tid < 256) ghist[tid] = 0u;  // read by wave 0: ready for the next scoring launch
+    const int hb = static_cast<int>(s_bin[0]);
+    const uint32_t gt_hi = s_bin[1];
+    const bool counted = s_bin[2] != 0u;
 
     const RowSelection sel =
         select_row<KPT>(kk, count, first, hb, gt_hi, s_hist, s_wave, [&](int pos, int tok) { s_out[pos] = tok; });
