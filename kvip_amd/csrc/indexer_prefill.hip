@@ -4,20 +4,21 @@
 //
 // Work unit = (query block, context segment): 8 consecutive query rows of one sequence
 // against 4096 key positions (one unit per workgroup, or a bounded grid whose workgroups
-// stride over the units, kvip_hip_indexer_prefill_grid). The workgroup's 4 waves own 2 query rows each and keep their
+// stride over the units, kvip_hip_indexer_prefill_grid). fp8: 4 waves own 2 query rows
+// each; bf16 (Q fragments twice as large): 8 waves own one row each. A wave keeps its rows'
 // Q fragments and per-lane head weights (w'_h = w_h * qscale_h for the 32 heads a lane
 // reduces) in registers. The segment streams through LDS in 32 KiB chunks (256 fp8 or 128
 // bf16 tokens), double buffered: every wave issues direct-to-LDS 16-byte loads
-// (global_load_lds_dwordx4) for a quarter of the next chunk, with the XOR swizzle applied
+// (global_load_lds_dwordx4) for its share of the next chunk, with the XOR swizzle applied
 // on the global side so that the fragment reads (lane n of a 32-token tile reads row n)
 // hit distinct bank groups. Each chunk tile (32 tokens) is one B fragment set read once
-// from LDS and reused by the wave's 2 rows x 2 head tiles: 2 K slices each of
+// from LDS and reused by the wave's rows x 2 head tiles: 2 K slices each of
 // v_mfma_scale_f32_32x32x64_f8f6f4 (fp8) or 8 of v_mfma_f32_32x32x16_bf16 (bf16). The
 // epilogue is the decode kernel's: ReLU, head weights, head reduction, key scale, bf16
 // half-away rounding, sortable key; keys go through a per-wave LDS strip to coalesced
 // stores, and a per-workgroup 256-bin histogram of the key high byte (two 16-bit counters
-// per word: bins b and b + 128) is added to the row histograms at the end. bf16 holds twice the Q fragment
-// registers, so its kernel runs one workgroup (one wave per SIMD) per CU.
+// per word: bins b and b + 128) is added to the row histograms at the end. fp8 runs two
+// workgroups per CU, bf16 one (two waves per SIMD either way).
 //
 // Reference: the native prefill LI (torch_npu.npu_quant_lightning_indexer, TND layout,
 // sparse_mode 3) that the vLLM selector runs for prefill rows (python/kvip/adapters/vllm/
@@ -31,10 +32,17 @@
 namespace kvip {
 namespace {
 
-constexpr int kPfWaves = 4;
-constexpr int kPfThreads = kPfWaves * 64;
-constexpr int kPfRowsPerWave = 2;                           // one row per lane half at the finish
-constexpr int kPfBlockRows = kPfWaves * kPfRowsPerWave;     // 8 query rows per workgroup
+constexpr int kPfBlockRows = 8;                             // query rows per workgroup
+// Waves per workgroup and query rows per wave: fp8 runs 4 waves of 2 rows (one row per lane
+// half at the finish) and two workgroups per CU; bf16 Q fragments are twice as large, so it
+// runs 8 waves of 1 row, which keeps a wave under 256 registers and gives two waves per SIMD
+// in the one workgroup per CU.
+template <int ELEM>
+struct PfShape {
+    static constexpr int kWaves = ELEM == 1 ? 4 : 8;
+    static constexpr int kRows = kPfBlockRows / kWaves;
+    static constexpr int kThreads = kWaves * 64;
+};
 constexpr int kPfChunkBytes = 256 * kIndexDim;             // 32 KiB of K rows per LDS chunk
 constexpr int kPfSegment = 4096;                            // key positions per workgroup
 constexpr int kPfPages = kPfSegment / kBlockTokens;         // 32
@@ -58,7 +66,10 @@ KVIP_DEVICE float pf_weight(const KvipPrefillArgs& p, size_t idx) {
 }
 
 template <int ELEM, int HEADS, bool W_BF16>
-__global__ __launch_bounds__(kPfThreads, 3 - ELEM) void indexer_prefill_kernel(const KvipPrefillArgs p) {
+__global__ __launch_bounds__(PfShape<ELEM>::kThreads, 3 - ELEM) void indexer_prefill_kernel(const KvipPrefillArgs p) {
+    constexpr int kPfWaves = PfShape<ELEM>::kWaves;
+    constexpr int kPfRowsPerWave = PfShape<ELEM>::kRows;
+    constexpr int kPfThreads = PfShape<ELEM>::kThreads;
     constexpr int MT = HEADS / 32;
     constexpr int NV = Mma<ELEM>::NV;              // 16-byte pieces of a half row per lane
     constexpr int STEPS = Mma<ELEM>::STEPS;        // MFMAs per 128-dim contraction
@@ -68,8 +79,9 @@ __global__ __launch_bounds__(kPfThreads, 3 - ELEM) void indexer_prefill_kernel(c
     constexpr int kPfTiles = kPfChunk / 32;
     constexpr int kChunkPages = kPfChunk / kBlockTokens;  // pages per chunk (2 or 1)
     constexpr int kRowsPerLoad = 64 / kPieces;     // K rows one 64-lane 16-byte load fills
-    static_assert(kPfRowsPerWave == 2, "the finish maps row q to lane half q");
-    static_assert((kPfChunk / kPfWaves) / kRowsPerLoad == 8, "8 staging loads per wave and chunk");
+    static_assert(kPfRowsPerWave == 1 || kPfRowsPerWave == 2, "the finish maps row q to lane half q");
+    constexpr int kStageLoads = (kPfChunk / kPfWaves) / kRowsPerLoad;  // staging loads per wave and chunk
+    static_assert(kStageLoads * kRowsPerLoad * kPfWaves == kPfChunk, "whole staging loads");
     __shared__ __align__(16) uint8_t s_k[2][kPfChunkBytes];
     __shared__ __align__(16) float s_ks[2][kPfChunk];
     __shared__ __align__(16) uint16_t s_keys[kPfWaves][kPfRowsPerWave][kPfChunk];
@@ -181,7 +193,7 @@ __global__ __launch_bounds__(kPfThreads, 3 - ELEM) void indexer_prefill_kernel(c
     auto stage = [&](int c, int buf) {
         const int pg = __builtin_amdgcn_readlane(my_page, c * kChunkPages + (wave * kWaveRows) / kBlockTokens);
 #pragma unroll
-        for (int v = 0; v < 8; ++v) {
+        for (int v = 0; v < kStageLoads; ++v) {
             const int row = wave * kWaveRows + v * kRowsPerLoad + lane / kPieces;
             const int piece = (lane % kPieces) ^ pf_swizzle<ELEM>(row);
             const uint8_t* src = kbase + static_cast<size_t>(pg) * p.key_block_stride +
@@ -204,15 +216,24 @@ __global__ __launch_bounds__(kPfThreads, 3 - ELEM) void indexer_prefill_kernel(c
         __syncthreads();
     }
 
-    const int vis_mine = g == 0 ? vis[0] : vis[1];          // this lane half's row
-    const int hist_row = wave * kPfRowsPerWave + g;
+    // This lane half's row (one row per wave: the row of both halves; its keys and
+    // histogram come from lanes 0-31).
+    int vis_mine, vis_max_wave;
+    if constexpr (kPfRowsPerWave == 2) {
+        vis_mine = g == 0 ? vis[0] : vis[1];
+        vis_max_wave = max(vis[0], vis[1]);
+    } else {
+        vis_mine = g == 0 ? vis[0] : 0;
+        vis_max_wave = vis[0];
+    }
+    const int hist_row = wave * kPfRowsPerWave + (kPfRowsPerWave == 2 ? g : 0);
     // Per-lane LDS addresses: the tile row's four swizzled K pieces (the swizzle of row
     // k*32 + n does not depend on k), its key scale, and the key strip slots.
     uint32_t ka[NV];
 #pragma unroll
     for (int u = 0; u < NV; ++u) ka[u] = lds_addr(&s_k[0][n * kRowBytes + (((g * NV + u) ^ pf_swizzle<ELEM>(n)) * 16)]);
     const uint32_t ksa = lds_addr(&s_ks[0][n]);
-    const uint32_t keya = lds_addr(&s_keys[wave][g][n]);
+    const uint32_t keya = lds_addr(&s_keys[wave][kPfRowsPerWave == 2 ? g : 0][n]);
     const uint32_t hista = lds_addr(&s_hist[hist_row][0]);
     constexpr uint32_t kKBuf = kPfChunkBytes;          // bytes between the two K buffers
     constexpr uint32_t kSBuf = kPfChunk * 4;           // bytes between the two scale buffers
@@ -231,7 +252,7 @@ __global__ __launch_bounds__(kPfThreads, 3 - ELEM) void indexer_prefill_kernel(c
 #pragma unroll 1
         for (int k = 0; k < kPfTiles; ++k) {
             const int t0 = cstart + k * 32;
-            if (t0 >= vis[0] && t0 >= vis[1]) break;  // uniform per wave: later tiles are masked too
+            if (t0 >= vis_max_wave) break;  // uniform per wave: later tiles are masked too
             v4i kb[NV];
             float ks_raw;
             const uint32_t toff = buf * kKBuf + k * 32 * kRowBytes;
@@ -284,17 +305,21 @@ __global__ __launch_bounds__(kPfThreads, 3 - ELEM) void indexer_prefill_kernel(c
                     __builtin_amdgcn_sched_barrier(0);
                 }
             }
-            // Both rows finish together: after the swap, lanes 0-31 hold row 0's total for
+            // Two rows finish together: after the swap, lanes 0-31 hold row 0's total for
             // token n and lanes 32-63 row 1's (each the sum of the two lane halves' heads).
+            // One row: both halves hold its total.
             const float part0 = (pj[0][0] + pj[0][1]) + (pj[0][2] + pj[0][3]);
-            const float part1 = (pj[1][0] + pj[1][1]) + (pj[1][2] + pj[1][3]);
-            const float mine = g == 0 ? part0 : part1;
-            const float other = g == 0 ? part1 : part0;
+            float mine = part0, other = part0;
+            if constexpr (kPfRowsPerWave == 2) {
+                const float part1 = (pj[1][0] + pj[1][1]) + (pj[1][2] + pj[1][3]);
+                mine = g == 0 ? part0 : part1;
+                other = g == 0 ? part1 : part0;
+            }
             const auto swapped =
                 __builtin_amdgcn_permlane32_swap(__float_as_int(other), __float_as_int(other), false, false);
             const float total = mine + __int_as_float(g == 0 ? swapped[1] : swapped[0]);
             const uint32_t key = sortable_key(bf16_bits_half_away(total * ks));
-            lds_write_b16(keya + k * 64, key);
+            if (kPfRowsPerWave == 2 || g == 0) lds_write_b16(keya + k * 64, key);
             if (t0 + n < vis_mine) {
                 // Bins b and b ^ 128 share a word: the populated bins of a row are adjacent
                 // and would otherwise serialise on one word's atomics.
@@ -346,9 +371,11 @@ hipError_t launch_heads(const KvipPrefillArgs& a, int workgroups, hipStream_t st
     const int64_t items = prefill_items(a);
     const dim3 grid(static_cast<unsigned>(workgroups > 0 ? std::min<int64_t>(items, workgroups) : items));
     if (a.weight_dtype == KVIP_DTYPE_BF16) {
-        hipLaunchKernelGGL((indexer_prefill_kernel<ELEM, HEADS, true>), grid, dim3(kPfThreads), 0, stream, a);
+        hipLaunchKernelGGL((indexer_prefill_kernel<ELEM, HEADS, true>), grid, dim3(PfShape<ELEM>::kThreads), 0, stream,
+                           a);
     } else {
-        hipLaunchKernelGGL((indexer_prefill_kernel<ELEM, HEADS, false>), grid, dim3(kPfThreads), 0, stream, a);
+        hipLaunchKernelGGL((indexer_prefill_kernel<ELEM, HEADS, false>), grid, dim3(PfShape<ELEM>::kThreads), 0, stream,
+                           a);
     }
     return hipGetLastError();
 }
