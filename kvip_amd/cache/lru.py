@@ -6,8 +6,9 @@ committed prefix shrinks or starts); `commit(destinations)` moves the unique des
 slots below `active` to the most-recent end in ascending slot-id order. After each call
 `slots` ([1, 2048] int32) holds the min(2048, active) least recently used slots, oldest
 first, -1 padded, and `bitmap` ([1, words] int32, words rounded up to a multiple of 8) their
-membership bits. State lives on the device as the LRU order array, so `commit` takes a
-device tensor and enqueues on the current stream without a host sync (graph-capturable).
+membership bits. State lives on the device as the LRU order array: `commit` of a device
+int32 tensor enqueues on the current stream without a host sync (graph-capturable); host
+arrays (the reference's numpy call) are copied to the device first.
 """
 from __future__ import annotations
 
@@ -81,14 +82,25 @@ class SlotLRU:
             self.version += 1
 
     def commit(self, destinations):
-        """Consume the accessed slots (a device int32 tensor); slots outside [0, active) are
-        ignored, as ABC hits do not enter the chain (lru.py:96-118)."""
+        """Consume the accessed slots; slots outside [0, active) are ignored, as ABC hits do
+        not enter the chain (lru.py:96-118). `destinations` is a contiguous int32 tensor on
+        the LRU's device (enqueued without a host sync, graph-capturable) or, as the
+        reference takes it, any integer array or tensor elsewhere, which is first copied to
+        the device as int32 (a blocking copy)."""
         torch = self.torch
         if self.active == 0:
             return
-        if not isinstance(destinations, torch.Tensor) or destinations.device != self.device \
-                or destinations.dtype != torch.int32 or not destinations.is_contiguous():
-            raise ValueError("SlotLRU.commit takes a contiguous int32 tensor on the LRU's device")
+        if not isinstance(destinations, torch.Tensor):
+            import numpy as np
+
+            arr = np.asarray(destinations)
+            if arr.dtype.kind not in "iu":
+                raise ValueError("SlotLRU.commit takes integer slot ids")
+            destinations = torch.from_numpy(np.ascontiguousarray(arr.reshape(-1), dtype=np.int32))
+        elif destinations.dtype.is_floating_point or destinations.dtype.is_complex or destinations.dtype == torch.bool:
+            raise ValueError("SlotLRU.commit takes integer slot ids")
+        if destinations.device != self.device or destinations.dtype != torch.int32 or not destinations.is_contiguous():
+            destinations = destinations.reshape(-1).to(device=self.device, dtype=torch.int32).contiguous()
         lib = abi.load_library()
         abi.check(lib.kvip_hip_lru_commit(ctypes.byref(self._args), abi.ptr(destinations), destinations.numel(),
                                           self.active, self._stream()), "SlotLRU commit")

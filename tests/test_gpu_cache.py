@@ -101,7 +101,9 @@ def test_slot_lru_matches_oracle(torch_gpu):
             cpu.resize(40000, 30000)
         else:
             dest = rng.integers(-3, cpu.active + 20, int(rng.integers(0, 9000))).astype(np.int32)
-            gpu.commit(torch.from_numpy(dest).cuda())
+            # Device int32 tensors, and the reference's host numpy call (int32 / int64).
+            host = dest if step % 3 == 1 else dest.astype(np.int64)
+            gpu.commit(host if step % 3 else torch.from_numpy(dest).cuda())
             cpu.commit(dest)
         torch.cuda.synchronize()
         check_lru(torch, gpu, cpu)
