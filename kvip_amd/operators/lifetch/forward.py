@@ -41,6 +41,7 @@ class LIFetchForward:
             raise ValueError("Fetch and Index update must use the same device")
         self.rotating, self.update, self.torch = rotating, update, rotating.torch
         self.library = abi.load_library()
+        self.set_options()
         # Called with the launch stream right after the round's scoring is enqueued; None:
         # nothing (the point from which a caller may fork work that should overlap the TopK
         # and what follows rather than the HBM-bound scoring).
@@ -103,6 +104,27 @@ class LIFetchForward:
         if self.topk_args.histogram and self.topk_args.key_stride <= abi.TOPK_REGS_MAX_KEYS:
             self.topk_args.segments = 0
         self._topk_fwd = ctypes.byref(self.topk_args)
+
+    def set_options(self, *, diagnostics=False, deferred_fetch=False):
+        """The reference's start-up option call (python/kvip/operators/lifetch/streaming.py:
+        133-146, made with the defaults by forward.py:17 and by the test harness's
+        set_deferred_fetch / set_diagnostics, tests/operators/lifetch/support/
+        execution.py:3753-3757). Like the reference it touches no device memory and never
+        runs inside forward().
+
+        deferred_fetch: recorded and accepted either way. The reference packs it as bit 30 of
+        its workspace option word, and no kernel of the reference reads that bit, so it
+        changes no launched work there and none here.
+        diagnostics: only False. True asks for the reference's in-kernel cycle stamps (bit
+        31, read back through its `times` tensor), which this build does not record: per-
+        kernel timings come from rocprofv3 and HIP events instead, so it raises ValueError
+        rather than leaving a caller to read stamps that were never written."""
+        if type(diagnostics) is not bool or type(deferred_fetch) is not bool:
+            raise ValueError("set_options takes bool diagnostics and deferred_fetch")
+        if diagnostics:
+            raise ValueError("diagnostics=True: in-kernel cycle stamps are not recorded by this build "
+                             "(profile the launches with rocprofv3 or HIP events)")
+        self.diagnostics, self.deferred_fetch = diagnostics, deferred_fetch
 
     def _stream(self):
         return abi.stream_handle(self.torch, self.rotating.device)

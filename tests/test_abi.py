@@ -156,6 +156,32 @@ def test_binding_validation_cpu():
         rot.indexer_args()
 
 
+def test_forward_set_options_cpu():
+    """LIFetch.set_options keeps the reference's keyword-only call
+    (python/kvip/operators/lifetch/streaming.py:133): construction applies the defaults,
+    deferred_fetch is recorded, diagnostics=True (in-kernel cycle stamps) and non-bool
+    values are refused; nothing is launched."""
+    torch = pytest.importorskip("torch")
+    import kvip_amd
+
+    rot = kvip_amd.LIFetchBinding(torch, batch=2, max_context=4096, device="cpu")
+    rot.bind_index_cache(torch.zeros((rot.batch * rot.max_blocks, 128, 128), dtype=torch.float8_e4m3fn))
+    upd = kvip_amd.ContiguousFetch(torch, rot, torch.zeros((rot.batch * rot.max_blocks, 128, 656), dtype=torch.uint8))
+    fwd = kvip_amd.LIFetch(rot, upd)
+    assert (fwd.diagnostics, fwd.deferred_fetch) == (False, False)
+    fwd.set_options(deferred_fetch=True)
+    assert fwd.deferred_fetch is True
+    fwd.set_options()
+    assert fwd.deferred_fetch is False
+    with pytest.raises(ValueError):
+        fwd.set_options(diagnostics=True)
+    with pytest.raises(ValueError):
+        fwd.set_options(deferred_fetch=1)
+    with pytest.raises(TypeError):
+        fwd.set_options(True)
+    assert fwd.plan == "three"
+
+
 def test_lifetch_plan_query():
     """kvip_hip_lifetch_plan picks the forward's launch plan from the arguments alone."""
     lib = abi.load_library()

@@ -247,6 +247,26 @@ def test_forward_end_to_end_against_oracle_scores(torch_gpu):
     assert np.array_equal(out, ref.fetch_gather(wl.kv_cache.cpu().numpy(), wl.block_table.cpu().numpy(), topk))
 
 
+def test_forward_deferred_fetch_option_changes_nothing(torch_gpu):
+    """set_options(deferred_fetch=True), the reference harness's set_deferred_fetch, leaves
+    the round's TopK and gathered rows byte-identical to the default forward's."""
+    torch = torch_gpu
+    wl = synthetic.decode_workload(torch, batch=4, ctx_low=4096, ctx_high=12000, device="cuda", seed=77)
+    rot, upd, fwd = synthetic.bind(torch, kvip_amd, wl)
+    results = []
+    for deferred in (False, True, False):
+        say(f"forward deferred_fetch={deferred}")
+        fwd.set_options(deferred_fetch=deferred)
+        rot.topk.fill_(-5)
+        upd.output.fill_(0xAB)
+        fwd()
+        torch.cuda.synchronize()
+        assert int(rot.status.item()) == 0
+        results.append((rot.topk.cpu().numpy(), upd.output.cpu().numpy()))
+    for topk, out in results[1:]:
+        assert np.array_equal(topk, results[0][0]) and np.array_equal(out, results[0][1])
+
+
 def test_forward_mtp_rows_against_oracle(torch_gpu):
     """Four query rows per request (decode + 3 MTP rows) with per-row visible bounds: the
     forward's scores, TopK (bit-exact on the GPU's keys, inside the oracle's cutoff band) and
