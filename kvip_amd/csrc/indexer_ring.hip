@@ -343,13 +343,91 @@ __global__ __launch_bounds__(kRgThreads, 2) void indexer_ring_kernel(const KvipI
     report(p.status, err);
 }
 
+// Keys of two 32-token tiles A and B for one query row: the same arithmetic as rg_key per
+// tile (MFMA over the heads, ReLU, head weights, four FMA chains per lane half in head
+// order), with one v_permlane32_swap joining the lane halves of both tiles, so that lanes
+// 0-31 finish token n of A and lanes 32-63 token n of B (ks: that token's key scale).
+template <int MT>
+KVIP_DEVICE uint32_t rg_key2(const v4i (&qa)[MT][4], const float (&wr)[MT * 16], const v4i (&ka)[4],
+                             const v4i (&kbb)[4], float ks) {
+    float pa[4] = {0.f, 0.f, 0.f, 0.f};
+    float pb[4] = {0.f, 0.f, 0.f, 0.f};
+    v16f acc[2];
+    acc[0] = v16f{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    Mma<1>::step(0, qa[0], ka, acc[0]);
+    Mma<1>::step(1, qa[0], ka, acc[0]);
+    __builtin_amdgcn_sched_barrier(0);
+    // Groups j = 2 mt + t: head tile mt of tile t (t = 0: A, 1: B).
+#pragma unroll
+    for (int j = 0; j < 2 * MT; ++j) {
+        v16f& cur = acc[j & 1];
+        if (j + 1 < 2 * MT) {
+            const int mn = (j + 1) >> 1;
+            v16f& nxt = acc[(j + 1) & 1];
+            nxt = v16f{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            if ((j + 1) & 1) {
+                Mma<1>::step(0, qa[mn], kbb, nxt);
+                Mma<1>::step(1, qa[mn], kbb, nxt);
+            } else {
+                Mma<1>::step(0, qa[mn], ka, nxt);
+                Mma<1>::step(1, qa[mn], ka, nxt);
+            }
+        }
+        const int mt = j >> 1;
+        float (&pj)[4] = (j & 1) ? pb : pa;
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float relu = __int_as_float(max(__float_as_int(cur[r4 * 4 + q]), 0));
+                pj[q] = fmaf(relu, wr[mt * 16 + r4 * 4 + q], pj[q]);
+            }
+        }
+        if (j + 1 < 2 * MT) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    const float part_a = (pa[0] + pa[1]) + (pa[2] + pa[3]);
+    const float part_b = (pb[0] + pb[1]) + (pb[2] + pb[3]);
+    // [A lanes 0-31, B lanes 0-31] and [A lanes 32-63, B lanes 32-63].
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_int(part_a), __float_as_int(part_b), false, false);
+    const float part = __int_as_float(sw[0]) + __int_as_float(sw[1]);
+    return sortable_key(bf16_bits_half_away(part * ks));
+}
+
+// The eight 16-byte K fragment pieces of token rows n (A) and 32 + n (B, 4 KiB further) and
+// one 4-byte value (the lane's key scale), then wait for them.
+KVIP_DEVICE void lds_read_tile2(uint32_t a0, uint32_t a1, uint32_t a2, uint32_t a3, uint32_t as, v4i (&ka)[4],
+                                v4i (&kbb)[4], float& ks) {
+    asm volatile(
+        "ds_read_b128 %0, %9\n"
+        "ds_read_b128 %1, %10\n"
+        "ds_read_b128 %2, %11\n"
+        "ds_read_b128 %3, %12\n"
+        "ds_read_b128 %4, %9 offset:4096\n"
+        "ds_read_b128 %5, %10 offset:4096\n"
+        "ds_read_b128 %6, %11 offset:4096\n"
+        "ds_read_b128 %7, %12 offset:4096\n"
+        "ds_read_b32 %8, %13\n"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(ka[0]), "=&v"(ka[1]), "=&v"(ka[2]), "=&v"(ka[3]), "=&v"(kbb[0]), "=&v"(kbb[1]), "=&v"(kbb[2]),
+          "=&v"(kbb[3]), "=&v"(ks)
+        : "v"(a0), "v"(a1), "v"(a2), "v"(a3), "v"(as));
+}
+
 // Decode with ROWS = 2 or 4 query rows per request (the MTP rows): one workgroup of ROWS
-// waves per tile stream, wave w scoring row w of each tile's request. The workgroup shares
-// one LDS ring: every wave loads its share of each tile (4 / ROWS KiB of K rows and 128 /
-// ROWS bytes of key scales, same fragment swizzle as above), waits for its own loads with
-// an exact vmcnt and meets the others at a barrier, after which every wave reads the whole
-// tile. A tile is thus read from HBM once for all rows of its request, and each wave keeps
-// the Q fragments and weights of one row in registers, as the one-row kernel does.
+// waves per tile stream, wave w scoring row w of each tile's request, over 64-token tiles
+// (half an index-K block). The workgroup shares one LDS ring: every wave loads its share of
+// each tile (8 / ROWS KiB of K rows and 256 / ROWS bytes of key scales, same fragment
+// swizzle as the one-row kernel), waits for its own loads with an exact vmcnt and meets the
+// others at a barrier, after which every wave reads the whole tile. A tile is thus read from
+// HBM once for all rows of its request; each wave keeps the Q fragments and weights of one
+// row in registers and finishes the keys of 64 tokens at once (lanes 0-31 the first 32,
+// lanes 32-63 the next 32: one key store and one histogram add per lane and tile).
 // Slots: kRrDepth tiles are in flight while tile i is scored, and the loads of tile
 // i + kRrDepth are issued while slow waves may still read tile i - 1, so the ring needs
 // kRrDepth + 2 slots (rounded up to a power of two; a full pass of kRgPass tiles then ends
@@ -358,17 +436,20 @@ __global__ __launch_bounds__(kRgThreads, 2) void indexer_ring_kernel(const KvipI
 // the same barriers.
 constexpr int kRrDepth = 1;
 constexpr int kRrSlots = kRrDepth + 2 <= 4 ? 4 : 8;
+constexpr int kRrTile = 64;                                // tokens per tile
+constexpr int kRrTileBytes = kRrTile * kIndexDim;          // 8 KiB of fp8 K rows
+constexpr int kRrSlotBytes = kRrTileBytes + kRrTile * 4;   // + 64 key scales
 static_assert(kRgPass % kRrSlots == 0, "a full pass ends on the last slot");
 static_assert(kRrDepth >= 1 && kRrDepth <= 4, "the waits below cover up to 4 tiles in flight");
 
 template <int ROWS, int HEADS, bool W_BF16>
-__global__ __launch_bounds__(ROWS * 64) void indexer_rows_kernel(const KvipIndexerArgs p, int lead_blocks) {
+__global__ __launch_bounds__(ROWS * 64, 3) void indexer_rows_kernel(const KvipIndexerArgs p, int lead_blocks) {
     constexpr int MT = HEADS / 32;
     constexpr int kThreads = ROWS * 64;
-    constexpr int kChunks = 4 / ROWS;  // KiB of K rows each wave loads per tile
-    constexpr int kScaleLanes = 8 / ROWS;
+    constexpr int kChunks = 8 / ROWS;  // KiB of K rows each wave loads per tile
+    constexpr int kScaleLanes = 16 / ROWS;
     constexpr int kOps = kChunks + 1;  // vector memory instructions per tile and wave
-    __shared__ __align__(16) uint8_t s_ring[kRrSlots][kRgSlotBytes];
+    __shared__ __align__(16) uint8_t s_ring[kRrSlots][kRrSlotBytes];
     __shared__ __align__(16) uint32_t s_hist[ROWS][256];
     __shared__ int s_prefix[kRgMaxBatch + 1];
     __shared__ uint32_t s_scan[ROWS];
@@ -379,7 +460,7 @@ __global__ __launch_bounds__(ROWS * 64) void indexer_rows_kernel(const KvipIndex
     const int n = lane & 31;
     const int g = lane >> 5;
 
-    // Tiles per request (the longest of its rows) -> prefix sums.
+    // 64-token tiles per request (the longest of its rows) -> prefix sums.
     int running = 0;
     for (int base = 0; base < p.batch; base += kThreads) {
         const int b = base + tid;
@@ -388,7 +469,7 @@ __global__ __launch_bounds__(ROWS * 64) void indexer_rows_kernel(const KvipIndex
             int vmax = 0;
 #pragma unroll
             for (int q = 0; q < ROWS; ++q) vmax = max(vmax, rg_valid(p, b, b * ROWS + q));
-            c = (vmax + 31) / 32;
+            c = (vmax + kRrTile - 1) / kRrTile;
         }
         uint32_t total;
         const uint32_t excl = block_exclusive_scan(static_cast<uint32_t>(c), s_scan, &total);
@@ -413,10 +494,11 @@ __global__ __launch_bounds__(ROWS * 64) void indexer_rows_kernel(const KvipIndex
 
     uint8_t* ring = &s_ring[0][0];
     const uint32_t ring_lds = lds_addr(ring);
+    // Fragment reads of token row n (the B rows 32 + n sit 4 KiB further, same swizzle).
     uint32_t ka[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) ka[u] = ring_lds + n * kIndexDim + (((g * 4 + u) ^ (n & 7)) * 16);
-    const uint32_t ksa = ring_lds + kRgTileBytes + n * 4;
+    const uint32_t ksa = ring_lds + kRrTileBytes + lane * 4;  // key scale of token `lane`
     const uint32_t hist_lds = lds_addr(&s_hist[wave][0]);
     const int src_lane = (lane >> 3) * kIndexDim + (((lane & 7) ^ (lane >> 3)) * 16);
     const uint8_t* kbase = static_cast<const uint8_t*>(p.keys);
@@ -455,7 +537,7 @@ __global__ __launch_bounds__(ROWS * 64) void indexer_rows_kernel(const KvipIndex
             }
             d_b = lo;
             d_k = tt - s_prefix[lo];
-            const int id = p.block_table[static_cast<size_t>(d_b) * p.max_blocks + (d_k >> 2)];
+            const int id = p.block_table[static_cast<size_t>(d_b) * p.max_blocks + (d_k >> 1)];
             const bool ok = static_cast<unsigned>(id) < static_cast<unsigned>(p.num_blocks);
             d_page = ok ? id : 0;
             d_ok = ok ? 1.0f : 0.0f;
@@ -470,34 +552,32 @@ __global__ __launch_bounds__(ROWS * 64) void indexer_rows_kernel(const KvipIndex
             const int jj = min(j, cnt - 1);
             const int page = __builtin_amdgcn_readlane(d_page, jj);
             const int k = __builtin_amdgcn_readlane(d_k, jj);
-            uint8_t* dst = ring + (j & (kRrSlots - 1)) * kRgSlotBytes;
-            const uint8_t* src = kbase + static_cast<size_t>(page) * p.key_block_stride + (k & 3) * kRgTileBytes + src_lane;
+            uint8_t* dst = ring + (j & (kRrSlots - 1)) * kRrSlotBytes;
+            const uint8_t* src = kbase + static_cast<size_t>(page) * p.key_block_stride + (k & 1) * kRrTileBytes + src_lane;
 #pragma unroll
             for (int c = 0; c < kChunks; ++c) {
                 const int v = wave * kChunks + c;
                 __builtin_amdgcn_global_load_lds(src + v * 1024, LDS_PTR(dst + v * 1024), 16, 0, kNonTemporal);
             }
             if (lane < kScaleLanes) {
-                const float* ssrc = kscale + static_cast<size_t>(page) * kscale_stride + (k & 3) * 32 +
+                const float* ssrc = kscale + static_cast<size_t>(page) * kscale_stride + (k & 1) * kRrTile +
                                     (wave * kScaleLanes + lane) * 4;
-                __builtin_amdgcn_global_load_lds(ssrc, LDS_PTR(dst + kRgTileBytes + wave * kScaleLanes * 16), 16, 0,
+                __builtin_amdgcn_global_load_lds(ssrc, LDS_PTR(dst + kRrTileBytes + wave * kScaleLanes * 16), 16, 0,
                                                  kNonTemporal);
             }
         };
 
         auto score = [&](int i) {
-            const uint32_t so = (i & (kRrSlots - 1)) * kRgSlotBytes;
-            v4i kb[4];
+            const uint32_t so = (i & (kRrSlots - 1)) * kRrSlotBytes;
+            v4i kba[4], kbb[4];
             float ks_raw;
-            lds_read_tile(ka[0] + so, ka[1] + so, ka[2] + so, ka[3] + so, ksa + so, kb, ks_raw);
+            lds_read_tile2(ka[0] + so, ka[1] + so, ka[2] + so, ka[3] + so, ksa + so, kba, kbb, ks_raw);
             const float ks = ks_raw * __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, d_ok), i));
-            const uint32_t key = rg_key<MT>(qa, wr, kb, ks, g);
+            const uint32_t key = rg_key2<MT>(qa, wr, kba, kbb, ks);
             const int row = __builtin_amdgcn_readlane(d_b, i) * ROWS + wave;
-            const int tok = __builtin_amdgcn_readlane(d_k, i) * 32 + n;
-            if (g == 0) {
-                p.score_keys[static_cast<size_t>(row) * p.key_stride + tok] = static_cast<uint16_t>(key);
-                if (tok < __builtin_amdgcn_readlane(d_valid, i)) lds_add_u32(hist_lds + (key >> 8) * 4, 1u);
-            }
+            const int tok = __builtin_amdgcn_readlane(d_k, i) * kRrTile + lane;
+            p.score_keys[static_cast<size_t>(row) * p.key_stride + tok] = static_cast<uint16_t>(key);
+            if (tok < __builtin_amdgcn_readlane(d_valid, i)) lds_add_u32(hist_lds + (key >> 8) * 4, 1u);
         };
 
         const int b_first = __builtin_amdgcn_readlane(d_b, 0);
