@@ -101,7 +101,12 @@ KVIP_DEVICE bf16x8 as_bf16x8(v4i v) {
 // dequantisation); group g runs on waves 4 g .. 4 g + 3, which keep its Q fragments,
 // online-softmax state and value accumulators in registers (G waves per SIMD).
 __host__ __device__ inline int sa_group_set(int heads) { return heads > kSaHeads ? 2 : 1; }
+// Workgroups per row before index splits: more than 32 heads run on the wave-pair kernel
+// (sparse_attention_pair_kernel, kPrPairs pairs of 32 heads per workgroup).
+constexpr int kPrPairs = 2;
+__host__ __device__ inline bool sa_pairs(int heads) { return heads > 2 * kSaHeads; }
 __host__ __device__ inline int sa_sets(int heads) {
+    if (sa_pairs(heads)) return ((heads + 31) / 32 + kPrPairs - 1) / kPrPairs;
     const int groups = (heads + kSaHeads - 1) / kSaHeads;
     return (groups + sa_group_set(heads) - 1) / sa_group_set(heads);
 }
@@ -371,6 +376,315 @@ __global__ __launch_bounds__(kSaThreads * G, 1) void sparse_attention_kernel(con
     report(p.status, err);
 }
 
+// More than 32 heads: wave pairs of 32 heads. A workgroup (row, index split) holds kPrPairs
+// pairs, i.e. up to 128 heads, so a staged tile of 32 rows serves every head of the row
+// once. Both waves of a pair hold the 32 heads' query fragments for half the key features
+// (288 each): each computes its half of the logits S^T (v_mfma_f32_32x32x16_bf16, the tile's
+// 32 tokens as M, the 32 heads as N), the halves are exchanged through LDS and added (the
+// same sum in both waves), and both run the identical online softmax. The probabilities
+// leave the MFMA output in the layout of the value product's A operand (lane: one head,
+// 8 tokens), so they go straight into the second MFMA, in which each wave accumulates
+// half of the 512 value features (8 blocks of 32). The running maximum is rescaled
+// lazily: only when a tile's maximum exceeds it by kPrMargin (the probabilities are then
+// at most e^kPrMargin, well inside bf16 and fp32), which after the first tiles of a row
+// is rare, so the 128 accumulators per lane are seldom touched outside the MFMAs.
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+constexpr int kPrTile = 32;                  // tokens per tile
+constexpr int kPrHalfDim = kKeyDim / 2;      // 288 logit features per wave
+constexpr int kPrKSteps = kPrHalfDim / 16;   // 18 MFMA K steps
+constexpr int kPrBlocks = kValueDim / 2 / 32;  // 8 value blocks of 32 features per wave
+constexpr int kPrKPitch = kKeyDim + 8;       // bf16 per K row: an odd number of 16-byte units
+constexpr int kPrVPitch = kPrTile + 4;       // bf16 per value row (feature-major)
+constexpr float kPrLog2e = 1.44269504088896341f;
+constexpr float kPrMargin = 8.0f;            // natural-log units
+
+// bf16 offset of the 4-token group q (0..7) in value row f, XOR-swizzled by f's 16-feature
+// block so that staging writes of features 16 apart and fragment reads of consecutive
+// features spread over the banks.
+KVIP_DEVICE int pr_slot(int f, int q) { return (q ^ ((f >> 4) & 7)) * 4; }
+
+KVIP_DEVICE float lane_half_other(float x, int g) {  // x of lane l ^ 32
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
+    return __int_as_float(g == 0 ? sw[1] : sw[0]);
+}
+
+template <int PAIRS>
+__global__ __launch_bounds__(PAIRS * 128, 1) void sparse_attention_pair_kernel(const KvipSparseAttnArgs p) {
+    constexpr int kThreads = PAIRS * 128;
+    constexpr int kTokPer = kPrTile * 32 / kThreads;  // tokens each thread stages (2 or 4)
+    static_assert(kTokPer == 2 || kTokPer == 4, "staging map");
+    __shared__ __align__(16) uint16_t s_k[kPrTile * kPrKPitch];     // keys, token-major
+    __shared__ __align__(16) uint16_t s_vt[kValueDim * kPrVPitch];  // values, feature-major
+    __shared__ __align__(16) float s_x[2 * PAIRS][16][64];          // each wave's half logits
+    __shared__ __align__(16) float s_h[2 * PAIRS][32];              // per-head values for the O layout
+    __shared__ int32_t s_row[kTopK];
+
+    const int pairs_needed = (p.heads + 31) / 32;
+    const int sets = (pairs_needed + PAIRS - 1) / PAIRS;
+    const int splits = sa_splits(p.rows, sets);
+    const int units = sets * splits;
+    // XCD-aware order as in the 16-head kernel: a row's workgroups share blockIdx % 8.
+    const int chunk = blockIdx.x / (8 * units), within = blockIdx.x % (8 * units);
+    const int r = chunk * 8 + within % 8;
+    const int unit = within / 8, hs = unit % sets, sp = unit / sets;
+    if (r >= p.rows) return;
+    const int b = r / p.rows_per_request;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int pair = hs * PAIRS + (w >> 1), hf = w & 1;
+    const bool live = pair < pairs_needed;  // uniform per wave
+    const int n = lane & 31, g = lane >> 5;
+    uint32_t err = 0;
+
+    // Cache rows of the split's indices, resolved once through the block table.
+    const int span = kTopK / splits;
+    const int* idx_row = p.indices + static_cast<size_t>(r) * kTopK + sp * span;
+    const int capacity = p.max_blocks * kBlockTokens;
+    for (int i = tid; i < span; i += kThreads) {
+        const int t = idx_row[i];
+        int row = -1;
+        if (t >= capacity) {
+            err |= KVIP_STATUS_BAD_TOKEN;
+        } else if (t >= 0) {
+            const int blk = p.block_table[static_cast<size_t>(b) * p.max_blocks + (t >> 7)];
+            if (static_cast<unsigned>(blk) < static_cast<unsigned>(p.num_blocks)) {
+                row = blk * kBlockTokens + (t & 127);
+            } else {
+                err |= KVIP_STATUS_BAD_BLOCK;
+            }
+        }
+        s_row[i] = row;
+    }
+
+    // Query fragments (B operand of the logits): head 32 pair + n, features
+    // 288 hf + 16 k + 8 g .. + 8; heads past p.heads read as zero.
+    bf16x8 qf[kPrKSteps];
+    {
+        const int h = pair * 32 + n;
+        const bool hl = live && h < p.heads;
+        const uint16_t* q = p.query + (static_cast<size_t>(r) * p.heads + (hl ? h : 0)) * kKeyDim + hf * kPrHalfDim + g * 8;
+#pragma unroll
+        for (int k = 0; k < kPrKSteps; ++k) {
+            const v4i v = hl ? *reinterpret_cast<const v4i*>(q + k * 16) : v4i{0, 0, 0, 0};
+            qf[k] = as_bf16x8(v);
+        }
+    }
+    v16f o[kPrBlocks];
+#pragma unroll
+    for (int t = 0; t < kPrBlocks; ++t) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[t][i] = 0.f;
+    }
+    float m_ref = -INFINITY;  // reference maximum of head 32 pair + n (natural-log units)
+    float l_sum = 0.f;        // this lane's share of the head's probability sum
+    bool o_zero = true;       // no tile has been accumulated yet (uniform)
+    __syncthreads();
+
+    // Staging map: thread (token group tg, nope slice pc) holds the 16 nope features
+    // 16 pc .. of kTokPer consecutive tokens; the tile's 256 rope pieces go to threads 0-255.
+    const int tg = tid >> 5, pc = tid & 31;
+    const int f0 = pc * 16;
+    v4i nope[kTokPer];
+    float sc[kTokPer];
+    v4i rope = v4i{0, 0, 0, 0};
+    auto row_base = [&](int row) {
+        return p.kv_cache + static_cast<int64_t>(row >> 7) * p.kv_block_stride +
+               static_cast<int64_t>(row & 127) * p.row_stride;
+    };
+    auto load_tile = [&](int k) {
+#pragma unroll
+        for (int u = 0; u < kTokPer; ++u) {
+            const int row = s_row[k * kPrTile + tg * kTokPer + u];
+            nope[u] = v4i{0, 0, 0, 0};
+            sc[u] = 0.f;
+            if (row >= 0) {
+                const uint8_t* base = row_base(row);
+                nope[u] = *reinterpret_cast<const v4i*>(base + f0);
+                sc[u] = *reinterpret_cast<const float*>(base + 640 + (pc >> 3) * 4);
+            }
+        }
+        if (tid < kPrTile * 8) {
+            const int row = s_row[k * kPrTile + (tid >> 3)];
+            rope = row >= 0 ? *reinterpret_cast<const v4i*>(row_base(row) + 512 + (tid & 7) * 16) : v4i{0, 0, 0, 0};
+        }
+    };
+    // Dequantisation to bf16: keys [nope * scale, rope] token-major in s_k, values
+    // nope * scale feature-major in s_vt.
+    auto stage_tile = [&]() {
+        uint32_t out[kTokPer][8];  // out[u][k]: features f0 + 2k, 2k + 1 of token u
+#pragma unroll
+        for (int u = 0; u < kTokPer; ++u) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const f32x2 a = __builtin_amdgcn_cvt_pk_f32_fp8(nope[u][k], false);
+                const f32x2 c = __builtin_amdgcn_cvt_pk_f32_fp8(nope[u][k], true);
+                out[u][2 * k] = pack_bf16(a[0] * sc[u], a[1] * sc[u]);
+                out[u][2 * k + 1] = pack_bf16(c[0] * sc[u], c[1] * sc[u]);
+            }
+            uint16_t* d = s_k + (tg * kTokPer + u) * kPrKPitch + f0;
+            reinterpret_cast<v4i*>(d)[0] = v4i{static_cast<int>(out[u][0]), static_cast<int>(out[u][1]),
+                                               static_cast<int>(out[u][2]), static_cast<int>(out[u][3])};
+            reinterpret_cast<v4i*>(d)[1] = v4i{static_cast<int>(out[u][4]), static_cast<int>(out[u][5]),
+                                               static_cast<int>(out[u][6]), static_cast<int>(out[u][7])};
+        }
+        const int t0 = tg * kTokPer;  // first token of this thread
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            // Features f0 + 2k (lo halves) and f0 + 2k + 1 (hi halves) of the thread's tokens.
+            const int f = f0 + 2 * k;
+            if constexpr (kTokPer == 2) {
+                const uint32_t x = out[0][k], y = out[1][k];
+                *reinterpret_cast<uint32_t*>(s_vt + f * kPrVPitch + pr_slot(f, t0 >> 2) + (t0 & 3)) =
+                    (x & 0xFFFFu) | (y << 16);
+                *reinterpret_cast<uint32_t*>(s_vt + (f + 1) * kPrVPitch + pr_slot(f + 1, t0 >> 2) + (t0 & 3)) =
+                    (x >> 16) | (y & 0xFFFF0000u);
+            } else {
+                const uint32_t x0 = out[0][k], x1 = out[1][k], x2 = out[2][k], x3 = out[3][k];
+                *reinterpret_cast<i32x2*>(s_vt + f * kPrVPitch + pr_slot(f, t0 >> 2)) =
+                    i32x2{static_cast<int>((x0 & 0xFFFFu) | (x1 << 16)), static_cast<int>((x2 & 0xFFFFu) | (x3 << 16))};
+                *reinterpret_cast<i32x2*>(s_vt + (f + 1) * kPrVPitch + pr_slot(f + 1, t0 >> 2)) =
+                    i32x2{static_cast<int>((x0 >> 16) | (x1 & 0xFFFF0000u)),
+                        static_cast<int>((x2 >> 16) | (x3 & 0xFFFF0000u))};
+            }
+        }
+        if (tid < kPrTile * 8) {
+            *reinterpret_cast<v4i*>(s_k + (tid >> 3) * kPrKPitch + 512 + (tid & 7) * 8) = rope;
+        }
+    };
+
+    const int tiles = span / kPrTile;
+    load_tile(0);
+    for (int k = 0; k < tiles; ++k) {
+        stage_tile();
+        __syncthreads();  // s_k / s_vt hold tile k
+        if (k + 1 < tiles) load_tile(k + 1);
+        // Tokens of the tile that have a row (bit t: token t).
+        const uint32_t vmask =
+            static_cast<uint32_t>(__ballot(lane < kPrTile && s_row[k * kPrTile + (lane & 31)] >= 0));
+        v16f sv;
+        if (live) {
+            // Half logits S^T: lane (head n, half g) gets tokens 8 (i / 4) + 4 g + i % 4.
+            v16f acc = v16f{};
+            const uint16_t* kr = s_k + n * kPrKPitch + hf * kPrHalfDim + g * 8;
+#pragma unroll
+            for (int s = 0; s < kPrKSteps; ++s) {
+                const bf16x8 kv = as_bf16x8(*reinterpret_cast<const v4i*>(kr + s * 16));
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kv, qf[s], acc, 0, 0, 0);
+            }
+            sv = acc;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) s_x[w][i][lane] = acc[i];
+        }
+        __syncthreads();  // both halves' logits in s_x
+        if (live) {
+            float mx = -INFINITY;
+            const bool all_valid = vmask == 0xFFFFFFFFu;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                // The same sum in both waves of the pair (addition commutes exactly).
+                float s = (sv[i] + s_x[w ^ 1][i][lane]) * p.scale;
+                if (!all_valid && !((vmask >> (8 * (i >> 2) + 4 * g + (i & 3))) & 1u)) s = -INFINITY;
+                sv[i] = s;
+                mx = fmaxf(mx, s);
+            }
+            mx = fmaxf(mx, lane_half_other(mx, g));  // the head's tile maximum
+            const bool need = mx > m_ref + kPrMargin;  // also the first finite maximum
+            if (__ballot(need) != 0ull) {
+                const float m_new = need ? mx : m_ref;
+                const float alpha = (m_ref == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f((m_ref - m_new) * kPrLog2e);
+                l_sum *= need ? alpha : 1.f;
+                if (!o_zero) {
+                    if (g == 0) s_h[w][n] = need ? alpha : 1.f;
+                    // Wave-local: this wave's LDS write precedes its reads.
+                    f32x4 a4[4];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) a4[q] = *reinterpret_cast<const f32x4*>(&s_h[w][8 * q + 4 * g]);
+#pragma unroll
+                    for (int t = 0; t < kPrBlocks; ++t) {
+#pragma unroll
+                        for (int i = 0; i < 16; ++i) o[t][i] *= a4[i >> 2][i & 3];
+                    }
+                }
+                m_ref = m_new;
+            }
+            const float bias = m_ref == -INFINITY ? 0.f : -m_ref * kPrLog2e;
+            bf16x8 pa[2];
+            float lsum = 0.f;
+#pragma unroll
+            for (int s2 = 0; s2 < 2; ++s2) {
+                uint32_t pk[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float p0 = __builtin_amdgcn_exp2f(fmaf(sv[8 * s2 + 2 * j], kPrLog2e, bias));
+                    const float p1 = __builtin_amdgcn_exp2f(fmaf(sv[8 * s2 + 2 * j + 1], kPrLog2e, bias));
+                    lsum += p0 + p1;
+                    pk[j] = pack_bf16(p0, p1);
+                }
+                pa[s2] = as_bf16x8(v4i{static_cast<int>(pk[0]), static_cast<int>(pk[1]), static_cast<int>(pk[2]),
+                                       static_cast<int>(pk[3])});
+            }
+            l_sum += lsum;
+            // Value product: features 256 hf + 32 t + n; K step s2 covers tokens 16 s2 .. + 16
+            // in the probabilities' order (groups 4 s2 + g and 4 s2 + 2 + g of 4 tokens).
+#pragma unroll
+            for (int t = 0; t < kPrBlocks; ++t) {
+                const int f = hf * (kValueDim / 2) + t * 32 + n;
+                const uint16_t* vr = s_vt + f * kPrVPitch;
+#pragma unroll
+                for (int s2 = 0; s2 < 2; ++s2) {
+                    const i32x2 lo = *reinterpret_cast<const i32x2*>(vr + pr_slot(f, 4 * s2 + g));
+                    const i32x2 hi = *reinterpret_cast<const i32x2*>(vr + pr_slot(f, 4 * s2 + 2 + g));
+                    const bf16x8 vb = as_bf16x8(v4i{lo[0], lo[1], hi[0], hi[1]});
+                    o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pa[s2], vb, o[t], 0, 0, 0);
+                }
+            }
+            o_zero = false;
+        }
+        __syncthreads();  // s_k, s_vt and s_x are rewritten by the next tile
+    }
+
+    // Probability sums of the heads (both lane halves), then the split's partial record
+    // (max, sum, unnormalised output per head) or the normalised output. Output lane
+    // (feature 256 hf + 32 t + n) holds heads 32 pair + 8 (i / 4) + 4 g + i % 4 of o[t][i].
+    if (live) {
+        const float l_tot = l_sum + lane_half_other(l_sum, g);
+        const int groups = (p.heads + kSaHeads - 1) / kSaHeads;
+        if (splits > 1) {
+            if (g == 0 && hf == 0) {
+                const int h = pair * 32 + n;
+                if (h < p.heads) {
+                    float* ws = p.workspace + ((static_cast<size_t>(r) * groups + h / kSaHeads) * splits + sp) * kPartial;
+                    ws[h % kSaHeads] = m_ref;
+                    ws[kSaHeads + h % kSaHeads] = l_tot;
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int h = pair * 32 + 8 * (i >> 2) + 4 * g + (i & 3);
+                if (h >= p.heads) continue;
+                float* ws = p.workspace + ((static_cast<size_t>(r) * groups + h / kSaHeads) * splits + sp) * kPartial +
+                            2 * kSaHeads + (h % kSaHeads) * kValueDim + hf * (kValueDim / 2) + n;
+#pragma unroll
+                for (int t = 0; t < kPrBlocks; ++t) ws[t * 32] = o[t][i];
+            }
+        } else {
+            if (g == 0) s_h[w][n] = l_tot > 0.f ? 1.f / l_tot : 0.f;
+            f32x4 inv[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) inv[q] = *reinterpret_cast<const f32x4*>(&s_h[w][8 * q + 4 * g]);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int h = pair * 32 + 8 * (i >> 2) + 4 * g + (i & 3);
+                if (h >= p.heads) continue;
+                float* out = p.output + (static_cast<size_t>(r) * p.heads + h) * kValueDim + hf * (kValueDim / 2) + n;
+#pragma unroll
+                for (int t = 0; t < kPrBlocks; ++t) out[t * 32] = o[t][i] * inv[i >> 2][i & 3];
+            }
+        }
+    }
+    report(p.status, err);
+}
+
 // Merge of the splits: workgroup (row, head group, 64-feature chunk).
 __global__ __launch_bounds__(kSaThreads) void sparse_attention_merge_kernel(const KvipSparseAttnArgs p) {
     __shared__ float s_w[kMaxSplits][kSaHeads];
@@ -440,7 +754,10 @@ extern "C" uint32_t kvip_hip_sparse_attention(const KvipSparseAttnArgs* args, vo
     const int splits = kvip::sa_splits(args->rows, sets);
     const hipStream_t s = static_cast<hipStream_t>(stream);
     const dim3 grid(((args->rows + 7) / 8) * 8 * sets * splits);
-    if (kvip::sa_group_set(args->heads) == 2) {
+    if (kvip::sa_pairs(args->heads)) {
+        hipLaunchKernelGGL(kvip::sparse_attention_pair_kernel<kvip::kPrPairs>, grid, dim3(kvip::kPrPairs * 128), 0, s,
+                           *args);
+    } else if (kvip::sa_group_set(args->heads) == 2) {
         hipLaunchKernelGGL(kvip::sparse_attention_kernel<2>, grid, dim3(2 * kvip::kSaThreads), 0, s, *args);
     } else {
         hipLaunchKernelGGL(kvip::sparse_attention_kernel<1>, grid, dim3(kvip::kSaThreads), 0, s, *args);
