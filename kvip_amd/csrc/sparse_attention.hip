@@ -101,12 +101,14 @@ KVIP_DEVICE bf16x8 as_bf16x8(v4i v) {
 // dequantisation); group g runs on waves 4 g .. 4 g + 3, which keep its Q fragments,
 // online-softmax state and value accumulators in registers (G waves per SIMD).
 __host__ __device__ inline int sa_group_set(int heads) { return heads > kSaHeads ? 2 : 1; }
-// Workgroups per row before index splits: more than 32 heads run on the wave-pair kernel
-// (sparse_attention_pair_kernel, kPrPairs pairs of 32 heads per workgroup).
-constexpr int kPrPairs = 2;
+// Workgroups per row before index splits: more than 32 heads run on
+// sparse_attention_pair_kernel, kPrGroups groups of 32 heads per workgroup, kPrSplit waves
+// per group.
+constexpr int kPrGroups = 2;
+constexpr int kPrSplit = 4;
 __host__ __device__ inline bool sa_pairs(int heads) { return heads > 2 * kSaHeads; }
 __host__ __device__ inline int sa_sets(int heads) {
-    if (sa_pairs(heads)) return ((heads + 31) / 32 + kPrPairs - 1) / kPrPairs;
+    if (sa_pairs(heads)) return ((heads + 31) / 32 + kPrGroups - 1) / kPrGroups;
     const int groups = (heads + kSaHeads - 1) / kSaHeads;
     return (groups + sa_group_set(heads) - 1) / sa_group_set(heads);
 }
@@ -376,23 +378,20 @@ __global__ __launch_bounds__(kSaThreads * G, 1) void sparse_attention_kernel(con
     report(p.status, err);
 }
 
-// More than 32 heads: wave pairs of 32 heads. A workgroup (row, index split) holds kPrPairs
-// pairs, i.e. up to 128 heads, so a staged tile of 32 rows serves every head of the row
-// once. Both waves of a pair hold the 32 heads' query fragments for half the key features
-// (288 each): each computes its half of the logits S^T (v_mfma_f32_32x32x16_bf16, the tile's
-// 32 tokens as M, the 32 heads as N), the halves are exchanged through LDS and added (the
-// same sum in both waves), and both run the identical online softmax. The probabilities
-// leave the MFMA output in the layout of the value product's A operand (lane: one head,
-// 8 tokens), so they go straight into the second MFMA, in which each wave accumulates
-// half of the 512 value features (8 blocks of 32). The running maximum is rescaled
+// More than 32 heads: groups of SPLIT waves per 32 heads. A workgroup (row, index split)
+// holds GROUPS such groups (GROUPS x 32 heads), so a staged tile of 32 rows serves all of
+// them once. The SPLIT waves of a group hold the 32 heads' query fragments for 576 / SPLIT
+// key features each: each computes its part of the logits S^T (v_mfma_f32_32x32x16_bf16, the
+// tile's 32 tokens as M, the 32 heads as N), the parts are exchanged through LDS and added in
+// one fixed order (the same sum in every wave of the group), and all run the identical online
+// softmax. The probabilities leave the MFMA output in the layout of the value product's A
+// operand (lane: one head, 8 tokens), so they go straight into the second MFMA, in which each
+// wave accumulates 512 / SPLIT of the value features (blocks of 32). The running maximum is rescaled
 // lazily: only when a tile's maximum exceeds it by kPrMargin (the probabilities are then
 // at most e^kPrMargin, well inside bf16 and fp32), which after the first tiles of a row
 // is rare, so the 128 accumulators per lane are seldom touched outside the MFMAs.
 typedef int i32x2 __attribute__((ext_vector_type(2)));
 constexpr int kPrTile = 32;                  // tokens per tile
-constexpr int kPrHalfDim = kKeyDim / 2;      // 288 logit features per wave
-constexpr int kPrKSteps = kPrHalfDim / 16;   // 18 MFMA K steps
-constexpr int kPrBlocks = kValueDim / 2 / 32;  // 8 value blocks of 32 features per wave
 constexpr int kPrKPitch = kKeyDim + 8;       // bf16 per K row: an odd number of 16-byte units
 constexpr int kPrVPitch = kPrTile + 4;       // bf16 per value row (feature-major)
 constexpr float kPrLog2e = 1.44269504088896341f;
@@ -408,19 +407,23 @@ KVIP_DEVICE float lane_half_other(float x, int g) {  // x of lane l ^ 32
     return __int_as_float(g == 0 ? sw[1] : sw[0]);
 }
 
-template <int PAIRS>
-__global__ __launch_bounds__(PAIRS * 128, 1) void sparse_attention_pair_kernel(const KvipSparseAttnArgs p) {
-    constexpr int kThreads = PAIRS * 128;
+template <int GROUPS, int SPLIT>
+__global__ __launch_bounds__(GROUPS * SPLIT * 64, 1) void sparse_attention_pair_kernel(const KvipSparseAttnArgs p) {
+    constexpr int kThreads = GROUPS * SPLIT * 64;
+    constexpr int kPartDim = kKeyDim / SPLIT;      // logit features per wave (288 or 144)
+    constexpr int kKSteps = kPartDim / 16;         // MFMA K steps per wave
+    constexpr int kVPart = kValueDim / SPLIT;      // value features per wave
+    constexpr int kBlocks = kVPart / 32;           // value blocks of 32 features per wave
     constexpr int kTokPer = kPrTile * 32 / kThreads;  // tokens each thread stages (2 or 4)
     static_assert(kTokPer == 2 || kTokPer == 4, "staging map");
     __shared__ __align__(16) uint16_t s_k[kPrTile * kPrKPitch];     // keys, token-major
     __shared__ __align__(16) uint16_t s_vt[kValueDim * kPrVPitch];  // values, feature-major
-    __shared__ __align__(16) float s_x[2 * PAIRS][16][64];          // each wave's half logits
-    __shared__ __align__(16) float s_h[2 * PAIRS][32];              // per-head values for the O layout
+    __shared__ __align__(16) float s_x[GROUPS * SPLIT][16][64];      // each wave's part of the logits
+    __shared__ __align__(16) float s_h[GROUPS * SPLIT][32];          // per-head values for the O layout
     __shared__ int32_t s_row[kTopK];
 
     const int pairs_needed = (p.heads + 31) / 32;
-    const int sets = (pairs_needed + PAIRS - 1) / PAIRS;
+    const int sets = (pairs_needed + GROUPS - 1) / GROUPS;
     const int splits = sa_splits(p.rows, sets);
     const int units = sets * splits;
     // XCD-aware order as in the 16-head kernel: a row's workgroups share blockIdx % 8.
@@ -431,7 +434,7 @@ __global__ __launch_bounds__(PAIRS * 128, 1) void sparse_attention_pair_kernel(c
     const int b = r / p.rows_per_request;
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int pair = hs * PAIRS + (w >> 1), hf = w & 1;
+    const int pair = hs * GROUPS + w / SPLIT, hf = w % SPLIT;  // 32-head group, feature part
     const bool live = pair < pairs_needed;  // uniform per wave
     const int n = lane & 31, g = lane >> 5;
     uint32_t err = 0;
@@ -457,21 +460,21 @@ __global__ __launch_bounds__(PAIRS * 128, 1) void sparse_attention_pair_kernel(c
     }
 
     // Query fragments (B operand of the logits): head 32 pair + n, features
-    // 288 hf + 16 k + 8 g .. + 8; heads past p.heads read as zero.
-    bf16x8 qf[kPrKSteps];
+    // kPartDim hf + 16 k + 8 g .. + 8; heads past p.heads read as zero.
+    bf16x8 qf[kKSteps];
     {
         const int h = pair * 32 + n;
         const bool hl = live && h < p.heads;
-        const uint16_t* q = p.query + (static_cast<size_t>(r) * p.heads + (hl ? h : 0)) * kKeyDim + hf * kPrHalfDim + g * 8;
+        const uint16_t* q = p.query + (static_cast<size_t>(r) * p.heads + (hl ? h : 0)) * kKeyDim + hf * kPartDim + g * 8;
 #pragma unroll
-        for (int k = 0; k < kPrKSteps; ++k) {
+        for (int k = 0; k < kKSteps; ++k) {
             const v4i v = hl ? *reinterpret_cast<const v4i*>(q + k * 16) : v4i{0, 0, 0, 0};
             qf[k] = as_bf16x8(v);
         }
     }
-    v16f o[kPrBlocks];
+    v16f o[kBlocks];
 #pragma unroll
-    for (int t = 0; t < kPrBlocks; ++t) {
+    for (int t = 0; t < kBlocks; ++t) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) o[t][i] = 0.f;
     }
@@ -563,11 +566,11 @@ __global__ __launch_bounds__(PAIRS * 128, 1) void sparse_attention_pair_kernel(c
             static_cast<uint32_t>(__ballot(lane < kPrTile && s_row[k * kPrTile + (lane & 31)] >= 0));
         v16f sv;
         if (live) {
-            // Half logits S^T: lane (head n, half g) gets tokens 8 (i / 4) + 4 g + i % 4.
+            // This wave's part of S^T: lane (head n, half g) gets tokens 8 (i / 4) + 4 g + i % 4.
             v16f acc = v16f{};
-            const uint16_t* kr = s_k + n * kPrKPitch + hf * kPrHalfDim + g * 8;
+            const uint16_t* kr = s_k + n * kPrKPitch + hf * kPartDim + g * 8;
 #pragma unroll
-            for (int s = 0; s < kPrKSteps; ++s) {
+            for (int s = 0; s < kKSteps; ++s) {
                 const bf16x8 kv = as_bf16x8(*reinterpret_cast<const v4i*>(kr + s * 16));
                 acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kv, qf[s], acc, 0, 0, 0);
             }
@@ -575,14 +578,17 @@ __global__ __launch_bounds__(PAIRS * 128, 1) void sparse_attention_pair_kernel(c
 #pragma unroll
             for (int i = 0; i < 16; ++i) s_x[w][i][lane] = acc[i];
         }
-        __syncthreads();  // both halves' logits in s_x
+        __syncthreads();  // every part's logits in s_x
         if (live) {
             float mx = -INFINITY;
             const bool all_valid = vmask == 0xFFFFFFFFu;
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                // The same sum in both waves of the pair (addition commutes exactly).
-                float s = (sv[i] + s_x[w ^ 1][i][lane]) * p.scale;
+                // The parts summed in group order: the same value in every wave of the group.
+                float s = s_x[w - hf][i][lane];
+#pragma unroll
+                for (int j = 1; j < SPLIT; ++j) s += s_x[w - hf + j][i][lane];
+                s *= p.scale;
                 if (!all_valid && !((vmask >> (8 * (i >> 2) + 4 * g + (i & 3))) & 1u)) s = -INFINITY;
                 sv[i] = s;
                 mx = fmaxf(mx, s);
@@ -600,7 +606,7 @@ __global__ __launch_bounds__(PAIRS * 128, 1) void sparse_attention_pair_kernel(c
 #pragma unroll
                     for (int q = 0; q < 4; ++q) a4[q] = *reinterpret_cast<const f32x4*>(&s_h[w][8 * q + 4 * g]);
 #pragma unroll
-                    for (int t = 0; t < kPrBlocks; ++t) {
+                    for (int t = 0; t < kBlocks; ++t) {
 #pragma unroll
                         for (int i = 0; i < 16; ++i) o[t][i] *= a4[i >> 2][i & 3];
                     }
@@ -624,11 +630,11 @@ __global__ __launch_bounds__(PAIRS * 128, 1) void sparse_attention_pair_kernel(c
                                        static_cast<int>(pk[3])});
             }
             l_sum += lsum;
-            // Value product: features 256 hf + 32 t + n; K step s2 covers tokens 16 s2 .. + 16
+            // Value product: features kVPart hf + 32 t + n; K step s2 covers tokens 16 s2 .. + 16
             // in the probabilities' order (groups 4 s2 + g and 4 s2 + 2 + g of 4 tokens).
 #pragma unroll
-            for (int t = 0; t < kPrBlocks; ++t) {
-                const int f = hf * (kValueDim / 2) + t * 32 + n;
+            for (int t = 0; t < kBlocks; ++t) {
+                const int f = hf * kVPart + t * 32 + n;
                 const uint16_t* vr = s_vt + f * kPrVPitch;
 #pragma unroll
                 for (int s2 = 0; s2 < 2; ++s2) {
@@ -645,7 +651,7 @@ __global__ __launch_bounds__(PAIRS * 128, 1) void sparse_attention_pair_kernel(c
 
     // Probability sums of the heads (both lane halves), then the split's partial record
     // (max, sum, unnormalised output per head) or the normalised output. Output lane
-    // (feature 256 hf + 32 t + n) holds heads 32 pair + 8 (i / 4) + 4 g + i % 4 of o[t][i].
+    // (feature kVPart hf + 32 t + n) holds heads 32 pair + 8 (i / 4) + 4 g + i % 4 of o[t][i].
     if (live) {
         const float l_tot = l_sum + lane_half_other(l_sum, g);
         const int groups = (p.heads + kSaHeads - 1) / kSaHeads;
@@ -663,9 +669,9 @@ __global__ __launch_bounds__(PAIRS * 128, 1) void sparse_attention_pair_kernel(c
                 const int h = pair * 32 + 8 * (i >> 2) + 4 * g + (i & 3);
                 if (h >= p.heads) continue;
                 float* ws = p.workspace + ((static_cast<size_t>(r) * groups + h / kSaHeads) * splits + sp) * kPartial +
-                            2 * kSaHeads + (h % kSaHeads) * kValueDim + hf * (kValueDim / 2) + n;
+                            2 * kSaHeads + (h % kSaHeads) * kValueDim + hf * kVPart + n;
 #pragma unroll
-                for (int t = 0; t < kPrBlocks; ++t) ws[t * 32] = o[t][i];
+                for (int t = 0; t < kBlocks; ++t) ws[t * 32] = o[t][i];
             }
         } else {
             if (g == 0) s_h[w][n] = l_tot > 0.f ? 1.f / l_tot : 0.f;
@@ -676,9 +682,9 @@ __global__ __launch_bounds__(PAIRS * 128, 1) void sparse_attention_pair_kernel(c
             for (int i = 0; i < 16; ++i) {
                 const int h = pair * 32 + 8 * (i >> 2) + 4 * g + (i & 3);
                 if (h >= p.heads) continue;
-                float* out = p.output + (static_cast<size_t>(r) * p.heads + h) * kValueDim + hf * (kValueDim / 2) + n;
+                float* out = p.output + (static_cast<size_t>(r) * p.heads + h) * kValueDim + hf * kVPart + n;
 #pragma unroll
-                for (int t = 0; t < kPrBlocks; ++t) out[t * 32] = o[t][i] * inv[i >> 2][i & 3];
+                for (int t = 0; t < kBlocks; ++t) out[t * 32] = o[t][i] * inv[i >> 2][i & 3];
             }
         }
     }
@@ -755,8 +761,8 @@ extern "C" uint32_t kvip_hip_sparse_attention(const KvipSparseAttnArgs* args, vo
     const hipStream_t s = static_cast<hipStream_t>(stream);
     const dim3 grid(((args->rows + 7) / 8) * 8 * sets * splits);
     if (kvip::sa_pairs(args->heads)) {
-        hipLaunchKernelGGL(kvip::sparse_attention_pair_kernel<kvip::kPrPairs>, grid, dim3(kvip::kPrPairs * 128), 0, s,
-                           *args);
+        hipLaunchKernelGGL((kvip::sparse_attention_pair_kernel<kvip::kPrGroups, kvip::kPrSplit>), grid,
+                           dim3(kvip::kPrGroups * kvip::kPrSplit * 64), 0, s, *args);
     } else if (kvip::sa_group_set(args->heads) == 2) {
         hipLaunchKernelGGL(kvip::sparse_attention_kernel<2>, grid, dim3(2 * kvip::kSaThreads), 0, s, *args);
     } else {
