@@ -397,10 +397,10 @@ constexpr int kPrVPitch = kPrTile + 4;       // bf16 per value row (feature-majo
 constexpr float kPrLog2e = 1.44269504088896341f;
 constexpr float kPrMargin = 8.0f;            // natural-log units
 
-// bf16 offset of the 4-token group q (0..7) in value row f, XOR-swizzled by f's 16-feature
-// block so that staging writes of features 16 apart and fragment reads of consecutive
-// features spread over the banks.
-KVIP_DEVICE int pr_slot(int f, int q) { return (q ^ ((f >> 4) & 7)) * 4; }
+// bf16 offset of the 4-token group q (0..7) in value row f, XOR-swizzled by f's 8-feature
+// block: the staging writes (64 lanes: features 16 pc + 8 g + c of one token group) and the
+// fragment reads (consecutive features) then spread over the banks.
+KVIP_DEVICE int pr_slot(int f, int q) { return (q ^ ((f >> 3) & 7)) * 4; }
 
 KVIP_DEVICE float lane_half_other(float x, int g) {  // x of lane l ^ 32
     const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
@@ -536,11 +536,20 @@ __global__ __launch_bounds__(GROUPS * SPLIT * 64, 1) void sparse_attention_pair_
             // Features f0 + 2k (lo halves) and f0 + 2k + 1 (hi halves) of the thread's tokens.
             const int f = f0 + 2 * k;
             if constexpr (kTokPer == 2) {
-                const uint32_t x = out[0][k], y = out[1][k];
-                *reinterpret_cast<uint32_t*>(s_vt + f * kPrVPitch + pr_slot(f, t0 >> 2) + (t0 & 3)) =
-                    (x & 0xFFFFu) | (y << 16);
-                *reinterpret_cast<uint32_t*>(s_vt + (f + 1) * kPrVPitch + pr_slot(f + 1, t0 >> 2) + (t0 & 3)) =
-                    (x >> 16) | (y & 0xFFFF0000u);
+                // The wave's lane halves hold tokens 4 q + 2 g, + 1 (q = the wave) of the same
+                // 16 features: swap so that lane half g holds features f0 + 8 g .. + 8 of all
+                // four tokens, then write 8 bytes (one token group) per feature.
+                if (k >= 4) continue;
+                const int fk = f0 + 8 * g + 2 * k;
+                const auto s0 = __builtin_amdgcn_permlane32_swap(out[0][k], out[0][k + 4], false, false);
+                const auto s1 = __builtin_amdgcn_permlane32_swap(out[1][k], out[1][k + 4], false, false);
+                // Tokens 4 q + u in s_u[0], 4 q + 2 + u in s_u[1]; features fk (low halves), fk + 1.
+                const uint32_t a0 = s0[0], a1 = s1[0], b0 = s0[1], b1 = s1[1];
+                *reinterpret_cast<i32x2*>(s_vt + fk * kPrVPitch + pr_slot(fk, t0 >> 2)) =
+                    i32x2{static_cast<int>((a0 & 0xFFFFu) | (a1 << 16)), static_cast<int>((b0 & 0xFFFFu) | (b1 << 16))};
+                *reinterpret_cast<i32x2*>(s_vt + (fk + 1) * kPrVPitch + pr_slot(fk + 1, t0 >> 2)) =
+                    i32x2{static_cast<int>((a0 >> 16) | (a1 & 0xFFFF0000u)),
+                          static_cast<int>((b0 >> 16) | (b1 & 0xFFFF0000u))};
             } else {
                 const uint32_t x0 = out[0][k], x1 = out[1][k], x2 = out[2][k], x3 = out[3][k];
                 *reinterpret_cast<i32x2*>(s_vt + f * kPrVPitch + pr_slot(f, t0 >> 2)) =
