@@ -249,82 +249,158 @@ __global__ __launch_bounds__(PfShape<ELEM>::kThreads, 3 - ELEM) void indexer_pre
             __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_ok), c * kChunkPages));
         const float page_ok1 = __builtin_bit_cast(
             float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_ok), c * kChunkPages + kChunkPages - 1));
+        if constexpr (kPfRowsPerWave == 1) {
+            // One row per wave (bf16): two tiles per step, finished together. Lane half g
+            // finishes tile k + g: one lane-half swap joins both tiles' head halves, so every
+            // lane stores a key and counts it (the same sums, in the same order, as one tile
+            // at a time).
 #pragma unroll 1
-        for (int k = 0; k < kPfTiles; ++k) {
-            const int t0 = cstart + k * 32;
-            if (t0 >= vis_max_wave) break;  // uniform per wave: later tiles are masked too
-            v4i kb[NV];
-            float ks_raw;
-            const uint32_t toff = buf * kKBuf + k * 32 * kRowBytes;
-            if constexpr (ELEM == 1) {
-                lds_read_tile(ka[0] + toff, ka[1] + toff, ka[2] + toff, ka[3] + toff, ksa + buf * kSBuf + k * 128, kb,
-                              ks_raw);
-            } else {
-                lds_read_tile8(ka, toff, ksa + buf * kSBuf + k * 128, kb, ks_raw);
-            }
-            const float ks = ks_raw * (k < kPfTiles / 2 ? page_ok0 : page_ok1);
-            // Units u = (row q = u / MT, head tile mt = u % MT), two dependent K-slice MFMAs
-            // each. Unit u+1's MFMAs are issued between the 32 VALU ops (ReLU, weight FMA) of
-            // unit u's epilogue so that the matrix core and the VALU work side by side.
-            constexpr int U = kPfRowsPerWave * MT;
-            float pj[kPfRowsPerWave][4];
+            for (int k = 0; k < kPfTiles; k += 2) {
+                const int t0 = cstart + k * 32;
+                if (t0 >= vis_max_wave) break;  // uniform per wave: later tiles are masked too
+                float part2[2];
+                float ks = 0.f;
 #pragma unroll
-            for (int q = 0; q < kPfRowsPerWave; ++q) pj[q][0] = pj[q][1] = pj[q][2] = pj[q][3] = 0.f;
-            v16f acc[2];
-            acc[0] = v16f{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+                for (int h = 0; h < 2; ++h) {
+                    const int kt = k + h;
+                    v4i kb[NV];
+                    float ks_raw;
+                    const uint32_t toff = buf * kKBuf + kt * 32 * kRowBytes;
+                    lds_read_tile8(ka, toff, ksa + buf * kSBuf + kt * 128, kb, ks_raw);
+                    if (g == h) ks = ks_raw * (kt < kPfTiles / 2 ? page_ok0 : page_ok1);
+                // Units u = (row q = u / MT, head tile mt = u % MT), two dependent K-slice MFMAs
+                // each. Unit u+1's MFMAs are issued between the 32 VALU ops (ReLU, weight FMA) of
+                // unit u's epilogue so that the matrix core and the VALU work side by side.
+                constexpr int U = kPfRowsPerWave * MT;
+                float pj[kPfRowsPerWave][4];
 #pragma unroll
-            for (int st = 0; st < STEPS; ++st) Mma<ELEM>::step(st, qa[0][0], kb, acc[0]);
-            __builtin_amdgcn_sched_barrier(0);
+                for (int q = 0; q < kPfRowsPerWave; ++q) pj[q][0] = pj[q][1] = pj[q][2] = pj[q][3] = 0.f;
+                v16f acc[2];
+                acc[0] = v16f{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const int q = u / MT, mt = u % MT;
-                v16f& cur = acc[u & 1];
-                v16f& nxt = acc[(u + 1) & 1];
-                if (u + 1 < U) {
-                    nxt = v16f{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+                for (int st = 0; st < STEPS; ++st) Mma<ELEM>::step(st, qa[0][0], kb, acc[0]);
+                __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                    for (int st = 0; st < STEPS; ++st) Mma<ELEM>::step(st, qa[(u + 1) / MT][(u + 1) % MT], kb, nxt);
-                }
+                for (int u = 0; u < U; ++u) {
+                    const int q = u / MT, mt = u % MT;
+                    v16f& cur = acc[u & 1];
+                    v16f& nxt = acc[(u + 1) & 1];
+                    if (u + 1 < U) {
+                        nxt = v16f{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int r4 = 0; r4 < 4; ++r4) {
+                        for (int st = 0; st < STEPS; ++st) Mma<ELEM>::step(st, qa[(u + 1) / MT][(u + 1) % MT], kb, nxt);
+                    }
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const float relu = __int_as_float(max(__float_as_int(cur[r4 * 4 + j]), 0));
-                        pj[q][j] = fmaf(relu, wr[q][mt * 16 + r4 * 4 + j], pj[q][j]);
+                    for (int r4 = 0; r4 < 4; ++r4) {
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                                const float relu = __int_as_float(max(__float_as_int(cur[r4 * 4 + j]), 0));
+                                pj[q][j] = fmaf(relu, wr[q][mt * 16 + r4 * 4 + j], pj[q][j]);
+                        }
+                    }
+                    if (u + 1 < U) {
+                        // The next unit's STEPS MFMAs spread over this unit's 32 VALU ops (fp8:
+                        // 1 MFMA, 16 VALU, 1 MFMA, 16 VALU; bf16: 1 MFMA, 4 VALU, ...); nothing
+                        // crosses into the next unit.
+#pragma unroll
+                        for (int st = 0; st < STEPS; ++st) {
+                                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                                __builtin_amdgcn_sched_group_barrier(0x002, 32 / STEPS, 0);
+                        }
+                        __builtin_amdgcn_sched_barrier(0);
                     }
                 }
-                if (u + 1 < U) {
-                    // The next unit's STEPS MFMAs spread over this unit's 32 VALU ops (fp8:
-                    // 1 MFMA, 16 VALU, 1 MFMA, 16 VALU; bf16: 1 MFMA, 4 VALU, ...); nothing
-                    // crosses into the next unit.
-#pragma unroll
-                    for (int st = 0; st < STEPS; ++st) {
-                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                        __builtin_amdgcn_sched_group_barrier(0x002, 32 / STEPS, 0);
-                    }
-                    __builtin_amdgcn_sched_barrier(0);
+                    part2[h] = (pj[0][0] + pj[0][1]) + (pj[0][2] + pj[0][3]);
+                }
+                // [tile k lanes 0-31, tile k + 1 lanes 0-31] + [tile k lanes 32-63, tile k + 1 lanes 32-63].
+                const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_int(part2[0]), __float_as_int(part2[1]),
+                                                                 false, false);
+                const float total = __int_as_float(sw[0]) + __int_as_float(sw[1]);
+                const uint32_t key = sortable_key(bf16_bits_half_away(total * ks));
+                lds_write_b16(keya + (k + g) * 64, key);
+                if (t0 + 32 * g + n < vis[0]) {
+                    const uint32_t bin = key >> 8;
+                    lds_add_u32(hista + (bin & 127) * 4, 1u << (16 * (bin >> 7)));
                 }
             }
-            // Two rows finish together: after the swap, lanes 0-31 hold row 0's total for
-            // token n and lanes 32-63 row 1's (each the sum of the two lane halves' heads).
-            // One row: both halves hold its total.
-            const float part0 = (pj[0][0] + pj[0][1]) + (pj[0][2] + pj[0][3]);
-            float mine = part0, other = part0;
-            if constexpr (kPfRowsPerWave == 2) {
-                const float part1 = (pj[1][0] + pj[1][1]) + (pj[1][2] + pj[1][3]);
-                mine = g == 0 ? part0 : part1;
-                other = g == 0 ? part1 : part0;
-            }
-            const auto swapped =
-                __builtin_amdgcn_permlane32_swap(__float_as_int(other), __float_as_int(other), false, false);
-            const float total = mine + __int_as_float(g == 0 ? swapped[1] : swapped[0]);
-            const uint32_t key = sortable_key(bf16_bits_half_away(total * ks));
-            if (kPfRowsPerWave == 2 || g == 0) lds_write_b16(keya + k * 64, key);
-            if (t0 + n < vis_mine) {
-                // Bins b and b ^ 128 share a word: the populated bins of a row are adjacent
-                // and would otherwise serialise on one word's atomics.
-                const uint32_t bin = key >> 8;
-                lds_add_u32(hista + (bin & 127) * 4, 1u << (16 * (bin >> 7)));
+        } else {
+    #pragma unroll 1
+            for (int k = 0; k < kPfTiles; ++k) {
+                const int t0 = cstart + k * 32;
+                if (t0 >= vis_max_wave) break;  // uniform per wave: later tiles are masked too
+                v4i kb[NV];
+                float ks_raw;
+                const uint32_t toff = buf * kKBuf + k * 32 * kRowBytes;
+                if constexpr (ELEM == 1) {
+                    lds_read_tile(ka[0] + toff, ka[1] + toff, ka[2] + toff, ka[3] + toff, ksa + buf * kSBuf + k * 128, kb,
+                                  ks_raw);
+                } else {
+                    lds_read_tile8(ka, toff, ksa + buf * kSBuf + k * 128, kb, ks_raw);
+                }
+                const float ks = ks_raw * (k < kPfTiles / 2 ? page_ok0 : page_ok1);
+                // Units u = (row q = u / MT, head tile mt = u % MT), two dependent K-slice MFMAs
+                // each. Unit u+1's MFMAs are issued between the 32 VALU ops (ReLU, weight FMA) of
+                // unit u's epilogue so that the matrix core and the VALU work side by side.
+                constexpr int U = kPfRowsPerWave * MT;
+                float pj[kPfRowsPerWave][4];
+    #pragma unroll
+                for (int q = 0; q < kPfRowsPerWave; ++q) pj[q][0] = pj[q][1] = pj[q][2] = pj[q][3] = 0.f;
+                v16f acc[2];
+                acc[0] = v16f{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    #pragma unroll
+                for (int st = 0; st < STEPS; ++st) Mma<ELEM>::step(st, qa[0][0], kb, acc[0]);
+                __builtin_amdgcn_sched_barrier(0);
+    #pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const int q = u / MT, mt = u % MT;
+                    v16f& cur = acc[u & 1];
+                    v16f& nxt = acc[(u + 1) & 1];
+                    if (u + 1 < U) {
+                        nxt = v16f{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    #pragma unroll
+                        for (int st = 0; st < STEPS; ++st) Mma<ELEM>::step(st, qa[(u + 1) / MT][(u + 1) % MT], kb, nxt);
+                    }
+    #pragma unroll
+                    for (int r4 = 0; r4 < 4; ++r4) {
+    #pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            const float relu = __int_as_float(max(__float_as_int(cur[r4 * 4 + j]), 0));
+                            pj[q][j] = fmaf(relu, wr[q][mt * 16 + r4 * 4 + j], pj[q][j]);
+                        }
+                    }
+                    if (u + 1 < U) {
+                        // The next unit's STEPS MFMAs spread over this unit's 32 VALU ops (fp8:
+                        // 1 MFMA, 16 VALU, 1 MFMA, 16 VALU; bf16: 1 MFMA, 4 VALU, ...); nothing
+                        // crosses into the next unit.
+    #pragma unroll
+                        for (int st = 0; st < STEPS; ++st) {
+                            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                            __builtin_amdgcn_sched_group_barrier(0x002, 32 / STEPS, 0);
+                        }
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                }
+                // Two rows finish together: after the swap, lanes 0-31 hold row 0's total for
+                // token n and lanes 32-63 row 1's (each the sum of the two lane halves' heads).
+                // One row: both halves hold its total.
+                const float part0 = (pj[0][0] + pj[0][1]) + (pj[0][2] + pj[0][3]);
+                float mine = part0, other = part0;
+                if constexpr (kPfRowsPerWave == 2) {
+                    const float part1 = (pj[1][0] + pj[1][1]) + (pj[1][2] + pj[1][3]);
+                    mine = g == 0 ? part0 : part1;
+                    other = g == 0 ? part1 : part0;
+                }
+                const auto swapped =
+                    __builtin_amdgcn_permlane32_swap(__float_as_int(other), __float_as_int(other), false, false);
+                const float total = mine + __int_as_float(g == 0 ? swapped[1] : swapped[0]);
+                const uint32_t key = sortable_key(bf16_bits_half_away(total * ks));
+                if (kPfRowsPerWave == 2 || g == 0) lds_write_b16(keya + k * 64, key);
+                if (t0 + n < vis_mine) {
+                    // Bins b and b ^ 128 share a word: the populated bins of a row are adjacent
+                    // and would otherwise serialise on one word's atomics.
+                    const uint32_t bin = key >> 8;
+                    lds_add_u32(hista + (bin & 127) * 4, 1u << (16 * (bin >> 7)));
+                }
             }
         }
         // Flush the chunk's keys of the wave's rows (8-byte stores, inside the row stride).
