@@ -6,7 +6,8 @@ correctness.py:329-330) and, tighter, a maximum absolute error below 3e-3; rows 
 valid index give zeros; bad positions are reported in status. Three sources of rows: a paged
 cache with random indices (8, 16, 40, 72 and 128 heads: one head group per workgroup, two
 groups sharing each staged tile, a set whose second group holds no heads; absent and repeated
-indices), the gathered
+indices; and, with enough rows that no index split is needed, 256 rows at 16 heads and 128
+rows at 128 heads, whose workgroups write the normalised output themselves), the gathered
 buffer of the contiguous LIFetch forward, and the resident hot cache addressed by the slot
 outputs (the reference's check_sfa flow: slots from the round, values from the logical
 tokens' payload)."""
@@ -65,6 +66,33 @@ def test_sparse_attention_paged_matches_oracle(torch_gpu, heads, rpr):
         want[r] = sfa.sparse_attention(qh[r], h_kv[table[r // rpr][t // 128], t % 128], SCALE)
     check(out, want, f"paged h{heads}")
     assert not out[rows - 1].any()
+
+
+@pytest.mark.parametrize("heads,rows", [(16, 256), (128, 128)])
+def test_sparse_attention_unsplit_rows_match_oracle(torch_gpu, heads, rows):
+    """Enough rows that the launch fills the GPU without index splits: each workgroup
+    normalises and writes its heads' output itself (no partials, no merge launch), for
+    the 16-head kernel and for the kernel of four waves per 32 heads."""
+    torch = torch_gpu
+    rng = np.random.default_rng(heads + rows)
+    say(f"case unsplit heads={heads} rows={rows}")
+    blocks, max_blocks = 40, 20
+    h_kv = np.concatenate([sfa.kv_payload(int(b % 3), np.arange(128) + b * 128) for b in range(blocks)])
+    h_kv = h_kv.reshape(blocks, 128, ROW)
+    table = np.stack([rng.permutation(blocks)[:max_blocks] for _ in range(rows)]).astype(np.int32)
+    idx = rng.integers(0, max_blocks * 128, (rows, TOPK)).astype(np.int32)
+    idx[rng.random((rows, TOPK)) < 0.75] = -1
+    q, qh = bf16_query(torch, rng, rows, heads)
+    out = sparse_attention(q, torch.from_numpy(h_kv).cuda(), torch.from_numpy(table).cuda(),
+                           torch.from_numpy(idx).cuda(), SCALE).cpu().numpy()
+    for r in range(rows):
+        t = idx[r][idx[r] >= 0]
+        want = sfa.sparse_attention(qh[r], h_kv[table[r][t // 128], t % 128], SCALE)
+        if r % 32 == 0:
+            say(f"  row {r}: max abs error {float(np.max(np.abs(out[r] - want))):.2e}")
+        assert np.all(np.isfinite(out[r])), r
+        assert np.allclose(out[r], want, atol=0.006, rtol=0.025), r
+        assert float(np.max(np.abs(out[r] - want))) < 3e-3, r
 
 
 def test_sparse_attention_reports_bad_positions(torch_gpu):
