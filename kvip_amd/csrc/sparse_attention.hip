@@ -11,9 +11,9 @@
 // i.e. softmax attention with bf16 probabilities in the value product (the reference rounds
 // the normalised probabilities to bf16; here the unnormalised ones, divided once at the end).
 //
-// One workgroup per (query row, set of one or two groups of 16 heads, split of the 2048
-// indices) resolves its indices to cache rows once (block table), then streams them in tiles
-// of 64 tokens: a tile's rows are gathered into registers while the previous tile is computed,
+// Up to 32 heads, one workgroup per (query row, set of one or two groups of 16 heads, split
+// of the 2048 indices) resolves its indices to cache rows once (block table), then streams them
+// in tiles of 64 tokens: a tile's rows are gathered into registers while the previous tile is computed,
 // dequantised to bf16 in LDS with the hardware conversions (v_cvt_pk_f32_fp8, OCP e4m3 on
 // gfx950, and v_cvt_pk_bf16_f32) once for every head group of the set, the logits of the
 // tile come from bf16 MFMA
@@ -22,6 +22,8 @@
 // features x 32 tokens) accumulated in registers. Splits (up to 8, enough workgroups to fill
 // the chip) leave (max, sum, unnormalised output) per head in the workspace and a second
 // launch merges them. HBM traffic is one read of each selected row plus the partials.
+// More than 32 heads run on sparse_attention_pair_kernel (groups of four waves per 32 heads,
+// 32x32x16 MFMAs, described there), which leaves the same partial records.
 #include "kvip_device.h"
 
 namespace kvip {
