@@ -570,6 +570,12 @@ def sfa_leg(torch, kvip_amd, device, seed, iters=20):
     for layout, per_row in (("gathered", TOPK), ("hot_cache", 16384)):
         blocks = rows * per_row // 128
         kv = torch.randint(0, 256, (blocks, 128, 656), generator=gen, device=device, dtype=torch.uint8) & 0x77
+        # Finite rope features and key scales (as random bytes they would be arbitrary bf16 and
+        # fp32 values, up to ~2^112, whose logits overflow fp32).
+        rope = (torch.rand((blocks, 128, 64), generator=gen, device=device) * 2 - 1).to(torch.bfloat16)
+        kv[:, :, 512:640] = rope.view(torch.uint8).view(blocks, 128, 128)
+        scales = torch.rand((blocks, 128, 4), generator=gen, device=device) * 0.01 + 0.001
+        kv[:, :, 640:656] = scales.view(torch.uint8).view(blocks, 128, 16)
         table = (torch.arange(rows, dtype=torch.int32, device=device)[:, None] * (per_row // 128) +
                  torch.arange(per_row // 128, dtype=torch.int32, device=device)[None, :]).contiguous()
         if per_row == TOPK:

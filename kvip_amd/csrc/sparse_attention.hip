@@ -422,6 +422,7 @@ __global__ __launch_bounds__(GROUPS * SPLIT * 64, 1) void sparse_attention_pair_
     __shared__ __align__(16) uint16_t s_vt[kValueDim * kPrVPitch];  // values, feature-major
     __shared__ __align__(16) float s_x[GROUPS * SPLIT][16][64];      // each wave's part of the logits
     __shared__ __align__(16) float s_h[GROUPS * SPLIT][32];          // per-head values for the O layout
+    __shared__ __align__(16) float s_y[GROUPS][16][64];              // the group's summed logits
     __shared__ int32_t s_row[kTopK];
 
     const int pairs_needed = (p.heads + 31) / 32;
@@ -591,15 +592,25 @@ __global__ __launch_bounds__(GROUPS * SPLIT * 64, 1) void sparse_attention_pair_
         }
         __syncthreads();  // every part's logits in s_x
         if (live) {
+            // Wave hf of the group sums logits 16 / SPLIT * hf .. of every lane (parts in
+            // group order) and shares them.
+#pragma unroll
+            for (int i0 = 0; i0 < 16 / SPLIT; ++i0) {
+                const int i = (16 / SPLIT) * hf + i0;
+                float s = s_x[w - hf][i][lane];
+#pragma unroll
+                for (int j = 1; j < SPLIT; ++j) s += s_x[w - hf + j][i][lane];
+                s_y[w / SPLIT][i][lane] = s;
+            }
+        }
+        __syncthreads();  // the group's summed logits in s_y
+        if (live) {
             float mx = -INFINITY;
             const bool all_valid = vmask == 0xFFFFFFFFu;
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 // The parts summed in group order: the same value in every wave of the group.
-                float s = s_x[w - hf][i][lane];
-#pragma unroll
-                for (int j = 1; j < SPLIT; ++j) s += s_x[w - hf + j][i][lane];
-                s *= p.scale;
+                float s = s_y[w / SPLIT][i][lane] * p.scale;
                 if (!all_valid && !((vmask >> (8 * (i >> 2) + 4 * g + (i & 3))) & 1u)) s = -INFINITY;
                 sv[i] = s;
                 mx = fmaxf(mx, s);
