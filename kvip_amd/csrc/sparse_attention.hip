@@ -13,13 +13,15 @@
 //
 // Up to 32 heads, one workgroup per (query row, set of one or two groups of 16 heads, split
 // of the 2048 indices) resolves its indices to cache rows once (block table), then streams them
-// in tiles of 64 tokens: a tile's rows are gathered into registers while the previous tile is computed,
-// dequantised to bf16 in LDS with the hardware conversions (v_cvt_pk_f32_fp8, OCP e4m3 on
-// gfx950, and v_cvt_pk_bf16_f32) once for every head group of the set, the logits of the
-// tile come from bf16 MFMA
+// in tiles of 64 tokens: a tile's rows are gathered into registers two tiles ahead,
+// dequantised to bf16 with the hardware conversions (v_cvt_pk_f32_fp8, OCP e4m3 on gfx950,
+// and v_cvt_pk_bf16_f32) into one of two token-major LDS tile buffers once for every head
+// group of the set, the logits of the tile come from bf16 MFMA
 // (v_mfma_f32_16x16x32_bf16: 16 heads x 16 tokens x 32 features), an online softmax keeps the
 // running maximum and sum per head, and the value product is a second MFMA (16 heads x 16
-// features x 32 tokens) accumulated in registers. Splits (up to 8, enough workgroups to fill
+// features x 32 tokens) accumulated in registers, its value fragments (8 tokens of one
+// feature per lane) read from the same key tile by gfx950's transpose loads
+// (ds_read_b64_tr_b16); the next tile is staged beside it. Splits (up to 8, enough workgroups to fill
 // the chip) leave (max, sum, unnormalised output) per head in the workspace and a second
 // launch merges them. HBM traffic is one read of each selected row plus the partials.
 // More than 32 heads run on sparse_attention_pair_kernel (groups of four waves per 32 heads,
@@ -33,6 +35,8 @@ typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
 typedef __attribute__((ext_vector_type(4))) float f32x4;
 typedef __attribute__((ext_vector_type(2))) float f32x2;
 typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef short v8s __attribute__((ext_vector_type(8)));
 
 constexpr int kSaThreads = 256;
 constexpr int kSaTile = 64;                 // tokens per tile
@@ -42,12 +46,6 @@ constexpr int kValueDim = 512;
 constexpr int kPieces = KVIP_KV_ROW_BYTES / 16;  // 41 pieces of a row, the last holds the scales
 constexpr int kPitch = kKeyDim + 8;         // bf16 per LDS key row (16 bytes of padding)
 constexpr int kPPitch = kSaTile + 8;        // bf16 per LDS probability row
-constexpr int kVtPitch = kSaTile + 8;       // bf16 per LDS value row (feature-major, one row per feature)
-// 16-byte token-group slot of value row f holding tokens 8 tg .. 8 tg + 7: XOR-swizzled by the
-// row's 16-feature block, so that the staging writes (8 lanes: one token group, features 16
-// apart) and the fragment reads (16 lanes: consecutive features, one token group) each hit
-// distinct banks.
-KVIP_DEVICE int vt_slot(int f, int tg) { return (tg ^ ((f >> 4) & 7)) * 8; }
 constexpr int kTokGroup = 8;  // tokens staged per thread
 constexpr int kPartial = 2 * kSaHeads + kSaHeads * kValueDim;  // floats per split: max, sum, output
 constexpr int kMaxSplits = 8;
@@ -119,8 +117,7 @@ template <int G>
 __global__ __launch_bounds__(kSaThreads * G, 1) void sparse_attention_kernel(const KvipSparseAttnArgs p) {
     constexpr int kThreads = kSaThreads * G;
     constexpr int kFeat = 16 / G;  // nope features per thread and token (16-byte or 8-byte pieces)
-    __shared__ __align__(16) uint16_t s_k[kSaTile * kPitch];         // keys, token-major
-    __shared__ __align__(16) uint16_t s_vt[kValueDim * kVtPitch];    // values, feature-major
+    __shared__ __align__(16) uint16_t s_k[2][kSaTile * kPitch];      // keys, token-major, two tiles
     __shared__ __align__(16) uint16_t s_p[G][kSaHeads * kPPitch];
     __shared__ float s_red[G][4][kSaHeads];
     __shared__ int32_t s_row[kTopK];  // cache row (block * 128 + offset) of each index, -1 = none
@@ -192,8 +189,8 @@ __global__ __launch_bounds__(kSaThreads * G, 1) void sparse_attention_kernel(con
     // Staging map: thread (token group tg, nope slice pc) holds kFeat nope features
     // [16 pc' + kFeat h, + kFeat) of the 8 tokens 8 tg .. 8 tg + 7 (pc' = pc % 32, h = the
     // thread's half of the piece when two workgroup halves share it), and the tile's 512
-    // rope pieces are dealt over every thread. The next tile's pieces are requested right
-    // after the current tile is staged, so that their latency passes under its MFMA work.
+    // rope pieces are dealt over every thread. Tile k + 2's pieces are requested right after
+    // tile k + 1 is staged (during tile k), so that their latency passes under a whole tile.
     const int tg = (tid >> 5) & 7, pc = tid & 31, half = tid >> 8;
     const int f0 = pc * 16 + half * kFeat;  // first nope feature of the thread
     constexpr int kRope = kSaTile * 8 / kThreads;
@@ -224,64 +221,56 @@ __global__ __launch_bounds__(kSaThreads * G, 1) void sparse_attention_kernel(con
             rope[j] = row >= 0 ? *reinterpret_cast<const v4i*>(row_base(row) + 512 + (q & 7) * 16) : v4i{0, 0, 0, 0};
         }
     };
-    // Dequantisation to bf16: keys [nope * scale, rope] token-major in s_k, values
-    // nope * scale feature-major in s_vt (the 8-token block transposed in registers).
-    auto stage_tile = [&]() {
-        uint32_t out[kTokGroup][kFeat / 2];  // out[u][k]: features f0 + 2k, 2k + 1 of token u
+    // Dequantisation to bf16: keys [nope * scale, rope] token-major into tile buffer kb. The
+    // values are the same nope * scale features, read feature-wise by the transpose loads.
+    auto stage_tile = [&](uint16_t* kb) {
 #pragma unroll
         for (int u = 0; u < kTokGroup; ++u) {
+            uint32_t out[kFeat / 2];  // features f0 + 2k, 2k + 1
 #pragma unroll
             for (int k = 0; k < kFeat / 4; ++k) {
                 const f32x2 a = __builtin_amdgcn_cvt_pk_f32_fp8(nope[u][k], false);
                 const f32x2 c = __builtin_amdgcn_cvt_pk_f32_fp8(nope[u][k], true);
-                out[u][2 * k] = pack_bf16(a[0] * sc[u], a[1] * sc[u]);
-                out[u][2 * k + 1] = pack_bf16(c[0] * sc[u], c[1] * sc[u]);
+                out[2 * k] = pack_bf16(a[0] * sc[u], a[1] * sc[u]);
+                out[2 * k + 1] = pack_bf16(c[0] * sc[u], c[1] * sc[u]);
             }
-            uint16_t* d = s_k + (tg * kTokGroup + u) * kPitch + f0;
+            uint16_t* d = kb + (tg * kTokGroup + u) * kPitch + f0;
             if constexpr (kFeat == 16) {
-                reinterpret_cast<v4i*>(d)[0] = v4i{static_cast<int>(out[u][0]), static_cast<int>(out[u][1]),
-                                                   static_cast<int>(out[u][2]), static_cast<int>(out[u][3])};
-                reinterpret_cast<v4i*>(d)[1] = v4i{static_cast<int>(out[u][4]), static_cast<int>(out[u][5]),
-                                                   static_cast<int>(out[u][6]), static_cast<int>(out[u][7])};
+                reinterpret_cast<v4i*>(d)[0] = v4i{static_cast<int>(out[0]), static_cast<int>(out[1]),
+                                                   static_cast<int>(out[2]), static_cast<int>(out[3])};
+                reinterpret_cast<v4i*>(d)[1] = v4i{static_cast<int>(out[4]), static_cast<int>(out[5]),
+                                                   static_cast<int>(out[6]), static_cast<int>(out[7])};
             } else {
-                *reinterpret_cast<v4i*>(d) = v4i{static_cast<int>(out[u][0]), static_cast<int>(out[u][1]),
-                                                 static_cast<int>(out[u][2]), static_cast<int>(out[u][3])};
+                *reinterpret_cast<v4i*>(d) = v4i{static_cast<int>(out[0]), static_cast<int>(out[1]),
+                                                 static_cast<int>(out[2]), static_cast<int>(out[3])};
             }
-        }
-#pragma unroll
-        for (int k = 0; k < kFeat / 2; ++k) {
-            uint32_t lo[4], hi[4];  // tokens (2 m, 2 m + 1) of feature f0 + 2k (lo) and + 1 (hi)
-#pragma unroll
-            for (int m = 0; m < 4; ++m) {
-                const uint32_t x = out[2 * m][k], y = out[2 * m + 1][k];
-                lo[m] = (x & 0xFFFFu) | (y << 16);
-                hi[m] = (x >> 16) | (y & 0xFFFF0000u);
-            }
-            const int f = f0 + 2 * k;
-            *reinterpret_cast<v4i*>(s_vt + f * kVtPitch + vt_slot(f, tg)) =
-                v4i{static_cast<int>(lo[0]), static_cast<int>(lo[1]), static_cast<int>(lo[2]), static_cast<int>(lo[3])};
-            *reinterpret_cast<v4i*>(s_vt + (f + 1) * kVtPitch + vt_slot(f + 1, tg)) =
-                v4i{static_cast<int>(hi[0]), static_cast<int>(hi[1]), static_cast<int>(hi[2]), static_cast<int>(hi[3])};
         }
 #pragma unroll
         for (int j = 0; j < kRope; ++j) {
             const int q = j * kThreads + tid;
-            *reinterpret_cast<v4i*>(s_k + (q >> 3) * kPitch + 512 + (q & 7) * 8) = rope[j];
+            *reinterpret_cast<v4i*>(kb + (q >> 3) * kPitch + 512 + (q & 7) * 8) = rope[j];
         }
     };
+    // Transpose-load address of this lane within a tile: in 16-lane block lg, lane lr reads 4
+    // features of one token and receives one feature (lr) of 4 consecutive tokens, i.e. block lg
+    // covers tokens 8 lg + 4 j .. + 4 (j = 0, 1: two loads) of 16 features: the B operand lane
+    // (feature lr, tokens 8 lg .. + 8) of the value MFMA.
+    const int tr_off = (8 * lg + (lr >> 2)) * kPitch + 4 * (lr & 3);
 
     const int tiles = span / kSaTile;
     load_tile(0);
+    stage_tile(s_k[0]);
+    if (tiles > 1) load_tile(1);
+    __syncthreads();  // s_k[0] holds tile 0
     for (int k = 0; k < tiles; ++k) {
-        stage_tile();
-        __syncthreads();  // s_k / s_vt hold tile k
-        if (k + 1 < tiles) load_tile(k + 1);
+        const uint16_t* kt = s_k[k & 1];
+        const bool more = k + 1 < tiles;
         const bool tok_live = s_row[k * kSaTile + w * 16 + lr] >= 0;
         // Logits of tokens 16 w .. 16 w + 15: lane holds heads 4 lg + i of token 16 w + lr.
         float lg_v[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
         if (live) {
             f32x4 sv = f32x4{0.f, 0.f, 0.f, 0.f};
-            const uint16_t* kr = s_k + (w * 16 + lr) * kPitch + lg * 8;
+            const uint16_t* kr = kt + (w * 16 + lr) * kPitch + lg * 8;
 #pragma unroll
             for (int s = 0; s < kKeyDim / 32; ++s) {
                 const bf16x8 kv = as_bf16x8(*reinterpret_cast<const v4i*>(kr + s * 32));
@@ -324,13 +313,25 @@ __global__ __launch_bounds__(kSaThreads * G, 1) void sparse_attention_kernel(con
                 // B fragment: tokens ks * 32 + 8 lg .. + 8 of feature 128 w + 16 t + lr.
 #pragma unroll
                 for (int t = 0; t < 8; ++t) {
-                    const int f = w * 128 + t * 16 + lr;
-                    const v4i vb = *reinterpret_cast<const v4i*>(s_vt + f * kVtPitch + vt_slot(f, ks * 4 + lg));
-                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, as_bf16x8(vb), acc[t], 0, 0, 0);
+                    const uint16_t* vr = kt + tr_off + ks * 32 * kPitch + w * 128 + t * 16;
+                    const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)(vr));
+                    const v4s hi =
+                        __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)(vr + 4 * kPitch));
+                    const bf16x8 vb = __builtin_bit_cast(bf16x8, v8s{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
+                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, vb, acc[t], 0, 0, 0);
                 }
             }
+            // The next tile's staging beside this tile's value MFMAs, then the loads of the
+            // tile after it.
+            if (more) {
+                stage_tile(s_k[(k + 1) & 1]);
+                if (k + 2 < tiles) load_tile(k + 2);
+            }
+        } else if (more) {
+            stage_tile(s_k[(k + 1) & 1]);
+            if (k + 2 < tiles) load_tile(k + 2);
         }
-        __syncthreads();  // s_k, s_vt and s_p are rewritten by the next tile
+        __syncthreads();  // tile k + 1 staged; tile k's buffer and s_p free
     }
 
     // Row sums: over the 16 lanes of a group, then over the group's waves; then this split's
@@ -388,21 +389,18 @@ __global__ __launch_bounds__(kSaThreads * G, 1) void sparse_attention_kernel(con
 // one fixed order (the same sum in every wave of the group), and all run the identical online
 // softmax. The probabilities leave the MFMA output in the layout of the value product's A
 // operand (lane: one head, 8 tokens), so they go straight into the second MFMA, in which each
-// wave accumulates 512 / SPLIT of the value features (blocks of 32). The running maximum is rescaled
+// wave accumulates 512 / SPLIT of the value features (blocks of 32). The values are the key
+// tile's nope features: the value MFMA's B operand (8 tokens of one feature per lane) comes
+// from the token-major key tile by gfx950's transpose loads (ds_read_b64_tr_b16), so a tile
+// is dequantised and written to LDS once, and two tile buffers let the next tile be staged
+// beside this tile's value MFMAs (three barriers per tile). The running maximum is rescaled
 // lazily: only when a tile's maximum exceeds it by kPrMargin (the probabilities are then
 // at most e^kPrMargin, well inside bf16 and fp32), which after the first tiles of a row
 // is rare, so the 128 accumulators per lane are seldom touched outside the MFMAs.
-typedef int i32x2 __attribute__((ext_vector_type(2)));
 constexpr int kPrTile = 32;                  // tokens per tile
 constexpr int kPrKPitch = kKeyDim + 8;       // bf16 per K row: an odd number of 16-byte units
-constexpr int kPrVPitch = kPrTile + 4;       // bf16 per value row (feature-major)
 constexpr float kPrLog2e = 1.44269504088896341f;
 constexpr float kPrMargin = 8.0f;            // natural-log units
-
-// bf16 offset of the 4-token group q (0..7) in value row f, XOR-swizzled by f's 8-feature
-// block: the staging writes (64 lanes: features 16 pc + 8 g + c of one token group) and the
-// fragment reads (consecutive features) then spread over the banks.
-KVIP_DEVICE int pr_slot(int f, int q) { return (q ^ ((f >> 3) & 7)) * 4; }
 
 KVIP_DEVICE float lane_half_other(float x, int g) {  // x of lane l ^ 32
     const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
@@ -418,8 +416,7 @@ __global__ __launch_bounds__(GROUPS * SPLIT * 64, 1) void sparse_attention_pair_
     constexpr int kBlocks = kVPart / 32;           // value blocks of 32 features per wave
     constexpr int kTokPer = kPrTile * 32 / kThreads;  // tokens each thread stages (2 or 4)
     static_assert(kTokPer == 2 || kTokPer == 4, "staging map");
-    __shared__ __align__(16) uint16_t s_k[kPrTile * kPrKPitch];     // keys, token-major
-    __shared__ __align__(16) uint16_t s_vt[kValueDim * kPrVPitch];  // values, feature-major
+    __shared__ __align__(16) uint16_t s_k[2][kPrTile * kPrKPitch];  // keys, token-major, two tiles
     __shared__ __align__(16) float s_x[GROUPS * SPLIT][16][64];      // each wave's part of the logits
     __shared__ __align__(16) float s_h[GROUPS * SPLIT][32];          // per-head values for the O layout
     __shared__ __align__(16) float s_y[GROUPS][16][64];              // the group's summed logits
@@ -514,65 +511,43 @@ __global__ __launch_bounds__(GROUPS * SPLIT * 64, 1) void sparse_attention_pair_
             rope = row >= 0 ? *reinterpret_cast<const v4i*>(row_base(row) + 512 + (tid & 7) * 16) : v4i{0, 0, 0, 0};
         }
     };
-    // Dequantisation to bf16: keys [nope * scale, rope] token-major in s_k, values
-    // nope * scale feature-major in s_vt.
-    auto stage_tile = [&]() {
-        uint32_t out[kTokPer][8];  // out[u][k]: features f0 + 2k, 2k + 1 of token u
+    // Dequantisation to bf16: keys [nope * scale, rope] token-major into tile buffer d. The
+    // values are the same nope * scale features, read feature-wise by the transpose loads.
+    auto stage_tile = [&](uint16_t* kb) {
 #pragma unroll
         for (int u = 0; u < kTokPer; ++u) {
+            uint32_t out[8];  // features f0 + 2k, 2k + 1
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
                 const f32x2 a = __builtin_amdgcn_cvt_pk_f32_fp8(nope[u][k], false);
                 const f32x2 c = __builtin_amdgcn_cvt_pk_f32_fp8(nope[u][k], true);
-                out[u][2 * k] = pack_bf16(a[0] * sc[u], a[1] * sc[u]);
-                out[u][2 * k + 1] = pack_bf16(c[0] * sc[u], c[1] * sc[u]);
+                out[2 * k] = pack_bf16(a[0] * sc[u], a[1] * sc[u]);
+                out[2 * k + 1] = pack_bf16(c[0] * sc[u], c[1] * sc[u]);
             }
-            uint16_t* d = s_k + (tg * kTokPer + u) * kPrKPitch + f0;
-            reinterpret_cast<v4i*>(d)[0] = v4i{static_cast<int>(out[u][0]), static_cast<int>(out[u][1]),
-                                               static_cast<int>(out[u][2]), static_cast<int>(out[u][3])};
-            reinterpret_cast<v4i*>(d)[1] = v4i{static_cast<int>(out[u][4]), static_cast<int>(out[u][5]),
-                                               static_cast<int>(out[u][6]), static_cast<int>(out[u][7])};
-        }
-        const int t0 = tg * kTokPer;  // first token of this thread
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            // Features f0 + 2k (lo halves) and f0 + 2k + 1 (hi halves) of the thread's tokens.
-            const int f = f0 + 2 * k;
-            if constexpr (kTokPer == 2) {
-                // The wave's lane halves hold tokens 4 q + 2 g, + 1 (q = the wave) of the same
-                // 16 features: swap so that lane half g holds features f0 + 8 g .. + 8 of all
-                // four tokens, then write 8 bytes (one token group) per feature.
-                if (k >= 4) continue;
-                const int fk = f0 + 8 * g + 2 * k;
-                const auto s0 = __builtin_amdgcn_permlane32_swap(out[0][k], out[0][k + 4], false, false);
-                const auto s1 = __builtin_amdgcn_permlane32_swap(out[1][k], out[1][k + 4], false, false);
-                // Tokens 4 q + u in s_u[0], 4 q + 2 + u in s_u[1]; features fk (low halves), fk + 1.
-                const uint32_t a0 = s0[0], a1 = s1[0], b0 = s0[1], b1 = s1[1];
-                *reinterpret_cast<i32x2*>(s_vt + fk * kPrVPitch + pr_slot(fk, t0 >> 2)) =
-                    i32x2{static_cast<int>((a0 & 0xFFFFu) | (a1 << 16)), static_cast<int>((b0 & 0xFFFFu) | (b1 << 16))};
-                *reinterpret_cast<i32x2*>(s_vt + (fk + 1) * kPrVPitch + pr_slot(fk + 1, t0 >> 2)) =
-                    i32x2{static_cast<int>((a0 >> 16) | (a1 & 0xFFFF0000u)),
-                          static_cast<int>((b0 >> 16) | (b1 & 0xFFFF0000u))};
-            } else {
-                const uint32_t x0 = out[0][k], x1 = out[1][k], x2 = out[2][k], x3 = out[3][k];
-                *reinterpret_cast<i32x2*>(s_vt + f * kPrVPitch + pr_slot(f, t0 >> 2)) =
-                    i32x2{static_cast<int>((x0 & 0xFFFFu) | (x1 << 16)), static_cast<int>((x2 & 0xFFFFu) | (x3 << 16))};
-                *reinterpret_cast<i32x2*>(s_vt + (f + 1) * kPrVPitch + pr_slot(f + 1, t0 >> 2)) =
-                    i32x2{static_cast<int>((x0 >> 16) | (x1 & 0xFFFF0000u)),
-                        static_cast<int>((x2 >> 16) | (x3 & 0xFFFF0000u))};
-            }
+            uint16_t* d = kb + (tg * kTokPer + u) * kPrKPitch + f0;
+            reinterpret_cast<v4i*>(d)[0] = v4i{static_cast<int>(out[0]), static_cast<int>(out[1]),
+                                               static_cast<int>(out[2]), static_cast<int>(out[3])};
+            reinterpret_cast<v4i*>(d)[1] = v4i{static_cast<int>(out[4]), static_cast<int>(out[5]),
+                                               static_cast<int>(out[6]), static_cast<int>(out[7])};
         }
         if (tid < kPrTile * 8) {
-            *reinterpret_cast<v4i*>(s_k + (tid >> 3) * kPrKPitch + 512 + (tid & 7) * 8) = rope;
+            *reinterpret_cast<v4i*>(kb + (tid >> 3) * kPrKPitch + 512 + (tid & 7) * 8) = rope;
         }
     };
+    // Transpose-load address of this lane within a tile: in each 16-lane block (j = lane % 16)
+    // lane j reads 4 features of one token, and lane j of the result holds one feature of 4
+    // consecutive tokens: block G = lane / 16 covers features 16 (G % 2) .. + 16 of tokens
+    // 4 (G / 2) .. + 4, i.e. the B operand lane (feature n, tokens 4 g ..) of the value MFMA.
+    const int tr_off = (4 * (lane >> 5) + ((lane & 15) >> 2)) * kPrKPitch + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
     const int tiles = span / kPrTile;
     load_tile(0);
+    stage_tile(s_k[0]);
+    if (tiles > 1) load_tile(1);
+    __syncthreads();  // s_k[0] holds tile 0
     for (int k = 0; k < tiles; ++k) {
-        stage_tile();
-        __syncthreads();  // s_k / s_vt hold tile k
-        if (k + 1 < tiles) load_tile(k + 1);
+        uint16_t* kt = s_k[k & 1];
+        const bool more = k + 1 < tiles;
         // Tokens of the tile that have a row (bit t: token t).
         const uint32_t vmask =
             static_cast<uint32_t>(__ballot(lane < kPrTile && s_row[k * kPrTile + (lane & 31)] >= 0));
@@ -580,7 +555,7 @@ __global__ __launch_bounds__(GROUPS * SPLIT * 64, 1) void sparse_attention_pair_
         if (live) {
             // This wave's part of S^T: lane (head n, half g) gets tokens 8 (i / 4) + 4 g + i % 4.
             v16f acc = v16f{};
-            const uint16_t* kr = s_k + n * kPrKPitch + hf * kPartDim + g * 8;
+            const uint16_t* kr = kt + n * kPrKPitch + hf * kPartDim + g * 8;
 #pragma unroll
             for (int s = 0; s < kKSteps; ++s) {
                 const bf16x8 kv = as_bf16x8(*reinterpret_cast<const v4i*>(kr + s * 16));
@@ -652,23 +627,34 @@ __global__ __launch_bounds__(GROUPS * SPLIT * 64, 1) void sparse_attention_pair_
                                        static_cast<int>(pk[3])});
             }
             l_sum += lsum;
-            // Value product: features kVPart hf + 32 t + n; K step s2 covers tokens 16 s2 .. + 16
-            // in the probabilities' order (groups 4 s2 + g and 4 s2 + 2 + g of 4 tokens).
+            // Value product: features kVPart hf + 32 t + n; K step s2 covers tokens 16 s2 + 4 g
+            // .. + 4 and 16 s2 + 8 + 4 g .. + 4 (the probabilities' order), read from the
+            // token-major tile by two transpose loads.
 #pragma unroll
             for (int t = 0; t < kBlocks; ++t) {
-                const int f = hf * kVPart + t * 32 + n;
-                const uint16_t* vr = s_vt + f * kPrVPitch;
+                const uint16_t* vr = kt + tr_off + hf * kVPart + t * 32;
 #pragma unroll
                 for (int s2 = 0; s2 < 2; ++s2) {
-                    const i32x2 lo = *reinterpret_cast<const i32x2*>(vr + pr_slot(f, 4 * s2 + g));
-                    const i32x2 hi = *reinterpret_cast<const i32x2*>(vr + pr_slot(f, 4 * s2 + 2 + g));
-                    const bf16x8 vb = as_bf16x8(v4i{lo[0], lo[1], hi[0], hi[1]});
+                    const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (__attribute__((address_space(3))) v4s*)(vr + 16 * s2 * kPrKPitch));
+                    const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (__attribute__((address_space(3))) v4s*)(vr + (16 * s2 + 8) * kPrKPitch));
+                    const bf16x8 vb = __builtin_bit_cast(bf16x8, v8s{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
                     o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pa[s2], vb, o[t], 0, 0, 0);
                 }
             }
             o_zero = false;
+            // The next tile's staging beside this tile's value MFMAs (inside the branch, so
+            // the scheduler can interleave them), then the loads of the tile after it.
+            if (more) {
+                stage_tile(s_k[(k + 1) & 1]);
+                if (k + 2 < tiles) load_tile(k + 2);
+            }
+        } else if (more) {
+            stage_tile(s_k[(k + 1) & 1]);
+            if (k + 2 < tiles) load_tile(k + 2);
         }
-        __syncthreads();  // s_k, s_vt and s_x are rewritten by the next tile
+        __syncthreads();  // tile k + 1 staged; tile k's buffer and s_y free
     }
 
     // Probability sums of the heads (both lane halves), then the split's partial record
