@@ -381,24 +381,27 @@ __global__ __launch_bounds__(kSaThreads * G, 1) void sparse_attention_kernel(con
     report(p.status, err);
 }
 
-// More than 32 heads: groups of SPLIT waves per 32 heads. A workgroup (row, index split)
+// More than 32 heads: groups of SPLIT = 4 waves per 32 heads. A workgroup (row, index split)
 // holds GROUPS such groups (GROUPS x 32 heads), so a staged tile of 32 rows serves all of
-// them once. The SPLIT waves of a group hold the 32 heads' query fragments for 576 / SPLIT
-// key features each: each computes its part of the logits S^T (v_mfma_f32_32x32x16_bf16, the
-// tile's 32 tokens as M, the 32 heads as N), the parts are exchanged through LDS and added in
-// one fixed order (the same sum in every wave of the group), and all run the identical online
-// softmax. The probabilities leave the MFMA output in the layout of the value product's A
-// operand (lane: one head, 8 tokens), so they go straight into the second MFMA, in which each
-// wave accumulates 512 / SPLIT of the value features (blocks of 32). The values are the key
-// tile's nope features: the value MFMA's B operand (8 tokens of one feature per lane) comes
-// from the token-major key tile by gfx950's transpose loads (ds_read_b64_tr_b16), so a tile
-// is dequantised and written to LDS once, and two tile buffers let the next tile be staged
-// beside this tile's value MFMAs (three barriers per tile). The running maximum is rescaled
-// lazily: only when a tile's maximum exceeds it by kPrMargin (the probabilities are then
-// at most e^kPrMargin, well inside bf16 and fp32), which after the first tiles of a row
+// them once. Wave (th, hh) of a group computes the logits of the tile's tokens 16 th .. + 16
+// for heads 16 hh .. + 16 over all 576 features (v_mfma_f32_16x16x32_bf16, tokens as M, its 16
+// heads' query fragments as N), so no partial logits are exchanged and each logit is
+// exponentiated once: the two token halves exchange only their per-head maxima (LDS), every
+// wave of the group derives the same reference maxima for all 32 heads from them, and each
+// writes its 16 x 16 block of bf16 probabilities to LDS. For the value product each wave then
+// takes all 32 heads (v_mfma_f32_32x32x16_bf16, heads as M, probabilities read from LDS as the
+// A operand) and accumulates 512 / SPLIT of the value features (blocks of 32). The values are
+// the key tile's nope features: the value MFMA's B operand (8 tokens of one feature per lane)
+// comes from the token-major key tile by gfx950's transpose loads (ds_read_b64_tr_b16), so a
+// tile is dequantised and written to LDS once, and two tile buffers let the next tile be
+// staged beside this tile's value MFMAs (three barriers per tile). The running maximum is
+// rescaled lazily: only when a tile's maximum exceeds it by kPrMargin (the probabilities are
+// then at most e^kPrMargin, well inside bf16 and fp32), which after the first tiles of a row
 // is rare, so the 128 accumulators per lane are seldom touched outside the MFMAs.
 constexpr int kPrTile = 32;                  // tokens per tile
 constexpr int kPrKPitch = kKeyDim + 8;       // bf16 per K row: an odd number of 16-byte units
+constexpr int kPrPPitch = kPrTile + 8;       // bf16 per probability row
+typedef int i32x2 __attribute__((ext_vector_type(2)));
 constexpr float kPrLog2e = 1.44269504088896341f;
 constexpr float kPrMargin = 8.0f;            // natural-log units
 
@@ -407,19 +410,32 @@ KVIP_DEVICE float lane_half_other(float x, int g) {  // x of lane l ^ 32
     return __int_as_float(g == 0 ? sw[1] : sw[0]);
 }
 
+KVIP_DEVICE float rows4_max(float x) {  // max over lanes l, l ^ 16, l ^ 32, l ^ 48
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+KVIP_DEVICE float rows4_sum(float x) {  // sum over lanes l, l ^ 16, l ^ 32, l ^ 48
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 template <int GROUPS, int SPLIT>
 __global__ __launch_bounds__(GROUPS * SPLIT * 64, 1) void sparse_attention_pair_kernel(const KvipSparseAttnArgs p) {
+    static_assert(SPLIT == 4, "four waves per 32 heads");
     constexpr int kThreads = GROUPS * SPLIT * 64;
-    constexpr int kPartDim = kKeyDim / SPLIT;      // logit features per wave (288 or 144)
-    constexpr int kKSteps = kPartDim / 16;         // MFMA K steps per wave
+    constexpr int kKSteps = kKeyDim / 32;          // logit MFMA steps (16x16x32)
     constexpr int kVPart = kValueDim / SPLIT;      // value features per wave
     constexpr int kBlocks = kVPart / 32;           // value blocks of 32 features per wave
     constexpr int kTokPer = kPrTile * 32 / kThreads;  // tokens each thread stages (2 or 4)
     static_assert(kTokPer == 2 || kTokPer == 4, "staging map");
     __shared__ __align__(16) uint16_t s_k[2][kPrTile * kPrKPitch];  // keys, token-major, two tiles
-    __shared__ __align__(16) float s_x[GROUPS * SPLIT][16][64];      // each wave's part of the logits
+    __shared__ __align__(16) uint16_t s_p[GROUPS][32 * kPrPPitch];  // probabilities, [head][token]
+    __shared__ float s_m[GROUPS][2][32];                             // per token half: head maxima / sums
     __shared__ __align__(16) float s_h[GROUPS * SPLIT][32];          // per-head values for the O layout
-    __shared__ __align__(16) float s_y[GROUPS][16][64];              // the group's summed logits
     __shared__ int32_t s_row[kTopK];
 
     const int pairs_needed = (p.heads + 31) / 32;
@@ -434,9 +450,12 @@ __global__ __launch_bounds__(GROUPS * SPLIT * 64, 1) void sparse_attention_pair_
     const int b = r / p.rows_per_request;
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int pair = hs * GROUPS + w / SPLIT, hf = w % SPLIT;  // 32-head group, feature part
-    const bool live = pair < pairs_needed;  // uniform per wave
-    const int n = lane & 31, g = lane >> 5;
+    const int gi = w / SPLIT, hf = w % SPLIT;        // group in the workgroup, wave in the group
+    const int pair = hs * GROUPS + gi;               // 32-head group
+    const int th = hf & 1, hh = hf >> 1;             // logits of tokens 16 th .., heads 16 hh ..
+    const bool live = pair < pairs_needed;           // uniform per wave
+    const int n = lane & 31, g = lane >> 5;          // value product: head / feature n, half g
+    const int c = lane & 15, qd = lane >> 4;         // logits: head 16 hh + c, tokens 16 th + 4 qd + i
     uint32_t err = 0;
 
     // Cache rows of the split's indices, resolved once through the block table.
@@ -459,17 +478,17 @@ __global__ __launch_bounds__(GROUPS * SPLIT * 64, 1) void sparse_attention_pair_
         s_row[i] = row;
     }
 
-    // Query fragments (B operand of the logits): head 32 pair + n, features
-    // kPartDim hf + 16 k + 8 g .. + 8; heads past p.heads read as zero.
+    // Query fragments (B operand of the logits): head 32 pair + 16 hh + c, features
+    // 32 s + 8 qd .. + 8; heads past p.heads read as zero.
     bf16x8 qf[kKSteps];
     {
-        const int h = pair * 32 + n;
+        const int h = pair * 32 + 16 * hh + c;
         const bool hl = live && h < p.heads;
-        const uint16_t* q = p.query + (static_cast<size_t>(r) * p.heads + (hl ? h : 0)) * kKeyDim + hf * kPartDim + g * 8;
+        const uint16_t* q = p.query + (static_cast<size_t>(r) * p.heads + (hl ? h : 0)) * kKeyDim + qd * 8;
 #pragma unroll
-        for (int k = 0; k < kKSteps; ++k) {
-            const v4i v = hl ? *reinterpret_cast<const v4i*>(q + k * 16) : v4i{0, 0, 0, 0};
-            qf[k] = as_bf16x8(v);
+        for (int s = 0; s < kKSteps; ++s) {
+            const v4i v = hl ? *reinterpret_cast<const v4i*>(q + s * 32) : v4i{0, 0, 0, 0};
+            qf[s] = as_bf16x8(v);
         }
     }
     v16f o[kBlocks];
@@ -478,8 +497,10 @@ __global__ __launch_bounds__(GROUPS * SPLIT * 64, 1) void sparse_attention_pair_
 #pragma unroll
         for (int i = 0; i < 16; ++i) o[t][i] = 0.f;
     }
-    float m_ref = -INFINITY;  // reference maximum of head 32 pair + n (natural-log units)
-    float l_sum = 0.f;        // this lane's share of the head's probability sum
+    // Reference maxima (natural-log units) of head 16 hh + c ("own") and 16 (1 - hh) + c:
+    // every wave of the group follows all 32 heads, from the same tile maxima in the same order.
+    float m_own = -INFINITY, m_oth = -INFINITY;
+    float l_sum = 0.f;        // this lane's share of the own head's probability sum
     bool o_zero = true;       // no tile has been accumulated yet (uniform)
     __syncthreads();
 
@@ -511,7 +532,7 @@ __global__ __launch_bounds__(GROUPS * SPLIT * 64, 1) void sparse_attention_pair_
             rope = row >= 0 ? *reinterpret_cast<const v4i*>(row_base(row) + 512 + (tid & 7) * 16) : v4i{0, 0, 0, 0};
         }
     };
-    // Dequantisation to bf16: keys [nope * scale, rope] token-major into tile buffer d. The
+    // Dequantisation to bf16: keys [nope * scale, rope] token-major into tile buffer kb. The
     // values are the same nope * scale features, read feature-wise by the transpose loads.
     auto stage_tile = [&](uint16_t* kb) {
 #pragma unroll
@@ -520,9 +541,9 @@ __global__ __launch_bounds__(GROUPS * SPLIT * 64, 1) void sparse_attention_pair_
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
                 const f32x2 a = __builtin_amdgcn_cvt_pk_f32_fp8(nope[u][k], false);
-                const f32x2 c = __builtin_amdgcn_cvt_pk_f32_fp8(nope[u][k], true);
+                const f32x2 cc = __builtin_amdgcn_cvt_pk_f32_fp8(nope[u][k], true);
                 out[2 * k] = pack_bf16(a[0] * sc[u], a[1] * sc[u]);
-                out[2 * k + 1] = pack_bf16(c[0] * sc[u], c[1] * sc[u]);
+                out[2 * k + 1] = pack_bf16(cc[0] * sc[u], cc[1] * sc[u]);
             }
             uint16_t* d = kb + (tg * kTokPer + u) * kPrKPitch + f0;
             reinterpret_cast<v4i*>(d)[0] = v4i{static_cast<int>(out[0]), static_cast<int>(out[1]),
@@ -537,8 +558,9 @@ __global__ __launch_bounds__(GROUPS * SPLIT * 64, 1) void sparse_attention_pair_
     // Transpose-load address of this lane within a tile: in each 16-lane block (j = lane % 16)
     // lane j reads 4 features of one token, and lane j of the result holds one feature of 4
     // consecutive tokens: block G = lane / 16 covers features 16 (G % 2) .. + 16 of tokens
-    // 4 (G / 2) .. + 4, i.e. the B operand lane (feature n, tokens 4 g ..) of the value MFMA.
-    const int tr_off = (4 * (lane >> 5) + ((lane & 15) >> 2)) * kPrKPitch + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+    // 8 (G / 2) .. + 4 (and + 4 .. + 8 by a second load), i.e. the B operand lane (feature n,
+    // tokens 8 g .. + 8) of the value MFMA.
+    const int tr_off = (8 * g + ((lane & 15) >> 2)) * kPrKPitch + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
     const int tiles = span / kPrTile;
     load_tile(0);
@@ -546,90 +568,80 @@ __global__ __launch_bounds__(GROUPS * SPLIT * 64, 1) void sparse_attention_pair_
     if (tiles > 1) load_tile(1);
     __syncthreads();  // s_k[0] holds tile 0
     for (int k = 0; k < tiles; ++k) {
-        uint16_t* kt = s_k[k & 1];
+        const uint16_t* kt = s_k[k & 1];
         const bool more = k + 1 < tiles;
         // Tokens of the tile that have a row (bit t: token t).
         const uint32_t vmask =
             static_cast<uint32_t>(__ballot(lane < kPrTile && s_row[k * kPrTile + (lane & 31)] >= 0));
-        v16f sv;
+        float sv[4];
         if (live) {
-            // This wave's part of S^T: lane (head n, half g) gets tokens 8 (i / 4) + 4 g + i % 4.
-            v16f acc = v16f{};
-            const uint16_t* kr = kt + n * kPrKPitch + hf * kPartDim + g * 8;
+            // Logits of tokens 16 th .. + 16 (M) and heads 16 hh .. + 16 (N) over all 576
+            // features: lane (head 16 hh + c) gets tokens 16 th + 4 qd + i.
+            f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+            const uint16_t* kr = kt + (16 * th + c) * kPrKPitch + 8 * qd;
 #pragma unroll
             for (int s = 0; s < kKSteps; ++s) {
-                const bf16x8 kv = as_bf16x8(*reinterpret_cast<const v4i*>(kr + s * 16));
-                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kv, qf[s], acc, 0, 0, 0);
+                const bf16x8 kv = as_bf16x8(*reinterpret_cast<const v4i*>(kr + s * 32));
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kv, qf[s], acc, 0, 0, 0);
             }
-            sv = acc;
-#pragma unroll
-            for (int i = 0; i < 16; ++i) s_x[w][i][lane] = acc[i];
-        }
-        __syncthreads();  // every part's logits in s_x
-        if (live) {
-            // Wave hf of the group sums logits 16 / SPLIT * hf .. of every lane (parts in
-            // group order) and shares them.
-#pragma unroll
-            for (int i0 = 0; i0 < 16 / SPLIT; ++i0) {
-                const int i = (16 / SPLIT) * hf + i0;
-                float s = s_x[w - hf][i][lane];
-#pragma unroll
-                for (int j = 1; j < SPLIT; ++j) s += s_x[w - hf + j][i][lane];
-                s_y[w / SPLIT][i][lane] = s;
-            }
-        }
-        __syncthreads();  // the group's summed logits in s_y
-        if (live) {
             float mx = -INFINITY;
-            const bool all_valid = vmask == 0xFFFFFFFFu;
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                // The parts summed in group order: the same value in every wave of the group.
-                float s = s_y[w / SPLIT][i][lane] * p.scale;
-                if (!all_valid && !((vmask >> (8 * (i >> 2) + 4 * g + (i & 3))) & 1u)) s = -INFINITY;
-                sv[i] = s;
-                mx = fmaxf(mx, s);
+            for (int i = 0; i < 4; ++i) {
+                float v = acc[i] * p.scale;
+                if (!((vmask >> (16 * th + 4 * qd + i)) & 1u)) v = -INFINITY;
+                sv[i] = v;
+                mx = fmaxf(mx, v);
             }
-            mx = fmaxf(mx, lane_half_other(mx, g));  // the head's tile maximum
-            const bool need = mx > m_ref + kPrMargin;  // also the first finite maximum
-            if (__ballot(need) != 0ull) {
-                const float m_new = need ? mx : m_ref;
-                const float alpha = (m_ref == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f((m_ref - m_new) * kPrLog2e);
-                l_sum *= need ? alpha : 1.f;
+            mx = rows4_max(mx);  // the head's maximum over this wave's 16 tokens
+            if (qd == 0) s_m[gi][th][16 * hh + c] = mx;
+        }
+        __syncthreads();  // both token halves' maxima of every head in s_m
+        if (live) {
+            const float t_own = fmaxf(s_m[gi][0][16 * hh + c], s_m[gi][1][16 * hh + c]);
+            const float t_oth = fmaxf(s_m[gi][0][16 * (1 - hh) + c], s_m[gi][1][16 * (1 - hh) + c]);
+            const bool n_own = t_own > m_own + kPrMargin;  // also the first finite maximum
+            const bool n_oth = t_oth > m_oth + kPrMargin;
+            if (__ballot(n_own || n_oth) != 0ull) {  // the same decision in every wave of the group
+                const float new_own = n_own ? t_own : m_own, new_oth = n_oth ? t_oth : m_oth;
+                const float a_own = (m_own == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f((m_own - new_own) * kPrLog2e);
+                const float a_oth = (m_oth == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f((m_oth - new_oth) * kPrLog2e);
+                l_sum *= n_own ? a_own : 1.f;
                 if (!o_zero) {
-                    if (g == 0) s_h[w][n] = need ? alpha : 1.f;
-                    // Wave-local: this wave's LDS write precedes its reads.
+                    if (qd == 0) {
+                        s_h[w][16 * hh + c] = n_own ? a_own : 1.f;
+                        s_h[w][16 * (1 - hh) + c] = n_oth ? a_oth : 1.f;
+                    }
+                    // Wave-local: this wave's LDS writes precede its reads.
                     f32x4 a4[4];
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) a4[q] = *reinterpret_cast<const f32x4*>(&s_h[w][8 * q + 4 * g]);
+                    for (int qq = 0; qq < 4; ++qq) a4[qq] = *reinterpret_cast<const f32x4*>(&s_h[w][8 * qq + 4 * g]);
 #pragma unroll
                     for (int t = 0; t < kBlocks; ++t) {
 #pragma unroll
                         for (int i = 0; i < 16; ++i) o[t][i] *= a4[i >> 2][i & 3];
                     }
                 }
-                m_ref = m_new;
+                m_own = new_own;
+                m_oth = new_oth;
             }
-            const float bias = m_ref == -INFINITY ? 0.f : -m_ref * kPrLog2e;
+            const float bias = m_own == -INFINITY ? 0.f : -m_own * kPrLog2e;
+            const float p0 = __builtin_amdgcn_exp2f(fmaf(sv[0], kPrLog2e, bias));
+            const float p1 = __builtin_amdgcn_exp2f(fmaf(sv[1], kPrLog2e, bias));
+            const float p2 = __builtin_amdgcn_exp2f(fmaf(sv[2], kPrLog2e, bias));
+            const float p3 = __builtin_amdgcn_exp2f(fmaf(sv[3], kPrLog2e, bias));
+            l_sum += (p0 + p1) + (p2 + p3);
+            *reinterpret_cast<i32x2*>(s_p[gi] + (16 * hh + c) * kPrPPitch + 16 * th + 4 * qd) =
+                i32x2{static_cast<int>(pack_bf16(p0, p1)), static_cast<int>(pack_bf16(p2, p3))};
+        }
+        __syncthreads();  // the group's probabilities in s_p
+        if (live) {
+            // Value product: features kVPart hf + 32 t + n; K step s2 covers tokens 16 s2 + 8 g
+            // .. + 8 of head n (A: probabilities, B: transpose loads of the key tile).
             bf16x8 pa[2];
-            float lsum = 0.f;
 #pragma unroll
             for (int s2 = 0; s2 < 2; ++s2) {
-                uint32_t pk[4];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const float p0 = __builtin_amdgcn_exp2f(fmaf(sv[8 * s2 + 2 * j], kPrLog2e, bias));
-                    const float p1 = __builtin_amdgcn_exp2f(fmaf(sv[8 * s2 + 2 * j + 1], kPrLog2e, bias));
-                    lsum += p0 + p1;
-                    pk[j] = pack_bf16(p0, p1);
-                }
-                pa[s2] = as_bf16x8(v4i{static_cast<int>(pk[0]), static_cast<int>(pk[1]), static_cast<int>(pk[2]),
-                                       static_cast<int>(pk[3])});
+                pa[s2] = as_bf16x8(*reinterpret_cast<const v4i*>(s_p[gi] + n * kPrPPitch + 16 * s2 + 8 * g));
             }
-            l_sum += lsum;
-            // Value product: features kVPart hf + 32 t + n; K step s2 covers tokens 16 s2 + 4 g
-            // .. + 4 and 16 s2 + 8 + 4 g .. + 4 (the probabilities' order), read from the
-            // token-major tile by two transpose loads.
 #pragma unroll
             for (int t = 0; t < kBlocks; ++t) {
                 const uint16_t* vr = kt + tr_off + hf * kVPart + t * 32;
@@ -638,7 +650,7 @@ __global__ __launch_bounds__(GROUPS * SPLIT * 64, 1) void sparse_attention_pair_
                     const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
                         (__attribute__((address_space(3))) v4s*)(vr + 16 * s2 * kPrKPitch));
                     const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                        (__attribute__((address_space(3))) v4s*)(vr + (16 * s2 + 8) * kPrKPitch));
+                        (__attribute__((address_space(3))) v4s*)(vr + (16 * s2 + 4) * kPrKPitch));
                     const bf16x8 vb = __builtin_bit_cast(bf16x8, v8s{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
                     o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pa[s2], vb, o[t], 0, 0, 0);
                 }
@@ -654,22 +666,29 @@ __global__ __launch_bounds__(GROUPS * SPLIT * 64, 1) void sparse_attention_pair_
             stage_tile(s_k[(k + 1) & 1]);
             if (k + 2 < tiles) load_tile(k + 2);
         }
-        __syncthreads();  // tile k + 1 staged; tile k's buffer and s_y free
+        __syncthreads();  // tile k + 1 staged; tile k's buffer, s_m and s_p free
     }
 
-    // Probability sums of the heads (both lane halves), then the split's partial record
-    // (max, sum, unnormalised output per head) or the normalised output. Output lane
-    // (feature kVPart hf + 32 t + n) holds heads 32 pair + 8 (i / 4) + 4 g + i % 4 of o[t][i].
+    // Probability sums: over the lane's four token rows, then the two token halves; then the
+    // split's partial record (max, sum, unnormalised output per head) or the normalised
+    // output. Output lane (feature kVPart hf + 32 t + n) holds heads 32 pair + 8 (i / 4) +
+    // 4 g + i % 4 of o[t][i].
     if (live) {
-        const float l_tot = l_sum + lane_half_other(l_sum, g);
+        const float l = rows4_sum(l_sum);
+        if (qd == 0) s_m[gi][th][16 * hh + c] = l;
+    }
+    __syncthreads();
+    if (live) {
+        const float l_n = s_m[gi][0][n] + s_m[gi][1][n];  // head n of the group
         const int groups = (p.heads + kSaHeads - 1) / kSaHeads;
         if (splits > 1) {
-            if (g == 0 && hf == 0) {
+            if (hf == 0 && g == 0) {
+                // Wave 0 (hh = 0) holds head c as its own and 16 + c as the other.
                 const int h = pair * 32 + n;
                 if (h < p.heads) {
                     float* ws = p.workspace + ((static_cast<size_t>(r) * groups + h / kSaHeads) * splits + sp) * kPartial;
-                    ws[h % kSaHeads] = m_ref;
-                    ws[kSaHeads + h % kSaHeads] = l_tot;
+                    ws[h % kSaHeads] = n < 16 ? m_own : m_oth;
+                    ws[kSaHeads + h % kSaHeads] = l_n;
                 }
             }
 #pragma unroll
@@ -682,10 +701,10 @@ __global__ __launch_bounds__(GROUPS * SPLIT * 64, 1) void sparse_attention_pair_
                 for (int t = 0; t < kBlocks; ++t) ws[t * 32] = o[t][i];
             }
         } else {
-            if (g == 0) s_h[w][n] = l_tot > 0.f ? 1.f / l_tot : 0.f;
+            if (g == 0) s_h[w][n] = l_n > 0.f ? 1.f / l_n : 0.f;
             f32x4 inv[4];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) inv[q] = *reinterpret_cast<const f32x4*>(&s_h[w][8 * q + 4 * g]);
+            for (int qq = 0; qq < 4; ++qq) inv[qq] = *reinterpret_cast<const f32x4*>(&s_h[w][8 * qq + 4 * g]);
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 const int h = pair * 32 + 8 * (i >> 2) + 4 * g + (i & 3);
