@@ -47,6 +47,20 @@ KVIP_DEVICE void wave_select_bin(const uint32_t (&h)[4], uint32_t target, int& s
     above = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(best_above), top));
 }
 
+// Packed 16-bit integer operations on the two halves of a register (v_pk_sub_u16 with
+// clamp: saturating subtraction; v_pk_min_u16), written out because the compiler turns the
+// saturate-and-min idiom into two compares and selects per half.
+KVIP_DEVICE uint32_t pk_sub_sat_u16(uint32_t a, uint32_t b) {
+    uint32_t d;
+    asm("v_pk_sub_u16 %0, %1, %2 clamp" : "=v"(d) : "v"(a), "v"(b));
+    return d;
+}
+KVIP_DEVICE uint32_t pk_min_u16(uint32_t a, uint32_t b) {
+    uint32_t d;
+    asm("v_pk_min_u16 %0, %1, %2" : "=v"(d) : "v"(a), "v"(b));
+    return d;
+}
+
 struct RowSelection {
     uint32_t kth;   // the 2048th largest key
     uint32_t n_gt;  // keys above it
@@ -93,7 +107,30 @@ KVIP_DEVICE RowSelection select_row(const uint32_t (&kk)[KPT / 2], int count, in
         gtm[m] = 0u;
         eqm[m] = 0u;
     }
-    if (count > 0) {
+    if constexpr (KPT % 32 == 0) {
+        // Two keys per instruction: register i of a 32-key group is repacked to hold keys i
+        // (low half) and 16 + i (high half), so that (x - kth) saturated at 0 and then
+        // min(., 1) per half put key i's bit at bit i and key 16 + i's at bit 16 + i of the
+        // shifted result; the same with x ^ kth marks the keys that differ from kth.
+        if (count > 0) {
+            const uint32_t kth2 = r.kth * 0x00010001u, one2 = 0x00010001u;
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                uint32_t gt = 0u, ne = 0u;
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const uint32_t wa = kk[16 * m + i / 2], wb = kk[16 * m + 8 + i / 2];
+                    const uint32_t x = __builtin_amdgcn_perm(wb, wa, (i & 1) ? 0x07060302u : 0x05040100u);
+                    gt |= pk_min_u16(pk_sub_sat_u16(x, kth2), one2) << i;
+                    ne |= pk_min_u16(x ^ kth2, one2) << i;
+                }
+                const int live = count - 32 * m;  // live keys of this group
+                const uint32_t lmask = live >= 32 ? 0xFFFFFFFFu : (live <= 0 ? 0u : (1u << live) - 1u);
+                gtm[m] = gt & lmask;
+                eqm[m] = ~ne & lmask;
+            }
+        }
+    } else if (count > 0) {
 #pragma unroll
         for (int j = 0; j < KPT; ++j) {
             const uint32_t k = key_at(j);
