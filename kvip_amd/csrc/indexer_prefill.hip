@@ -17,8 +17,9 @@
 // epilogue is the decode kernel's: ReLU, head weights, head reduction, key scale, bf16
 // half-away rounding, sortable key; keys go through a per-wave LDS strip to coalesced
 // stores, and a per-workgroup 256-bin histogram of the key high byte (two 16-bit counters
-// per word: bins b and b + 128) is added to the row histograms at the end. fp8 runs two
-// workgroups per CU, bf16 one (two waves per SIMD either way).
+// per word: bins b and b + 128; bf16, whose 64 lanes add to one row, keeps four copies per
+// row) is added to the row histograms at the end. fp8 runs two workgroups per CU, bf16 one
+// (two waves per SIMD either way).
 //
 // Reference: the native prefill LI (torch_npu.npu_quant_lightning_indexer, TND layout,
 // sparse_mode 3) that the vLLM selector runs for prefill rows (python/kvip/adapters/vllm/
@@ -85,7 +86,14 @@ __global__ __launch_bounds__(PfShape<ELEM>::kThreads, 3 - ELEM) void indexer_pre
     __shared__ __align__(16) uint8_t s_k[2][kPfChunkBytes];
     __shared__ __align__(16) float s_ks[2][kPfChunk];
     __shared__ __align__(16) uint16_t s_keys[kPfWaves][kPfRowsPerWave][kPfChunk];
-    __shared__ uint32_t s_hist[kPfBlockRows][128];  // bins b (low half) and b + 128 (high half)
+    // Row histograms: bins b (low half) and b + 128 (high half) of a word. bf16 (one row per
+    // wave, all 64 lanes adding to one row) keeps kHistCopies copies per row, lane l adding to
+    // copy l % kHistCopies, so that lanes whose keys share a bin do not serialise on one word;
+    // the copies sit 144 words apart, i.e. 16 banks apart.
+    constexpr int kHistCopies = kPfRowsPerWave == 1 ? 4 : 1;
+    constexpr int kHistStride = kHistCopies > 1 ? 144 : 128;
+    constexpr int kHistWords = kHistCopies * kHistStride;
+    __shared__ uint32_t s_hist[kPfBlockRows][kHistWords];
     __shared__ int s_prefix[kPfMaxSeq + 1];
     __shared__ uint32_t s_scan[kPfWaves];
 
@@ -106,7 +114,7 @@ __global__ __launch_bounds__(PfShape<ELEM>::kThreads, 3 - ELEM) void indexer_pre
         running += static_cast<int>(total);
     }
     if (tid == 0) s_prefix[p.sequences] = running;
-    for (int i = tid; i < kPfBlockRows * 128; i += kPfThreads) (&s_hist[0][0])[i] = 0u;
+    for (int i = tid; i < kPfBlockRows * kHistWords; i += kPfThreads) (&s_hist[0][0])[i] = 0u;
     __syncthreads();
     // Work items (query block, segment), block-fastest: the launch holds one workgroup per
     // item, or fewer that stride over them (a bounded grid, for callers that run other
@@ -234,7 +242,7 @@ __global__ __launch_bounds__(PfShape<ELEM>::kThreads, 3 - ELEM) void indexer_pre
     for (int u = 0; u < NV; ++u) ka[u] = lds_addr(&s_k[0][n * kRowBytes + (((g * NV + u) ^ pf_swizzle<ELEM>(n)) * 16)]);
     const uint32_t ksa = lds_addr(&s_ks[0][n]);
     const uint32_t keya = lds_addr(&s_keys[wave][kPfRowsPerWave == 2 ? g : 0][n]);
-    const uint32_t hista = lds_addr(&s_hist[hist_row][0]);
+    const uint32_t hista = lds_addr(&s_hist[hist_row][(lane % kHistCopies) * kHistStride]);
     constexpr uint32_t kKBuf = kPfChunkBytes;          // bytes between the two K buffers
     constexpr uint32_t kSBuf = kPfChunk * 4;           // bytes between the two scale buffers
 
@@ -424,12 +432,14 @@ __global__ __launch_bounds__(PfShape<ELEM>::kThreads, 3 - ELEM) void indexer_pre
         const int rq = i >> 8;
         const int bin = i & 255;
         const int j = j0 + rq;
-        const uint32_t c = (s_hist[rq][bin & 127] >> (16 * (bin >> 7))) & 0xFFFFu;
+        uint32_t c = 0u;
+#pragma unroll
+        for (int cp = 0; cp < kHistCopies; ++cp) c += (s_hist[rq][cp * kHistStride + (bin & 127)] >> (16 * (bin >> 7))) & 0xFFFFu;
         if (j < q_len && c != 0u) atomicAdd(&p.histogram[static_cast<size_t>(q0 + j) * 256 + bin], c);
     }
     if (item + gridDim.x < n_items) {  // uniform: clear the row histograms for the next item
         __syncthreads();
-        for (int i = tid; i < kPfBlockRows * 128; i += kPfThreads) (&s_hist[0][0])[i] = 0u;
+        for (int i = tid; i < kPfBlockRows * kHistWords; i += kPfThreads) (&s_hist[0][0])[i] = 0u;
         __syncthreads();
     }
     }
