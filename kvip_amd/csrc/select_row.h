@@ -111,8 +111,9 @@ KVIP_DEVICE RowSelection select_row(const uint32_t (&kk)[KPT / 2], int count, in
         // Two keys per instruction: register i of a 32-key group is repacked to hold keys i
         // (low half) and 16 + i (high half), so that (x - kth) saturated at 0 and then
         // min(., 1) per half put key i's bit at bit i and key 16 + i's at bit 16 + i of the
-        // shifted result; the same with x ^ kth marks the keys that differ from kth.
-        if (count > 0) {
+        // shifted result; the same with x ^ kth marks the keys that differ from kth. Without a
+        // valid kth (r.ok false: kth = 0x10000, which matches no key) the masks stay empty.
+        if (count > 0 && r.ok) {
             const uint32_t kth2 = r.kth * 0x00010001u, one2 = 0x00010001u;
 #pragma unroll
             for (int m = 0; m < M; ++m) {
