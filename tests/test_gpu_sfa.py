@@ -4,8 +4,9 @@ kvip_amd.sparse_attention) against oracle/sfa.py, on the reference's KV payload 
 Bars: the reference's own tolerance for this check (allclose atol 0.006, rtol 0.025,
 correctness.py:329-330) and, tighter, a maximum absolute error below 3e-3; rows with no
 valid index give zeros; bad positions are reported in status. Three sources of rows: a paged
-cache with random indices (8, 16, 40, 72 and 128 heads: one head group per workgroup, two
-groups sharing each staged tile, a set whose second group holds no heads; absent and repeated
+cache with random indices (8, 16, 24, 40, 72 and 128 heads: one head group per workgroup, two
+groups sharing each staged tile (24: the second group partly filled), a set whose second group
+holds no heads; absent and repeated
 indices; and, with enough rows that no index split is needed, 256 rows at 16 heads and 128
 rows at 128 heads, whose workgroups write the normalised output themselves), the gathered
 buffer of the contiguous LIFetch forward, and the resident hot cache addressed by the slot
@@ -43,7 +44,7 @@ def check(got, want, label):
     assert err < 3e-3, (label, err)
 
 
-@pytest.mark.parametrize("heads,rpr", [(8, 1), (16, 2), (40, 4), (72, 2), (128, 1)])
+@pytest.mark.parametrize("heads,rpr", [(8, 1), (16, 2), (24, 1), (40, 4), (72, 2), (128, 1)])
 def test_sparse_attention_paged_matches_oracle(torch_gpu, heads, rpr):
     torch = torch_gpu
     rng = np.random.default_rng(heads)
